@@ -1,0 +1,322 @@
+"""Benchmark of the gfx950 GDN decode step (one GPU).
+
+    python bench.py [--steps K] [--warmup W] [--config NAME]
+
+A step is one decode step (T=1) over one batch, updating the fp32 state in
+place, with every input already resident in HBM.  The headline workload is
+B=256 sequences of the qk16_v32 head layout (16 q/k heads, 32 v-heads,
+K=V=128, q/k L2-norm on): 1,080,066,304 algorithmic bytes per step.  Prints
+ONE JSON line on stdout:
+
+* ``value``: whole-job throughput in GB/s of algorithmic bytes, from the
+  wall clock over K back-to-back steps;
+* ``roofline``: the decode kernel's achieved HBM GB/s, from HIP events
+  around every timed launch on the launch stream, against MI355X's 8 TB/s;
+  ``traffic`` is the measured HBM bytes per launch from the committed
+  rocprofv3 counter summary, when there is one;
+* ``b1``: per-launch kernel time at B=1 (qk16_v32, L2-norm), warm and with
+  a cold cache;
+* ``per_config``: the same kernel times for every benchmark shape and for
+  the reference's qk4_v8 definition at its workload batch sizes;
+* ``cpu_baseline``: the reference's PyTorch-eager step (the oracle's
+  loop-for-loop restatement) timed on this host's cores on a bounded sample.
+
+Algorithmic bytes per step: state read + write (B*HV*128*128*4*2), q and k
+(2*B*H*128*2), v (B*HV*128*2), output (B*HV*128*2), a and b (2*B*HV*2),
+A_log and dt_bias (2*HV*4).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+import flashinfer_competition_codebase_amd as gdn  # noqa: E402
+from flashinfer_competition_codebase_amd import _lib  # noqa: E402
+
+METRIC = ("GDN decode µs/step at B=1; achieved HBM GB/s (% of peak) at B=256")
+PEAK_HBM_GBS = 8000.0
+TRAFFIC_SUMMARY = ROOT / "profiles" / "gdn_decode_b256_qk16v32_traffic.json"
+
+# name -> (B, H, HV, use_qk_l2norm)
+CONFIGS = {
+    "b1_qk16_v32_l2": (1, 16, 32, True),
+    "b8_qk16_v32_l2": (8, 16, 32, True),
+    "b64_qk16_v32_l2": (64, 16, 32, True),
+    "b256_qk16_v32_l2": (256, 16, 32, True),
+    "b128_qk8_v32_raw": (128, 8, 32, False),
+}
+REF_BATCHES = (1, 4, 8, 16, 32, 48, 64)
+
+
+def step_bytes(B: int, H: int, HV: int, K: int = 128, V: int = 128) -> int:
+    return (B * HV * K * V * 4 * 2 + 2 * B * H * K * 2 + B * HV * V * 2
+            + B * HV * V * 2 + 2 * B * HV * 2 + 2 * HV * 4)
+
+
+def make_device_inputs(B, H, HV, device, seed):
+    """Seeded synthetic inputs generated on the device: q, k, v ~ N(0,1)
+    bf16; state ~ N(0, 0.05^2) fp32; a, b ~ N(0,1) bf16 [B,1,HV];
+    A_log = log(U[1,16]); dt_bias ~ U[-1,1]; scale = 1/sqrt(128)."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    K = V = 128
+    f = dict(device=device)
+    q = torch.randn(B, 1, H, K, generator=g, **f).to(torch.bfloat16)
+    k = torch.randn(B, 1, H, K, generator=g, **f).to(torch.bfloat16)
+    v = torch.randn(B, 1, HV, V, generator=g, **f).to(torch.bfloat16)
+    state = torch.randn(B, HV, V, K, generator=g, **f).mul_(0.05)
+    a = torch.randn(B, 1, HV, generator=g, **f).to(torch.bfloat16)
+    b = torch.randn(B, 1, HV, generator=g, **f).to(torch.bfloat16)
+    A_log = torch.log(torch.rand(HV, generator=g, **f) * 15.0 + 1.0)
+    dt_bias = torch.rand(HV, generator=g, **f) * 2.0 - 1.0
+    output = torch.empty(B, 1, HV, V, dtype=torch.bfloat16, **f)
+    return dict(q=q, k=k, v=v, state=state, A_log=A_log, a=a, dt_bias=dt_bias, b=b,
+                scale=1.0 / math.sqrt(K), output=output, new_state=state)
+
+
+def _spin(us: float) -> None:
+    """Keep the GPU busy so that the next event/kernel/event triple is queued
+    before the GPU reaches it (host launch latency stays out of the interval)."""
+    if hasattr(torch.cuda, "_sleep"):
+        torch.cuda._sleep(int(us * 2000))
+
+
+def kernel_times_us(t, l2, iters, *, cold, flush=None):
+    """Per-launch kernel durations (HIP events on the launch stream), µs."""
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
+    for i in range(iters):
+        if cold:
+            flush.add_(1)              # rewrite > L2 + MALL between launches
+        else:
+            _spin(30.0)
+        starts[i].record(stream)
+        gdn.kernel_hip(**t, use_qk_l2norm=l2)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    return [s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends)]
+
+
+def timed_steps(t, l2, steps):
+    """Wall clock over ``steps`` back-to-back launches plus per-launch events."""
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record(stream)
+        gdn.kernel_hip(**t, use_qk_l2norm=l2)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    durs = [s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends)]
+    return wall, durs
+
+
+def cpu_baseline(seconds: float):
+    """The reference's eager PyTorch step (oracle_loop, a loop-for-loop
+    restatement of solution/triton/kernel.py:72-118) on this host's cores,
+    on a bounded sample of the B=256 qk16_v32 workload: the first Bs batch
+    rows, repeated until about ``seconds`` of CPU work."""
+    from oracle.gdn_decode_oracle import make_inputs, oracle_loop
+
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    torch.set_num_threads(threads)
+    torch.set_float32_matmul_precision("highest")
+    Bs = 8
+    t = make_inputs(Bs, 16, 32, seed=1003)
+    oracle_loop(**t, use_qk_l2norm=True)           # warmup
+    reps, elapsed = 0, 0.0
+    t0 = time.perf_counter()
+    while elapsed < seconds:
+        oracle_loop(**t, use_qk_l2norm=True)
+        reps += 1
+        elapsed = time.perf_counter() - t0
+    per_step = elapsed / reps
+    t1 = make_inputs(1, 16, 32, seed=1000)
+    b1 = []
+    for _ in range(5):
+        s = time.perf_counter()
+        oracle_loop(**t1, use_qk_l2norm=True)
+        b1.append((time.perf_counter() - s) * 1e6)
+    return {
+        "value": round(step_bytes(Bs, 16, 32) / per_step / 1e9, 4),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"B={Bs} of the B=256 qk16_v32 L2-norm workload ({Bs * 32} heads), "
+                   f"{reps} steps in {elapsed:.1f} s; {per_step * 1e3:.1f} ms/step"),
+        "b1_us_per_step": round(statistics.median(b1), 1),
+        "cpu": _cpu_model(),
+    }
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _traffic():
+    if not TRAFFIC_SUMMARY.exists():
+        return None
+    try:
+        return json.loads(TRAFFIC_SUMMARY.read_text()).get("traffic_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def pmc_pass(device):
+    """Short run for rocprofv3 counter passes: a plain copy of known size
+    (calibrates FETCH_SIZE / WRITE_SIZE) and a few B=256 decode steps."""
+    n = 256 * 1024 * 1024 // 4
+    src = torch.randn(n, device=device)
+    dst = torch.empty_like(src)
+    flush = torch.empty(1 << 28, device=device)
+    for _ in range(3):
+        flush.add_(1)
+        dst.copy_(src)
+    t = make_device_inputs(256, 16, 32, device, seed=1003)
+    for _ in range(3):
+        flush.add_(1)
+        gdn.kernel_hip(**t, use_qk_l2norm=True)
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_pass": "done", "copy_bytes": n * 4,
+                      "decode_bytes": step_bytes(256, 16, 32)}), flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="b256_qk16_v32_l2", choices=list(CONFIGS))
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-per-config", action="store_true")
+    ap.add_argument("--iters", type=int, default=100,
+                    help="launches per per-config kernel-time measurement")
+    ap.add_argument("--pmc-pass", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(the decode step shards by batch or v-head with no communication)",
+              file=sys.stderr)
+        sys.exit(1)
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    _lib.get_lib()
+    if args.pmc_pass:
+        pmc_pass(device)
+        return
+
+    log = lambda *a: print(*a, file=sys.stderr, flush=True)  # noqa: E731
+    B, H, HV, l2 = CONFIGS[args.config]
+    nbytes = step_bytes(B, H, HV)
+    t = make_device_inputs(B, H, HV, device, seed=1003)
+    ns, waves, blocks = _lib.launch_shape(B, HV)
+    log(f"[bench] {args.config}: B={B} H={H} HV={HV} l2={l2} bytes/step={nbytes} "
+        f"launch ns={ns} waves={waves} blocks={blocks}")
+    for _ in range(args.warmup):
+        gdn.kernel_hip(**t, use_qk_l2norm=l2)
+    torch.cuda.synchronize()
+    wall, durs = timed_steps(t, l2, args.steps)
+    ms_per_step = wall * 1e3 / args.steps
+    value = nbytes / (wall / args.steps) / 1e9
+    kavg = statistics.fmean(durs)
+    achieved = nbytes / (kavg * 1e-6) / 1e9
+    log(f"[bench] timed {args.steps} steps: {ms_per_step * 1e3:.2f} us/step wall, "
+        f"kernel avg {kavg:.2f} us (median {statistics.median(durs):.2f}), "
+        f"{achieved:.0f} GB/s = {achieved / PEAK_HBM_GBS:.1%} of peak")
+
+    flush = torch.empty(1 << 28, device=device)    # 1 GiB > 32 MiB L2 + 256 MiB MALL
+    per_config = {}
+    if not args.no_per_config:
+        shapes = [(n, *c) for n, c in CONFIGS.items()]
+        shapes += [(f"qk4_v8_b{bb}", bb, 4, 8, False) for bb in REF_BATCHES]
+        for name, b_, h_, hv_, l2_ in shapes:
+            tc = make_device_inputs(b_, h_, hv_, device, seed=7)
+            for _ in range(5):
+                gdn.kernel_hip(**tc, use_qk_l2norm=l2_)
+            warm = kernel_times_us(tc, l2_, args.iters, cold=False)
+            cold = kernel_times_us(tc, l2_, args.iters, cold=True, flush=flush)
+            nb = step_bytes(b_, h_, hv_)
+            wm, cm = statistics.median(warm), statistics.median(cold)
+            per_config[name] = {
+                "B": b_, "H": h_, "HV": hv_, "l2norm": l2_, "bytes": nb,
+                "launch": list(_lib.launch_shape(b_, hv_)),
+                "us_warm_median": round(wm, 3), "us_cold_median": round(cm, 3),
+                "cold_hbm_gbs": round(nb / (cm * 1e-6) / 1e9, 1),
+                "cold_frac_of_peak": round(nb / (cm * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+            }
+            log(f"[bench] {name}: warm {wm:.2f} us, cold {cm:.2f} us, "
+                f"cold {per_config[name]['cold_hbm_gbs']:.0f} GB/s")
+            del tc
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(args.cpu_seconds)
+        log(f"[bench] cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads "
+            f"({cpu['sample']}); B=1 {cpu['b1_us_per_step']} us/step")
+
+    b1 = per_config.get("b1_qk16_v32_l2")
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": ("synthetic, seeded on the device: q,k,v,a,b ~ N(0,1) bf16; state ~ "
+                 "N(0,0.05^2) fp32; A_log = log U[1,16]; dt_bias ~ U[-1,1]"),
+        "config": {
+            "workload": (f"GDN decode step, qk{H}_v{HV}_d128 k-last fp32 state, B={B}, "
+                         f"T=1, q/k L2-norm {'on' if l2 else 'off'}, in-place state update"),
+            "B": B, "H": H, "HV": HV, "K": 128, "V": 128,
+            "bytes_per_step": nbytes,
+            "launch": {"rows_per_lane_group": ns, "waves_per_block": waves,
+                       "blocks": blocks},
+        },
+        "b1": ({"us_per_step_kernel_warm": b1["us_warm_median"],
+                "us_per_step_kernel_cold": b1["us_cold_median"]} if b1 else None),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": _traffic(),
+            "kernel_us_avg": round(kavg, 3),
+        },
+        "cpu_baseline": cpu,
+        "per_config": per_config,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

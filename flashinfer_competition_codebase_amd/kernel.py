@@ -1,0 +1,212 @@
+"""Python entry points of the GDN decode step, in the reference's calling forms.
+
+Two forms, with the reference's argument names so callers can pass the
+tensors as keyword arguments (``fn(**tensors)``, scripts/bench_fi_timing.py:44):
+
+* ``run(q, k, v, state, A_log, a, dt_bias, b, scale)`` -- value-returning,
+  like ``kernel_pt_reference`` (solution/triton/kernel.py:22-118): returns
+  ``(output, new_state)`` and leaves ``state`` untouched.
+* ``kernel_hip(q, k, v, state, A_log, a, dt_bias, b, scale, output,
+  new_state)`` -- destination-passing, like ``kernel_fla_recurrent``
+  (solution/triton/kernel.py:150-197) and ``kernel_cuda_v4``
+  (solution/cuda/binding.py:44-60): writes both outputs and returns None.
+  ``new_state`` may be ``state`` itself for an in-place update (the
+  aliasing FlashInfer's entry uses, solution/triton/kernel.py:128-134).
+
+Both run one launch of the gfx950 kernel in ``libgdn_decode.so`` on the
+current HIP stream of the inputs' device; there is no CPU path.  The q/k
+L2-norm is a keyword-only flag (``use_qk_l2norm``, default off as in every
+reference decode entry, solution/triton/kernel.py:146), so the positional
+signature is the reference's.
+
+Tensor contract (reference shapes, solution/triton/kernel.py:33-48 and
+scripts/profile_proton.py:106-110): q, k ``[B, 1, H, 128]`` bf16; v
+``[B, 1, HV, 128]`` bf16 with ``HV % H == 0``; state ``[B, HV, 128, 128]``
+fp32 k-last or None (zeros); A_log, dt_bias ``[HV]`` fp32; a, b
+``[B, 1, HV]`` or ``[B, HV]`` bf16; scale float, 0-d tensor, None or 0
+(None/0 mean ``1/sqrt(K)``); output ``[B, 1, HV, 128]`` bf16; new_state
+``[B, HV, 128, 128]`` fp32.  All tensors dense (contiguous) on one device.
+Unlike the reference, malformed arguments raise ``TypeError`` /
+``ValueError`` before anything is launched.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+
+K_DIM = 128
+V_DIM = 128
+
+__all__ = ["run", "kernel_hip", "kernel_hip_shaped", "resolve_scale"]
+
+
+def resolve_scale(scale, K: int = K_DIM) -> float:
+    """``scale`` as a float; None or 0 mean ``1/sqrt(K)``.
+
+    Reference: solution/triton/kernel.py:69-70 and 163-164,
+    solution/cuda/binding.py:50-53 (``float(scale)`` for tensor scalars).
+    """
+    if scale is None:
+        return 1.0 / math.sqrt(K)
+    if isinstance(scale, torch.Tensor):
+        if scale.numel() != 1:
+            raise ValueError(f"scale must be a scalar, got shape {tuple(scale.shape)}")
+        scale = scale.item()
+    scale = float(scale)
+    if scale == 0.0:
+        return 1.0 / math.sqrt(K)
+    return scale
+
+
+def _expect(t, name: str, dtype: torch.dtype, shape: tuple) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if tuple(t.shape) != shape:
+        raise ValueError(f"{name} must have shape {shape}, got {tuple(t.shape)}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _gate_shape(t, B: int, HV: int) -> tuple:
+    shape = tuple(t.shape) if isinstance(t, torch.Tensor) else None
+    return (B, 1, HV) if shape == (B, 1, HV) else (B, HV)
+
+
+def check_inputs(q, k, v, state, A_log, a, dt_bias, b, output=None, new_state=None):
+    """Validate the decode-step tensors; returns ``(B, H, HV)``.
+
+    Shape and dtype rules are the reference's (solution/triton/kernel.py:
+    33-48, 58-67 generalised to any ``HV % H == 0``); the device check comes
+    last so that every other rule can be exercised without a GPU.
+    """
+    if not isinstance(q, torch.Tensor) or q.dim() != 4:
+        raise ValueError("q must be a 4-D tensor [B, T, H, K]")
+    if not isinstance(v, torch.Tensor) or v.dim() != 4:
+        raise ValueError("v must be a 4-D tensor [B, T, HV, V]")
+    B, T, H, K = q.shape
+    HV, V = v.shape[2], v.shape[3]
+    if T != 1:
+        raise ValueError(f"decode takes one token per sequence (T == 1), got T={T}")
+    if K != K_DIM or V != V_DIM:
+        raise ValueError(f"K and V must be {K_DIM}, got K={K}, V={V}")
+    if H <= 0 or HV <= 0 or HV % H != 0:
+        raise ValueError(f"v-heads must be a multiple of q/k heads, got H={H}, HV={HV}")
+    _expect(q, "q", torch.bfloat16, (B, 1, H, K))
+    _expect(k, "k", torch.bfloat16, (B, 1, H, K))
+    _expect(v, "v", torch.bfloat16, (B, 1, HV, V))
+    if state is not None:
+        _expect(state, "state", torch.float32, (B, HV, V, K))
+    _expect(A_log, "A_log", torch.float32, (HV,))
+    _expect(dt_bias, "dt_bias", torch.float32, (HV,))
+    _expect(a, "a", torch.bfloat16, _gate_shape(a, B, HV))
+    _expect(b, "b", torch.bfloat16, _gate_shape(b, B, HV))
+    if output is not None:
+        _expect(output, "output", torch.bfloat16, (B, 1, HV, V))
+    if new_state is not None:
+        _expect(new_state, "new_state", torch.float32, (B, HV, V, K))
+    tensors = [q, k, v, A_log, a, dt_bias, b]
+    tensors += [t for t in (state, output, new_state) if t is not None]
+    dev = q.device
+    for t in tensors:
+        if t.device != dev:
+            raise ValueError(f"all tensors must be on one device, got {dev} and {t.device}")
+    if dev.type != "cuda":
+        raise ValueError(
+            f"the GDN decode kernel runs on a HIP device; got tensors on {dev}"
+        )
+    if state is not None and new_state is not None and new_state is not state:
+        if new_state.data_ptr() != state.data_ptr() and _overlap(new_state, state):
+            raise ValueError("new_state must be state itself or not overlap it")
+    return B, H, HV
+
+
+def _overlap(x: torch.Tensor, y: torch.Tensor) -> bool:
+    x0, y0 = x.data_ptr(), y.data_ptr()
+    xn, yn = x.numel() * x.element_size(), y.numel() * y.element_size()
+    return x0 < y0 + yn and y0 < x0 + xn
+
+
+def _launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
+            B, H, HV, use_qk_l2norm, shape=None):
+    lib = _lib.get_lib()
+    stream = torch.cuda.current_stream(q.device).cuda_stream
+    ptrs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), state.data_ptr(),
+            A_log.data_ptr(), a.data_ptr(), dt_bias.data_ptr(), b.data_ptr())
+    with torch.cuda.device(q.device):
+        if shape is None:
+            code = lib.gdn_decode_step(
+                *ptrs, scale, output.data_ptr(), new_state.data_ptr(),
+                B, H, HV, K_DIM, V_DIM, int(bool(use_qk_l2norm)), stream)
+            _lib.check(code, "gdn_decode_step")
+        else:
+            ns, waves, policy = shape
+            code = lib.gdn_decode_step_shaped(
+                *ptrs, scale, output.data_ptr(), new_state.data_ptr(),
+                B, H, HV, K_DIM, V_DIM, int(bool(use_qk_l2norm)),
+                int(ns), int(waves), int(policy), stream)
+            _lib.check(code, "gdn_decode_step_shaped")
+
+
+@torch.no_grad()
+def kernel_hip(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
+               *, use_qk_l2norm: bool = False):
+    """Destination-passing decode step (reference DPS form,
+    solution/triton/kernel.py:150-197; solution/cuda/binding.py:44-60).
+
+    Writes ``output`` [B, 1, HV, 128] bf16 and ``new_state``
+    [B, HV, 128, 128] fp32.  ``new_state is state`` updates in place;
+    ``state=None`` starts from zeros (solution/triton/kernel.py:83-86).
+    """
+    if output is None or new_state is None:
+        raise ValueError("kernel_hip needs preallocated output and new_state")
+    B, H, HV = check_inputs(q, k, v, state, A_log, a, dt_bias, b, output, new_state)
+    scale = resolve_scale(scale, q.shape[-1])
+    if state is None:
+        new_state.zero_()
+        state = new_state
+    if B == 0:
+        return None
+    _launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
+            B, H, HV, use_qk_l2norm)
+    return None
+
+
+@torch.no_grad()
+def kernel_hip_shaped(q, k, v, state, A_log, a, dt_bias, b, scale, output,
+                      new_state, *, use_qk_l2norm: bool = False,
+                      rows_per_lane_group: int = 4, waves_per_block: int = 4,
+                      cache_policy: int = 0):
+    """``kernel_hip`` with an explicit launch shape (for launch-shape sweeps)."""
+    B, H, HV = check_inputs(q, k, v, state, A_log, a, dt_bias, b, output, new_state)
+    scale = resolve_scale(scale, q.shape[-1])
+    if state is None:
+        new_state.zero_()
+        state = new_state
+    if B == 0:
+        return None
+    _launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
+            B, H, HV, use_qk_l2norm,
+            shape=(rows_per_lane_group, waves_per_block, cache_policy))
+    return None
+
+
+@torch.no_grad()
+def run(q, k, v, state, A_log, a, dt_bias, b, scale, *, use_qk_l2norm: bool = False):
+    """Value-returning decode step with the reference's contract
+    (``kernel_pt_reference``, solution/triton/kernel.py:22-118).
+
+    Returns ``(output [B, 1, HV, 128] bf16, new_state [B, HV, 128, 128] fp32)``;
+    ``state`` is not modified.
+    """
+    B, H, HV = check_inputs(q, k, v, state, A_log, a, dt_bias, b)
+    output = torch.empty((B, 1, HV, V_DIM), dtype=torch.bfloat16, device=q.device)
+    new_state = torch.empty((B, HV, V_DIM, K_DIM), dtype=torch.float32, device=q.device)
+    kernel_hip(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
+               use_qk_l2norm=use_qk_l2norm)
+    return output, new_state

@@ -1,0 +1,106 @@
+/*
+ * gdn_decode.h - C ABI of the MI355X (gfx950) Gated Delta Net decode step.
+ *
+ * One single-token (T=1) decode step of the gated delta rule over a batch of
+ * recurrent states, in the reference's tensor layouts:
+ *
+ *   q, k       [B, 1, H,  K]   bf16   (K = 128)
+ *   v          [B, 1, HV, V]   bf16   (V = 128, HV % H == 0, GVA ratio HV/H)
+ *   state      [B, HV, V, K]   fp32   "k-last": element (k, v) at v*K + k
+ *   A_log      [HV]            fp32
+ *   a, b       [B, 1, HV]      bf16   ([B, HV] is the same memory)
+ *   dt_bias    [HV]            fp32
+ *   output     [B, 1, HV, V]   bf16
+ *   new_state  [B, HV, V, K]   fp32   may be the same buffer as state
+ *
+ * Per (batch b, v-head hv), with h = hv / (HV / H):
+ *   g     = exp(-exp(A_log[hv]) * softplus(a[b,hv] + dt_bias[hv]))
+ *   beta  = sigmoid(b[b,hv])
+ *   q, k  = l2norm(q[b,h]), l2norm(k[b,h])     only when use_qk_l2norm != 0
+ *   S     = g * state[b,hv]
+ *   S    += k (x) beta * (v[b,hv] - S k)       rank-1 delta-rule update
+ *   output[b,hv] = bf16(scale * S q);  new_state[b,hv] = S
+ *
+ * All pointers are device pointers, dense and row-major in the shapes above.
+ * Every entry point is asynchronous on `hip_stream` (a hipStream_t, NULL for
+ * the null stream), allocates nothing, and returns 0 on success or a nonzero
+ * hipError_t code.  Arguments are validated on the host before any launch
+ * (hipErrorInvalidValue = 1 for bad sizes, null or misaligned pointers).
+ */
+#ifndef GDN_DECODE_H
+#define GDN_DECODE_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/*
+ * One decode step with the library's launch-shape choice for (B, HV).
+ *
+ * Replaces the reference's native decode entry points, which take the same
+ * eleven tensors plus `scale` and launch the fused decode kernel on the
+ * caller's current stream:
+ *   solution/cuda/kernel.cu:405-443  KernelCudaV4 / kernel_cuda_v4 (TVM FFI)
+ *   solution/cuda/kernel.cu:216-254  KernelCuda   / kernel_cuda    (TVM FFI)
+ *   solution/triton/kernel.py:150-197 kernel_fla_recurrent (Triton launch)
+ * Differences: sizes are explicit integers instead of DLPack views, K and V
+ * must be 128 (the reference hard-codes BK = 128, kernel.cu:24), the q/k
+ * L2-norm is an explicit flag (off in every reference decode entry,
+ * kernel.py:146), and bad arguments return an error instead of launching.
+ * `scale` must already be resolved (the reference's None/0 -> 1/sqrt(K)
+ * default, kernel.py:163-164, is applied by the Python caller).
+ */
+int gdn_decode_step(const void* q, const void* k, const void* v,
+                    const float* state, const float* A_log, const void* a,
+                    const float* dt_bias, const void* b, float scale,
+                    void* output, float* new_state,
+                    int B, int H, int HV, int K, int V,
+                    int use_qk_l2norm, void* hip_stream);
+
+/*
+ * The same step with an explicit launch shape: each wavefront owns
+ * 4 * rows_per_lane_group consecutive-row groups of state rows (16 lanes per
+ * row), each workgroup holds `waves_per_block` wavefronts, and a (b, hv) head
+ * is split over 128 / (4 * rows_per_lane_group * waves_per_block) workgroups.
+ * rows_per_lane_group and waves_per_block are each one of 1, 2, 4, 8 and
+ * their product is at most 32.  cache_policy selects how the state stream
+ * is accessed: 0 ordinary loads and stores, 1 nontemporal loads and stores,
+ * 2 nontemporal stores only.  Used for launch-shape sweeps.
+ * Counterpart of the reference's fixed launch choice (BV = 8 rows and
+ * num_warps = 8 if B <= 4 else 4, solution/triton/kernel.py:168-197; grid
+ * (V/8, B*HV), solution/cuda/kernel.cu:229-235,418-424).
+ */
+int gdn_decode_step_shaped(const void* q, const void* k, const void* v,
+                           const float* state, const float* A_log,
+                           const void* a, const float* dt_bias, const void* b,
+                           float scale, void* output, float* new_state,
+                           int B, int H, int HV, int K, int V,
+                           int use_qk_l2norm, int rows_per_lane_group,
+                           int waves_per_block, int cache_policy,
+                           void* hip_stream);
+
+/*
+ * Launch shape gdn_decode_step would use for (B, HV): writes
+ * rows_per_lane_group, waves_per_block and the workgroup count.
+ * Returns 0, or hipErrorInvalidValue for B < 0, HV <= 0 or null outputs.
+ * No reference counterpart (the reference's choice is inline in its
+ * wrappers, solution/triton/kernel.py:168-174).
+ */
+int gdn_decode_launch_shape(int B, int HV, int* rows_per_lane_group,
+                            int* waves_per_block, long long* num_blocks);
+
+/*
+ * Human-readable text for a return code of the functions above
+ * (hipGetErrorString).  The reference has no error path
+ * (solution/cuda/kernel.cu:216-252 never checks a launch).
+ */
+const char* gdn_decode_error_string(int code);
+
+/* ABI version of this header: 1. */
+int gdn_decode_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDN_DECODE_H */

@@ -1,0 +1,99 @@
+"""The C-ABI library loads and exports exactly what include/gdn_decode.h declares.
+
+No compute call is made: the only native calls here either query metadata or
+pass arguments that the library's host-side validation rejects before any
+HIP call.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from flashinfer_competition_codebase_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "gdn_decode.h"
+
+
+def header_functions() -> dict:
+    """name -> number of parameters, for every prototype in the header."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    protos = re.findall(r"^\s*(?:const\s+)?\w+\*?\s+(gdn_decode_\w+)\s*\(([^;]*?)\)\s*;",
+                        text, flags=re.M | re.S)
+    out = {}
+    for name, params in protos:
+        params = params.strip()
+        out[name] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_header_declares_the_abi():
+    funcs = header_functions()
+    assert set(funcs) == {"gdn_decode_step", "gdn_decode_step_shaped",
+                          "gdn_decode_launch_shape", "gdn_decode_error_string",
+                          "gdn_decode_abi_version"}
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.get_lib()
+    funcs = header_functions()
+    for name, nparams in funcs.items():
+        assert hasattr(lib, name), f"{name} missing from {_lib.LIB_PATH}"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+        assert len(_lib.SIGNATURES[name][1]) == nparams, name
+
+
+def test_abi_version_and_error_text():
+    lib = _lib.get_lib()
+    assert lib.gdn_decode_abi_version() == _lib.ABI_VERSION
+    assert _lib.error_string(1) == "invalid argument"
+
+
+def test_launch_shape_query():
+    ns, w, blocks = _lib.launch_shape(1, 32)
+    assert ns in (1, 2, 4, 8) and w in (1, 2, 4, 8)
+    assert blocks == 32 * 128 // (4 * ns * w)
+    assert _lib.launch_shape(0, 32)[2] == 0
+    with pytest.raises(RuntimeError):
+        _lib.launch_shape(-1, 32)
+
+
+def _step(lib, *, B=1, H=16, HV=32, K=128, V=128, ptr=None, new_state=None):
+    p = ptr
+    return lib.gdn_decode_step(p, p, p, p, p, p, p, p, ctypes.c_float(0.1), p,
+                               new_state if new_state is not None else p,
+                               B, H, HV, K, V, 1, None)
+
+
+def test_validation_rejects_bad_sizes_without_launching():
+    lib = _lib.get_lib()
+    assert _step(lib, K=64) == 1
+    assert _step(lib, V=256) == 1
+    assert _step(lib, H=3) == 1          # 32 % 3 != 0
+    assert _step(lib, H=0) == 1
+    assert _step(lib, B=-1) == 1
+    assert _step(lib) == 1               # null pointers
+    assert _step(lib, B=0) == 0          # empty batch: nothing to do
+    shaped = lib.gdn_decode_step_shaped
+    nulls = [None] * 8
+    assert shaped(*nulls, ctypes.c_float(0.1), None, None, 1, 16, 32, 128, 128, 1,
+                  8, 8, 0, None) == 1    # 8 x 8 > 32 rows per block
+    assert shaped(*nulls, ctypes.c_float(0.1), None, None, 1, 16, 32, 128, 128, 1,
+                  3, 1, 0, None) == 1    # not a power of two
+    assert shaped(*nulls, ctypes.c_float(0.1), None, None, 1, 16, 32, 128, 128, 1,
+                  1, 1, 3, None) == 1    # unknown cache policy
+
+
+def test_validation_rejects_misaligned_and_overlapping_state():
+    """Only on hosts without a HIP device: a validation bug here would
+    otherwise launch on made-up addresses."""
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("made-up pointers are only passed where no device exists")
+    lib = _lib.get_lib()
+    assert _step(lib, ptr=0x100002) == 1                       # 2-byte aligned
+    assert _step(lib, ptr=0x100000, new_state=0x100010) == 1   # partial overlap
