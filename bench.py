@@ -14,8 +14,9 @@ ONE JSON line on stdout:
   around every timed launch on the launch stream, against MI355X's 8 TB/s;
   ``traffic`` is the measured HBM bytes per launch from the committed
   rocprofv3 counter summary, when there is one;
-* ``b1``: per-launch kernel time at B=1 (qk16_v32, L2-norm), warm and with
-  a cold cache;
+* ``b1``: kernel time per step at B=1 (qk16_v32, L2-norm), warm and with a
+  cold cache, stamped by the kernel dispatch itself (the analogue of the
+  reference's CUPTI timings);
 * ``per_config``: the same kernel times for every benchmark shape and for
   the reference's qk4_v8 definition at its workload batch sizes;
 * ``cpu_baseline``: the reference's PyTorch-eager step (the oracle's
@@ -29,6 +30,7 @@ A_log and dt_bias (2*HV*4).
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -85,28 +87,60 @@ def make_device_inputs(B, H, HV, device, seed):
                 scale=1.0 / math.sqrt(K), output=output, new_state=state)
 
 
-def _spin(us: float) -> None:
-    """Keep the GPU busy so that the next event/kernel/event triple is queued
-    before the GPU reaches it (host launch latency stays out of the interval)."""
-    if hasattr(torch.cuda, "_sleep"):
-        torch.cuda._sleep(int(us * 2000))
+class KernelStamps:
+    """HIP events that a launch stamps with the kernel's own start and end
+    timestamps (hipExtLaunchKernelGGL through gdn_decode_step_shaped), so the
+    elapsed time is the kernel's duration, free of event-marker overhead.
+    Uses the HIP runtime already loaded by torch (same soname)."""
+
+    def __init__(self, n: int):
+        self.hip = ctypes.CDLL("libamdhip64.so.7")
+        self.start = [self._create() for _ in range(n)]
+        self.stop = [self._create() for _ in range(n)]
+
+    def _create(self):
+        ev = ctypes.c_void_p()
+        if self.hip.hipEventCreate(ctypes.byref(ev)) != 0:
+            raise RuntimeError("hipEventCreate failed")
+        return ev
+
+    def elapsed_us(self, i: int) -> float:
+        ms = ctypes.c_float()
+        if self.hip.hipEventSynchronize(self.stop[i]) != 0:
+            raise RuntimeError("hipEventSynchronize failed")
+        if self.hip.hipEventElapsedTime(ctypes.byref(ms), self.start[i], self.stop[i]) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value * 1e3
+
+    def close(self) -> None:
+        for ev in self.start + self.stop:
+            self.hip.hipEventDestroy(ev)
 
 
 def kernel_times_us(t, l2, iters, *, cold, flush=None):
-    """Per-launch kernel durations (HIP events on the launch stream), µs."""
-    stream = torch.cuda.current_stream()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
-    for i in range(iters):
-        if cold:
-            flush.add_(1)              # rewrite > L2 + MALL between launches
-        else:
-            _spin(30.0)
-        starts[i].record(stream)
-        gdn.kernel_hip(**t, use_qk_l2norm=l2)
-        ends[i].record(stream)
-    torch.cuda.synchronize()
-    return [s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends)]
+    """Per-launch kernel durations in µs, stamped by the kernel dispatch
+    itself, with the launch shape gdn_decode_step uses.
+
+    Warm: back-to-back launches.  Cold: before each launch, read a 1 GiB
+    buffer (more than the 32 MiB of L2 plus the 256 MiB MALL; a read leaves
+    no dirty lines to be written back during the timed launch), then
+    synchronize."""
+    B, HV = t["v"].shape[0], t["v"].shape[2]
+    ns, waves, policy, _ = _lib.launch_shape(B, HV)
+    stamps = KernelStamps(iters)
+    try:
+        for i in range(iters):
+            if cold:
+                flush.sum()
+                torch.cuda.synchronize()
+            gdn.kernel_hip_shaped(**t, use_qk_l2norm=l2, rows_per_lane_group=ns,
+                                  waves_per_block=waves, cache_policy=policy,
+                                  start_event=stamps.start[i].value,
+                                  stop_event=stamps.stop[i].value)
+        torch.cuda.synchronize()
+        return [stamps.elapsed_us(i) for i in range(iters)]
+    finally:
+        stamps.close()
 
 
 def timed_steps(t, l2, steps):
@@ -233,9 +267,9 @@ def main():
     B, H, HV, l2 = CONFIGS[args.config]
     nbytes = step_bytes(B, H, HV)
     t = make_device_inputs(B, H, HV, device, seed=1003)
-    ns, waves, blocks = _lib.launch_shape(B, HV)
+    ns, waves, policy, blocks = _lib.launch_shape(B, HV)
     log(f"[bench] {args.config}: B={B} H={H} HV={HV} l2={l2} bytes/step={nbytes} "
-        f"launch ns={ns} waves={waves} blocks={blocks}")
+        f"launch ns={ns} waves={waves} policy={policy} blocks={blocks}")
     for _ in range(args.warmup):
         gdn.kernel_hip(**t, use_qk_l2norm=l2)
     torch.cuda.synchronize()
@@ -248,7 +282,7 @@ def main():
         f"kernel avg {kavg:.2f} us (median {statistics.median(durs):.2f}), "
         f"{achieved:.0f} GB/s = {achieved / PEAK_HBM_GBS:.1%} of peak")
 
-    flush = torch.empty(1 << 28, device=device)    # 1 GiB > 32 MiB L2 + 256 MiB MALL
+    flush = torch.ones(1 << 28, device=device)     # 1 GiB > 32 MiB L2 + 256 MiB MALL
     per_config = {}
     if not args.no_per_config:
         shapes = [(n, *c) for n, c in CONFIGS.items()]
@@ -299,7 +333,7 @@ def main():
             "B": B, "H": H, "HV": HV, "K": 128, "V": 128,
             "bytes_per_step": nbytes,
             "launch": {"rows_per_lane_group": ns, "waves_per_block": waves,
-                       "blocks": blocks},
+                       "cache_policy": policy, "blocks": blocks},
         },
         "b1": ({"us_per_step_kernel_warm": b1["us_warm_median"],
                 "us_per_step_kernel_cold": b1["us_cold_median"]} if b1 else None),

@@ -26,11 +26,11 @@ SIGNATURES = {
     "gdn_decode_step_shaped": (
         _I,
         [_P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _I, _I, _I, _I, _I,
-         _I, _I, _I, _P],
+         _I, _I, _I, _P, _P, _P],
     ),
     "gdn_decode_launch_shape": (
         _I,
-        [_I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I),
+        [_I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I),
          ctypes.POINTER(ctypes.c_longlong)],
     ),
     "gdn_decode_error_string": (ctypes.c_char_p, [_I]),
@@ -86,13 +86,15 @@ def check(code: int, what: str) -> None:
         raise RuntimeError(f"{what} failed: {error_string(code)} (hipError_t {code})")
 
 
-def launch_shape(B: int, HV: int) -> tuple[int, int, int]:
-    """(rows_per_lane_group, waves_per_block, num_blocks) chosen for (B, HV)."""
-    ns, w, nb = ctypes.c_int(), ctypes.c_int(), ctypes.c_longlong()
+def launch_shape(B: int, HV: int) -> tuple[int, int, int, int]:
+    """(rows_per_lane_group, waves_per_block, cache_policy, num_blocks)
+    that gdn_decode_step uses for (B, HV)."""
+    ns, w, pol, nb = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_longlong()
     check(
         get_lib().gdn_decode_launch_shape(
-            int(B), int(HV), ctypes.byref(ns), ctypes.byref(w), ctypes.byref(nb)
+            int(B), int(HV), ctypes.byref(ns), ctypes.byref(w), ctypes.byref(pol),
+            ctypes.byref(nb)
         ),
         "gdn_decode_launch_shape",
     )
-    return ns.value, w.value, nb.value
+    return ns.value, w.value, pol.value, nb.value

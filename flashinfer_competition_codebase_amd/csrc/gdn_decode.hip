@@ -24,6 +24,7 @@
 // so k.S and q.S reduce together and k.q is one per-head reduction.  This
 // only reorders fp32 rounding.
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -178,6 +179,12 @@ __device__ __forceinline__ void unpack4(u32x2 w, float* f) {
   f[2] = bf16_lo(w.y); f[3] = bf16_hi(w.y);
 }
 
+// Block order: block i covers head i / tiles, so consecutive blocks -- which
+// the dispatcher hands round-robin to the 8 XCDs -- stream adjacent state
+// rows.  Renumbering blocks so that each XCD works on its own contiguous
+// eighth (sharing q/k in that XCD's L2) measured 5% slower at B=256 and 18%
+// slower at B=64 (qk16_v32) than this natural order, so none is applied.
+
 // One decode step for 4*NS*WAVES rows of one (b, hv) head per workgroup.
 template <int NS, int WAVES, bool L2NORM, int POLICY>
 __global__ __launch_bounds__(64 * WAVES) void gdn_decode_k128(Params p) {
@@ -313,15 +320,28 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_decode_k128(Params p) {
 // Host side: validation, launch-shape choice and template dispatch.
 // ---------------------------------------------------------------------------
 
+// Launch bundle: stream plus optional events that hipExtLaunchKernelGGL
+// stamps with the kernel's own start and end timestamps.
+struct Launch {
+  hipStream_t stream;
+  hipEvent_t start;
+  hipEvent_t stop;
+};
+
 template <int NS, int W, bool L2, int POL>
-hipError_t launch_one(const Params& p, unsigned blocks, hipStream_t s) {
-  hipLaunchKernelGGL((gdn_decode_k128<NS, W, L2, POL>), dim3(blocks),
-                     dim3(64 * W), 0, s, p);
+hipError_t launch_one(const Params& p, unsigned blocks, const Launch& l) {
+  if (l.start || l.stop) {
+    hipExtLaunchKernelGGL((gdn_decode_k128<NS, W, L2, POL>), dim3(blocks),
+                          dim3(64 * W), 0, l.stream, l.start, l.stop, 0, p);
+  } else {
+    hipLaunchKernelGGL((gdn_decode_k128<NS, W, L2, POL>), dim3(blocks),
+                       dim3(64 * W), 0, l.stream, p);
+  }
   return hipGetLastError();
 }
 
 template <int NS, int W, bool L2>
-hipError_t by_policy(int pol, const Params& p, unsigned blocks, hipStream_t s) {
+hipError_t by_policy(int pol, const Params& p, unsigned blocks, const Launch& s) {
   switch (pol) {
     case kPolicyDefault: return launch_one<NS, W, L2, kPolicyDefault>(p, blocks, s);
     case kPolicyNtBoth: return launch_one<NS, W, L2, kPolicyNtBoth>(p, blocks, s);
@@ -331,14 +351,14 @@ hipError_t by_policy(int pol, const Params& p, unsigned blocks, hipStream_t s) {
 }
 
 template <int NS, int W>
-hipError_t by_norm(bool l2, int pol, const Params& p, unsigned blocks, hipStream_t s) {
+hipError_t by_norm(bool l2, int pol, const Params& p, unsigned blocks, const Launch& s) {
   return l2 ? by_policy<NS, W, true>(pol, p, blocks, s)
             : by_policy<NS, W, false>(pol, p, blocks, s);
 }
 
 template <int NS>
 hipError_t by_waves(int w, bool l2, int pol, const Params& p, unsigned blocks,
-                    hipStream_t s) {
+                    const Launch& s) {
   switch (w) {
     case 1: return by_norm<NS, 1>(l2, pol, p, blocks, s);
     case 2: return by_norm<NS, 2>(l2, pol, p, blocks, s);
@@ -351,7 +371,7 @@ hipError_t by_waves(int w, bool l2, int pol, const Params& p, unsigned blocks,
 }
 
 hipError_t dispatch(int ns, int w, bool l2, int pol, const Params& p,
-                    unsigned blocks, hipStream_t s) {
+                    unsigned blocks, const Launch& s) {
   switch (ns) {
     case 1: return by_waves<1>(w, l2, pol, p, blocks, s);
     case 2: return by_waves<2>(w, l2, pol, p, blocks, s);
@@ -367,24 +387,23 @@ bool aligned(const void* p, uintptr_t a) {
   return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
 }
 
-// Launch shape for B*HV heads.  Small batches split each head over many
-// workgroups so every CU has a short, latency-bound piece; large batches
-// give each wavefront more rows to keep more bytes in flight per CU.
-void choose_shape(long long heads, int* ns, int* waves) {
-  if (heads <= 128) {
-    *ns = 1; *waves = 2;       // 8 rows per block, 16 blocks per head
-  } else if (heads <= 1024) {
-    *ns = 2; *waves = 2;       // 16 rows per block
-  } else {
-    *ns = 4; *waves = 4;       // 64 rows per block
-  }
+// Launch shape for B*HV heads, from a rocprofv3 sweep of every shape and
+// cache policy on MI355X: two rows per lane group with nontemporal state
+// loads and stores is fastest from B*HV = 256 (B=8 qk16_v32, 7.0 us) to
+// 8192 (B=256, 168 us = 6.4 TB/s); below that every shape sits within
+// 0.1 us of a fixed ~3 us launch-plus-round-trip floor.
+void choose_shape(long long heads, int* ns, int* waves, int* policy) {
+  *ns = 2;
+  *policy = kPolicyNtBoth;
+  *waves = heads <= 64 ? 2 : 4;  // 16 or 32 rows per block
 }
 
 int step_impl(const void* q, const void* k, const void* v, const float* state,
               const float* A_log, const void* a, const float* dt_bias,
               const void* b, float scale, void* output, float* new_state,
               int B, int H, int HV, int K, int V, int use_qk_l2norm, int ns,
-              int waves, int policy, void* hip_stream) {
+              int waves, int policy, void* start_event, void* stop_event,
+              void* hip_stream) {
   if (B < 0 || H <= 0 || HV <= 0 || HV % H != 0) return hipErrorInvalidValue;
   if (K != kDim || V != kDim) return hipErrorInvalidValue;
   if (!is_pow2_upto8(ns) || !is_pow2_upto8(waves) || ns * waves > 32)
@@ -424,7 +443,6 @@ int step_impl(const void* q, const void* k, const void* v, const float* state,
   p.H = H;
   p.HV = HV;
   p.ratio = HV / H;
-  hipStream_t s = static_cast<hipStream_t>(hip_stream);
   for (long long b0 = 0; b0 < B; b0 += batches_per_launch) {
     const long long nb = (B - b0) < batches_per_launch ? (B - b0) : batches_per_launch;
     p.q = static_cast<const uint16_t*>(q) + b0 * H * kDim;
@@ -436,7 +454,12 @@ int step_impl(const void* q, const void* k, const void* v, const float* state,
     p.out = static_cast<uint16_t*>(output) + b0 * HV * kDim;
     p.new_state = new_state + b0 * HV * kDim * kDim;
     const unsigned blocks = static_cast<unsigned>(nb * HV * tiles);
-    const hipError_t e = dispatch(ns, waves, use_qk_l2norm != 0, policy, p, blocks, s);
+    // Start stamp on the first launch, stop stamp on the last.
+    Launch l;
+    l.stream = static_cast<hipStream_t>(hip_stream);
+    l.start = b0 == 0 ? static_cast<hipEvent_t>(start_event) : nullptr;
+    l.stop = b0 + nb == B ? static_cast<hipEvent_t>(stop_event) : nullptr;
+    const hipError_t e = dispatch(ns, waves, use_qk_l2norm != 0, policy, p, blocks, l);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
@@ -454,11 +477,11 @@ int gdn_decode_step(const void* q, const void* k, const void* v,
                     void* output, float* new_state, int B, int H, int HV,
                     int K, int V, int use_qk_l2norm, void* hip_stream) {
   if (B < 0 || HV <= 0) return hipErrorInvalidValue;
-  int ns = 0, waves = 0;
-  choose_shape(static_cast<long long>(B) * HV, &ns, &waves);
+  int ns = 0, waves = 0, policy = 0;
+  choose_shape(static_cast<long long>(B) * HV, &ns, &waves, &policy);
   return step_impl(q, k, v, state, A_log, a, dt_bias, b, scale, output,
                    new_state, B, H, HV, K, V, use_qk_l2norm, ns, waves,
-                   kPolicyDefault, hip_stream);
+                   policy, nullptr, nullptr, hip_stream);
 }
 
 int gdn_decode_step_shaped(const void* q, const void* k, const void* v,
@@ -467,21 +490,25 @@ int gdn_decode_step_shaped(const void* q, const void* k, const void* v,
                            float scale, void* output, float* new_state, int B,
                            int H, int HV, int K, int V, int use_qk_l2norm,
                            int rows_per_lane_group, int waves_per_block,
-                           int cache_policy, void* hip_stream) {
+                           int cache_policy, void* start_event,
+                           void* stop_event, void* hip_stream) {
   return step_impl(q, k, v, state, A_log, a, dt_bias, b, scale, output,
                    new_state, B, H, HV, K, V, use_qk_l2norm,
                    rows_per_lane_group, waves_per_block, cache_policy,
-                   hip_stream);
+                   start_event, stop_event, hip_stream);
 }
 
 int gdn_decode_launch_shape(int B, int HV, int* rows_per_lane_group,
-                            int* waves_per_block, long long* num_blocks) {
-  if (B < 0 || HV <= 0 || !rows_per_lane_group || !waves_per_block || !num_blocks)
+                            int* waves_per_block, int* cache_policy,
+                            long long* num_blocks) {
+  if (B < 0 || HV <= 0 || !rows_per_lane_group || !waves_per_block ||
+      !cache_policy || !num_blocks)
     return hipErrorInvalidValue;
-  int ns = 0, waves = 0;
-  choose_shape(static_cast<long long>(B) * HV, &ns, &waves);
+  int ns = 0, waves = 0, policy = 0;
+  choose_shape(static_cast<long long>(B) * HV, &ns, &waves, &policy);
   *rows_per_lane_group = ns;
   *waves_per_block = waves;
+  *cache_policy = policy;
   *num_blocks = static_cast<long long>(B) * HV * (kDim / (kLaneGroups * ns * waves));
   return hipSuccess;
 }

@@ -145,11 +145,11 @@ def _launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
                 B, H, HV, K_DIM, V_DIM, int(bool(use_qk_l2norm)), stream)
             _lib.check(code, "gdn_decode_step")
         else:
-            ns, waves, policy = shape
+            ns, waves, policy, start_event, stop_event = shape
             code = lib.gdn_decode_step_shaped(
                 *ptrs, scale, output.data_ptr(), new_state.data_ptr(),
                 B, H, HV, K_DIM, V_DIM, int(bool(use_qk_l2norm)),
-                int(ns), int(waves), int(policy), stream)
+                int(ns), int(waves), int(policy), start_event, stop_event, stream)
             _lib.check(code, "gdn_decode_step_shaped")
 
 
@@ -180,9 +180,12 @@ def kernel_hip(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
 @torch.no_grad()
 def kernel_hip_shaped(q, k, v, state, A_log, a, dt_bias, b, scale, output,
                       new_state, *, use_qk_l2norm: bool = False,
-                      rows_per_lane_group: int = 4, waves_per_block: int = 4,
-                      cache_policy: int = 0):
-    """``kernel_hip`` with an explicit launch shape (for launch-shape sweeps)."""
+                      rows_per_lane_group: int = 2, waves_per_block: int = 4,
+                      cache_policy: int = 1, start_event=None, stop_event=None):
+    """``kernel_hip`` with an explicit launch shape, for launch-shape sweeps
+    and timing.  ``start_event`` / ``stop_event`` are raw ``hipEvent_t``
+    handles (ints) that the launch stamps with the kernel's own start and end
+    timestamps."""
     B, H, HV = check_inputs(q, k, v, state, A_log, a, dt_bias, b, output, new_state)
     scale = resolve_scale(scale, q.shape[-1])
     if state is None:
@@ -192,7 +195,8 @@ def kernel_hip_shaped(q, k, v, state, A_log, a, dt_bias, b, scale, output,
         return None
     _launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
             B, H, HV, use_qk_l2norm,
-            shape=(rows_per_lane_group, waves_per_block, cache_policy))
+            shape=(rows_per_lane_group, waves_per_block, cache_policy,
+                   start_event, stop_event))
     return None
 
 

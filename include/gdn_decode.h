@@ -65,7 +65,10 @@ int gdn_decode_step(const void* q, const void* k, const void* v,
  * rows_per_lane_group and waves_per_block are each one of 1, 2, 4, 8 and
  * their product is at most 32.  cache_policy selects how the state stream
  * is accessed: 0 ordinary loads and stores, 1 nontemporal loads and stores,
- * 2 nontemporal stores only.  Used for launch-shape sweeps.
+ * 2 nontemporal stores only.  start_event / stop_event (hipEvent_t, may be
+ * NULL) are stamped with the kernel's own start and end timestamps
+ * (hipExtLaunchKernelGGL), so hipEventElapsedTime gives the kernel duration
+ * without event-marker overhead.  Used for launch-shape sweeps and timing.
  * Counterpart of the reference's fixed launch choice (BV = 8 rows and
  * num_warps = 8 if B <= 4 else 4, solution/triton/kernel.py:168-197; grid
  * (V/8, B*HV), solution/cuda/kernel.cu:229-235,418-424).
@@ -77,17 +80,20 @@ int gdn_decode_step_shaped(const void* q, const void* k, const void* v,
                            int B, int H, int HV, int K, int V,
                            int use_qk_l2norm, int rows_per_lane_group,
                            int waves_per_block, int cache_policy,
+                           void* start_event, void* stop_event,
                            void* hip_stream);
 
 /*
  * Launch shape gdn_decode_step would use for (B, HV): writes
- * rows_per_lane_group, waves_per_block and the workgroup count.
- * Returns 0, or hipErrorInvalidValue for B < 0, HV <= 0 or null outputs.
+ * rows_per_lane_group, waves_per_block, cache_policy and the workgroup
+ * count.  Returns 0, or hipErrorInvalidValue for B < 0, HV <= 0 or null
+ * outputs.
  * No reference counterpart (the reference's choice is inline in its
  * wrappers, solution/triton/kernel.py:168-174).
  */
 int gdn_decode_launch_shape(int B, int HV, int* rows_per_lane_group,
-                            int* waves_per_block, long long* num_blocks);
+                            int* waves_per_block, int* cache_policy,
+                            long long* num_blocks);
 
 /*
  * Human-readable text for a return code of the functions above

@@ -53,10 +53,12 @@ def test_abi_version_and_error_text():
 
 
 def test_launch_shape_query():
-    ns, w, blocks = _lib.launch_shape(1, 32)
-    assert ns in (1, 2, 4, 8) and w in (1, 2, 4, 8)
+    ns, w, pol, blocks = _lib.launch_shape(1, 32)
+    assert ns in (1, 2, 4, 8) and w in (1, 2, 4, 8) and pol in (0, 1, 2)
     assert blocks == 32 * 128 // (4 * ns * w)
-    assert _lib.launch_shape(0, 32)[2] == 0
+    assert _lib.launch_shape(0, 32)[3] == 0
+    ns, w, pol, blocks = _lib.launch_shape(256, 32)
+    assert blocks == 256 * 32 * 128 // (4 * ns * w)
     with pytest.raises(RuntimeError):
         _lib.launch_shape(-1, 32)
 
@@ -80,11 +82,11 @@ def test_validation_rejects_bad_sizes_without_launching():
     shaped = lib.gdn_decode_step_shaped
     nulls = [None] * 8
     assert shaped(*nulls, ctypes.c_float(0.1), None, None, 1, 16, 32, 128, 128, 1,
-                  8, 8, 0, None) == 1    # 8 x 8 > 32 rows per block
+                  8, 8, 0, None, None, None) == 1    # 8 x 8 > 32 rows per block
     assert shaped(*nulls, ctypes.c_float(0.1), None, None, 1, 16, 32, 128, 128, 1,
-                  3, 1, 0, None) == 1    # not a power of two
+                  3, 1, 0, None, None, None) == 1    # not a power of two
     assert shaped(*nulls, ctypes.c_float(0.1), None, None, 1, 16, 32, 128, 128, 1,
-                  1, 1, 3, None) == 1    # unknown cache policy
+                  1, 1, 3, None, None, None) == 1    # unknown cache policy
 
 
 def test_validation_rejects_misaligned_and_overlapping_state():

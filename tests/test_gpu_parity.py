@@ -267,3 +267,29 @@ def test_full_size_write_read_property(hip_device):
     o_expect = t["scale"] * v
     err = (out[:, 0].float() - o_expect).abs()
     assert bool((err <= 2.0 ** -8 * o_expect.abs() + 1e-6).all())   # within one bf16 ulp
+
+
+def test_stamped_launch_matches_and_times(hip_device):
+    """Event-stamped launches (hipExtLaunchKernelGGL) give the same bits as
+    plain launches and a positive kernel duration."""
+    import ctypes
+
+    _announce("stamped launch")
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    evs = [ctypes.c_void_p(), ctypes.c_void_p()]
+    for ev in evs:
+        assert hip.hipEventCreate(ctypes.byref(ev)) == 0
+    try:
+        t = _dev(make_inputs(4, 16, 32, seed=4011), hip_device)
+        ref_o, ref_s = gdn.run(**t, use_qk_l2norm=True)
+        out, st = torch.empty_like(ref_o), torch.empty_like(ref_s)
+        gdn.kernel_hip_shaped(**t, output=out, new_state=st, use_qk_l2norm=True,
+                              start_event=evs[0].value, stop_event=evs[1].value)
+        assert hip.hipEventSynchronize(evs[1]) == 0
+        ms = ctypes.c_float()
+        assert hip.hipEventElapsedTime(ctypes.byref(ms), evs[0], evs[1]) == 0
+        assert 0.0 < ms.value < 100.0
+        assert torch.equal(out, ref_o) and torch.equal(st, ref_s)
+    finally:
+        for ev in evs:
+            hip.hipEventDestroy(ev)
