@@ -5,20 +5,26 @@
 A step is one decode step (T=1) over one batch, updating the fp32 state in
 place, with every input already resident in HBM.  The headline workload is
 B=256 sequences of the qk16_v32 head layout (16 q/k heads, 32 v-heads,
-K=V=128, q/k L2-norm on): 1,080,066,304 algorithmic bytes per step.  Prints
-ONE JSON line on stdout:
+K=V=128, q/k L2-norm on): 1,080,066,304 algorithmic bytes per step.
+
+Steps run back to back and rotate over several layer states (as consecutive
+GDN layers of a model do) totalling at least 1 GiB, so each step reads a
+state that is no longer cached and pays for the write-back of the previous
+step's dirty lines: the steady state of serving.  Prints ONE JSON line:
 
 * ``value``: whole-job throughput in GB/s of algorithmic bytes, from the
-  wall clock over K back-to-back steps;
+  wall clock over K timed steps;
 * ``roofline``: the decode kernel's achieved HBM GB/s, from HIP events
   around every timed launch on the launch stream, against MI355X's 8 TB/s;
   ``traffic`` is the measured HBM bytes per launch from the committed
   rocprofv3 counter summary, when there is one;
-* ``b1``: kernel time per step at B=1 (qk16_v32, L2-norm), warm and with a
-  cold cache, stamped by the kernel dispatch itself (the analogue of the
-  reference's CUPTI timings);
-* ``per_config``: the same kernel times for every benchmark shape and for
-  the reference's qk4_v8 definition at its workload batch sizes;
+* ``b1``: kernel time per step at B=1 (qk16_v32, L2-norm), stamped by the
+  kernel dispatch itself (the analogue of the reference's CUPTI timings);
+* ``per_config``: kernel times for every benchmark shape and for the
+  reference's qk4_v8 definition at its workload batch sizes, in three
+  regimes: steady (as above), warm (one state, repeatedly: cache-resident
+  below 256 MiB) and cold (a 1 GiB read evicts the caches just before the
+  launch; the launch's own writes may still be in cache when it ends);
 * ``cpu_baseline``: the reference's PyTorch-eager step (the oracle's
   loop-for-loop restatement) timed on this host's cores on a bounded sample.
 
@@ -117,42 +123,58 @@ class KernelStamps:
             self.hip.hipEventDestroy(ev)
 
 
-def kernel_times_us(t, l2, iters, *, cold, flush=None):
+STEADY_BYTES = 1 << 30
+
+
+def layer_states(state: torch.Tensor) -> list:
+    """``state`` plus copies: at least two, and at least 1 GiB in total."""
+    n = max(2, -(-STEADY_BYTES // (state.numel() * state.element_size())))
+    return [state] + [state.clone() for _ in range(n - 1)]
+
+
+def kernel_times_us(t, l2, iters, *, mode, flush=None):
     """Per-launch kernel durations in µs, stamped by the kernel dispatch
     itself, with the launch shape gdn_decode_step uses.
 
-    Warm: back-to-back launches.  Cold: before each launch, read a 1 GiB
-    buffer (more than the 32 MiB of L2 plus the 256 MiB MALL; a read leaves
-    no dirty lines to be written back during the timed launch), then
-    synchronize."""
+    steady: back-to-back launches rotating over ``layer_states``;
+    warm: back-to-back launches on one state;
+    cold: each launch right after reading a 1 GiB buffer (more than the
+    32 MiB of L2 plus the 256 MiB MALL; a read leaves no dirty lines)."""
     B, HV = t["v"].shape[0], t["v"].shape[2]
     ns, waves, policy, _ = _lib.launch_shape(B, HV)
+    states = layer_states(t["state"]) if mode == "steady" else [t["state"]]
+    iters = max(iters, 2 * len(states)) if mode == "steady" else iters
     stamps = KernelStamps(iters)
     try:
         for i in range(iters):
-            if cold:
+            if mode == "cold":
                 flush.sum()
-                torch.cuda.synchronize()
-            gdn.kernel_hip_shaped(**t, use_qk_l2norm=l2, rows_per_lane_group=ns,
-                                  waves_per_block=waves, cache_policy=policy,
-                                  start_event=stamps.start[i].value,
+            s = states[i % len(states)]
+            gdn.kernel_hip_shaped(**{**t, "state": s, "new_state": s}, use_qk_l2norm=l2,
+                                  rows_per_lane_group=ns, waves_per_block=waves,
+                                  cache_policy=policy, start_event=stamps.start[i].value,
                                   stop_event=stamps.stop[i].value)
         torch.cuda.synchronize()
-        return [stamps.elapsed_us(i) for i in range(iters)]
+        d = [stamps.elapsed_us(i) for i in range(iters)]
+        # steady: drop the first pass over the states (still warm from setup)
+        return d[len(states):] if mode == "steady" else d
     finally:
         stamps.close()
 
 
-def timed_steps(t, l2, steps):
-    """Wall clock over ``steps`` back-to-back launches plus per-launch events."""
+def timed_steps(t, l2, steps, states):
+    """Wall clock over ``steps`` back-to-back launches of the product entry
+    point, rotating over ``states``, plus HIP event markers around every
+    launch on the launch stream."""
     stream = torch.cuda.current_stream()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    views = [{**t, "state": s, "new_state": s} for s in states]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
         starts[i].record(stream)
-        gdn.kernel_hip(**t, use_qk_l2norm=l2)
+        gdn.kernel_hip(**views[i % len(views)], use_qk_l2norm=l2)
         ends[i].record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -217,20 +239,44 @@ def _traffic():
         return None
 
 
+def reference_stream(device, iters: int = 20):
+    """GB/s of torch's in-place elementwise add over a 512 MiB fp32 buffer:
+    512 MiB read and 512 MiB written, the state traffic of one B=256
+    qk16_v32 step, through a plain streaming kernel.  A reference point for
+    the practical read+write bandwidth of the box, timed with event markers."""
+    buf = torch.zeros(1 << 27, device=device)
+    for _ in range(3):
+        buf.add_(1.0)
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(iters)]
+    for a, b in ev:
+        a.record(stream)
+        buf.add_(1.0)
+        b.record(stream)
+    torch.cuda.synchronize()
+    us = statistics.median(a.elapsed_time(b) * 1e3 for a, b in ev)
+    return {"kernel": "torch add_ (in place), 512 MiB fp32", "us": round(us, 2),
+            "gbs": round(2 * buf.numel() * 4 / (us * 1e-6) / 1e9, 1)}
+
+
 def pmc_pass(device):
-    """Short run for rocprofv3 counter passes: a plain copy of known size
-    (calibrates FETCH_SIZE / WRITE_SIZE) and a few B=256 decode steps."""
+    """Short run for rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE): three
+    plain 256 MiB copies (calibrate the counters against known bytes), then
+    six B=256 qk16_v32 decode steps rotating over two layer states, as in the
+    timed region."""
     n = 256 * 1024 * 1024 // 4
     src = torch.randn(n, device=device)
     dst = torch.empty_like(src)
-    flush = torch.empty(1 << 28, device=device)
     for _ in range(3):
-        flush.add_(1)
         dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
     t = make_device_inputs(256, 16, 32, device, seed=1003)
-    for _ in range(3):
-        flush.add_(1)
-        gdn.kernel_hip(**t, use_qk_l2norm=True)
+    states = layer_states(t["state"])
+    for i in range(6):
+        s_ = states[i % len(states)]
+        gdn.kernel_hip(**{**t, "state": s_, "new_state": s_}, use_qk_l2norm=True)
     torch.cuda.synchronize()
     print(json.dumps({"pmc_pass": "done", "copy_bytes": n * 4,
                       "decode_bytes": step_bytes(256, 16, 32)}), flush=True)
@@ -270,10 +316,14 @@ def main():
     ns, waves, policy, blocks = _lib.launch_shape(B, HV)
     log(f"[bench] {args.config}: B={B} H={H} HV={HV} l2={l2} bytes/step={nbytes} "
         f"launch ns={ns} waves={waves} policy={policy} blocks={blocks}")
-    for _ in range(args.warmup):
-        gdn.kernel_hip(**t, use_qk_l2norm=l2)
+    states = layer_states(t["state"])
+    log(f"[bench] rotating over {len(states)} layer states")
+    for i in range(args.warmup):
+        s_ = states[i % len(states)]
+        gdn.kernel_hip(**{**t, "state": s_, "new_state": s_}, use_qk_l2norm=l2)
     torch.cuda.synchronize()
-    wall, durs = timed_steps(t, l2, args.steps)
+    wall, durs = timed_steps(t, l2, args.steps, states)
+    del states
     ms_per_step = wall * 1e3 / args.steps
     value = nbytes / (wall / args.steps) / 1e9
     kavg = statistics.fmean(durs)
@@ -291,20 +341,25 @@ def main():
             tc = make_device_inputs(b_, h_, hv_, device, seed=7)
             for _ in range(5):
                 gdn.kernel_hip(**tc, use_qk_l2norm=l2_)
-            warm = kernel_times_us(tc, l2_, args.iters, cold=False)
-            cold = kernel_times_us(tc, l2_, args.iters, cold=True, flush=flush)
+            med = {m: statistics.median(kernel_times_us(tc, l2_, args.iters, mode=m,
+                                                        flush=flush))
+                   for m in ("steady", "warm", "cold")}
             nb = step_bytes(b_, h_, hv_)
-            wm, cm = statistics.median(warm), statistics.median(cold)
+            sm = med["steady"]
             per_config[name] = {
                 "B": b_, "H": h_, "HV": hv_, "l2norm": l2_, "bytes": nb,
                 "launch": list(_lib.launch_shape(b_, hv_)),
-                "us_warm_median": round(wm, 3), "us_cold_median": round(cm, 3),
-                "cold_hbm_gbs": round(nb / (cm * 1e-6) / 1e9, 1),
-                "cold_frac_of_peak": round(nb / (cm * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+                "us_steady": round(sm, 3), "us_warm": round(med["warm"], 3),
+                "us_cold": round(med["cold"], 3),
+                "steady_hbm_gbs": round(nb / (sm * 1e-6) / 1e9, 1),
+                "steady_frac_of_peak": round(nb / (sm * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
             }
-            log(f"[bench] {name}: warm {wm:.2f} us, cold {cm:.2f} us, "
-                f"cold {per_config[name]['cold_hbm_gbs']:.0f} GB/s")
+            log(f"[bench] {name}: steady {sm:.2f} us ({per_config[name]['steady_hbm_gbs']:.0f}"
+                f" GB/s), warm {med['warm']:.2f} us, cold {med['cold']:.2f} us")
             del tc
+
+    ref_stream = reference_stream(device)
+    log(f"[bench] reference stream: {ref_stream['gbs']:.0f} GB/s ({ref_stream['us']} us)")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -335,8 +390,10 @@ def main():
             "launch": {"rows_per_lane_group": ns, "waves_per_block": waves,
                        "cache_policy": policy, "blocks": blocks},
         },
-        "b1": ({"us_per_step_kernel_warm": b1["us_warm_median"],
-                "us_per_step_kernel_cold": b1["us_cold_median"]} if b1 else None),
+        "b1": ({"us_per_step_steady": b1["us_steady"], "us_per_step_warm": b1["us_warm"],
+                "us_per_step_cold": b1["us_cold"],
+                "timer": "kernel-stamped HIP events (hipExtLaunchKernelGGL)"}
+               if b1 else None),
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 1),
@@ -345,6 +402,7 @@ def main():
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": _traffic(),
             "kernel_us_avg": round(kavg, 3),
+            "reference_stream": ref_stream,
         },
         "cpu_baseline": cpu,
         "per_config": per_config,

@@ -46,6 +46,7 @@ enum : int {
   kPolicyDefault = 0,   // ordinary loads and stores
   kPolicyNtBoth = 1,    // nontemporal state loads and stores
   kPolicyNtStore = 2,   // nontemporal state stores only
+  kPolicyNtLoad = 3,    // nontemporal state loads only
 };
 
 struct Params {
@@ -97,7 +98,7 @@ __device__ __forceinline__ void row16_sum(float (&x)[N]) {
 
 template <int POLICY>
 __device__ __forceinline__ f32x4 load_state(const float* p) {
-  if constexpr (POLICY == kPolicyNtBoth) {
+  if constexpr (POLICY == kPolicyNtBoth || POLICY == kPolicyNtLoad) {
     return __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
   } else {
     return *reinterpret_cast<const f32x4*>(p);
@@ -346,6 +347,7 @@ hipError_t by_policy(int pol, const Params& p, unsigned blocks, const Launch& s)
     case kPolicyDefault: return launch_one<NS, W, L2, kPolicyDefault>(p, blocks, s);
     case kPolicyNtBoth: return launch_one<NS, W, L2, kPolicyNtBoth>(p, blocks, s);
     case kPolicyNtStore: return launch_one<NS, W, L2, kPolicyNtStore>(p, blocks, s);
+    case kPolicyNtLoad: return launch_one<NS, W, L2, kPolicyNtLoad>(p, blocks, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -408,7 +410,7 @@ int step_impl(const void* q, const void* k, const void* v, const float* state,
   if (K != kDim || V != kDim) return hipErrorInvalidValue;
   if (!is_pow2_upto8(ns) || !is_pow2_upto8(waves) || ns * waves > 32)
     return hipErrorInvalidValue;
-  if (policy < kPolicyDefault || policy > kPolicyNtStore) return hipErrorInvalidValue;
+  if (policy < kPolicyDefault || policy > kPolicyNtLoad) return hipErrorInvalidValue;
   if (B == 0) return hipSuccess;
   if (!q || !k || !v || !state || !A_log || !a || !dt_bias || !b || !output ||
       !new_state)

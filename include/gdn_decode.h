@@ -65,7 +65,7 @@ int gdn_decode_step(const void* q, const void* k, const void* v,
  * rows_per_lane_group and waves_per_block are each one of 1, 2, 4, 8 and
  * their product is at most 32.  cache_policy selects how the state stream
  * is accessed: 0 ordinary loads and stores, 1 nontemporal loads and stores,
- * 2 nontemporal stores only.  start_event / stop_event (hipEvent_t, may be
+ * 2 nontemporal stores only, 3 nontemporal loads only.  start_event / stop_event (hipEvent_t, may be
  * NULL) are stamped with the kernel's own start and end timestamps
  * (hipExtLaunchKernelGGL), so hipEventElapsedTime gives the kernel duration
  * without event-marker overhead.  Used for launch-shape sweeps and timing.

@@ -1,6 +1,6 @@
 """CPU oracle of the GDN decode step -- TEST INFRASTRUCTURE ONLY.
 
-This module is the checker for the gfx950 kernel.  Only ``tests/``,
+This module checks the gfx950 kernel; it is not part of it.  Only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
 import it, and only to check or to time the reference's CPU algorithm; the
 product path (``flashinfer_competition_codebase_amd``) never calls it.

@@ -86,7 +86,7 @@ def test_validation_rejects_bad_sizes_without_launching():
     assert shaped(*nulls, ctypes.c_float(0.1), None, None, 1, 16, 32, 128, 128, 1,
                   3, 1, 0, None, None, None) == 1    # not a power of two
     assert shaped(*nulls, ctypes.c_float(0.1), None, None, 1, 16, 32, 128, 128, 1,
-                  1, 1, 3, None, None, None) == 1    # unknown cache policy
+                  1, 1, 4, None, None, None) == 1    # unknown cache policy
 
 
 def test_validation_rejects_misaligned_and_overlapping_state():
