@@ -239,6 +239,39 @@ def _traffic():
         return None
 
 
+def b1_serving(device, layers: int = 48, reps: int = 20):
+    """Host-inclusive time per decode step at B=1 qk16_v32 (L2-norm) when a
+    model issues one step per GDN layer: eager Python calls of ``kernel_hip``
+    back to back, and the same ``layers`` steps captured once in a HIP graph
+    and replayed.  Wall clock per step, median over ``reps`` passes."""
+    t = make_device_inputs(1, 16, 32, device, seed=11)
+    states = [t["state"]] + [t["state"].clone() for _ in range(layers - 1)]
+    views = [{**t, "state": s_, "new_state": s_} for s_ in states]
+
+    def eager():
+        for v_ in views:
+            gdn.kernel_hip(**v_, use_qk_l2norm=True)
+
+    eager()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        eager()
+    torch.cuda.synchronize()
+    res = {}
+    for name, fn in (("eager", eager), ("graph", graph.replay)):
+        per = []
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            per.append((time.perf_counter() - t0) * 1e6 / layers)
+        res[f"{name}_us_per_step"] = round(statistics.median(per), 2)
+    res["layers"] = layers
+    return res
+
+
 def reference_stream(device, iters: int = 20):
     """GB/s of torch's in-place elementwise add over a 512 MiB fp32 buffer:
     512 MiB read and 512 MiB written, the state traffic of one B=256
@@ -358,6 +391,9 @@ def main():
                 f" GB/s), warm {med['warm']:.2f} us, cold {med['cold']:.2f} us")
             del tc
 
+    serving = b1_serving(device)
+    log(f"[bench] B=1 serving, {serving['layers']} layer steps: eager "
+        f"{serving['eager_us_per_step']} us/step, HIP graph {serving['graph_us_per_step']} us/step")
     ref_stream = reference_stream(device)
     log(f"[bench] reference stream: {ref_stream['gbs']:.0f} GB/s ({ref_stream['us']} us)")
 
@@ -392,8 +428,9 @@ def main():
         },
         "b1": ({"us_per_step_steady": b1["us_steady"], "us_per_step_warm": b1["us_warm"],
                 "us_per_step_cold": b1["us_cold"],
-                "timer": "kernel-stamped HIP events (hipExtLaunchKernelGGL)"}
-               if b1 else None),
+                "timer": "kernel-stamped HIP events (hipExtLaunchKernelGGL)",
+                "serving": serving}
+               if b1 else {"serving": serving}),
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 1),

@@ -13,7 +13,11 @@
 //   * a wavefront holds 4 lane groups x NS rows each (NS "slots"), i.e. it
 //     keeps 4*NS*512 B of state in flight per load burst;
 //   * a workgroup of WAVES wavefronts covers 4*NS*WAVES consecutive rows of
-//     one (b, hv) head; a head is split over 128/(4*NS*WAVES) workgroups.
+//     one (b, hv) head; a head is split over T = 128/(4*NS*WAVES) workgroups;
+//   * grid (ratio*T, H, B) with ratio = HV/H: x = (v-head within its GVA
+//     group, row tile), y = q/k head, z = batch.  Every index is a shift or
+//     a multiply-add (no integer division before the first load), and the
+//     x-fastest dispatch order walks the state in memory order.
 //   * dot products over K reduce inside the 16-lane row with four DPP adds
 //     (quad_perm xor1, quad_perm xor2, row_half_mirror, row_mirror), so no
 //     LDS or cross-row traffic is needed.
@@ -180,11 +184,11 @@ __device__ __forceinline__ void unpack4(u32x2 w, float* f) {
   f[2] = bf16_lo(w.y); f[3] = bf16_hi(w.y);
 }
 
-// Block order: block i covers head i / tiles, so consecutive blocks -- which
-// the dispatcher hands round-robin to the 8 XCDs -- stream adjacent state
-// rows.  Renumbering blocks so that each XCD works on its own contiguous
-// eighth (sharing q/k in that XCD's L2) measured 5% slower at B=256 and 18%
-// slower at B=64 (qk16_v32) than this natural order, so none is applied.
+// Block order: consecutive blocks -- which the dispatcher hands round-robin
+// to the 8 XCDs -- stream adjacent state rows.  Renumbering blocks so that
+// each XCD works on its own contiguous eighth (sharing q/k in that XCD's L2)
+// measured 5% slower at B=256 and 18% slower at B=64 (qk16_v32) than this
+// natural order, so none is applied.
 
 // One decode step for 4*NS*WAVES rows of one (b, hv) head per workgroup.
 template <int NS, int WAVES, bool L2NORM, int POLICY>
@@ -199,11 +203,12 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_decode_k128(Params p) {
   const int grp = lane >> 4;
   const int j = lane & 15;
 
-  const int head = blockIdx.x / kTiles;  // b * HV + hv
-  const int tile = blockIdx.x - head * kTiles;
-  const int bi = head / p.HV;
-  const int hv = head - bi * p.HV;
-  const int hq = hv / p.ratio;           // GVA: q/k head of this v-head
+  static_assert((kTiles & (kTiles - 1)) == 0, "tiles per head is a power of two");
+  const int tile = static_cast<int>(blockIdx.x) & (kTiles - 1);
+  const int hq = static_cast<int>(blockIdx.y);          // q/k head
+  const int bi = static_cast<int>(blockIdx.z);
+  const int hv = hq * p.ratio + static_cast<int>(blockIdx.x) / kTiles;
+  const int head = bi * p.HV + hv;
   const int row0 = tile * kRowsPerBlock + wave * kRowsPerWave + grp * NS;
 
   // Issue every global load before any arithmetic.  Loads retire in issue
@@ -331,11 +336,15 @@ struct Launch {
 
 template <int NS, int W, bool L2, int POL>
 hipError_t launch_one(const Params& p, unsigned blocks, const Launch& l) {
+  constexpr unsigned kT = kDim / (kLaneGroups * NS * W);
+  const unsigned per_batch = static_cast<unsigned>(p.HV) * kT;
+  const dim3 grid_xyz(static_cast<unsigned>(p.ratio) * kT, static_cast<unsigned>(p.H),
+                      blocks / per_batch);
   if (l.start || l.stop) {
-    hipExtLaunchKernelGGL((gdn_decode_k128<NS, W, L2, POL>), dim3(blocks),
+    hipExtLaunchKernelGGL((gdn_decode_k128<NS, W, L2, POL>), grid_xyz,
                           dim3(64 * W), 0, l.stream, l.start, l.stop, 0, p);
   } else {
-    hipLaunchKernelGGL((gdn_decode_k128<NS, W, L2, POL>), dim3(blocks),
+    hipLaunchKernelGGL((gdn_decode_k128<NS, W, L2, POL>), grid_xyz,
                        dim3(64 * W), 0, l.stream, p);
   }
   return hipGetLastError();
@@ -407,6 +416,7 @@ int step_impl(const void* q, const void* k, const void* v, const float* state,
               int waves, int policy, void* start_event, void* stop_event,
               void* hip_stream) {
   if (B < 0 || H <= 0 || HV <= 0 || HV % H != 0) return hipErrorInvalidValue;
+  if (H > 65535) return hipErrorInvalidValue;  // grid y
   if (K != kDim || V != kDim) return hipErrorInvalidValue;
   if (!is_pow2_upto8(ns) || !is_pow2_upto8(waves) || ns * waves > 32)
     return hipErrorInvalidValue;
@@ -436,6 +446,7 @@ int step_impl(const void* q, const void* k, const void* v, const float* state,
   // Keep each launch's work-item count well inside 32 bits.
   const long long max_blocks = (1LL << 31) / threads_per_block;
   long long batches_per_launch = max_blocks / (tiles * HV);
+  if (batches_per_launch > 65535) batches_per_launch = 65535;  // grid z limit
   if (batches_per_launch < 1) return hipErrorInvalidValue;
 
   Params p;

@@ -113,7 +113,7 @@ def test_golden_vectors(name, hip_device):
     assert_state_close(new_state.cpu(), torch.from_numpy(exp_state), what=name)
 
 
-@pytest.mark.parametrize("H,HV", [(32, 32), (1, 32), (4, 8), (2, 64)])
+@pytest.mark.parametrize("H,HV", [(32, 32), (1, 32), (4, 8), (2, 64), (2, 6), (5, 15)])
 def test_gva_ratios(H, HV, hip_device):
     _announce(f"gva H={H} HV={HV}")
     t = make_inputs(3, H, HV, seed=3000 + H + HV)
@@ -293,3 +293,36 @@ def test_stamped_launch_matches_and_times(hip_device):
     finally:
         for ev in evs:
             hip.hipEventDestroy(ev)
+
+
+def test_hip_graph_capture_and_replay(hip_device):
+    """The decode step captured in a HIP graph (torch.cuda.CUDAGraph on the
+    capture stream) replays to the eager result, step after step, with eager
+    work and synchronisations between replays."""
+    _announce("hip graph capture")
+    t = _dev(make_inputs(1, 16, 32, seed=4012), hip_device)
+    state_g = t["state"].clone()
+    state_e = t["state"].clone()
+    out_g = torch.empty(1, 1, 32, 128, dtype=torch.bfloat16, device=hip_device)
+    out_e = torch.empty_like(out_g)
+    graph = torch.cuda.CUDAGraph()
+    warm = torch.cuda.Stream(device=hip_device)
+    warm.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(warm):   # warm the library up off the capture
+        scratch = state_g.clone()
+        gdn.kernel_hip(**{**t, "state": scratch}, output=out_g, new_state=scratch,
+                       use_qk_l2norm=True)
+    torch.cuda.current_stream().wait_stream(warm)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        gdn.kernel_hip(**{**t, "state": state_g}, output=out_g, new_state=state_g,
+                       use_qk_l2norm=True)
+    torch.cuda.synchronize()
+    assert torch.equal(state_g, t["state"]), "capture must not execute the step"
+    for step in range(4):
+        graph.replay()
+        gdn.kernel_hip(**{**t, "state": state_e}, output=out_e, new_state=state_e,
+                       use_qk_l2norm=True)
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, out_e), step
+        assert torch.equal(state_g, state_e), step
