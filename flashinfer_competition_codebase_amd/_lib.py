@@ -23,10 +23,13 @@ SIGNATURES = {
         _I,
         [_P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _I, _I, _I, _I, _I, _P],
     ),
+    "gdn_decode_steps": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P] + [_I] * 8 + [_P],
+    ),
     "gdn_decode_step_shaped": (
         _I,
-        [_P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _I, _I, _I, _I, _I,
-         _I, _I, _I, _P, _P, _P],
+        [_P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P] + [_I] * 11 + [_P, _P, _P],
     ),
     "gdn_decode_launch_shape": (
         _I,
@@ -37,7 +40,7 @@ SIGNATURES = {
     "gdn_decode_abi_version": (_I, []),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lock = threading.Lock()
 _lib = None

@@ -1,23 +1,28 @@
-// gdn_decode.hip - Gated Delta Net single-token decode step for gfx950.
+// gdn_decode.hip - Gated Delta Net decode step for gfx950 (MI355X).
 //
-// One fused kernel per step: gate math, optional q/k L2-norm, state decay,
+// One fused kernel per call: gate math, optional q/k L2-norm, state decay,
 // delta-rule correction, rank-1 update and output mat-vec, reading and
-// writing the contiguous k-last fp32 state [B, HV, V=128, K=128] in place
-// (or into a second buffer).  Semantics follow the reference's decode step
-// (solution/triton/kernel.py:72-118, fused form kernel.py:289-335).
+// writing the contiguous k-last state [B, HV, V=128, K=128] in place (or
+// into a second buffer).  Semantics follow the reference's decode step
+// (solution/triton/kernel.py:72-118, fused form kernel.py:289-335); T > 1
+// tokens per sequence apply that step token after token against the state
+// kept in registers (the per-token recurrence of
+// solution/triton/prefill_kernel.py:144-178), and the state may be stored
+// as fp32 (the reference's) or bf16 (fp32 arithmetic either way).
 //
 // Work mapping (wave64):
-//   * one state row (128 fp32 = 512 B) is owned by one 16-lane DPP row of a
-//     wavefront; lane j holds elements [4j, 4j+4) and [64+4j, 64+4j+4), so
-//     each of the two 128-bit loads of a row reads 256 contiguous bytes;
-//   * a wavefront holds 4 lane groups x NS rows each (NS "slots"), i.e. it
-//     keeps 4*NS*512 B of state in flight per load burst;
+//   * one state row (128 elements) is owned by one 16-lane DPP row of a
+//     wavefront, 8 elements per lane: for an fp32 state lane j holds
+//     [4j, 4j+4) and [64+4j, 64+4j+4), so each of the row's two 128-bit
+//     loads reads 256 contiguous bytes; for a bf16 state lane j holds
+//     [8j, 8j+8), one 128-bit load over the 256-byte row;
+//   * a wavefront holds 4 lane groups x NS rows each (NS "slots");
 //   * a workgroup of WAVES wavefronts covers 4*NS*WAVES consecutive rows of
-//     one (b, hv) head; a head is split over T = 128/(4*NS*WAVES) workgroups;
-//   * grid (ratio*T, H, B) with ratio = HV/H: x = (v-head within its GVA
+//     one (b, hv) head; a head is split over R = 128/(4*NS*WAVES) workgroups;
+//   * grid (ratio*R, H, B) with ratio = HV/H: x = (v-head within its GVA
 //     group, row tile), y = q/k head, z = batch.  Every index is a shift or
 //     a multiply-add (no integer division before the first load), and the
-//     x-fastest dispatch order walks the state in memory order.
+//     x-fastest dispatch order walks the state in memory order;
 //   * dot products over K reduce inside the 16-lane row with four DPP adds
 //     (quad_perm xor1, quad_perm xor2, row_half_mirror, row_mirror), so no
 //     LDS or cross-row traffic is needed.
@@ -54,17 +59,18 @@ enum : int {
 };
 
 struct Params {
-  const uint16_t* q;        // [B, H, 128] bf16
-  const uint16_t* k;        // [B, H, 128] bf16
-  const uint16_t* v;        // [B, HV, 128] bf16
-  const float* state;       // [B, HV, 128, 128] fp32
+  const uint16_t* q;        // [B, T, H, 128] bf16
+  const uint16_t* k;        // [B, T, H, 128] bf16
+  const uint16_t* v;        // [B, T, HV, 128] bf16
+  const void* state;        // [B, HV, 128, 128] fp32 or bf16
   const float* A_log;       // [HV]
-  const uint16_t* a;        // [B, HV] bf16
+  const uint16_t* a;        // [B, T, HV] bf16
   const float* dt_bias;     // [HV]
-  const uint16_t* b;        // [B, HV] bf16
-  uint16_t* out;            // [B, HV, 128] bf16
-  float* new_state;         // [B, HV, 128, 128] fp32, may equal state
+  const uint16_t* b;        // [B, T, HV] bf16
+  uint16_t* out;            // [B, T, HV, 128] bf16
+  void* new_state;          // [B, HV, 128, 128], may equal state
   float scale;
+  int T;                    // tokens per sequence
   int H;
   int HV;
   int ratio;                // HV / H
@@ -78,6 +84,9 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) {
 // Round-to-nearest-even fp32 -> bf16 (v_cvt_pk_bf16_f32 on gfx950).
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float x) {
   return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(x)));
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
 }
 
 template <int CTRL>
@@ -100,68 +109,149 @@ __device__ __forceinline__ void row16_sum(float (&x)[N]) {
   for (int i = 0; i < N; ++i) x[i] += dpp<0x140>(x[i]);  // row_mirror
 }
 
-template <int POLICY>
-__device__ __forceinline__ f32x4 load_state(const float* p) {
+template <typename V, int POLICY>
+__device__ __forceinline__ V load_stream(const void* p) {
   if constexpr (POLICY == kPolicyNtBoth || POLICY == kPolicyNtLoad) {
-    return __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+    return __builtin_nontemporal_load(reinterpret_cast<const V*>(p));
   } else {
-    return *reinterpret_cast<const f32x4*>(p);
+    return *reinterpret_cast<const V*>(p);
   }
 }
 
-template <int POLICY>
-__device__ __forceinline__ void store_state(float* p, f32x4 x) {
+template <typename V, int POLICY>
+__device__ __forceinline__ void store_stream(void* p, V x) {
   if constexpr (POLICY == kPolicyNtBoth || POLICY == kPolicyNtStore) {
-    __builtin_nontemporal_store(x, reinterpret_cast<f32x4*>(p));
+    __builtin_nontemporal_store(x, reinterpret_cast<V*>(p));
   } else {
-    *reinterpret_cast<f32x4*>(p) = x;
+    *reinterpret_cast<V*>(p) = x;
   }
 }
 
-// NS consecutive bf16 values starting at an NS-aligned element.
+// The 8 elements lane j owns in a 128-element row, as two 8-byte (fp32
+// state layout) or one 16-byte (bf16 state layout) slice of bf16 values.
+template <bool BF16>
+__device__ __forceinline__ u32x4 load_lane_bf16x8(const uint16_t* row, int j) {
+  if constexpr (BF16) {
+    return *reinterpret_cast<const u32x4*>(row + 8 * j);
+  } else {
+    const u32x2 lo = *reinterpret_cast<const u32x2*>(row + 4 * j);
+    const u32x2 hi = *reinterpret_cast<const u32x2*>(row + 64 + 4 * j);
+    return u32x4{lo.x, lo.y, hi.x, hi.y};
+  }
+}
+
+__device__ __forceinline__ void unpack_bf16x8(u32x4 w, float (&f)[8]) {
+  f[0] = bf16_lo(w.x); f[1] = bf16_hi(w.x);
+  f[2] = bf16_lo(w.y); f[3] = bf16_hi(w.y);
+  f[4] = bf16_lo(w.z); f[5] = bf16_hi(w.z);
+  f[6] = bf16_lo(w.w); f[7] = bf16_hi(w.w);
+}
+
+// One state row slice of a lane, as loaded (before conversion to fp32).
+template <bool BF16>
+struct RowRaw;
+template <>
+struct RowRaw<false> { f32x4 c[2]; };
+template <>
+struct RowRaw<true> { u32x4 c; };
+
+template <bool BF16, int POLICY>
+__device__ __forceinline__ RowRaw<BF16> load_row(const void* state, size_t row, int j) {
+  RowRaw<BF16> r;
+  if constexpr (BF16) {
+    r.c = load_stream<u32x4, POLICY>(static_cast<const uint16_t*>(state) + row * kDim + 8 * j);
+  } else {
+    const float* p = static_cast<const float*>(state) + row * kDim + 4 * j;
+    r.c[0] = load_stream<f32x4, POLICY>(p);
+    r.c[1] = load_stream<f32x4, POLICY>(p + 64);
+  }
+  return r;
+}
+
+template <bool BF16>
+__device__ __forceinline__ void unpack_row(const RowRaw<BF16>& r, float (&s)[8]) {
+  if constexpr (BF16) {
+    unpack_bf16x8(r.c, s);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      s[i] = r.c[0][i];
+      s[4 + i] = r.c[1][i];
+    }
+  }
+}
+
+template <bool BF16, int POLICY>
+__device__ __forceinline__ void store_row(void* state, size_t row, int j, const float (&s)[8]) {
+  if constexpr (BF16) {
+    const u32x4 w{pack_bf16x2(s[0], s[1]), pack_bf16x2(s[2], s[3]),
+                  pack_bf16x2(s[4], s[5]), pack_bf16x2(s[6], s[7])};
+    store_stream<u32x4, POLICY>(static_cast<uint16_t*>(state) + row * kDim + 8 * j, w);
+  } else {
+    float* p = static_cast<float*>(state) + row * kDim + 4 * j;
+    store_stream<f32x4, POLICY>(p, f32x4{s[0], s[1], s[2], s[3]});
+    store_stream<f32x4, POLICY>(p + 64, f32x4{s[4], s[5], s[6], s[7]});
+  }
+}
+
+// NS consecutive bf16 values (NS-aligned), as raw bits: one load of 2, 4,
+// 8 or 16 bytes.  Kept raw until after the state loads are issued, so that
+// no conversion forces a wait on this load before the state stream starts.
 template <int NS>
-__device__ __forceinline__ void load_bf16_run(const uint16_t* p, float (&o)[NS]) {
+struct Bf16Run;
+template <>
+struct Bf16Run<1> { uint16_t w; };
+template <>
+struct Bf16Run<2> { uint32_t w; };
+template <>
+struct Bf16Run<4> { u32x2 w; };
+template <>
+struct Bf16Run<8> { u32x4 w; };
+
+template <int NS>
+__device__ __forceinline__ Bf16Run<NS> load_bf16_run(const uint16_t* p) {
+  Bf16Run<NS> r;
   if constexpr (NS == 1) {
-    o[0] = bf16_bits_to_f32(*p);
+    r.w = *p;
   } else if constexpr (NS == 2) {
-    const uint32_t w = *reinterpret_cast<const uint32_t*>(p);
-    o[0] = bf16_lo(w);
-    o[1] = bf16_hi(w);
+    r.w = *reinterpret_cast<const uint32_t*>(p);
   } else if constexpr (NS == 4) {
-    const u32x2 w = *reinterpret_cast<const u32x2*>(p);
-    o[0] = bf16_lo(w.x); o[1] = bf16_hi(w.x);
-    o[2] = bf16_lo(w.y); o[3] = bf16_hi(w.y);
+    r.w = *reinterpret_cast<const u32x2*>(p);
   } else {
     static_assert(NS == 8, "NS must be 1, 2, 4 or 8");
-    const u32x4 w = *reinterpret_cast<const u32x4*>(p);
-    o[0] = bf16_lo(w.x); o[1] = bf16_hi(w.x);
-    o[2] = bf16_lo(w.y); o[3] = bf16_hi(w.y);
-    o[4] = bf16_lo(w.z); o[5] = bf16_hi(w.z);
-    o[6] = bf16_lo(w.w); o[7] = bf16_hi(w.w);
+    r.w = *reinterpret_cast<const u32x4*>(p);
+  }
+  return r;
+}
+
+template <int NS>
+__device__ __forceinline__ void unpack_bf16_run(const Bf16Run<NS>& r, float (&o)[NS]) {
+  if constexpr (NS == 1) {
+    o[0] = bf16_bits_to_f32(r.w);
+  } else if constexpr (NS == 2) {
+    o[0] = bf16_lo(r.w); o[1] = bf16_hi(r.w);
+  } else if constexpr (NS == 4) {
+    o[0] = bf16_lo(r.w.x); o[1] = bf16_hi(r.w.x);
+    o[2] = bf16_lo(r.w.y); o[3] = bf16_hi(r.w.y);
+  } else {
+    o[0] = bf16_lo(r.w.x); o[1] = bf16_hi(r.w.x);
+    o[2] = bf16_lo(r.w.y); o[3] = bf16_hi(r.w.y);
+    o[4] = bf16_lo(r.w.z); o[5] = bf16_hi(r.w.z);
+    o[6] = bf16_lo(r.w.w); o[7] = bf16_hi(r.w.w);
   }
 }
 
 template <int NS>
 __device__ __forceinline__ void store_bf16_run(uint16_t* p, const float (&x)[NS]) {
-  uint32_t h[NS];
-#pragma unroll
-  for (int i = 0; i < NS; ++i) h[i] = f32_to_bf16_bits(x[i]);
   if constexpr (NS == 1) {
-    *p = static_cast<uint16_t>(h[0]);
+    *p = static_cast<uint16_t>(f32_to_bf16_bits(x[0]));
   } else if constexpr (NS == 2) {
-    *reinterpret_cast<uint32_t*>(p) = h[0] | (h[1] << 16);
+    *reinterpret_cast<uint32_t*>(p) = pack_bf16x2(x[0], x[1]);
   } else if constexpr (NS == 4) {
-    u32x2 w;
-    w.x = h[0] | (h[1] << 16);
-    w.y = h[2] | (h[3] << 16);
-    *reinterpret_cast<u32x2*>(p) = w;
+    *reinterpret_cast<u32x2*>(p) = u32x2{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])};
   } else {
-    u32x4 w;
-    w.x = h[0] | (h[1] << 16);
-    w.y = h[2] | (h[3] << 16);
-    w.z = h[4] | (h[5] << 16);
-    w.w = h[6] | (h[7] << 16);
-    *reinterpret_cast<u32x4*>(p) = w;
+    *reinterpret_cast<u32x4*>(p) = u32x4{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]),
+                                         pack_bf16x2(x[4], x[5]), pack_bf16x2(x[6], x[7])};
   }
 }
 
@@ -179,78 +269,45 @@ __device__ __forceinline__ void gates(float a, float dt_bias, float A_log,
   beta = __builtin_amdgcn_rcpf(1.0f + __expf(-b));
 }
 
-__device__ __forceinline__ void unpack4(u32x2 w, float* f) {
-  f[0] = bf16_lo(w.x); f[1] = bf16_hi(w.x);
-  f[2] = bf16_lo(w.y); f[3] = bf16_hi(w.y);
+// Per-token inputs of one lane, as loaded (raw bits, converted on use).
+template <int NS>
+struct TokenIn {
+  uint16_t a_bits;
+  uint16_t b_bits;
+  u32x4 q;          // 8 bf16: this lane's elements of q
+  u32x4 k;
+  Bf16Run<NS> v;    // v of this lane group's NS rows
+};
+
+template <int NS, bool BF16>
+__device__ __forceinline__ void load_token(const Params& p, int bi, int t, int hq,
+                                           int hv, int row0, int j, TokenIn<NS>& in) {
+  const size_t bt = static_cast<size_t>(bi) * p.T + t;
+  in.a_bits = p.a[bt * p.HV + hv];
+  in.b_bits = p.b[bt * p.HV + hv];
+  const size_t qk = (bt * p.H + hq) * kDim;
+  in.q = load_lane_bf16x8<BF16>(p.q + qk, j);
+  in.k = load_lane_bf16x8<BF16>(p.k + qk, j);
+  in.v = load_bf16_run<NS>(p.v + (bt * p.HV + hv) * kDim + row0);
 }
 
-// Block order: consecutive blocks -- which the dispatcher hands round-robin
-// to the 8 XCDs -- stream adjacent state rows.  Renumbering blocks so that
-// each XCD works on its own contiguous eighth (sharing q/k in that XCD's L2)
-// measured 5% slower at B=256 and 18% slower at B=64 (qk16_v32) than this
-// natural order, so none is applied.
-
-// One decode step for 4*NS*WAVES rows of one (b, hv) head per workgroup.
-template <int NS, int WAVES, bool L2NORM, int POLICY>
-__global__ __launch_bounds__(64 * WAVES) void gdn_decode_k128(Params p) {
-  constexpr int kRowsPerWave = kLaneGroups * NS;
-  constexpr int kRowsPerBlock = kRowsPerWave * WAVES;
-  constexpr int kTiles = kDim / kRowsPerBlock;
-  static_assert(kDim % kRowsPerBlock == 0, "rows per block must divide 128");
-
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int grp = lane >> 4;
-  const int j = lane & 15;
-
-  static_assert((kTiles & (kTiles - 1)) == 0, "tiles per head is a power of two");
-  const int tile = static_cast<int>(blockIdx.x) & (kTiles - 1);
-  const int hq = static_cast<int>(blockIdx.y);          // q/k head
-  const int bi = static_cast<int>(blockIdx.z);
-  const int hv = hq * p.ratio + static_cast<int>(blockIdx.x) / kTiles;
-  const int head = bi * p.HV + hv;
-  const int row0 = tile * kRowsPerBlock + wave * kRowsPerWave + grp * NS;
-
-  // Issue every global load before any arithmetic.  Loads retire in issue
-  // order, so the small per-head operands (gate scalars, q, k, v) go first:
-  // their math then overlaps the state stream instead of waiting behind it.
-  const float A_log = p.A_log[hv];
-  const float dt_bias = p.dt_bias[hv];
-  const uint16_t a_bits = p.a[head];
-  const uint16_t b_bits = p.b[head];
-
-  const size_t qk_off = (static_cast<size_t>(bi) * p.H + hq) * kDim + 4 * j;
-  const u32x2 qa = *reinterpret_cast<const u32x2*>(p.q + qk_off);
-  const u32x2 qb = *reinterpret_cast<const u32x2*>(p.q + qk_off + 64);
-  const u32x2 ka = *reinterpret_cast<const u32x2*>(p.k + qk_off);
-  const u32x2 kb = *reinterpret_cast<const u32x2*>(p.k + qk_off + 64);
-
-  const size_t row_base = static_cast<size_t>(head) * kDim + row0;  // row index
-  float vrow[NS];
-  load_bf16_run<NS>(p.v + row_base, vrow);
-  __builtin_amdgcn_sched_barrier(0);
-
-  const float* sp = p.state + row_base * kDim + 4 * j;
-  f32x4 s[NS][2];
-#pragma unroll
-  for (int n = 0; n < NS; ++n) {
-    s[n][0] = load_state<POLICY>(sp + n * kDim);
-    s[n][1] = load_state<POLICY>(sp + n * kDim + 64);
-  }
-  __builtin_amdgcn_sched_barrier(0);
-
-  // Gates (uniform per head), reference kernel.py:73-75 / 289-305.
+// One token of the recurrence on the NS rows a lane group holds:
+// decay, delta rule, rank-1 update (in s) and outputs o (reference
+// kernel.py:73-75, 101-113).
+template <int NS, bool L2NORM>
+__device__ __forceinline__ void token_update(float (&s)[NS][8], const TokenIn<NS>& in,
+                                             float A_log, float dt_bias, float scale,
+                                             float (&o)[NS]) {
   float g, beta;
-  gates(bf16_bits_to_f32(a_bits), dt_bias, A_log, bf16_bits_to_f32(b_bits), g, beta);
+  gates(bf16_bits_to_f32(in.a_bits), dt_bias, A_log, bf16_bits_to_f32(in.b_bits), g, beta);
 
-  float qf[8], kf[8];
-  unpack4(qa, qf);
-  unpack4(qb, qf + 4);
-  unpack4(ka, kf);
-  unpack4(kb, kf + 4);
+  float qf[8], kf[8], vrow[NS];
+  unpack_bf16x8(in.q, qf);
+  unpack_bf16x8(in.k, kf);
+  unpack_bf16_run<NS>(in.v, vrow);
 
   // Per-head reductions: |q|^2, |k|^2 (L2-norm only) and k.q.
-  float qscale = p.scale;
+  float qscale = scale;
   float kscale = 1.0f;
   float kq;
   if constexpr (L2NORM) {
@@ -285,41 +342,91 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_decode_k128(Params p) {
   for (int n = 0; n < NS; ++n) {
     float ak = 0.0f, aq = 0.0f;
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        ak = fmaf(s[n][c][i], kf[4 * c + i], ak);
-        aq = fmaf(s[n][c][i], qf[4 * c + i], aq);
-      }
+    for (int i = 0; i < 8; ++i) {
+      ak = fmaf(s[n][i], kf[i], ak);
+      aq = fmaf(s[n][i], qf[i], aq);
     }
     red[2 * n] = ak;
     red[2 * n + 1] = aq;
   }
   row16_sum<2 * NS>(red);
 
-  // Delta rule, rank-1 update and output (reference kernel.py:101-113).
-  float o[NS];
 #pragma unroll
   for (int n = 0; n < NS; ++n) {
     const float old_v = g * red[2 * n];             // k_hat . (g S)
     const float d = beta * (vrow[n] - old_v);       // beta * (v - old_v)
     o[n] = fmaf(d, kq, g * red[2 * n + 1]);         // q' . S_new
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
+    for (int i = 0; i < 8; ++i) s[n][i] = fmaf(d, kf[i], g * s[n][i]);
+  }
+}
+
+// Block order: consecutive blocks -- which the dispatcher hands round-robin
+// to the 8 XCDs -- stream adjacent state rows.  Renumbering blocks so that
+// each XCD works on its own contiguous eighth (sharing q/k in that XCD's L2)
+// measured 5% slower at B=256 and 18% slower at B=64 (qk16_v32) than this
+// natural order, so none is applied.
+
+// T tokens (T = 1 at compile time unless MULTI) of 4*NS*WAVES rows of one
+// (b, hv) head per workgroup.
+template <int NS, int WAVES, bool L2NORM, int POLICY, bool BF16, bool MULTI>
+__global__ __launch_bounds__(64 * WAVES) void gdn_decode_k128(Params p) {
+  constexpr int kRowsPerWave = kLaneGroups * NS;
+  constexpr int kRowsPerBlock = kRowsPerWave * WAVES;
+  constexpr int kTiles = kDim / kRowsPerBlock;
+  static_assert(kDim % kRowsPerBlock == 0, "rows per block must divide 128");
+  static_assert((kTiles & (kTiles - 1)) == 0, "tiles per head is a power of two");
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int grp = lane >> 4;
+  const int j = lane & 15;
+
+  const int tile = static_cast<int>(blockIdx.x) & (kTiles - 1);
+  const int hq = static_cast<int>(blockIdx.y);          // q/k head
+  const int bi = static_cast<int>(blockIdx.z);
+  const int hv = hq * p.ratio + static_cast<int>(blockIdx.x) / kTiles;
+  const int head = bi * p.HV + hv;
+  const int row0 = tile * kRowsPerBlock + wave * kRowsPerWave + grp * NS;
+  const int T = MULTI ? p.T : 1;
+
+  // Issue every global load before any arithmetic.  Loads retire in issue
+  // order, so the small per-head operands (gate scalars, q, k, v) go first:
+  // their math then overlaps the state stream instead of waiting behind it.
+  const float A_log = p.A_log[hv];
+  const float dt_bias = p.dt_bias[hv];
+  TokenIn<NS> cur;
+  load_token<NS, BF16>(p, bi, 0, hq, hv, row0, j, cur);
+  __builtin_amdgcn_sched_barrier(0);
+
+  const size_t row_base = static_cast<size_t>(head) * kDim + row0;  // row index
+  RowRaw<BF16> raw[NS];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        s[n][c][i] = fmaf(d, kf[4 * c + i], g * s[n][c][i]);
-      }
+  for (int n = 0; n < NS; ++n) raw[n] = load_row<BF16, POLICY>(p.state, row_base + n, j);
+  __builtin_amdgcn_sched_barrier(0);
+
+  float s[NS][8];
+#pragma unroll
+  for (int n = 0; n < NS; ++n) unpack_row<BF16>(raw[n], s[n]);
+
+  for (int t = 0; t < T; ++t) {
+    TokenIn<NS> nxt;
+    if constexpr (MULTI) {
+      if (t + 1 < T) load_token<NS, BF16>(p, bi, t + 1, hq, hv, row0, j, nxt);  // prefetch
+    }
+    float o[NS];
+    token_update<NS, L2NORM>(s, cur, A_log, dt_bias, p.scale, o);
+    if (j == 0) {
+      const size_t out_row = ((static_cast<size_t>(bi) * T + t) * p.HV + hv) * kDim + row0;
+      store_bf16_run<NS>(p.out + out_row, o);
+    }
+    if constexpr (MULTI) {
+      if (t + 1 < T) cur = nxt;
     }
   }
 
-  if (j == 0) store_bf16_run<NS>(p.out + row_base, o);
-  float* dp = p.new_state + row_base * kDim + 4 * j;
 #pragma unroll
-  for (int n = 0; n < NS; ++n) {
-    store_state<POLICY>(dp + n * kDim, s[n][0]);
-    store_state<POLICY>(dp + n * kDim + 64, s[n][1]);
-  }
+  for (int n = 0; n < NS; ++n) store_row<BF16, POLICY>(p.new_state, row_base + n, j, s[n]);
 }
 
 // ---------------------------------------------------------------------------
@@ -334,74 +441,108 @@ struct Launch {
   hipEvent_t stop;
 };
 
-template <int NS, int W, bool L2, int POL>
-hipError_t launch_one(const Params& p, unsigned blocks, const Launch& l) {
+// Kernel variant: the fp32 single-token kernel is built for every launch
+// shape and cache policy (the sweep space); bf16-state and multi-token
+// kernels for 1, 2 or 4 rows per lane group and policies 0 and 1.
+struct Variant {
+  bool l2;
+  bool bf16;
+  bool multi;
+};
+
+template <int NS, int W, int POL, bool BF16, bool MULTI>
+hipError_t launch_one(bool l2, const Params& p, unsigned nb, const Launch& l) {
   constexpr unsigned kT = kDim / (kLaneGroups * NS * W);
-  const unsigned per_batch = static_cast<unsigned>(p.HV) * kT;
-  const dim3 grid_xyz(static_cast<unsigned>(p.ratio) * kT, static_cast<unsigned>(p.H),
-                      blocks / per_batch);
+  const dim3 grid(static_cast<unsigned>(p.ratio) * kT, static_cast<unsigned>(p.H), nb);
+  const dim3 block(64 * W);
   if (l.start || l.stop) {
-    hipExtLaunchKernelGGL((gdn_decode_k128<NS, W, L2, POL>), grid_xyz,
-                          dim3(64 * W), 0, l.stream, l.start, l.stop, 0, p);
+    if (l2) {
+      hipExtLaunchKernelGGL((gdn_decode_k128<NS, W, true, POL, BF16, MULTI>), grid, block,
+                            0, l.stream, l.start, l.stop, 0, p);
+    } else {
+      hipExtLaunchKernelGGL((gdn_decode_k128<NS, W, false, POL, BF16, MULTI>), grid, block,
+                            0, l.stream, l.start, l.stop, 0, p);
+    }
   } else {
-    hipLaunchKernelGGL((gdn_decode_k128<NS, W, L2, POL>), grid_xyz,
-                       dim3(64 * W), 0, l.stream, p);
+    if (l2) {
+      hipLaunchKernelGGL((gdn_decode_k128<NS, W, true, POL, BF16, MULTI>), grid, block, 0,
+                         l.stream, p);
+    } else {
+      hipLaunchKernelGGL((gdn_decode_k128<NS, W, false, POL, BF16, MULTI>), grid, block, 0,
+                         l.stream, p);
+    }
   }
   return hipGetLastError();
 }
 
-template <int NS, int W, bool L2>
-hipError_t by_policy(int pol, const Params& p, unsigned blocks, const Launch& s) {
+template <int NS, int W, bool BF16, bool MULTI>
+hipError_t by_policy(int pol, bool l2, const Params& p, unsigned nb, const Launch& l) {
+  constexpr bool kFull = !BF16 && !MULTI;
   switch (pol) {
-    case kPolicyDefault: return launch_one<NS, W, L2, kPolicyDefault>(p, blocks, s);
-    case kPolicyNtBoth: return launch_one<NS, W, L2, kPolicyNtBoth>(p, blocks, s);
-    case kPolicyNtStore: return launch_one<NS, W, L2, kPolicyNtStore>(p, blocks, s);
-    case kPolicyNtLoad: return launch_one<NS, W, L2, kPolicyNtLoad>(p, blocks, s);
-    default: return hipErrorInvalidValue;
-  }
-}
-
-template <int NS, int W>
-hipError_t by_norm(bool l2, int pol, const Params& p, unsigned blocks, const Launch& s) {
-  return l2 ? by_policy<NS, W, true>(pol, p, blocks, s)
-            : by_policy<NS, W, false>(pol, p, blocks, s);
-}
-
-template <int NS>
-hipError_t by_waves(int w, bool l2, int pol, const Params& p, unsigned blocks,
-                    const Launch& s) {
-  switch (w) {
-    case 1: return by_norm<NS, 1>(l2, pol, p, blocks, s);
-    case 2: return by_norm<NS, 2>(l2, pol, p, blocks, s);
-    case 4: return by_norm<NS, 4>(l2, pol, p, blocks, s);
-    case 8:
-      if constexpr (NS * 8 <= 32) return by_norm<NS, 8>(l2, pol, p, blocks, s);
+    case kPolicyDefault: return launch_one<NS, W, kPolicyDefault, BF16, MULTI>(l2, p, nb, l);
+    case kPolicyNtBoth: return launch_one<NS, W, kPolicyNtBoth, BF16, MULTI>(l2, p, nb, l);
+    case kPolicyNtStore:
+      if constexpr (kFull) return launch_one<NS, W, kPolicyNtStore, BF16, MULTI>(l2, p, nb, l);
+      return hipErrorInvalidValue;
+    case kPolicyNtLoad:
+      if constexpr (kFull) return launch_one<NS, W, kPolicyNtLoad, BF16, MULTI>(l2, p, nb, l);
       return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
 }
 
-hipError_t dispatch(int ns, int w, bool l2, int pol, const Params& p,
-                    unsigned blocks, const Launch& s) {
-  switch (ns) {
-    case 1: return by_waves<1>(w, l2, pol, p, blocks, s);
-    case 2: return by_waves<2>(w, l2, pol, p, blocks, s);
-    case 4: return by_waves<4>(w, l2, pol, p, blocks, s);
-    case 8: return by_waves<8>(w, l2, pol, p, blocks, s);
+template <int NS, bool BF16, bool MULTI>
+hipError_t by_waves(int w, int pol, bool l2, const Params& p, unsigned nb, const Launch& l) {
+  switch (w) {
+    case 1: return by_policy<NS, 1, BF16, MULTI>(pol, l2, p, nb, l);
+    case 2: return by_policy<NS, 2, BF16, MULTI>(pol, l2, p, nb, l);
+    case 4: return by_policy<NS, 4, BF16, MULTI>(pol, l2, p, nb, l);
+    case 8:
+      if constexpr (NS * 8 <= 32) return by_policy<NS, 8, BF16, MULTI>(pol, l2, p, nb, l);
+      return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
 }
 
-bool is_pow2_upto8(int x) { return x == 1 || x == 2 || x == 4 || x == 8; }
+template <bool BF16, bool MULTI>
+hipError_t by_ns(int ns, int w, int pol, bool l2, const Params& p, unsigned nb,
+                 const Launch& l) {
+  switch (ns) {
+    case 1: return by_waves<1, BF16, MULTI>(w, pol, l2, p, nb, l);
+    case 2: return by_waves<2, BF16, MULTI>(w, pol, l2, p, nb, l);
+    case 4: return by_waves<4, BF16, MULTI>(w, pol, l2, p, nb, l);
+    case 8:
+      if constexpr (!BF16 && !MULTI) return by_waves<8, BF16, MULTI>(w, pol, l2, p, nb, l);
+      return hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t dispatch(const Variant& v, int ns, int w, int pol, const Params& p, unsigned nb,
+                    const Launch& l) {
+  if (!v.bf16 && !v.multi) return by_ns<false, false>(ns, w, pol, v.l2, p, nb, l);
+  if (!v.bf16 && v.multi) return by_ns<false, true>(ns, w, pol, v.l2, p, nb, l);
+  if (v.bf16 && !v.multi) return by_ns<true, false>(ns, w, pol, v.l2, p, nb, l);
+  return by_ns<true, true>(ns, w, pol, v.l2, p, nb, l);
+}
+
+bool shape_supported(const Variant& v, int ns, int w, int pol) {
+  const bool pow2 = (ns == 1 || ns == 2 || ns == 4 || ns == 8) &&
+                    (w == 1 || w == 2 || w == 4 || w == 8);
+  if (!pow2 || ns * w > 32) return false;
+  if (v.bf16 || v.multi) return ns <= 4 && (pol == kPolicyDefault || pol == kPolicyNtBoth);
+  return pol >= kPolicyDefault && pol <= kPolicyNtLoad;
+}
 
 bool aligned(const void* p, uintptr_t a) {
   return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
 }
 
-// Launch shape for B*HV heads, from a rocprofv3 sweep of every shape and
-// cache policy on MI355X: two rows per lane group with nontemporal state
-// loads and stores is fastest from B*HV = 256 (B=8 qk16_v32, 7.0 us) to
-// 8192 (B=256, 168 us = 6.4 TB/s); below that every shape sits within
+// Launch shape for B*HV heads, from rocprofv3 and kernel-stamped sweeps of
+// every shape and cache policy on MI355X with steps rotating over >= 1 GiB
+// of states: two rows per lane group with nontemporal state loads and
+// stores is best or within 3% of best from B*HV = 8 to 8192 (B=256
+// qk16_v32: 165 us = 6.5 TB/s); below ~128 heads every shape sits within
 // 0.1 us of a fixed ~3 us launch-plus-round-trip floor.
 void choose_shape(long long heads, int* ns, int* waves, int* policy) {
   *ns = 2;
@@ -409,30 +550,29 @@ void choose_shape(long long heads, int* ns, int* waves, int* policy) {
   *waves = heads <= 64 ? 2 : 4;  // 16 or 32 rows per block
 }
 
-int step_impl(const void* q, const void* k, const void* v, const float* state,
-              const float* A_log, const void* a, const float* dt_bias,
-              const void* b, float scale, void* output, float* new_state,
-              int B, int H, int HV, int K, int V, int use_qk_l2norm, int ns,
-              int waves, int policy, void* start_event, void* stop_event,
-              void* hip_stream) {
-  if (B < 0 || H <= 0 || HV <= 0 || HV % H != 0) return hipErrorInvalidValue;
+int steps_impl(const void* q, const void* k, const void* v, const void* state,
+               const float* A_log, const void* a, const float* dt_bias, const void* b,
+               float scale, void* output, void* new_state, int B, int T, int H, int HV,
+               int K, int V, int state_bf16, int use_qk_l2norm, int ns, int waves,
+               int policy, void* start_event, void* stop_event, void* hip_stream) {
+  if (B < 0 || T < 1 || H <= 0 || HV <= 0 || HV % H != 0) return hipErrorInvalidValue;
   if (H > 65535) return hipErrorInvalidValue;  // grid y
   if (K != kDim || V != kDim) return hipErrorInvalidValue;
-  if (!is_pow2_upto8(ns) || !is_pow2_upto8(waves) || ns * waves > 32)
-    return hipErrorInvalidValue;
-  if (policy < kPolicyDefault || policy > kPolicyNtLoad) return hipErrorInvalidValue;
+  if (state_bf16 != 0 && state_bf16 != 1) return hipErrorInvalidValue;
+  const Variant var{use_qk_l2norm != 0, state_bf16 != 0, T > 1};
+  if (!shape_supported(var, ns, waves, policy)) return hipErrorInvalidValue;
   if (B == 0) return hipSuccess;
   if (!q || !k || !v || !state || !A_log || !a || !dt_bias || !b || !output ||
       !new_state)
     return hipErrorInvalidValue;
-  // 16-byte state rows chunks, 8-byte q/k chunks, up to 16-byte v/out runs.
-  if (!aligned(state, 16) || !aligned(new_state, 16) || !aligned(q, 8) ||
-      !aligned(k, 8) || !aligned(v, 16) || !aligned(output, 16) ||
+  // 16-byte state row slices, 8- or 16-byte q/k slices, up to 16-byte v/out runs.
+  if (!aligned(state, 16) || !aligned(new_state, 16) || !aligned(q, 16) ||
+      !aligned(k, 16) || !aligned(v, 16) || !aligned(output, 16) ||
       !aligned(A_log, 4) || !aligned(dt_bias, 4) || !aligned(a, 2) ||
       !aligned(b, 2))
     return hipErrorInvalidValue;
-  const size_t state_bytes =
-      static_cast<size_t>(B) * HV * kDim * kDim * sizeof(float);
+  const size_t elem = state_bf16 ? 2 : 4;
+  const size_t state_bytes = static_cast<size_t>(B) * HV * kDim * kDim * elem;
   if (new_state != state) {
     const uintptr_t s0 = reinterpret_cast<uintptr_t>(state);
     const uintptr_t d0 = reinterpret_cast<uintptr_t>(new_state);
@@ -440,8 +580,7 @@ int step_impl(const void* q, const void* k, const void* v, const float* state,
       return hipErrorInvalidValue;  // partial overlap: only exact aliasing
   }
 
-  const int rows_per_block = kLaneGroups * ns * waves;
-  const long long tiles = kDim / rows_per_block;
+  const long long tiles = kDim / (kLaneGroups * ns * waves);
   const long long threads_per_block = 64LL * waves;
   // Keep each launch's work-item count well inside 32 bits.
   const long long max_blocks = (1LL << 31) / threads_per_block;
@@ -453,26 +592,27 @@ int step_impl(const void* q, const void* k, const void* v, const float* state,
   p.A_log = A_log;
   p.dt_bias = dt_bias;
   p.scale = scale;
+  p.T = T;
   p.H = H;
   p.HV = HV;
   p.ratio = HV / H;
   for (long long b0 = 0; b0 < B; b0 += batches_per_launch) {
     const long long nb = (B - b0) < batches_per_launch ? (B - b0) : batches_per_launch;
-    p.q = static_cast<const uint16_t*>(q) + b0 * H * kDim;
-    p.k = static_cast<const uint16_t*>(k) + b0 * H * kDim;
-    p.v = static_cast<const uint16_t*>(v) + b0 * HV * kDim;
-    p.state = state + b0 * HV * kDim * kDim;
-    p.a = static_cast<const uint16_t*>(a) + b0 * HV;
-    p.b = static_cast<const uint16_t*>(b) + b0 * HV;
-    p.out = static_cast<uint16_t*>(output) + b0 * HV * kDim;
-    p.new_state = new_state + b0 * HV * kDim * kDim;
-    const unsigned blocks = static_cast<unsigned>(nb * HV * tiles);
+    const long long bt0 = b0 * T;
+    p.q = static_cast<const uint16_t*>(q) + bt0 * H * kDim;
+    p.k = static_cast<const uint16_t*>(k) + bt0 * H * kDim;
+    p.v = static_cast<const uint16_t*>(v) + bt0 * HV * kDim;
+    p.state = static_cast<const char*>(state) + b0 * HV * kDim * kDim * elem;
+    p.a = static_cast<const uint16_t*>(a) + bt0 * HV;
+    p.b = static_cast<const uint16_t*>(b) + bt0 * HV;
+    p.out = static_cast<uint16_t*>(output) + bt0 * HV * kDim;
+    p.new_state = static_cast<char*>(new_state) + b0 * HV * kDim * kDim * elem;
     // Start stamp on the first launch, stop stamp on the last.
     Launch l;
     l.stream = static_cast<hipStream_t>(hip_stream);
     l.start = b0 == 0 ? static_cast<hipEvent_t>(start_event) : nullptr;
     l.stop = b0 + nb == B ? static_cast<hipEvent_t>(stop_event) : nullptr;
-    const hipError_t e = dispatch(ns, waves, use_qk_l2norm != 0, policy, p, blocks, l);
+    const hipError_t e = dispatch(var, ns, waves, policy, p, static_cast<unsigned>(nb), l);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
@@ -489,26 +629,34 @@ int gdn_decode_step(const void* q, const void* k, const void* v,
                     const float* dt_bias, const void* b, float scale,
                     void* output, float* new_state, int B, int H, int HV,
                     int K, int V, int use_qk_l2norm, void* hip_stream) {
+  return gdn_decode_steps(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
+                          B, 1, H, HV, K, V, 0, use_qk_l2norm, hip_stream);
+}
+
+int gdn_decode_steps(const void* q, const void* k, const void* v, const void* state,
+                     const float* A_log, const void* a, const float* dt_bias,
+                     const void* b, float scale, void* output, void* new_state,
+                     int B, int T, int H, int HV, int K, int V, int state_bf16,
+                     int use_qk_l2norm, void* hip_stream) {
   if (B < 0 || HV <= 0) return hipErrorInvalidValue;
   int ns = 0, waves = 0, policy = 0;
   choose_shape(static_cast<long long>(B) * HV, &ns, &waves, &policy);
-  return step_impl(q, k, v, state, A_log, a, dt_bias, b, scale, output,
-                   new_state, B, H, HV, K, V, use_qk_l2norm, ns, waves,
-                   policy, nullptr, nullptr, hip_stream);
+  return steps_impl(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, B, T,
+                    H, HV, K, V, state_bf16, use_qk_l2norm, ns, waves, policy, nullptr,
+                    nullptr, hip_stream);
 }
 
 int gdn_decode_step_shaped(const void* q, const void* k, const void* v,
-                           const float* state, const float* A_log,
+                           const void* state, const float* A_log,
                            const void* a, const float* dt_bias, const void* b,
-                           float scale, void* output, float* new_state, int B,
-                           int H, int HV, int K, int V, int use_qk_l2norm,
-                           int rows_per_lane_group, int waves_per_block,
-                           int cache_policy, void* start_event,
-                           void* stop_event, void* hip_stream) {
-  return step_impl(q, k, v, state, A_log, a, dt_bias, b, scale, output,
-                   new_state, B, H, HV, K, V, use_qk_l2norm,
-                   rows_per_lane_group, waves_per_block, cache_policy,
-                   start_event, stop_event, hip_stream);
+                           float scale, void* output, void* new_state, int B,
+                           int T, int H, int HV, int K, int V, int state_bf16,
+                           int use_qk_l2norm, int rows_per_lane_group,
+                           int waves_per_block, int cache_policy,
+                           void* start_event, void* stop_event, void* hip_stream) {
+  return steps_impl(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, B, T,
+                    H, HV, K, V, state_bf16, use_qk_l2norm, rows_per_lane_group,
+                    waves_per_block, cache_policy, start_event, stop_event, hip_stream);
 }
 
 int gdn_decode_launch_shape(int B, int HV, int* rows_per_lane_group,
@@ -530,6 +678,6 @@ const char* gdn_decode_error_string(int code) {
   return hipGetErrorString(static_cast<hipError_t>(code));
 }
 
-int gdn_decode_abi_version(void) { return 1; }
+int gdn_decode_abi_version(void) { return 2; }
 
 }  // extern "C"

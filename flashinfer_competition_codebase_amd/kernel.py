@@ -20,14 +20,19 @@ reference decode entry, solution/triton/kernel.py:146), so the positional
 signature is the reference's.
 
 Tensor contract (reference shapes, solution/triton/kernel.py:33-48 and
-scripts/profile_proton.py:106-110): q, k ``[B, 1, H, 128]`` bf16; v
-``[B, 1, HV, 128]`` bf16 with ``HV % H == 0``; state ``[B, HV, 128, 128]``
-fp32 k-last or None (zeros); A_log, dt_bias ``[HV]`` fp32; a, b
-``[B, 1, HV]`` or ``[B, HV]`` bf16; scale float, 0-d tensor, None or 0
-(None/0 mean ``1/sqrt(K)``); output ``[B, 1, HV, 128]`` bf16; new_state
-``[B, HV, 128, 128]`` fp32.  All tensors dense (contiguous) on one device.
-Unlike the reference, malformed arguments raise ``TypeError`` /
-``ValueError`` before anything is launched.
+scripts/profile_proton.py:106-110): q, k ``[B, T, H, 128]`` bf16; v
+``[B, T, HV, 128]`` bf16 with ``HV % H == 0``; state ``[B, HV, 128, 128]``
+k-last, fp32 or bf16, or None (zeros); A_log, dt_bias ``[HV]`` fp32; a, b
+``[B, T, HV]`` bf16 (``[B, HV]`` also at T = 1); scale float, 0-d tensor,
+None or 0 (None/0 mean ``1/sqrt(K)``); output ``[B, T, HV, 128]`` bf16;
+new_state like state.  The reference's decode is T = 1 with an fp32 state;
+T > 1 (multi-token decode: the state is read once, the T tokens are applied
+in order, solution/triton/prefill_kernel.py:144-178) and a bf16 state (fp32
+arithmetic, stored rounded to nearest even) are the FlashInfer decode
+features the reference records (findings/fi-gdn-decode-kernel.md:11-16).
+All tensors dense (contiguous) on one device.  Unlike the reference,
+malformed arguments raise ``TypeError`` / ``ValueError`` before anything is
+launched.
 """
 
 from __future__ import annotations
@@ -73,17 +78,31 @@ def _expect(t, name: str, dtype: torch.dtype, shape: tuple) -> None:
         raise ValueError(f"{name} must be contiguous")
 
 
-def _gate_shape(t, B: int, HV: int) -> tuple:
+STATE_DTYPES = (torch.float32, torch.bfloat16)
+
+
+def _gate_shape(t, B: int, T: int, HV: int) -> tuple:
     shape = tuple(t.shape) if isinstance(t, torch.Tensor) else None
-    return (B, 1, HV) if shape == (B, 1, HV) else (B, HV)
+    return (B, HV) if (T == 1 and shape == (B, HV)) else (B, T, HV)
+
+
+def _expect_state(t, name: str, shape: tuple, dtype=None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
+    if t.dtype not in STATE_DTYPES:
+        raise TypeError(f"{name} must be float32 or bfloat16, got {t.dtype}")
+    if dtype is not None and t.dtype != dtype:
+        raise TypeError(f"{name} must have the state's dtype {dtype}, got {t.dtype}")
+    _expect(t, name, t.dtype, shape)
 
 
 def check_inputs(q, k, v, state, A_log, a, dt_bias, b, output=None, new_state=None):
-    """Validate the decode-step tensors; returns ``(B, H, HV)``.
+    """Validate the decode-step tensors; returns ``(B, T, H, HV)``.
 
     Shape and dtype rules are the reference's (solution/triton/kernel.py:
-    33-48, 58-67 generalised to any ``HV % H == 0``); the device check comes
-    last so that every other rule can be exercised without a GPU.
+    33-48, 58-67 generalised to any ``HV % H == 0``, T >= 1 and a bf16
+    state); the device check comes last so that every other rule can be
+    exercised without a GPU.
     """
     if not isinstance(q, torch.Tensor) or q.dim() != 4:
         raise ValueError("q must be a 4-D tensor [B, T, H, K]")
@@ -91,25 +110,26 @@ def check_inputs(q, k, v, state, A_log, a, dt_bias, b, output=None, new_state=No
         raise ValueError("v must be a 4-D tensor [B, T, HV, V]")
     B, T, H, K = q.shape
     HV, V = v.shape[2], v.shape[3]
-    if T != 1:
-        raise ValueError(f"decode takes one token per sequence (T == 1), got T={T}")
+    if T < 1:
+        raise ValueError(f"decode takes at least one token per sequence, got T={T}")
     if K != K_DIM or V != V_DIM:
         raise ValueError(f"K and V must be {K_DIM}, got K={K}, V={V}")
     if H <= 0 or HV <= 0 or HV % H != 0:
         raise ValueError(f"v-heads must be a multiple of q/k heads, got H={H}, HV={HV}")
-    _expect(q, "q", torch.bfloat16, (B, 1, H, K))
-    _expect(k, "k", torch.bfloat16, (B, 1, H, K))
-    _expect(v, "v", torch.bfloat16, (B, 1, HV, V))
+    _expect(q, "q", torch.bfloat16, (B, T, H, K))
+    _expect(k, "k", torch.bfloat16, (B, T, H, K))
+    _expect(v, "v", torch.bfloat16, (B, T, HV, V))
     if state is not None:
-        _expect(state, "state", torch.float32, (B, HV, V, K))
+        _expect_state(state, "state", (B, HV, V, K))
     _expect(A_log, "A_log", torch.float32, (HV,))
     _expect(dt_bias, "dt_bias", torch.float32, (HV,))
-    _expect(a, "a", torch.bfloat16, _gate_shape(a, B, HV))
-    _expect(b, "b", torch.bfloat16, _gate_shape(b, B, HV))
+    _expect(a, "a", torch.bfloat16, _gate_shape(a, B, T, HV))
+    _expect(b, "b", torch.bfloat16, _gate_shape(b, B, T, HV))
     if output is not None:
-        _expect(output, "output", torch.bfloat16, (B, 1, HV, V))
+        _expect(output, "output", torch.bfloat16, (B, T, HV, V))
     if new_state is not None:
-        _expect(new_state, "new_state", torch.float32, (B, HV, V, K))
+        _expect_state(new_state, "new_state", (B, HV, V, K),
+                      None if state is None else state.dtype)
     tensors = [q, k, v, A_log, a, dt_bias, b]
     tensors += [t for t in (state, output, new_state) if t is not None]
     dev = q.device
@@ -123,7 +143,7 @@ def check_inputs(q, k, v, state, A_log, a, dt_bias, b, output=None, new_state=No
     if state is not None and new_state is not None and new_state is not state:
         if new_state.data_ptr() != state.data_ptr() and _overlap(new_state, state):
             raise ValueError("new_state must be state itself or not overlap it")
-    return B, H, HV
+    return B, T, H, HV
 
 
 def _overlap(x: torch.Tensor, y: torch.Tensor) -> bool:
@@ -133,24 +153,31 @@ def _overlap(x: torch.Tensor, y: torch.Tensor) -> bool:
 
 
 def _launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
-            B, H, HV, use_qk_l2norm, shape=None):
+            B, T, H, HV, use_qk_l2norm, shape=None):
     lib = _lib.get_lib()
     stream = torch.cuda.current_stream(q.device).cuda_stream
     ptrs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), state.data_ptr(),
             A_log.data_ptr(), a.data_ptr(), dt_bias.data_ptr(), b.data_ptr())
+    l2 = int(bool(use_qk_l2norm))
+    bf16 = int(state.dtype == torch.bfloat16)
     with torch.cuda.device(q.device):
-        if shape is None:
-            code = lib.gdn_decode_step(
-                *ptrs, scale, output.data_ptr(), new_state.data_ptr(),
-                B, H, HV, K_DIM, V_DIM, int(bool(use_qk_l2norm)), stream)
-            _lib.check(code, "gdn_decode_step")
-        else:
+        if shape is not None:
             ns, waves, policy, start_event, stop_event = shape
             code = lib.gdn_decode_step_shaped(
                 *ptrs, scale, output.data_ptr(), new_state.data_ptr(),
-                B, H, HV, K_DIM, V_DIM, int(bool(use_qk_l2norm)),
+                B, T, H, HV, K_DIM, V_DIM, bf16, l2,
                 int(ns), int(waves), int(policy), start_event, stop_event, stream)
             _lib.check(code, "gdn_decode_step_shaped")
+        elif T == 1 and not bf16:
+            code = lib.gdn_decode_step(
+                *ptrs, scale, output.data_ptr(), new_state.data_ptr(),
+                B, H, HV, K_DIM, V_DIM, l2, stream)
+            _lib.check(code, "gdn_decode_step")
+        else:
+            code = lib.gdn_decode_steps(
+                *ptrs, scale, output.data_ptr(), new_state.data_ptr(),
+                B, T, H, HV, K_DIM, V_DIM, bf16, l2, stream)
+            _lib.check(code, "gdn_decode_steps")
 
 
 @torch.no_grad()
@@ -159,13 +186,13 @@ def kernel_hip(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
     """Destination-passing decode step (reference DPS form,
     solution/triton/kernel.py:150-197; solution/cuda/binding.py:44-60).
 
-    Writes ``output`` [B, 1, HV, 128] bf16 and ``new_state``
-    [B, HV, 128, 128] fp32.  ``new_state is state`` updates in place;
-    ``state=None`` starts from zeros (solution/triton/kernel.py:83-86).
+    Writes ``output`` [B, T, HV, 128] bf16 and ``new_state``
+    [B, HV, 128, 128] (the state's dtype).  ``new_state is state`` updates in
+    place; ``state=None`` starts from zeros (solution/triton/kernel.py:83-86).
     """
     if output is None or new_state is None:
         raise ValueError("kernel_hip needs preallocated output and new_state")
-    B, H, HV = check_inputs(q, k, v, state, A_log, a, dt_bias, b, output, new_state)
+    B, T, H, HV = check_inputs(q, k, v, state, A_log, a, dt_bias, b, output, new_state)
     scale = resolve_scale(scale, q.shape[-1])
     if state is None:
         new_state.zero_()
@@ -173,7 +200,7 @@ def kernel_hip(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
     if B == 0:
         return None
     _launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
-            B, H, HV, use_qk_l2norm)
+            B, T, H, HV, use_qk_l2norm)
     return None
 
 
@@ -186,7 +213,7 @@ def kernel_hip_shaped(q, k, v, state, A_log, a, dt_bias, b, scale, output,
     and timing.  ``start_event`` / ``stop_event`` are raw ``hipEvent_t``
     handles (ints) that the launch stamps with the kernel's own start and end
     timestamps."""
-    B, H, HV = check_inputs(q, k, v, state, A_log, a, dt_bias, b, output, new_state)
+    B, T, H, HV = check_inputs(q, k, v, state, A_log, a, dt_bias, b, output, new_state)
     scale = resolve_scale(scale, q.shape[-1])
     if state is None:
         new_state.zero_()
@@ -194,7 +221,7 @@ def kernel_hip_shaped(q, k, v, state, A_log, a, dt_bias, b, scale, output,
     if B == 0:
         return None
     _launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
-            B, H, HV, use_qk_l2norm,
+            B, T, H, HV, use_qk_l2norm,
             shape=(rows_per_lane_group, waves_per_block, cache_policy,
                    start_event, stop_event))
     return None
@@ -205,12 +232,14 @@ def run(q, k, v, state, A_log, a, dt_bias, b, scale, *, use_qk_l2norm: bool = Fa
     """Value-returning decode step with the reference's contract
     (``kernel_pt_reference``, solution/triton/kernel.py:22-118).
 
-    Returns ``(output [B, 1, HV, 128] bf16, new_state [B, HV, 128, 128] fp32)``;
-    ``state`` is not modified.
+    Returns ``(output [B, T, HV, 128] bf16, new_state [B, HV, 128, 128])``,
+    the new state in the state's dtype (fp32 for ``state=None``); ``state``
+    is not modified.
     """
-    B, H, HV = check_inputs(q, k, v, state, A_log, a, dt_bias, b)
-    output = torch.empty((B, 1, HV, V_DIM), dtype=torch.bfloat16, device=q.device)
-    new_state = torch.empty((B, HV, V_DIM, K_DIM), dtype=torch.float32, device=q.device)
+    B, T, H, HV = check_inputs(q, k, v, state, A_log, a, dt_bias, b)
+    sdtype = torch.float32 if state is None else state.dtype
+    output = torch.empty((B, T, HV, V_DIM), dtype=torch.bfloat16, device=q.device)
+    new_state = torch.empty((B, HV, V_DIM, K_DIM), dtype=sdtype, device=q.device)
     kernel_hip(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
                use_qk_l2norm=use_qk_l2norm)
     return output, new_state

@@ -1,31 +1,36 @@
 /*
  * gdn_decode.h - C ABI of the MI355X (gfx950) Gated Delta Net decode step.
  *
- * One single-token (T=1) decode step of the gated delta rule over a batch of
- * recurrent states, in the reference's tensor layouts:
+ * Decode steps of the gated delta rule over a batch of recurrent states, in
+ * the reference's tensor layouts (T = 1 token per sequence for the
+ * reference's decode; T > 1 for multi-token decode):
  *
- *   q, k       [B, 1, H,  K]   bf16   (K = 128)
- *   v          [B, 1, HV, V]   bf16   (V = 128, HV % H == 0, GVA ratio HV/H)
+ *   q, k       [B, T, H,  K]   bf16   (K = 128)
+ *   v          [B, T, HV, V]   bf16   (V = 128, HV % H == 0, GVA ratio HV/H)
  *   state      [B, HV, V, K]   fp32   "k-last": element (k, v) at v*K + k
+ *                                     (bf16 with gdn_decode_steps' state_bf16)
  *   A_log      [HV]            fp32
- *   a, b       [B, 1, HV]      bf16   ([B, HV] is the same memory)
+ *   a, b       [B, T, HV]      bf16   ([B, HV] is the same memory at T = 1)
  *   dt_bias    [HV]            fp32
- *   output     [B, 1, HV, V]   bf16
- *   new_state  [B, HV, V, K]   fp32   may be the same buffer as state
+ *   output     [B, T, HV, V]   bf16
+ *   new_state  [B, HV, V, K]   as state; may be the same buffer as state
  *
- * Per (batch b, v-head hv), with h = hv / (HV / H):
- *   g     = exp(-exp(A_log[hv]) * softplus(a[b,hv] + dt_bias[hv]))
- *   beta  = sigmoid(b[b,hv])
- *   q, k  = l2norm(q[b,h]), l2norm(k[b,h])     only when use_qk_l2norm != 0
- *   S     = g * state[b,hv]
- *   S    += k (x) beta * (v[b,hv] - S k)       rank-1 delta-rule update
- *   output[b,hv] = bf16(scale * S q);  new_state[b,hv] = S
+ * Per (batch b, v-head hv), with h = hv / (HV / H), for t = 0 .. T-1:
+ *   g     = exp(-exp(A_log[hv]) * softplus(a[b,t,hv] + dt_bias[hv]))
+ *   beta  = sigmoid(b[b,t,hv])
+ *   q, k  = l2norm(q[b,t,h]), l2norm(k[b,t,h])  only when use_qk_l2norm != 0
+ *   S     = g * S                                (S = state[b,hv] at t = 0)
+ *   S    += k (x) beta * (v[b,t,hv] - S k)       rank-1 delta-rule update
+ *   output[b,t,hv] = bf16(scale * S q)
+ * and new_state[b,hv] = S after the last token.  Arithmetic is fp32; a bf16
+ * state is widened on load and rounded to nearest even on store.
  *
  * All pointers are device pointers, dense and row-major in the shapes above.
  * Every entry point is asynchronous on `hip_stream` (a hipStream_t, NULL for
  * the null stream), allocates nothing, and returns 0 on success or a nonzero
  * hipError_t code.  Arguments are validated on the host before any launch
- * (hipErrorInvalidValue = 1 for bad sizes, null or misaligned pointers).
+ * (hipErrorInvalidValue = 1 for bad sizes, null or misaligned pointers;
+ * state, new_state, q, k, v and output must be 16-byte aligned).
  */
 #ifndef GDN_DECODE_H
 #define GDN_DECODE_H
@@ -58,14 +63,32 @@ int gdn_decode_step(const void* q, const void* k, const void* v,
                     int use_qk_l2norm, void* hip_stream);
 
 /*
- * The same step with an explicit launch shape: each wavefront owns
+ * T >= 1 tokens per sequence, with an fp32 (state_bf16 = 0) or bf16
+ * (state_bf16 = 1) state; otherwise as gdn_decode_step, which is this call
+ * with T = 1 and an fp32 state.  The state is read once and written once
+ * whatever T is.
+ * Counterpart of FlashInfer's gated_delta_rule_decode_pretranspose, which
+ * the reference calls for its fi-baseline entry
+ * (solution/triton/kernel.py:135-147) and whose T = 1..4 and bf16-state
+ * support the reference records (findings/fi-gdn-decode-kernel.md:11-16).
+ */
+int gdn_decode_steps(const void* q, const void* k, const void* v,
+                     const void* state, const float* A_log, const void* a,
+                     const float* dt_bias, const void* b, float scale,
+                     void* output, void* new_state,
+                     int B, int T, int H, int HV, int K, int V,
+                     int state_bf16, int use_qk_l2norm, void* hip_stream);
+
+/*
+ * gdn_decode_steps with an explicit launch shape: each wavefront owns
  * 4 * rows_per_lane_group consecutive-row groups of state rows (16 lanes per
  * row), each workgroup holds `waves_per_block` wavefronts, and a (b, hv) head
  * is split over 128 / (4 * rows_per_lane_group * waves_per_block) workgroups.
  * rows_per_lane_group and waves_per_block are each one of 1, 2, 4, 8 and
  * their product is at most 32.  cache_policy selects how the state stream
  * is accessed: 0 ordinary loads and stores, 1 nontemporal loads and stores,
- * 2 nontemporal stores only, 3 nontemporal loads only.  start_event / stop_event (hipEvent_t, may be
+ * 2 nontemporal stores only, 3 nontemporal loads only.  With T > 1 or a
+ * bf16 state, rows_per_lane_group is at most 4 and cache_policy 0 or 1.  start_event / stop_event (hipEvent_t, may be
  * NULL) are stamped with the kernel's own start and end timestamps
  * (hipExtLaunchKernelGGL), so hipEventElapsedTime gives the kernel duration
  * without event-marker overhead.  Used for launch-shape sweeps and timing.
@@ -74,11 +97,12 @@ int gdn_decode_step(const void* q, const void* k, const void* v,
  * (V/8, B*HV), solution/cuda/kernel.cu:229-235,418-424).
  */
 int gdn_decode_step_shaped(const void* q, const void* k, const void* v,
-                           const float* state, const float* A_log,
+                           const void* state, const float* A_log,
                            const void* a, const float* dt_bias, const void* b,
-                           float scale, void* output, float* new_state,
-                           int B, int H, int HV, int K, int V,
-                           int use_qk_l2norm, int rows_per_lane_group,
+                           float scale, void* output, void* new_state,
+                           int B, int T, int H, int HV, int K, int V,
+                           int state_bf16, int use_qk_l2norm,
+                           int rows_per_lane_group,
                            int waves_per_block, int cache_policy,
                            void* start_event, void* stop_event,
                            void* hip_stream);
@@ -102,7 +126,7 @@ int gdn_decode_launch_shape(int B, int HV, int* rows_per_lane_group,
  */
 const char* gdn_decode_error_string(int code);
 
-/* ABI version of this header: 1. */
+/* ABI version of this header: 2. */
 int gdn_decode_abi_version(void);
 
 #ifdef __cplusplus

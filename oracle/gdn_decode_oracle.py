@@ -27,6 +27,13 @@ flash-linear-attention ``l2norm`` uses, a dependency the reference names
 through ``use_qk_l2norm_in_kernel`` at solution/triton/fla_prefill_code.py:1797
 but does not vendor).
 
+``oracle_tokens`` extends any of the three to T > 1 tokens per sequence: the
+per-token loop of the reference's prefill oracle
+(solution/triton/prefill_kernel.py:144-178, one decode step per token
+against the running fp32 state, output per token) for fixed-length
+sequences, optionally storing the final state in bf16 (round to nearest
+even, as torch's ``.to(torch.bfloat16)``).
+
 Pinning status (see tests/test_oracle.py for each check): gates, GVA mapping,
 k-last layout, delta rule, output, state=None and the L2-norm are each pinned
 by closed forms, invariants or brute force; the reference itself holds no
@@ -204,21 +211,50 @@ def brute_fp64(q, k, v, state, A_log, a, dt_bias, b, scale, *,
     return out, S_out
 
 
+def oracle_tokens(step, q, k, v, state, A_log, a, dt_bias, b, scale, *,
+                  state_dtype=torch.float32, **kw):
+    """T tokens per sequence through the single-token oracle ``step``
+    (``oracle_loop``, ``oracle_vec`` or ``brute_fp64``), as the reference's
+    prefill oracle does for each sequence (prefill_kernel.py:144-178): token
+    t's step starts from the state token t-1 left, with no rounding in
+    between.  q, k ``[B, T, H, K]``, v ``[B, T, HV, V]``, a, b
+    ``[B, T, HV]``.  Returns ``(output [B, T, HV, V], new_state)`` with the
+    output as ``step`` gives it and the state cast to ``state_dtype`` (a
+    torch dtype; ``brute_fp64`` states stay float64 NumPy when it is None).
+    """
+    T = q.shape[1]
+    S = None if state is None else state.float()
+    outs = []
+    for t in range(T):
+        sl = slice(t, t + 1)
+        o, S = step(q[:, sl], k[:, sl], v[:, sl], S, A_log, a[:, sl], dt_bias, b[:, sl],
+                    scale, **kw)
+        if isinstance(S, np.ndarray):
+            S = torch.from_numpy(S)
+            o = torch.from_numpy(o)
+        outs.append(o)
+    out = torch.cat(outs, dim=1)
+    if state_dtype is not None:
+        S = S.to(state_dtype)
+    return out, S
+
+
 def make_inputs(B, H, HV, *, seed, state_std=0.05, device="cpu", K=128, V=128,
-                gate_shape="b1hv"):
+                gate_shape="b1hv", T=1):
     """Seeded decode inputs with the benchmark's distributions.
 
-    q, k, v ~ N(0, 1) bf16; state ~ N(0, state_std^2) fp32; a, b ~ N(0, 1)
-    bf16; A_log = log(U[1, 16]) fp32; dt_bias ~ U[-1, 1] fp32.  Generated on
+    q, k, v ~ N(0, 1) bf16 (T tokens); state ~ N(0, state_std^2) fp32; a, b
+    ~ N(0, 1) bf16; A_log = log(U[1, 16]) fp32; dt_bias ~ U[-1, 1] fp32.
+    ``gate_shape="bhv"`` (T = 1 only) gives a, b as ``[B, HV]``.  Generated on
     the CPU from ``torch.Generator().manual_seed(seed)`` and then moved to
     ``device``, so every device sees identical bits.
     """
     gen = torch.Generator().manual_seed(seed)
-    q = torch.randn(B, 1, H, K, generator=gen).to(torch.bfloat16)
-    k = torch.randn(B, 1, H, K, generator=gen).to(torch.bfloat16)
-    v = torch.randn(B, 1, HV, V, generator=gen).to(torch.bfloat16)
+    q = torch.randn(B, T, H, K, generator=gen).to(torch.bfloat16)
+    k = torch.randn(B, T, H, K, generator=gen).to(torch.bfloat16)
+    v = torch.randn(B, T, HV, V, generator=gen).to(torch.bfloat16)
     state = torch.randn(B, HV, V, K, generator=gen) * state_std
-    gshape = (B, 1, HV) if gate_shape == "b1hv" else (B, HV)
+    gshape = (B, T, HV) if gate_shape == "b1hv" else (B, HV)
     a = torch.randn(*gshape, generator=gen).to(torch.bfloat16)
     b = torch.randn(*gshape, generator=gen).to(torch.bfloat16)
     A_log = torch.log(torch.rand(HV, generator=gen) * 15.0 + 1.0)

@@ -32,7 +32,7 @@ def header_functions() -> dict:
 
 def test_header_declares_the_abi():
     funcs = header_functions()
-    assert set(funcs) == {"gdn_decode_step", "gdn_decode_step_shaped",
+    assert set(funcs) == {"gdn_decode_step", "gdn_decode_steps", "gdn_decode_step_shaped",
                           "gdn_decode_launch_shape", "gdn_decode_error_string",
                           "gdn_decode_abi_version"}
 
@@ -81,12 +81,22 @@ def test_validation_rejects_bad_sizes_without_launching():
     assert _step(lib, B=0) == 0          # empty batch: nothing to do
     shaped = lib.gdn_decode_step_shaped
     nulls = [None] * 8
-    assert shaped(*nulls, ctypes.c_float(0.1), None, None, 1, 16, 32, 128, 128, 1,
-                  8, 8, 0, None, None, None) == 1    # 8 x 8 > 32 rows per block
-    assert shaped(*nulls, ctypes.c_float(0.1), None, None, 1, 16, 32, 128, 128, 1,
-                  3, 1, 0, None, None, None) == 1    # not a power of two
-    assert shaped(*nulls, ctypes.c_float(0.1), None, None, 1, 16, 32, 128, 128, 1,
-                  1, 1, 4, None, None, None) == 1    # unknown cache policy
+    f = ctypes.c_float(0.1)
+
+    def sh(T, bf16, ns, w, pol):
+        return shaped(*nulls, f, None, None, 1, T, 16, 32, 128, 128, bf16, 1, ns, w, pol,
+                      None, None, None)
+
+    assert sh(1, 0, 8, 8, 0) == 1     # 8 x 8 > 32 rows per block
+    assert sh(1, 0, 3, 1, 0) == 1     # not a power of two
+    assert sh(1, 0, 1, 1, 4) == 1     # unknown cache policy
+    assert sh(2, 0, 8, 1, 0) == 1     # multi-token kernels take at most 4 rows per group
+    assert sh(1, 1, 2, 4, 2) == 1     # bf16-state kernels take cache policy 0 or 1
+    assert sh(0, 0, 2, 4, 1) == 1     # T < 1
+    assert sh(1, 2, 2, 4, 1) == 1     # state_bf16 is 0 or 1
+    steps = lib.gdn_decode_steps
+    assert steps(*nulls, f, None, None, 1, 0, 16, 32, 128, 128, 0, 1, None) == 1
+    assert steps(*nulls, f, None, None, 0, 4, 16, 32, 128, 128, 1, 1, None) == 0
 
 
 def test_validation_rejects_misaligned_and_overlapping_state():

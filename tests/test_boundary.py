@@ -69,14 +69,17 @@ def _bad(name, value):
 
 
 BAD_CASES = {
-    "T=2": ({**_inputs(), "q": torch.zeros(2, 2, 2, 128, dtype=torch.bfloat16)}, ValueError),
+    "T=0": ({**_inputs(), "q": torch.zeros(2, 0, 2, 128, dtype=torch.bfloat16)}, ValueError),
+    "T=2 q only": ({**_inputs(), "q": torch.zeros(2, 2, 2, 128, dtype=torch.bfloat16)}, ValueError),
     "K=64": ({**_inputs(), "q": torch.zeros(2, 1, 2, 64, dtype=torch.bfloat16)}, ValueError),
     "HV%H": ({**_inputs(), "q": torch.zeros(2, 1, 3, 128, dtype=torch.bfloat16)}, ValueError),
     "q fp32": (_bad("q", torch.zeros(2, 1, 2, 128)), TypeError),
     "k shape": (_bad("k", torch.zeros(2, 1, 1, 128, dtype=torch.bfloat16)), ValueError),
     "v noncontig": (_bad("v", torch.zeros(2, 1, 128, 4, dtype=torch.bfloat16).transpose(2, 3)),
                     ValueError),
-    "state bf16": (_bad("state", torch.zeros(2, 4, 128, 128, dtype=torch.bfloat16)), TypeError),
+    "state fp16": (_bad("state", torch.zeros(2, 4, 128, 128, dtype=torch.float16)), TypeError),
+    "new_state dtype": (_bad("new_state", torch.empty(2, 4, 128, 128, dtype=torch.bfloat16)),
+                        TypeError),
     "state shape": (_bad("state", torch.zeros(2, 4, 128, 64)), ValueError),
     "A_log shape": (_bad("A_log", torch.zeros(2)), ValueError),
     "dt_bias f64": (_bad("dt_bias", torch.zeros(4, dtype=torch.float64)), TypeError),
@@ -95,7 +98,7 @@ def test_malformed_arguments_raise_before_the_abi(case, no_lib):
     with pytest.raises(exc):
         gdn.kernel_hip(**t)
     t = {n: x for n, x in t.items() if n not in ("output", "new_state")}
-    if case not in ("output dtype", "new_state shape"):
+    if case not in ("output dtype", "new_state shape", "new_state dtype"):
         with pytest.raises(exc):
             gdn.run(**t)
 
@@ -128,6 +131,24 @@ def test_gate_tensors_accept_both_reference_shapes(no_lib):
     t["b"] = t["b"].reshape(2, 4)
     with pytest.raises(ValueError, match="HIP device"):   # shapes accepted, device refused
         gdn.kernel_hip(**t)
+
+
+def test_multi_token_and_bf16_state_shapes_are_accepted(no_lib):
+    t = make_inputs(2, 2, 4, seed=5, T=3)
+    t["output"] = torch.empty(2, 3, 4, 128, dtype=torch.bfloat16)
+    t["new_state"] = torch.empty(2, 4, 128, 128)
+    with pytest.raises(ValueError, match="HIP device"):   # shapes accepted, device refused
+        gdn.kernel_hip(**t)
+    t["state"] = t["state"].to(torch.bfloat16)
+    t["new_state"] = torch.empty(2, 4, 128, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="HIP device"):
+        gdn.kernel_hip(**t)
+    bad = {**t, "a": t["a"][:, :1]}                        # gates for one token only
+    with pytest.raises(ValueError):
+        gdn.kernel_hip(**bad)
+    bad = {**t, "output": torch.empty(2, 1, 4, 128, dtype=torch.bfloat16)}
+    with pytest.raises(ValueError):
+        gdn.kernel_hip(**bad)
 
 
 def test_nonzero_abi_code_raises(monkeypatch):

@@ -21,7 +21,8 @@ import pytest
 import torch
 
 from oracle.gdn_decode_oracle import (
-    brute_fp64, gates, l2norm, make_inputs, oracle_loop, oracle_vec, resolve_scale)
+    brute_fp64, gates, l2norm, make_inputs, oracle_loop, oracle_tokens, oracle_vec,
+    resolve_scale)
 from tests.gdn_cases import (
     OUT_TIGHT_ATOL, OUT_TIGHT_RTOL, assert_state_close, load_golden)
 
@@ -344,3 +345,96 @@ def test_golden_vectors(name):
     ob, _ = oracle_loop(**t, use_qk_l2norm=l2)
     d = (ob.double() - torch.from_numpy(exp_out)).abs()
     assert bool((d <= OUT_TIGHT_ATOL + OUT_TIGHT_RTOL * torch.from_numpy(exp_out).abs()).all())
+
+
+# --------------------------------------------------------------------------
+# Multi-token steps and the bf16 state.
+# --------------------------------------------------------------------------
+
+def _no_carry_tokens(step, q, k, v, state, A_log, a, dt_bias, b, scale, **kw):
+    """Planted mistake: every token starts from the input state."""
+    outs, S = [], None
+    for t in range(q.shape[1]):
+        sl = slice(t, t + 1)
+        o, S = step(q[:, sl], k[:, sl], v[:, sl], state, A_log, a[:, sl], dt_bias,
+                    b[:, sl], scale, **kw)
+        outs.append(o)
+    return torch.cat(outs, dim=1), S
+
+
+def check_tokens_orthogonal_writes(multi):
+    """Two tokens with beta = 1, g = 1 and one-hot keys e1, e2 (q = k): each
+    token stores its v under its key without disturbing the other, so the
+    outputs are scale*v1, scale*v2, the final state reads v1 at e1 and v2 at
+    e2, and every other column is the input state's."""
+    K = V = 8
+    t = make_inputs(1, 1, 1, seed=31, K=K, V=V, T=2)
+    k = torch.zeros(1, 2, 1, K, dtype=torch.bfloat16)
+    k[0, 0, 0, 1] = 1.0
+    k[0, 1, 0, 2] = 1.0
+    t.update(k=k, q=k.clone(), A_log=torch.tensor([NEG_INF]), scale=0.5,
+             b=torch.full((1, 2, 1), POS_INF, dtype=torch.bfloat16))
+    out, S = multi(**t)
+    v = t["v"][0, :, 0].double()                       # [2, V]
+    S = _f64(S)[0, 0]                                  # [V, K] storage
+    assert torch.allclose(_f64(out)[0, :, 0], 0.5 * v, atol=1e-6), "tokens: outputs"
+    assert torch.allclose(S[:, 1], v[0], atol=1e-6), "tokens: first write lost"
+    assert torch.allclose(S[:, 2], v[1], atol=1e-6), "tokens: second write"
+    keep = [0] + list(range(3, K))
+    assert torch.allclose(S[:, keep], t["state"].double()[0, 0][:, keep], atol=1e-7)
+
+
+def _fp32_out(step):
+    return lambda *args, **kw: step(*args, **kw, output_fp32=True)
+
+
+def test_multi_token_known_answer_and_planted_mistake():
+    for step in (_fp32_out(oracle_loop), _fp32_out(oracle_vec), brute_fp64):
+        check_tokens_orthogonal_writes(
+            lambda **t: oracle_tokens(step, **t, state_dtype=None))
+    with pytest.raises(AssertionError):
+        check_tokens_orthogonal_writes(
+            lambda **t: _no_carry_tokens(_fp32_out(oracle_vec), **t))
+
+
+def test_multi_token_scalar_brute_force():
+    """T = 3 at K = 3, V = 2 with plain Python floats, carrying the state."""
+    K, V, T = 3, 2, 3
+    t = make_inputs(1, 1, 1, seed=32, K=K, V=V, T=T)
+    out, st = oracle_tokens(oracle_loop, **t, output_fp32=True)
+    S = [[float(t["state"][0, 0, r, i]) for i in range(K)] for r in range(V)]
+    for tok in range(T):
+        x = float(t["a"][0, tok, 0]) + float(t["dt_bias"][0])
+        g = math.exp(-math.exp(float(t["A_log"][0])) * math.log1p(math.exp(x)))
+        beta = 1.0 / (1.0 + math.exp(-float(t["b"][0, tok, 0])))
+        kv = [float(t["k"][0, tok, 0, i]) for i in range(K)]
+        qv = [float(t["q"][0, tok, 0, i]) for i in range(K)]
+        for r in range(V):
+            S[r] = [g * S[r][i] for i in range(K)]
+            d = beta * (float(t["v"][0, tok, 0, r]) - sum(S[r][i] * kv[i] for i in range(K)))
+            S[r] = [S[r][i] + d * kv[i] for i in range(K)]
+            o = t["scale"] * sum(S[r][i] * qv[i] for i in range(K))
+            assert math.isclose(float(out[0, tok, 0, r]), o, rel_tol=1e-5, abs_tol=1e-6)
+    for r in range(V):
+        for i in range(K):
+            assert math.isclose(float(st[0, 0, r, i]), S[r][i], rel_tol=1e-5, abs_tol=1e-6)
+
+
+@pytest.mark.parametrize("l2", [False, True])
+def test_multi_token_restatements_agree(l2):
+    t = make_inputs(2, 2, 4, seed=33, T=4)
+    o64, s64 = oracle_tokens(brute_fp64, **t, use_qk_l2norm=l2, state_dtype=None)
+    for step in (oracle_loop, oracle_vec):
+        o, s = oracle_tokens(step, **t, use_qk_l2norm=l2, output_fp32=True)
+        assert (o.double() - o64).abs().max().item() < 2e-6
+        assert (s.double() - s64).abs().max().item() < 4e-6
+
+
+def test_bf16_state_is_rne_of_the_fp32_result():
+    t = make_inputs(2, 2, 4, seed=34, T=2)
+    t["state"] = t["state"].to(torch.bfloat16)         # a bf16 state as input
+    o32, s32 = oracle_tokens(oracle_loop, **t, use_qk_l2norm=True)
+    o16, s16 = oracle_tokens(oracle_loop, **t, use_qk_l2norm=True,
+                             state_dtype=torch.bfloat16)
+    assert s16.dtype == torch.bfloat16 and torch.equal(o16, o32)
+    assert torch.equal(s16, s32.to(torch.bfloat16))
