@@ -21,16 +21,21 @@ step's dirty lines: the steady state of serving.  Prints ONE JSON line:
 * ``b1``: kernel time per step at B=1 (qk16_v32, L2-norm), stamped by the
   kernel dispatch itself (the analogue of the reference's CUPTI timings);
 * ``per_config``: kernel times for every benchmark shape and for the
-  reference's qk4_v8 definition at its workload batch sizes, in three
-  regimes: steady (as above), warm (one state, repeatedly: cache-resident
-  below 256 MiB) and cold (a 1 GiB read evicts the caches just before the
-  launch; the launch's own writes may still be in cache when it ends);
+  reference's qk4_v8 definition at its workload batch sizes, plus bf16-state
+  and multi-token (T = 2, 4) steps, in three regimes: steady (as above),
+  warm (one state, repeatedly: cache-resident below 256 MiB) and cold (a
+  1 GiB read evicts the caches just before the launch; the launch's own
+  writes may still be in cache when it ends);
+* ``b1.floor_same_timer``: the same timer on reference kernels that move
+  only the state bytes (an in-place read-modify-write of the B=1 and B=256
+  states) and on an empty kernel, so that the decode times read against the
+  floor of their own traffic;
 * ``cpu_baseline``: the reference's PyTorch-eager step (the oracle's
   loop-for-loop restatement) timed on this host's cores on a bounded sample.
 
-Algorithmic bytes per step: state read + write (B*HV*128*128*4*2), q and k
-(2*B*H*128*2), v (B*HV*128*2), output (B*HV*128*2), a and b (2*B*HV*2),
-A_log and dt_bias (2*HV*4).
+Algorithmic bytes per step: state read + write (B*HV*128*128*4*2, half that
+for a bf16 state), and per token q and k (2*B*H*128*2), v (B*HV*128*2),
+output (B*HV*128*2), a and b (2*B*HV*2); A_log and dt_bias (2*HV*4).
 """
 
 from __future__ import annotations
@@ -68,27 +73,31 @@ CONFIGS = {
 REF_BATCHES = (1, 4, 8, 16, 32, 48, 64)
 
 
-def step_bytes(B: int, H: int, HV: int, K: int = 128, V: int = 128) -> int:
-    return (B * HV * K * V * 4 * 2 + 2 * B * H * K * 2 + B * HV * V * 2
-            + B * HV * V * 2 + 2 * B * HV * 2 + 2 * HV * 4)
+def step_bytes(B: int, H: int, HV: int, K: int = 128, V: int = 128, T: int = 1,
+               state_elem: int = 4) -> int:
+    """Algorithmic bytes of one launch: the state read and written once,
+    q, k, v, output, a and b for each of T tokens, A_log and dt_bias."""
+    return (B * HV * K * V * state_elem * 2 + T * (2 * B * H * K * 2 + B * HV * V * 2
+            + B * HV * V * 2 + 2 * B * HV * 2) + 2 * HV * 4)
 
 
-def make_device_inputs(B, H, HV, device, seed):
+def make_device_inputs(B, H, HV, device, seed, T=1, state_dtype=torch.float32):
     """Seeded synthetic inputs generated on the device: q, k, v ~ N(0,1)
-    bf16; state ~ N(0, 0.05^2) fp32; a, b ~ N(0,1) bf16 [B,1,HV];
-    A_log = log(U[1,16]); dt_bias ~ U[-1,1]; scale = 1/sqrt(128)."""
+    bf16; state ~ N(0, 0.05^2) (fp32, or rounded to bf16); a, b ~ N(0,1)
+    bf16 [B,T,HV]; A_log = log(U[1,16]); dt_bias ~ U[-1,1];
+    scale = 1/sqrt(128)."""
     g = torch.Generator(device=device).manual_seed(seed)
     K = V = 128
     f = dict(device=device)
-    q = torch.randn(B, 1, H, K, generator=g, **f).to(torch.bfloat16)
-    k = torch.randn(B, 1, H, K, generator=g, **f).to(torch.bfloat16)
-    v = torch.randn(B, 1, HV, V, generator=g, **f).to(torch.bfloat16)
-    state = torch.randn(B, HV, V, K, generator=g, **f).mul_(0.05)
-    a = torch.randn(B, 1, HV, generator=g, **f).to(torch.bfloat16)
-    b = torch.randn(B, 1, HV, generator=g, **f).to(torch.bfloat16)
+    q = torch.randn(B, T, H, K, generator=g, **f).to(torch.bfloat16)
+    k = torch.randn(B, T, H, K, generator=g, **f).to(torch.bfloat16)
+    v = torch.randn(B, T, HV, V, generator=g, **f).to(torch.bfloat16)
+    state = torch.randn(B, HV, V, K, generator=g, **f).mul_(0.05).to(state_dtype)
+    a = torch.randn(B, T, HV, generator=g, **f).to(torch.bfloat16)
+    b = torch.randn(B, T, HV, generator=g, **f).to(torch.bfloat16)
     A_log = torch.log(torch.rand(HV, generator=g, **f) * 15.0 + 1.0)
     dt_bias = torch.rand(HV, generator=g, **f) * 2.0 - 1.0
-    output = torch.empty(B, 1, HV, V, dtype=torch.bfloat16, **f)
+    output = torch.empty(B, T, HV, V, dtype=torch.bfloat16, **f)
     return dict(q=q, k=k, v=v, state=state, A_log=A_log, a=a, dt_bias=dt_bias, b=b,
                 scale=1.0 / math.sqrt(K), output=output, new_state=state)
 
@@ -140,8 +149,8 @@ def kernel_times_us(t, l2, iters, *, mode, flush=None):
     warm: back-to-back launches on one state;
     cold: each launch right after reading a 1 GiB buffer (more than the
     32 MiB of L2 plus the 256 MiB MALL; a read leaves no dirty lines)."""
-    B, HV = t["v"].shape[0], t["v"].shape[2]
-    ns, waves, policy, _ = _lib.launch_shape(B, HV)
+    B, T, HV = t["v"].shape[0], t["v"].shape[1], t["v"].shape[2]
+    ns, waves, policy, _ = _lib.launch_shape(B, HV, T, t["state"].dtype == torch.bfloat16)
     states = layer_states(t["state"]) if mode == "steady" else [t["state"]]
     iters = max(iters, 2 * len(states)) if mode == "steady" else iters
     stamps = KernelStamps(iters)
@@ -293,6 +302,69 @@ def reference_stream(device, iters: int = 20):
             "gbs": round(2 * buf.numel() * 4 / (us * 1e-6) / 1e9, 1)}
 
 
+class Calib:
+    """The reference kernels of ``libgdn_calib.so`` (same-bytes in-place
+    read-modify-write, empty kernel), launched with kernel stamps."""
+
+    def __init__(self):
+        from flashinfer_competition_codebase_amd.build import CALIB_PATH
+
+        if not CALIB_PATH.exists():
+            raise RuntimeError(f"{CALIB_PATH} not built; run "
+                               "`python -m flashinfer_competition_codebase_amd.build`")
+        self.lib = ctypes.CDLL(str(CALIB_PATH))
+        P, LL, F, I = ctypes.c_void_p, ctypes.c_longlong, ctypes.c_float, ctypes.c_int
+        self.lib.gdn_calib_rmw.argtypes = [P, LL, F, I, P, P, P]
+        self.lib.gdn_calib_rmw.restype = I
+        self.lib.gdn_calib_empty.argtypes = [LL, P, P, P]
+        self.lib.gdn_calib_empty.restype = I
+
+    def rmw(self, buf, start, stop):
+        code = self.lib.gdn_calib_rmw(buf.data_ptr(), buf.numel(), 0.999, 1, start, stop,
+                                      torch.cuda.current_stream().cuda_stream)
+        _lib.check(code, "gdn_calib_rmw")
+
+    def empty(self, blocks, start, stop):
+        code = self.lib.gdn_calib_empty(blocks, start, stop,
+                                        torch.cuda.current_stream().cuda_stream)
+        _lib.check(code, "gdn_calib_empty")
+
+
+def traffic_floor(device, iters: int):
+    """Kernel-stamped medians, steady regime, of the reference kernels that
+    move only a decode step's state bytes: an in-place nontemporal
+    read-modify-write of the B=1 qk16_v32 state (2 MiB, 256 workgroups of
+    128 threads, as the decode launch at B=1) and of the B=256 state
+    (512 MiB), and an empty kernel on 256 workgroups.  The decode kernel's
+    times under the same timer compare directly."""
+    cal = Calib()
+    out = {}
+    for name, nfloat in (("b1", 32 * 128 * 128), ("b256", 256 * 32 * 128 * 128)):
+        bufs = layer_states(torch.zeros(nfloat, device=device))
+        n = max(iters, 2 * len(bufs))
+        stamps = KernelStamps(n)
+        try:
+            for i in range(n):
+                cal.rmw(bufs[i % len(bufs)], stamps.start[i].value, stamps.stop[i].value)
+            torch.cuda.synchronize()
+            d = [stamps.elapsed_us(i) for i in range(len(bufs), n)]
+        finally:
+            stamps.close()
+        us = statistics.median(d)
+        out[f"{name}_rmw_us"] = round(us, 3)
+        out[f"{name}_rmw_gbs"] = round(2 * nfloat * 4 / (us * 1e-6) / 1e9, 1)
+        del bufs
+    stamps = KernelStamps(iters)
+    try:
+        for i in range(iters):
+            cal.empty(256, stamps.start[i].value, stamps.stop[i].value)
+        torch.cuda.synchronize()
+        out["empty_us"] = round(statistics.median(stamps.elapsed_us(i) for i in range(iters)), 3)
+    finally:
+        stamps.close()
+    return out
+
+
 def pmc_pass(device):
     """Short run for rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE): three
     plain 256 MiB copies (calibrate the counters against known bytes), then
@@ -368,20 +440,26 @@ def main():
     flush = torch.ones(1 << 28, device=device)     # 1 GiB > 32 MiB L2 + 256 MiB MALL
     per_config = {}
     if not args.no_per_config:
-        shapes = [(n, *c) for n, c in CONFIGS.items()]
-        shapes += [(f"qk4_v8_b{bb}", bb, 4, 8, False) for bb in REF_BATCHES]
-        for name, b_, h_, hv_, l2_ in shapes:
-            tc = make_device_inputs(b_, h_, hv_, device, seed=7)
+        f32, bf16 = torch.float32, torch.bfloat16
+        shapes = [(n, *c, 1, f32) for n, c in CONFIGS.items()]
+        shapes += [(f"qk4_v8_b{bb}", bb, 4, 8, False, 1, f32) for bb in REF_BATCHES]
+        shapes += [(f"{n}_bf16_state", *CONFIGS[n], 1, bf16)
+                   for n in ("b1_qk16_v32_l2", "b8_qk16_v32_l2", "b256_qk16_v32_l2")]
+        shapes += [(f"{n}_t{tt}", *CONFIGS[n], tt, f32)
+                   for n in ("b1_qk16_v32_l2", "b256_qk16_v32_l2") for tt in (2, 4)]
+        for name, b_, h_, hv_, l2_, t_, sd_ in shapes:
+            tc = make_device_inputs(b_, h_, hv_, device, seed=7, T=t_, state_dtype=sd_)
             for _ in range(5):
                 gdn.kernel_hip(**tc, use_qk_l2norm=l2_)
             med = {m: statistics.median(kernel_times_us(tc, l2_, args.iters, mode=m,
                                                         flush=flush))
                    for m in ("steady", "warm", "cold")}
-            nb = step_bytes(b_, h_, hv_)
+            nb = step_bytes(b_, h_, hv_, T=t_, state_elem=tc["state"].element_size())
             sm = med["steady"]
             per_config[name] = {
-                "B": b_, "H": h_, "HV": hv_, "l2norm": l2_, "bytes": nb,
-                "launch": list(_lib.launch_shape(b_, hv_)),
+                "B": b_, "H": h_, "HV": hv_, "T": t_, "l2norm": l2_,
+                "state": "bf16" if sd_ == bf16 else "fp32", "bytes": nb,
+                "launch": list(_lib.launch_shape(b_, hv_, t_, sd_ == bf16)),
                 "us_steady": round(sm, 3), "us_warm": round(med["warm"], 3),
                 "us_cold": round(med["cold"], 3),
                 "steady_hbm_gbs": round(nb / (sm * 1e-6) / 1e9, 1),
@@ -390,6 +468,11 @@ def main():
             log(f"[bench] {name}: steady {sm:.2f} us ({per_config[name]['steady_hbm_gbs']:.0f}"
                 f" GB/s), warm {med['warm']:.2f} us, cold {med['cold']:.2f} us")
             del tc
+
+    floor = traffic_floor(device, args.iters)
+    log(f"[bench] floor, same timer: B=1 state bytes in-place RMW {floor['b1_rmw_us']} us, "
+        f"empty kernel {floor['empty_us']} us; B=256 state RMW {floor['b256_rmw_us']} us "
+        f"({floor['b256_rmw_gbs']} GB/s)")
 
     serving = b1_serving(device)
     log(f"[bench] B=1 serving, {serving['layers']} layer steps: eager "
@@ -429,8 +512,8 @@ def main():
         "b1": ({"us_per_step_steady": b1["us_steady"], "us_per_step_warm": b1["us_warm"],
                 "us_per_step_cold": b1["us_cold"],
                 "timer": "kernel-stamped HIP events (hipExtLaunchKernelGGL)",
-                "serving": serving}
-               if b1 else {"serving": serving}),
+                "floor_same_timer": floor, "serving": serving}
+               if b1 else {"floor_same_timer": floor, "serving": serving}),
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 1),

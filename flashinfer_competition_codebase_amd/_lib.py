@@ -33,14 +33,14 @@ SIGNATURES = {
     ),
     "gdn_decode_launch_shape": (
         _I,
-        [_I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I),
+        [_I, _I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I),
          ctypes.POINTER(ctypes.c_longlong)],
     ),
     "gdn_decode_error_string": (ctypes.c_char_p, [_I]),
     "gdn_decode_abi_version": (_I, []),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lock = threading.Lock()
 _lib = None
@@ -89,14 +89,15 @@ def check(code: int, what: str) -> None:
         raise RuntimeError(f"{what} failed: {error_string(code)} (hipError_t {code})")
 
 
-def launch_shape(B: int, HV: int) -> tuple[int, int, int, int]:
+def launch_shape(B: int, HV: int, T: int = 1, state_bf16: bool = False
+                 ) -> tuple[int, int, int, int]:
     """(rows_per_lane_group, waves_per_block, cache_policy, num_blocks)
-    that gdn_decode_step uses for (B, HV)."""
+    that gdn_decode_steps uses for B sequences of T tokens over HV v-heads."""
     ns, w, pol, nb = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_longlong()
     check(
         get_lib().gdn_decode_launch_shape(
-            int(B), int(HV), ctypes.byref(ns), ctypes.byref(w), ctypes.byref(pol),
-            ctypes.byref(nb)
+            int(B), int(T), int(HV), int(bool(state_bf16)), ctypes.byref(ns),
+            ctypes.byref(w), ctypes.byref(pol), ctypes.byref(nb)
         ),
         "gdn_decode_launch_shape",
     )

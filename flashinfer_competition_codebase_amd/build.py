@@ -1,9 +1,14 @@
-"""Build the gfx950 decode library in-tree with hipcc.
+"""Build the gfx950 libraries in-tree with hipcc.
 
-``python -m flashinfer_competition_codebase_amd.build`` compiles
-``csrc/gdn_decode.hip`` into ``libgdn_decode.so`` next to this file.  The
-library is a plain C-ABI shared object (declared in ``include/gdn_decode.h``)
-that the Python host side loads with ctypes.
+``python -m flashinfer_competition_codebase_amd.build`` compiles, next to
+this file:
+
+* ``csrc/gdn_decode.hip`` into ``libgdn_decode.so``: the decode step, a
+  plain C-ABI shared object (declared in ``include/gdn_decode.h``) that the
+  Python host side loads with ctypes;
+* ``csrc/calib.hip`` into ``libgdn_calib.so``: reference kernels (same-bytes
+  read-modify-write, empty kernel) that only ``bench.py`` loads, to report
+  the floor of the decode step's traffic.
 """
 
 from __future__ import annotations
@@ -20,7 +25,12 @@ CSRC = PKG_DIR / "csrc" / "gdn_decode.hip"
 INCLUDE_DIR = REPO_ROOT / "include"
 LIB_NAME = "libgdn_decode.so"
 LIB_PATH = PKG_DIR / LIB_NAME
+CALIB_SRC = PKG_DIR / "csrc" / "calib.hip"
+CALIB_PATH = PKG_DIR / "libgdn_calib.so"
+# library -> source
+LIBRARIES = {LIB_PATH: CSRC, CALIB_PATH: CALIB_SRC}
 OFFLOAD_ARCH = "gfx950"
+KERNARG_PRELOAD_ARGS = int(os.environ.get("GDN_KERNARG_PRELOAD_ARGS", "8"))
 
 
 def hipcc_path() -> str:
@@ -34,7 +44,7 @@ def hipcc_path() -> str:
     return found
 
 
-def compile_command(out: Path = LIB_PATH) -> list[str]:
+def compile_command(out: Path = LIB_PATH, src: Path = CSRC) -> list[str]:
     return [
         hipcc_path(),
         f"--offload-arch={OFFLOAD_ARCH}",
@@ -44,24 +54,37 @@ def compile_command(out: Path = LIB_PATH) -> list[str]:
         "-shared",
         # Packed fp32 VALU ops stay disabled in device code.
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # The decode kernel's first 8 arguments (14 dwords: the pointers and
+        # sizes its first loads need) are preloaded into SGPRs at dispatch.
+        "-mllvm", f"-amdgpu-kernarg-preload-count={KERNARG_PRELOAD_ARGS}",
         "-Wall",
         f"-I{INCLUDE_DIR}",
-        str(CSRC),
+        str(src),
         "-o", str(out),
     ]
 
 
 def build(verbose: bool = False) -> Path:
-    """Compile the library (always, even when a built copy exists)."""
-    tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = compile_command(tmp)
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    if proc.returncode != 0:
-        sys.stderr.write(proc.stdout + proc.stderr)
-        raise RuntimeError(f"hipcc failed with exit code {proc.returncode}")
-    os.replace(tmp, LIB_PATH)
+    """Compile every library (always, even when built copies exist), in
+    parallel; returns the decode library's path."""
+    jobs = []
+    for lib, src in LIBRARIES.items():
+        tmp = lib.with_suffix(".so.tmp")
+        cmd = compile_command(tmp, src)
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        jobs.append((lib, tmp, subprocess.Popen(cmd, stdout=subprocess.PIPE,
+                                                stderr=subprocess.STDOUT, text=True)))
+    failed = []
+    for lib, tmp, proc in jobs:
+        out, _ = proc.communicate()
+        if proc.returncode != 0:
+            sys.stderr.write(out)
+            failed.append(f"{lib.name} (exit code {proc.returncode})")
+        else:
+            os.replace(tmp, lib)
+    if failed:
+        raise RuntimeError("hipcc failed: " + ", ".join(failed))
     return LIB_PATH
 
 

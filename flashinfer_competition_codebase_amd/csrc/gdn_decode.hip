@@ -49,6 +49,7 @@ constexpr int kDim = 128;          // K == V == 128
 constexpr int kLaneGroups = 4;     // 16-lane DPP rows per wave64
 constexpr float kL2Eps = 1e-6f;    // l2norm: x * rsqrt(sum(x^2) + eps)
 constexpr float kSoftplusThreshold = 20.0f;  // torch softplus default
+constexpr float kLn2 = 0.693147180559945309f;
 
 // Cache policy for the state stream.
 enum : int {
@@ -264,7 +265,10 @@ __device__ __forceinline__ void store_bf16_run(uint16_t* p, const float (&x)[NS]
 __device__ __forceinline__ void gates(float a, float dt_bias, float A_log,
                                       float b, float& g, float& beta) {
   const float x = a + dt_bias;
-  const float softplus = x > kSoftplusThreshold ? x : __logf(1.0f + __expf(x));
+  // ln(1 + e^x) = log2(1 + e^x) * ln 2; the argument is >= 1, so the raw
+  // v_log_f32 needs none of the library's denormal-input scaling.
+  const float softplus =
+      x > kSoftplusThreshold ? x : __builtin_amdgcn_logf(1.0f + __expf(x)) * kLn2;
   g = __expf(-__expf(A_log) * softplus);
   beta = __builtin_amdgcn_rcpf(1.0f + __expf(-b));
 }
@@ -306,10 +310,12 @@ __device__ __forceinline__ void token_update(float (&s)[NS][8], const TokenIn<NS
   unpack_bf16x8(in.k, kf);
   unpack_bf16_run<NS>(in.v, vrow);
 
-  // Per-head reductions: |q|^2, |k|^2 (L2-norm only) and k.q.
+  // Per-head reductions on the raw values: |q|^2, |k|^2 (L2-norm only) and
+  // k.q.  The normalised, scaled vectors q' = qscale*q and k_hat = kscale*k
+  // are never formed: their scales multiply the reduced dots instead.
   float qscale = scale;
   float kscale = 1.0f;
-  float kq;
+  float kq_raw;
   if constexpr (L2NORM) {
     float hs[3] = {0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -319,24 +325,22 @@ __device__ __forceinline__ void token_update(float (&s)[NS][8], const TokenIn<NS
       hs[2] = fmaf(qf[i], kf[i], hs[2]);
     }
     row16_sum<3>(hs);
-    const float iq = rsqrtf(hs[0] + kL2Eps);
-    kscale = rsqrtf(hs[1] + kL2Eps);
-    qscale *= iq;
-    kq = hs[2] * (qscale * kscale);
+    // |x|^2 + eps >= eps is a normal number: the raw v_rsq_f32 suffices.
+    qscale *= __builtin_amdgcn_rsqf(hs[0] + kL2Eps);
+    kscale = __builtin_amdgcn_rsqf(hs[1] + kL2Eps);
+    kq_raw = hs[2];
   } else {
     float hs[1] = {0.0f};
 #pragma unroll
     for (int i = 0; i < 8; ++i) hs[0] = fmaf(qf[i], kf[i], hs[0]);
     row16_sum<1>(hs);
-    kq = hs[0] * qscale;
+    kq_raw = hs[0];
   }
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    qf[i] *= qscale;  // q' = scale * q_hat
-    kf[i] *= kscale;  // k_hat
-  }
+  const float kq = kq_raw * (qscale * kscale);  // k_hat . q'
+  const float gk = g * kscale;
+  const float gq = g * qscale;
 
-  // Per-row reductions k_hat.S and q'.S on the undecayed state.
+  // Per-row reductions k.S and q.S on the undecayed state.
   float red[2 * NS];
 #pragma unroll
   for (int n = 0; n < NS; ++n) {
@@ -353,11 +357,12 @@ __device__ __forceinline__ void token_update(float (&s)[NS][8], const TokenIn<NS
 
 #pragma unroll
   for (int n = 0; n < NS; ++n) {
-    const float old_v = g * red[2 * n];             // k_hat . (g S)
+    const float old_v = gk * red[2 * n];            // k_hat . (g S)
     const float d = beta * (vrow[n] - old_v);       // beta * (v - old_v)
-    o[n] = fmaf(d, kq, g * red[2 * n + 1]);         // q' . S_new
+    o[n] = fmaf(d, kq, gq * red[2 * n + 1]);        // q' . S_new
+    const float dk = d * kscale;                    // S_new = g S + d (x) k_hat
 #pragma unroll
-    for (int i = 0; i < 8; ++i) s[n][i] = fmaf(d, kf[i], g * s[n][i]);
+    for (int i = 0; i < 8; ++i) s[n][i] = fmaf(dk, kf[i], g * s[n][i]);
   }
 }
 
@@ -369,8 +374,33 @@ __device__ __forceinline__ void token_update(float (&s)[NS][8], const TokenIn<NS
 
 // T tokens (T = 1 at compile time unless MULTI) of 4*NS*WAVES rows of one
 // (b, hv) head per workgroup.
+//
+// The arguments are scalars rather than one struct so that the first 14
+// dwords (every pointer and size the first loads need) are preloaded into
+// SGPRs by the dispatcher (-amdgpu-kernarg-preload-count): the state stream
+// then starts without waiting for a kernarg memory read.  The remaining
+// arguments are read while the first loads are in flight.
 template <int NS, int WAVES, bool L2NORM, int POLICY, bool BF16, bool MULTI>
-__global__ __launch_bounds__(64 * WAVES) void gdn_decode_k128(Params p) {
+__global__ __launch_bounds__(64 * WAVES) void gdn_decode_k128(
+    const void* state, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+    const uint16_t* a, const uint16_t* b, int H, int ratio, const float* A_log_p,
+    const float* dt_bias_p, uint16_t* out, void* new_state, float scale, int T_arg) {
+  Params p;
+  p.state = state;
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.a = a;
+  p.b = b;
+  p.A_log = A_log_p;
+  p.dt_bias = dt_bias_p;
+  p.out = out;
+  p.new_state = new_state;
+  p.scale = scale;
+  p.T = MULTI ? T_arg : 1;
+  p.H = H;
+  p.ratio = ratio;
+  p.HV = H * ratio;
   constexpr int kRowsPerWave = kLaneGroups * NS;
   constexpr int kRowsPerBlock = kRowsPerWave * WAVES;
   constexpr int kTiles = kDim / kRowsPerBlock;
@@ -388,7 +418,7 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_decode_k128(Params p) {
   const int hv = hq * p.ratio + static_cast<int>(blockIdx.x) / kTiles;
   const int head = bi * p.HV + hv;
   const int row0 = tile * kRowsPerBlock + wave * kRowsPerWave + grp * NS;
-  const int T = MULTI ? p.T : 1;
+  const int T = p.T;
 
   // Issue every global load before any arithmetic.  Loads retire in issue
   // order, so the small per-head operands (gate scalars, q, k, v) go first:
@@ -443,7 +473,7 @@ struct Launch {
 
 // Kernel variant: the fp32 single-token kernel is built for every launch
 // shape and cache policy (the sweep space); bf16-state and multi-token
-// kernels for 1, 2 or 4 rows per lane group and policies 0 and 1.
+// kernels for every launch shape with policies 0 and 1.
 struct Variant {
   bool l2;
   bool bf16;
@@ -455,22 +485,15 @@ hipError_t launch_one(bool l2, const Params& p, unsigned nb, const Launch& l) {
   constexpr unsigned kT = kDim / (kLaneGroups * NS * W);
   const dim3 grid(static_cast<unsigned>(p.ratio) * kT, static_cast<unsigned>(p.H), nb);
   const dim3 block(64 * W);
+  auto* kern = l2 ? gdn_decode_k128<NS, W, true, POL, BF16, MULTI>
+                  : gdn_decode_k128<NS, W, false, POL, BF16, MULTI>;
   if (l.start || l.stop) {
-    if (l2) {
-      hipExtLaunchKernelGGL((gdn_decode_k128<NS, W, true, POL, BF16, MULTI>), grid, block,
-                            0, l.stream, l.start, l.stop, 0, p);
-    } else {
-      hipExtLaunchKernelGGL((gdn_decode_k128<NS, W, false, POL, BF16, MULTI>), grid, block,
-                            0, l.stream, l.start, l.stop, 0, p);
-    }
+    hipExtLaunchKernelGGL(kern, grid, block, 0, l.stream, l.start, l.stop, 0, p.state, p.q,
+                          p.k, p.v, p.a, p.b, p.H, p.ratio, p.A_log, p.dt_bias, p.out,
+                          p.new_state, p.scale, p.T);
   } else {
-    if (l2) {
-      hipLaunchKernelGGL((gdn_decode_k128<NS, W, true, POL, BF16, MULTI>), grid, block, 0,
-                         l.stream, p);
-    } else {
-      hipLaunchKernelGGL((gdn_decode_k128<NS, W, false, POL, BF16, MULTI>), grid, block, 0,
-                         l.stream, p);
-    }
+    hipLaunchKernelGGL(kern, grid, block, 0, l.stream, p.state, p.q, p.k, p.v, p.a, p.b, p.H,
+                       p.ratio, p.A_log, p.dt_bias, p.out, p.new_state, p.scale, p.T);
   }
   return hipGetLastError();
 }
@@ -511,9 +534,7 @@ hipError_t by_ns(int ns, int w, int pol, bool l2, const Params& p, unsigned nb,
     case 1: return by_waves<1, BF16, MULTI>(w, pol, l2, p, nb, l);
     case 2: return by_waves<2, BF16, MULTI>(w, pol, l2, p, nb, l);
     case 4: return by_waves<4, BF16, MULTI>(w, pol, l2, p, nb, l);
-    case 8:
-      if constexpr (!BF16 && !MULTI) return by_waves<8, BF16, MULTI>(w, pol, l2, p, nb, l);
-      return hipErrorInvalidValue;
+    case 8: return by_waves<8, BF16, MULTI>(w, pol, l2, p, nb, l);
     default: return hipErrorInvalidValue;
   }
 }
@@ -530,7 +551,7 @@ bool shape_supported(const Variant& v, int ns, int w, int pol) {
   const bool pow2 = (ns == 1 || ns == 2 || ns == 4 || ns == 8) &&
                     (w == 1 || w == 2 || w == 4 || w == 8);
   if (!pow2 || ns * w > 32) return false;
-  if (v.bf16 || v.multi) return ns <= 4 && (pol == kPolicyDefault || pol == kPolicyNtBoth);
+  if (v.bf16 || v.multi) return pol == kPolicyDefault || pol == kPolicyNtBoth;
   return pol >= kPolicyDefault && pol <= kPolicyNtLoad;
 }
 
@@ -538,16 +559,55 @@ bool aligned(const void* p, uintptr_t a) {
   return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
 }
 
-// Launch shape for B*HV heads, from rocprofv3 and kernel-stamped sweeps of
-// every shape and cache policy on MI355X with steps rotating over >= 1 GiB
-// of states: two rows per lane group with nontemporal state loads and
-// stores is best or within 3% of best from B*HV = 8 to 8192 (B=256
-// qk16_v32: 165 us = 6.5 TB/s); below ~128 heads every shape sits within
-// 0.1 us of a fixed ~3 us launch-plus-round-trip floor.
-void choose_shape(long long heads, int* ns, int* waves, int* policy) {
-  *ns = 2;
+// Launch shape for B*HV heads: (rows per lane group, waves per block), with
+// nontemporal state loads and stores.  From rocprofv3 kernel-trace sweeps of
+// every shape on MI355X, in steps rotating over >= 1 GiB of states, at
+// 8..8192 heads (qk4_v8 B = 1..64, qk16_v32 B = 1..256, qk8_v32 B = 128),
+// separately for an fp32 state at T = 1, T = 2 and T = 4 and for a bf16
+// state.  Few heads want many small blocks (every CU busy); a few hundred
+// heads want fewer waves with more rows each (4-8 rows per lane group, one
+// wave per block: 6-14% faster there than 2 rows x 4 waves); large batches
+// stream at ~6.5 TB/s with 2 rows x 4 waves at T = 1, while at T = 4 the
+// per-token arithmetic is large enough that 4 rows per lane group (per-head
+// work shared by more rows) wins.
+struct ShapeRow {
+  long long max_heads;
+  int ns;
+  int waves;
+};
+constexpr ShapeRow kShapeFp32[] = {
+    {16, 1, 1}, {64, 2, 2}, {256, 4, 1}, {384, 8, 1}, {-1, 2, 4}};
+constexpr ShapeRow kShapeT2[] = {
+    {16, 1, 1}, {32, 1, 4}, {64, 2, 1}, {128, 2, 4}, {256, 4, 1}, {768, 8, 1}, {-1, 2, 4}};
+constexpr ShapeRow kShapeT3Plus[] = {
+    {16, 1, 1}, {32, 1, 4}, {64, 2, 1}, {256, 2, 2}, {384, 4, 1}, {768, 4, 2},
+    {1536, 8, 1}, {-1, 4, 2}};
+constexpr ShapeRow kShapeBf16[] = {
+    {16, 1, 2}, {32, 1, 4}, {64, 2, 4}, {128, 2, 2}, {256, 2, 1}, {384, 2, 4},
+    {768, 4, 4}, {2048, 2, 4}, {-1, 4, 4}};
+
+template <size_t N>
+void pick_row(const ShapeRow (&table)[N], long long heads, int* ns, int* waves) {
+  for (const ShapeRow& r : table) {
+    if (r.max_heads < 0 || heads <= r.max_heads) {
+      *ns = r.ns;
+      *waves = r.waves;
+      return;
+    }
+  }
+}
+
+void choose_shape(long long heads, bool bf16, int T, int* ns, int* waves, int* policy) {
   *policy = kPolicyNtBoth;
-  *waves = heads <= 64 ? 2 : 4;  // 16 or 32 rows per block
+  if (bf16) {
+    pick_row(kShapeBf16, heads, ns, waves);
+  } else if (T >= 3) {
+    pick_row(kShapeT3Plus, heads, ns, waves);
+  } else if (T == 2) {
+    pick_row(kShapeT2, heads, ns, waves);
+  } else {
+    pick_row(kShapeFp32, heads, ns, waves);
+  }
 }
 
 int steps_impl(const void* q, const void* k, const void* v, const void* state,
@@ -640,7 +700,7 @@ int gdn_decode_steps(const void* q, const void* k, const void* v, const void* st
                      int use_qk_l2norm, void* hip_stream) {
   if (B < 0 || HV <= 0) return hipErrorInvalidValue;
   int ns = 0, waves = 0, policy = 0;
-  choose_shape(static_cast<long long>(B) * HV, &ns, &waves, &policy);
+  choose_shape(static_cast<long long>(B) * HV, state_bf16 != 0, T, &ns, &waves, &policy);
   return steps_impl(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, B, T,
                     H, HV, K, V, state_bf16, use_qk_l2norm, ns, waves, policy, nullptr,
                     nullptr, hip_stream);
@@ -659,14 +719,14 @@ int gdn_decode_step_shaped(const void* q, const void* k, const void* v,
                     waves_per_block, cache_policy, start_event, stop_event, hip_stream);
 }
 
-int gdn_decode_launch_shape(int B, int HV, int* rows_per_lane_group,
-                            int* waves_per_block, int* cache_policy,
-                            long long* num_blocks) {
-  if (B < 0 || HV <= 0 || !rows_per_lane_group || !waves_per_block ||
-      !cache_policy || !num_blocks)
+int gdn_decode_launch_shape(int B, int T, int HV, int state_bf16,
+                            int* rows_per_lane_group, int* waves_per_block,
+                            int* cache_policy, long long* num_blocks) {
+  if (B < 0 || T < 1 || HV <= 0 || (state_bf16 != 0 && state_bf16 != 1) ||
+      !rows_per_lane_group || !waves_per_block || !cache_policy || !num_blocks)
     return hipErrorInvalidValue;
   int ns = 0, waves = 0, policy = 0;
-  choose_shape(static_cast<long long>(B) * HV, &ns, &waves, &policy);
+  choose_shape(static_cast<long long>(B) * HV, state_bf16 != 0, T, &ns, &waves, &policy);
   *rows_per_lane_group = ns;
   *waves_per_block = waves;
   *cache_policy = policy;
@@ -678,6 +738,6 @@ const char* gdn_decode_error_string(int code) {
   return hipGetErrorString(static_cast<hipError_t>(code));
 }
 
-int gdn_decode_abi_version(void) { return 2; }
+int gdn_decode_abi_version(void) { return 3; }
 
 }  // extern "C"

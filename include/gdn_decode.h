@@ -88,7 +88,7 @@ int gdn_decode_steps(const void* q, const void* k, const void* v,
  * their product is at most 32.  cache_policy selects how the state stream
  * is accessed: 0 ordinary loads and stores, 1 nontemporal loads and stores,
  * 2 nontemporal stores only, 3 nontemporal loads only.  With T > 1 or a
- * bf16 state, rows_per_lane_group is at most 4 and cache_policy 0 or 1.  start_event / stop_event (hipEvent_t, may be
+ * bf16 state, cache_policy is 0 or 1.  start_event / stop_event (hipEvent_t, may be
  * NULL) are stamped with the kernel's own start and end timestamps
  * (hipExtLaunchKernelGGL), so hipEventElapsedTime gives the kernel duration
  * without event-marker overhead.  Used for launch-shape sweeps and timing.
@@ -108,16 +108,17 @@ int gdn_decode_step_shaped(const void* q, const void* k, const void* v,
                            void* hip_stream);
 
 /*
- * Launch shape gdn_decode_step would use for (B, HV): writes
+ * Launch shape gdn_decode_steps would use for B sequences of T tokens over
+ * HV v-heads with an fp32 (state_bf16 = 0) or bf16 (1) state: writes
  * rows_per_lane_group, waves_per_block, cache_policy and the workgroup
- * count.  Returns 0, or hipErrorInvalidValue for B < 0, HV <= 0 or null
- * outputs.
+ * count.  Returns 0, or hipErrorInvalidValue for B < 0, T < 1, HV <= 0, a
+ * state_bf16 other than 0 or 1, or null outputs.
  * No reference counterpart (the reference's choice is inline in its
  * wrappers, solution/triton/kernel.py:168-174).
  */
-int gdn_decode_launch_shape(int B, int HV, int* rows_per_lane_group,
-                            int* waves_per_block, int* cache_policy,
-                            long long* num_blocks);
+int gdn_decode_launch_shape(int B, int T, int HV, int state_bf16,
+                            int* rows_per_lane_group, int* waves_per_block,
+                            int* cache_policy, long long* num_blocks);
 
 /*
  * Human-readable text for a return code of the functions above
@@ -126,7 +127,7 @@ int gdn_decode_launch_shape(int B, int HV, int* rows_per_lane_group,
  */
 const char* gdn_decode_error_string(int code);
 
-/* ABI version of this header: 2. */
+/* ABI version of this header: 3. */
 int gdn_decode_abi_version(void);
 
 #ifdef __cplusplus

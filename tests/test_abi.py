@@ -54,13 +54,29 @@ def test_abi_version_and_error_text():
 
 def test_launch_shape_query():
     ns, w, pol, blocks = _lib.launch_shape(1, 32)
-    assert ns in (1, 2, 4, 8) and w in (1, 2, 4, 8) and pol in (0, 1, 2)
+    assert ns in (1, 2, 4, 8) and w in (1, 2, 4, 8) and pol in (0, 1, 2, 3)
     assert blocks == 32 * 128 // (4 * ns * w)
     assert _lib.launch_shape(0, 32)[3] == 0
     ns, w, pol, blocks = _lib.launch_shape(256, 32)
     assert blocks == 256 * 32 * 128 // (4 * ns * w)
     with pytest.raises(RuntimeError):
         _lib.launch_shape(-1, 32)
+    with pytest.raises(RuntimeError):
+        _lib.launch_shape(1, 32, T=0)
+
+
+@pytest.mark.parametrize("T,bf16", [(1, False), (1, True), (2, False), (3, False),
+                                    (4, False), (4, True)])
+def test_launch_shape_table_stays_in_the_supported_space(T, bf16):
+    """Every head count gets a shape the kernel is built for: at most 32
+    rows per lane group x waves, power-of-two tiles per head, and a cache
+    policy every variant has (0 or 1)."""
+    for heads in (1, 7, 8, 9, 16, 32, 33, 64, 100, 128, 256, 257, 384, 512, 1000, 8192,
+                  1 << 20):
+        ns, w, pol, blocks = _lib.launch_shape(heads, 1, T=T, state_bf16=bf16)
+        assert ns in (1, 2, 4, 8) and w in (1, 2, 4, 8) and ns * w <= 32
+        assert pol in (0, 1)
+        assert blocks == heads * 128 // (4 * ns * w)
 
 
 def _step(lib, *, B=1, H=16, HV=32, K=128, V=128, ptr=None, new_state=None):
@@ -84,13 +100,19 @@ def test_validation_rejects_bad_sizes_without_launching():
     f = ctypes.c_float(0.1)
 
     def sh(T, bf16, ns, w, pol):
-        return shaped(*nulls, f, None, None, 1, T, 16, 32, 128, 128, bf16, 1, ns, w, pol,
+        # B = 0: a supported request returns 0 (nothing to launch), an
+        # unsupported one is rejected first
+        return shaped(*nulls, f, None, None, 0, T, 16, 32, 128, 128, bf16, 1, ns, w, pol,
                       None, None, None)
 
+    assert sh(1, 0, 2, 4, 1) == 0     # the B=256 fp32 shape
+    assert sh(1, 0, 8, 4, 3) == 0     # 32 rows per block, nontemporal loads only
+    assert sh(4, 0, 8, 1, 1) == 0     # multi-token, 8 rows per lane group
+    assert sh(1, 1, 8, 2, 0) == 0     # bf16 state, 8 rows per lane group
     assert sh(1, 0, 8, 8, 0) == 1     # 8 x 8 > 32 rows per block
     assert sh(1, 0, 3, 1, 0) == 1     # not a power of two
     assert sh(1, 0, 1, 1, 4) == 1     # unknown cache policy
-    assert sh(2, 0, 8, 1, 0) == 1     # multi-token kernels take at most 4 rows per group
+    assert sh(2, 0, 2, 1, 3) == 1     # multi-token kernels take cache policy 0 or 1
     assert sh(1, 1, 2, 4, 2) == 1     # bf16-state kernels take cache policy 0 or 1
     assert sh(0, 0, 2, 4, 1) == 1     # T < 1
     assert sh(1, 2, 2, 4, 1) == 1     # state_bf16 is 0 or 1

@@ -141,7 +141,7 @@ def test_launch_shapes_agree_bitwise(T, bf16, hip_device):
     if bf16:
         t["state"] = t["state"].to(torch.bfloat16)
     ref_o, ref_s = gdn.run(**t, use_qk_l2norm=True)
-    for ns, w, pol in itertools.product((1, 2, 4), (1, 2, 4, 8), (0, 1)):
+    for ns, w, pol in itertools.product((1, 2, 4, 8), (1, 2, 4, 8), (0, 1)):
         if ns * w > 32:
             continue
         out, st = torch.empty_like(ref_o), torch.empty_like(ref_s)
@@ -151,9 +151,9 @@ def test_launch_shapes_agree_bitwise(T, bf16, hip_device):
         assert torch.equal(out, ref_o), (ns, w, pol)
         assert torch.equal(st, ref_s), (ns, w, pol)
     out, st = torch.empty_like(ref_o), torch.empty_like(ref_s)
-    with pytest.raises(RuntimeError):   # 8 rows per lane group: single-token fp32 only
-        gdn.kernel_hip_shaped(**t, output=out, new_state=st, rows_per_lane_group=8,
-                              waves_per_block=1, cache_policy=0)
+    with pytest.raises(RuntimeError):   # split cache policies: single-token fp32 only
+        gdn.kernel_hip_shaped(**t, output=out, new_state=st, rows_per_lane_group=2,
+                              waves_per_block=1, cache_policy=2)
 
 
 def test_multi_token_full_size(hip_device):
