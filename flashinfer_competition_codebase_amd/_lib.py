@@ -1,4 +1,5 @@
-"""ctypes binding of ``libgdn_decode.so`` (the C ABI in ``include/gdn_decode.h``).
+"""ctypes bindings of ``libgdn_decode.so`` and ``libgdn_prefill.so`` (the C ABIs
+in ``include/gdn_decode.h`` and ``include/gdn_prefill.h``).
 
 There is no fallback: if the library is missing or fails to load, every entry
 point raises ``RuntimeError`` naming the build command.  The reference builds
@@ -13,6 +14,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libgdn_decode.so"
+PREFILL_LIB_PATH = Path(__file__).resolve().parent / "libgdn_prefill.so"
 
 # Names and argument types of every exported function, in header order.
 _P = ctypes.c_void_p
@@ -42,31 +44,50 @@ SIGNATURES = {
 
 ABI_VERSION = 3
 
+_S = ctypes.c_size_t
+PREFILL_SIGNATURES = {
+    "gdn_prefill_workspace_bytes": (_S, [_I, _I, _I]),
+    "gdn_prefill": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P] + [_I] * 7 + [_P, _S, _P],
+    ),
+    "gdn_prefill_abi_version": (_I, []),
+}
+PREFILL_ABI_VERSION = 1
+
 _lock = threading.Lock()
 _lib = None
+_prefill_lib = None
 
 
-def load(path: Path = LIB_PATH) -> ctypes.CDLL:
-    """Load the library at ``path`` and declare every signature."""
+def _load(path: Path, signatures: dict, version_fn: str, version: int) -> ctypes.CDLL:
     if not path.exists():
         raise RuntimeError(
-            f"HIP decode library not found at {path}; build it with "
+            f"HIP library not found at {path}; build it with "
             "`python -m flashinfer_competition_codebase_amd.build`"
         )
     try:
         lib = ctypes.CDLL(str(path))
     except OSError as exc:
-        raise RuntimeError(f"failed to load HIP decode library {path}: {exc}") from exc
-    for name, (restype, argtypes) in SIGNATURES.items():
+        raise RuntimeError(f"failed to load HIP library {path}: {exc}") from exc
+    for name, (restype, argtypes) in signatures.items():
         fn = getattr(lib, name)
         fn.restype = restype
         fn.argtypes = argtypes
-    version = lib.gdn_decode_abi_version()
-    if version != ABI_VERSION:
-        raise RuntimeError(
-            f"{path} has ABI version {version}, expected {ABI_VERSION}; rebuild it"
-        )
+    got = getattr(lib, version_fn)()
+    if got != version:
+        raise RuntimeError(f"{path} has ABI version {got}, expected {version}; rebuild it")
     return lib
+
+
+def load(path: Path = LIB_PATH) -> ctypes.CDLL:
+    """Load the decode library at ``path`` and declare every signature."""
+    return _load(path, SIGNATURES, "gdn_decode_abi_version", ABI_VERSION)
+
+
+def load_prefill(path: Path = PREFILL_LIB_PATH) -> ctypes.CDLL:
+    """Load the prefill library at ``path`` and declare every signature."""
+    return _load(path, PREFILL_SIGNATURES, "gdn_prefill_abi_version", PREFILL_ABI_VERSION)
 
 
 def get_lib() -> ctypes.CDLL:
@@ -77,6 +98,16 @@ def get_lib() -> ctypes.CDLL:
             if _lib is None:
                 _lib = load()
     return _lib
+
+
+def get_prefill_lib() -> ctypes.CDLL:
+    """Process-wide prefill library handle, loaded on first use."""
+    global _prefill_lib
+    if _prefill_lib is None:
+        with _lock:
+            if _prefill_lib is None:
+                _prefill_lib = load_prefill()
+    return _prefill_lib
 
 
 def error_string(code: int) -> str:

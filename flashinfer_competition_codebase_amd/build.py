@@ -6,6 +6,8 @@ this file:
 * ``csrc/gdn_decode.hip`` into ``libgdn_decode.so``: the decode step, a
   plain C-ABI shared object (declared in ``include/gdn_decode.h``) that the
   Python host side loads with ctypes;
+* ``csrc/gdn_prefill.hip`` into ``libgdn_prefill.so``: the variable-length
+  prefill (declared in ``include/gdn_prefill.h``);
 * ``csrc/calib.hip`` into ``libgdn_calib.so``: reference kernels (same-bytes
   read-modify-write, empty kernel) that only ``bench.py`` loads, to report
   the floor of the decode step's traffic.
@@ -27,8 +29,10 @@ LIB_NAME = "libgdn_decode.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 CALIB_SRC = PKG_DIR / "csrc" / "calib.hip"
 CALIB_PATH = PKG_DIR / "libgdn_calib.so"
+PREFILL_SRC = PKG_DIR / "csrc" / "gdn_prefill.hip"
+PREFILL_PATH = PKG_DIR / "libgdn_prefill.so"
 # library -> source
-LIBRARIES = {LIB_PATH: CSRC, CALIB_PATH: CALIB_SRC}
+LIBRARIES = {LIB_PATH: CSRC, PREFILL_PATH: PREFILL_SRC, CALIB_PATH: CALIB_SRC}
 OFFLOAD_ARCH = "gfx950"
 KERNARG_PRELOAD_ARGS = int(os.environ.get("GDN_KERNARG_PRELOAD_ARGS", "8"))
 

@@ -413,8 +413,10 @@ def main(argv=None) -> int:
 
     from . import ENTRY_POINTS, NO_DPS
 
-    if args.algo not in ENTRY_POINTS:
-        raise SystemExit(f"unknown algo {args.algo!r}; available: {sorted(ENTRY_POINTS)}")
+    decode_algos = sorted(a for a in ENTRY_POINTS if not a.startswith("prefill"))
+    if args.algo not in decode_algos:
+        raise SystemExit(f"algo {args.algo!r} is not a decode entry point of this package; "
+                         f"available for {args.definition}: {decode_algos}")
     workloads = _select(contest_decode_workloads(), args.num_workloads, args.workload_id)
     manifest = Manifest() if args.manifest else None
     print(f"Algorithm: {args.algo} ({'value-returning' if args.algo in NO_DPS else 'DPS'}), "

@@ -1,0 +1,147 @@
+"""Python entry points of the GDN prefill, in the reference's calling forms.
+
+Two forms, with the reference's argument names (``fn(**tensors)`` works):
+
+* ``prefill_run(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale)`` --
+  value-returning, like ``kernel_prefill_reference``
+  (solution/triton/prefill_kernel.py:85-183): returns ``(output, new_state)``
+  and leaves ``state`` untouched.
+* ``kernel_prefill_hip(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens,
+  scale, output, new_state)`` -- destination-passing, like
+  ``kernel_prefill_fla_chunk`` (solution/triton/prefill_kernel.py:10-58):
+  writes both outputs, returns None.  ``new_state`` may be ``state`` itself.
+
+Both launch the gfx950 prefill of ``libgdn_prefill.so`` (chunk offsets,
+per-chunk preparation, sequential scan) on the current HIP stream; there is
+no CPU path.  The device workspace for the per-chunk intermediates comes
+from torch's caching allocator.
+
+Tensor contract (solution/triton/prefill_kernel.py:96-114): q, k
+``[L, H, 128]`` bf16; v ``[L, HV, 128]`` bf16 with ``HV % H == 0``; state
+``[N, HV, 128, 128]`` fp32 k-last or None (zeros); A_log, dt_bias ``[HV]``
+fp32; a, b ``[L, HV]`` bf16; cu_seqlens ``[N + 1]`` int32 (int64 is
+converted) on the same device, non-decreasing from 0 to L; scale float,
+0-d tensor, None or 0 (None/0 mean ``1/sqrt(128)``); output ``[L, HV, 128]``
+bf16; new_state ``[N, HV, 128, 128]`` fp32.  A sequence with no tokens gets
+a zero ``new_state``, as the reference's loop leaves it
+(prefill_kernel.py:147-150).  The q/k L2-norm is a keyword-only flag,
+off by default as in the reference's prefill (prefill_kernel.py:45).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .kernel import K_DIM, V_DIM, _expect, _overlap, resolve_scale
+
+__all__ = ["prefill_run", "kernel_prefill_hip", "workspace_bytes"]
+
+
+def workspace_bytes(total_seq_len: int, num_seqs: int, HV: int) -> int:
+    """Device workspace bytes a prefill of this size needs."""
+    n = _lib.get_prefill_lib().gdn_prefill_workspace_bytes(int(total_seq_len), int(num_seqs),
+                                                          int(HV))
+    if n == 0:
+        raise ValueError(f"invalid prefill sizes L={total_seq_len}, N={num_seqs}, HV={HV}")
+    return n
+
+
+def check_prefill_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, output=None,
+                         new_state=None):
+    """Validate the prefill tensors; returns ``(L, N, H, HV)``.  Shape and dtype
+    rules are the reference's (prefill_kernel.py:96-129, generalised to any
+    ``HV % H == 0``); the device check comes last."""
+    if not isinstance(q, torch.Tensor) or q.dim() != 3:
+        raise ValueError("q must be a 3-D tensor [L, H, K]")
+    if not isinstance(v, torch.Tensor) or v.dim() != 3:
+        raise ValueError("v must be a 3-D tensor [L, HV, V]")
+    if not isinstance(cu_seqlens, torch.Tensor) or cu_seqlens.dim() != 1 or cu_seqlens.numel() < 1:
+        raise ValueError("cu_seqlens must be a 1-D tensor [N + 1]")
+    if cu_seqlens.dtype not in (torch.int32, torch.int64):
+        raise TypeError(f"cu_seqlens must be int32 or int64, got {cu_seqlens.dtype}")
+    L, H, K = q.shape
+    HV, V = v.shape[1], v.shape[2]
+    N = cu_seqlens.numel() - 1
+    if K != K_DIM or V != V_DIM:
+        raise ValueError(f"K and V must be {K_DIM}, got K={K}, V={V}")
+    if H <= 0 or HV <= 0 or HV % H != 0:
+        raise ValueError(f"v-heads must be a multiple of q/k heads, got H={H}, HV={HV}")
+    if v.shape[0] != L:
+        raise ValueError(f"v must have {L} tokens, got {v.shape[0]}")
+    _expect(q, "q", torch.bfloat16, (L, H, K))
+    _expect(k, "k", torch.bfloat16, (L, H, K))
+    _expect(v, "v", torch.bfloat16, (L, HV, V))
+    if state is not None:
+        _expect(state, "state", torch.float32, (N, HV, V, K))
+    _expect(A_log, "A_log", torch.float32, (HV,))
+    _expect(dt_bias, "dt_bias", torch.float32, (HV,))
+    _expect(a, "a", torch.bfloat16, (L, HV))
+    _expect(b, "b", torch.bfloat16, (L, HV))
+    if not cu_seqlens.is_contiguous():
+        raise ValueError("cu_seqlens must be contiguous")
+    if output is not None:
+        _expect(output, "output", torch.bfloat16, (L, HV, V))
+    if new_state is not None:
+        _expect(new_state, "new_state", torch.float32, (N, HV, V, K))
+    tensors = [q, k, v, A_log, a, dt_bias, b, cu_seqlens]
+    tensors += [t for t in (state, output, new_state) if t is not None]
+    dev = q.device
+    for t in tensors:
+        if t.device != dev:
+            raise ValueError(f"all tensors must be on one device, got {dev} and {t.device}")
+    if dev.type != "cuda":
+        raise ValueError(f"the GDN prefill kernels run on a HIP device; got tensors on {dev}")
+    if state is not None and new_state is not None and new_state is not state:
+        if new_state.data_ptr() != state.data_ptr() and _overlap(new_state, state):
+            raise ValueError("new_state must be state itself or not overlap it")
+    return L, N, H, HV
+
+
+@torch.no_grad()
+def kernel_prefill_hip(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output,
+                       new_state, *, use_qk_l2norm: bool = False):
+    """Destination-passing prefill (reference DPS form,
+    solution/triton/prefill_kernel.py:10-58): writes ``output`` and
+    ``new_state``; ``new_state is state`` updates in place."""
+    if output is None or new_state is None:
+        raise ValueError("kernel_prefill_hip needs preallocated output and new_state")
+    L, N, H, HV = check_prefill_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens,
+                                       output, new_state)
+    scale = resolve_scale(scale, q.shape[-1])
+    if N == 0:
+        return None
+    if cu_seqlens.dtype != torch.int32:
+        cu_seqlens = cu_seqlens.to(torch.int32)
+    lib = _lib.get_prefill_lib()
+    ws_bytes = workspace_bytes(L, N, HV)
+    workspace = torch.empty(ws_bytes + 256, dtype=torch.uint8, device=q.device)
+    ws_ptr = (workspace.data_ptr() + 255) & ~255
+    stream = torch.cuda.current_stream(q.device).cuda_stream
+    with torch.cuda.device(q.device):
+        code = lib.gdn_prefill(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(),
+            None if state is None else state.data_ptr(),
+            A_log.data_ptr(), a.data_ptr(), dt_bias.data_ptr(), b.data_ptr(),
+            cu_seqlens.data_ptr(), scale, output.data_ptr(), new_state.data_ptr(),
+            L, N, H, HV, K_DIM, V_DIM, int(bool(use_qk_l2norm)), ws_ptr, ws_bytes, stream)
+    _lib.check(code, "gdn_prefill")
+    # keep the workspace (and a converted cu_seqlens) alive until the kernels ran
+    workspace.record_stream(torch.cuda.current_stream(q.device))
+    cu_seqlens.record_stream(torch.cuda.current_stream(q.device))
+    return None
+
+
+@torch.no_grad()
+def prefill_run(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, *,
+                use_qk_l2norm: bool = False):
+    """Value-returning prefill with the reference's contract
+    (``kernel_prefill_reference``, solution/triton/prefill_kernel.py:85-183):
+    returns ``(output [L, HV, 128] bf16, new_state [N, HV, 128, 128] fp32)``;
+    ``state`` is not modified."""
+    L, N, H, HV = check_prefill_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens)
+    output = torch.empty((L, HV, V_DIM), dtype=torch.bfloat16, device=q.device)
+    new_state = torch.empty((N, HV, V_DIM, K_DIM), dtype=torch.float32, device=q.device)
+    kernel_prefill_hip(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output,
+                       new_state, use_qk_l2norm=use_qk_l2norm)
+    return output, new_state

@@ -1,0 +1,81 @@
+/*
+ * gdn_prefill.h - C ABI of the MI355X (gfx950) Gated Delta Net prefill.
+ *
+ * Variable-length prefill over N sequences packed along the token axis, in
+ * the reference's tensor layouts (solution/triton/prefill_kernel.py:96-114):
+ *
+ *   q, k        [L, H,  K]        bf16   (K = 128; L = total tokens)
+ *   v           [L, HV, V]        bf16   (V = 128, HV % H == 0)
+ *   state       [N, HV, V, K]     fp32   k-last; NULL means zeros
+ *   A_log       [HV]              fp32
+ *   a, b        [L, HV]           bf16
+ *   dt_bias     [HV]              fp32
+ *   cu_seqlens  [N + 1]           int32  sequence s is tokens
+ *                                        [cu_seqlens[s], cu_seqlens[s+1])
+ *   output      [L, HV, V]        bf16
+ *   new_state   [N, HV, V, K]     fp32   may be the same buffer as state
+ *
+ * For each sequence and v-head hv (q/k head hv / (HV/H)), token after token,
+ * the decode step of gdn_decode.h against the running state; the state
+ * after the sequence's last token goes to new_state (zeros for a sequence
+ * with no tokens, as the reference).  Evaluated chunkwise (64 tokens) with
+ * MFMA; arithmetic in fp32 except the bf16 x bf16 products of the inputs
+ * themselves (K K^T, Q K^T), which are exact in fp32 accumulation.
+ *
+ * cu_seqlens is read on the device.  It should be non-decreasing with
+ * cu_seqlens[0] = 0 and cu_seqlens[N] = L, as the reference requires; token
+ * ranges are clamped to [0, L] on the device, so other contents give
+ * unspecified results but no out-of-bounds access.
+ *
+ * All pointers are device pointers.  The call is asynchronous on
+ * `hip_stream`, allocates nothing, and returns 0 or a nonzero hipError_t
+ * (hipErrorInvalidValue = 1 for bad sizes, null or misaligned pointers, a
+ * short workspace, or a new_state that partly overlaps state).
+ */
+#ifndef GDN_PREFILL_H
+#define GDN_PREFILL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/*
+ * Bytes of device workspace gdn_prefill needs for L total tokens, N
+ * sequences and HV v-heads (per-chunk intermediates: about 81 KiB per 64
+ * tokens per v-head, plus 64-token slack per sequence).  0 for invalid sizes.
+ * The reference's FLA path allocates its intermediates per call inside
+ * chunk_gated_delta_rule (solution/triton/fla_prefill_code.py:1726-1776);
+ * here the caller provides them.
+ */
+size_t gdn_prefill_workspace_bytes(int total_seq_len, int num_seqs, int HV);
+
+/*
+ * One prefill over all sequences.  Replaces the reference's prefill entry
+ * points, which take the same tensors, cu_seqlens and scale:
+ *   solution/triton/prefill_kernel.py:10-58   kernel_prefill_fla_chunk (DPS)
+ *   solution/triton/prefill_kernel.py:85-183  kernel_prefill_reference
+ * Differences: sizes are explicit, K and V must be 128, the q/k L2-norm is an
+ * explicit flag (off in the reference's prefill, prefill_kernel.py:45), the
+ * workspace (256-byte aligned, gdn_prefill_workspace_bytes long) comes from
+ * the caller, `scale` is already resolved (None/0 -> 1/sqrt(K) in the
+ * Python caller), and bad arguments return an error instead of launching.
+ * q, k, v, output, state and new_state must be 16-byte aligned.
+ */
+int gdn_prefill(const void* q, const void* k, const void* v, const float* state,
+                const float* A_log, const void* a, const float* dt_bias, const void* b,
+                const int32_t* cu_seqlens, float scale, void* output, float* new_state,
+                int total_seq_len, int num_seqs, int H, int HV, int K, int V,
+                int use_qk_l2norm, void* workspace, size_t workspace_size,
+                void* hip_stream);
+
+/* ABI version of this header: 1. */
+int gdn_prefill_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDN_PREFILL_H */

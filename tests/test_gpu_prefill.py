@@ -1,0 +1,141 @@
+"""Parity of the gfx950 prefill with the CPU oracle (needs a HIP device).
+
+Bars, per element: output within atol = rtol = 1e-2 of the oracle loop's bf16
+output (the contest's criterion, CLAUDE.md:158) and within two bf16 ulps
+(2^-7 relative) + 1e-5 of the float64 chunked result; new state within
+1e-3 relative + 1e-5 of the float64 result and within 1e-4 in relative
+Frobenius norm.  Inputs: unit-norm q/k rows (the model's normalisation; raw
+N(0,1) keys make the recurrence grow without bound), seeded on the CPU.
+"""
+
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import flashinfer_competition_codebase_amd as gdn
+from flashinfer_competition_codebase_amd import _lib
+from oracle.gdn_prefill_oracle import make_prefill_inputs, prefill_chunked_fp64, prefill_loop
+
+pytestmark = pytest.mark.gpu
+
+
+def _announce(case):
+    sys.stdout.write(f"[gpu case] {case}\n")
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _library_present():
+    _lib.get_prefill_lib()
+
+
+def _dev(t, device):
+    return {n: (x.to(device) if isinstance(x, torch.Tensor) else x) for n, x in t.items()}
+
+
+def _check(t, out, st, l2=False, loop=True):
+    out, st = out.cpu(), st.cpu()
+    o64, s64 = prefill_chunked_fp64(**t, use_qk_l2norm=l2)
+    of = out.double().numpy()
+    assert np.all(np.isfinite(of))
+    d64 = np.abs(of - o64)
+    assert np.all(d64 <= 2.0 ** -7 * np.abs(o64) + 1e-5), f"output vs fp64: max {d64.max():.3e}"
+    if loop:
+        ref_o, ref_s = prefill_loop(**t, use_qk_l2norm=l2)
+        dl = (out.float() - ref_o.float()).abs()
+        assert bool((dl <= 1e-2 + 1e-2 * ref_o.float().abs()).all()), f"output vs loop {dl.max()}"
+    sd = st.double().numpy()
+    ds = np.abs(sd - s64)
+    assert np.all(ds <= 1e-3 * np.abs(s64) + 1e-5), f"state vs fp64: max {ds.max():.3e}"
+    rel = np.linalg.norm(sd - s64) / max(np.linalg.norm(s64), 1e-30)
+    assert rel <= 1e-4, rel
+    return d64.max(), ds.max()
+
+
+@pytest.mark.parametrize("seqlens,H,HV", [
+    ([6], 4, 8),                      # the size of the reference's prefill workload 0
+    ([1], 4, 8),
+    ([64], 4, 8),
+    ([65], 4, 8),
+    ([5, 70, 1, 0, 33], 4, 8),
+    ([130, 3], 2, 2),
+    ([100], 1, 4),
+    ([200, 129], 16, 32),
+])
+def test_prefill_matches_the_oracle(seqlens, H, HV, hip_device):
+    _announce(f"prefill seqlens={seqlens} H={H} HV={HV}")
+    t = make_prefill_inputs(seqlens, H, HV, seed=100 + sum(seqlens) + H)
+    out, st = gdn.prefill_run(**_dev(t, hip_device))
+    torch.cuda.synchronize()
+    assert out.shape == (sum(seqlens), HV, 128) and st.shape == (len(seqlens), HV, 128, 128)
+    _check(t, out, st)
+
+
+def test_long_sequence_and_many_sequences(hip_device):
+    _announce("prefill long + many")
+    g = torch.Generator().manual_seed(3)
+    lens = [int(x) for x in torch.randint(0, 160, (24,), generator=g)] + [1000]
+    t = make_prefill_inputs(lens, 4, 8, seed=11)
+    out, st = gdn.prefill_run(**_dev(t, hip_device))
+    torch.cuda.synchronize()
+    _check(t, out, st, loop=False)
+
+
+def test_l2norm_and_no_state(hip_device):
+    _announce("prefill l2norm, state=None, raw-scale q/k")
+    t = make_prefill_inputs([40, 90], 4, 8, seed=12, with_state=False, unit_qk=False)
+    out, st = gdn.prefill_run(**_dev(t, hip_device), use_qk_l2norm=True)
+    torch.cuda.synchronize()
+    _check(t, out, st, l2=True)
+
+
+def test_in_place_and_dps_forms_agree_bitwise(hip_device):
+    _announce("prefill in place / DPS / int64 cu_seqlens")
+    t = _dev(make_prefill_inputs([70, 10], 4, 8, seed=13), hip_device)
+    ref_o, ref_s = gdn.prefill_run(**t)
+    state = t["state"].clone()
+    out = torch.empty_like(ref_o)
+    gdn.kernel_prefill_hip(**{**t, "state": state, "cu_seqlens": t["cu_seqlens"].long()},
+                           output=out, new_state=state)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref_o) and torch.equal(state, ref_s)
+
+
+def test_empty_sequences_get_a_zero_state(hip_device):
+    _announce("prefill empty sequences")
+    t = make_prefill_inputs([0, 5, 0], 4, 8, seed=14)
+    out, st = gdn.prefill_run(**_dev(t, hip_device))
+    torch.cuda.synchronize()
+    st = st.cpu()
+    assert torch.count_nonzero(st[0]) == 0 and torch.count_nonzero(st[2]) == 0
+    _check(t, out, st)
+    t0 = make_prefill_inputs([0, 0], 4, 8, seed=15)          # no tokens at all
+    out0, st0 = gdn.prefill_run(**_dev(t0, hip_device))
+    torch.cuda.synchronize()
+    assert out0.shape == (0, 8, 128) and torch.count_nonzero(st0) == 0
+
+
+def test_prefill_equals_chained_decode_steps(hip_device):
+    """A sequence's prefill equals its tokens through the decode kernel one by
+    one (different algorithms: equal within the output and state bars)."""
+    _announce("prefill vs chained decode")
+    t = _dev(make_prefill_inputs([90], 4, 8, seed=16), hip_device)
+    out, st = gdn.prefill_run(**t)
+    state = t["state"].clone()
+    outs = []
+    for i in range(90):
+        o = torch.empty(1, 1, 8, 128, dtype=torch.bfloat16, device=hip_device)
+        gdn.kernel_hip(q=t["q"][i].view(1, 1, 4, 128), k=t["k"][i].view(1, 1, 4, 128),
+                       v=t["v"][i].view(1, 1, 8, 128), state=state, A_log=t["A_log"],
+                       a=t["a"][i].view(1, 1, 8), dt_bias=t["dt_bias"], b=t["b"][i].view(1, 1, 8),
+                       scale=t["scale"], output=o, new_state=state)
+        outs.append(o.view(8, 128))
+    torch.cuda.synchronize()
+    dec = torch.stack(outs).float().cpu()
+    assert bool(((out.float().cpu() - dec).abs() <= 1e-2 + 1e-2 * dec.abs()).all())
+    ds = (st.cpu() - state.cpu()).abs()
+    assert bool((ds <= 1e-3 * state.cpu().abs() + 1e-5).all()), ds.max()

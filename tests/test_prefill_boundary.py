@@ -1,0 +1,98 @@
+"""Prefill boundary on the host: argument validation, the C ABI's exports and
+its own validation (no compute call: every native call here is rejected, or
+has nothing to launch, before any HIP call)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+import flashinfer_competition_codebase_amd as gdn
+from flashinfer_competition_codebase_amd import _lib
+from flashinfer_competition_codebase_amd.prefill import check_prefill_inputs
+from oracle.gdn_prefill_oracle import make_prefill_inputs
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "gdn_prefill.h"
+
+
+def _header_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    protos = re.findall(r"^\s*(?:const\s+)?\w+\*?\s+(gdn_prefill\w*)\s*\(([^;]*?)\)\s*;",
+                        text, flags=re.M | re.S)
+    return {n: (0 if p.strip() in ("", "void") else p.count(",") + 1) for n, p in protos}
+
+
+def test_header_and_library_agree():
+    funcs = _header_functions()
+    assert set(funcs) == {"gdn_prefill_workspace_bytes", "gdn_prefill",
+                          "gdn_prefill_abi_version"}
+    lib = _lib.get_prefill_lib()
+    for name, nparams in funcs.items():
+        assert hasattr(lib, name)
+        assert len(_lib.PREFILL_SIGNATURES[name][1]) == nparams, name
+    assert lib.gdn_prefill_abi_version() == _lib.PREFILL_ABI_VERSION
+
+
+def test_workspace_size_formula():
+    lib = _lib.get_prefill_lib()
+    slot = (2 * 64 * 128 + 64 * 64 + 3 * 64) * 4            # W, U, P, row scales
+    for L, N, HV in ((6, 1, 8), (16384, 1, 8), (1000, 37, 32), (0, 3, 8)):
+        chunks = (L + 63) // 64 + N
+        offs = ((N + 1) * 4 + 255) // 256 * 256
+        assert lib.gdn_prefill_workspace_bytes(L, N, HV) == offs + chunks * HV * slot
+    assert lib.gdn_prefill_workspace_bytes(-1, 1, 8) == 0
+    assert lib.gdn_prefill_workspace_bytes(1, 1, 0) == 0
+
+
+def test_c_side_validation_rejects_before_launching():
+    lib = _lib.get_prefill_lib()
+    n = [None] * 8
+    f = ctypes.c_float(0.1)
+
+    def call(L=6, N=1, H=4, HV=8, K=128, V=128, ws=None, ws_size=0, cu=None, new_state=None):
+        return lib.gdn_prefill(*n, cu, f, None, new_state, L, N, H, HV, K, V, 0, ws, ws_size, None)
+
+    assert call(N=0) == 0                     # nothing to do
+    assert call(K=64) == 1
+    assert call(H=3) == 1                     # 8 % 3 != 0
+    assert call(L=-1) == 1
+    assert call() == 1                        # null pointers
+    if not torch.cuda.is_available():         # made-up pointers only where no device exists
+        assert call(cu=0x1000, new_state=0x2000, ws=0x3000, ws_size=10) == 1   # short workspace
+
+
+def _cpu_inputs():
+    return make_prefill_inputs([3, 2], 4, 8, seed=0)
+
+
+def test_python_validation():
+    t = _cpu_inputs()
+    with pytest.raises(ValueError, match="HIP device"):
+        check_prefill_inputs(**{k: v for k, v in t.items() if k != "scale"})
+    bad = dict(t, q=t["q"].float())
+    with pytest.raises(TypeError):
+        check_prefill_inputs(**{k: v for k, v in bad.items() if k != "scale"})
+    bad = dict(t, v=t["v"][:, :6].contiguous())                   # 6 % 4 != 0
+    with pytest.raises(ValueError, match="multiple"):
+        check_prefill_inputs(**{k: v for k, v in bad.items() if k != "scale"})
+    bad = dict(t, state=t["state"][:1].contiguous())                # N mismatch
+    with pytest.raises(ValueError, match="state"):
+        check_prefill_inputs(**{k: v for k, v in bad.items() if k != "scale"})
+    bad = dict(t, cu_seqlens=t["cu_seqlens"].float())
+    with pytest.raises(TypeError, match="cu_seqlens"):
+        check_prefill_inputs(**{k: v for k, v in bad.items() if k != "scale"})
+    bad = dict(t, a=t["a"].unsqueeze(1))
+    with pytest.raises(ValueError, match="a must have shape"):
+        check_prefill_inputs(**{k: v for k, v in bad.items() if k != "scale"})
+
+
+def test_entry_points_are_registered_like_the_reference():
+    assert gdn.ENTRY_POINTS["prefill-hip"] is gdn.kernel_prefill_hip
+    assert gdn.ENTRY_POINTS["prefill-hip-run"] is gdn.prefill_run
+    assert "prefill-hip-run" in gdn.NO_DPS and "prefill-hip" not in gdn.NO_DPS
+    with pytest.raises(ValueError):
+        gdn.prefill_run(**_cpu_inputs())      # CPU tensors: no CPU path
