@@ -30,7 +30,15 @@ def test_signatures_match_reference_names():
         REF_ARGS + ["output", "new_state"])
     assert gdn.ENTRY_POINTS["hip"] is gdn.kernel_hip
     assert gdn.ENTRY_POINTS["hip-run"] is gdn.run
-    assert gdn.NO_DPS == {"hip-run"}
+    assert gdn.NO_DPS == {"hip-run", "prefill-hip-run"}
+    # prefill: kernel_prefill_reference / kernel_prefill_fla_chunk argument names
+    # (solution/triton/prefill_kernel.py:10-12, 85-87)
+    pref = REF_ARGS[:8] + ["cu_seqlens", "scale"]
+    p = inspect.signature(gdn.prefill_run).parameters
+    assert [n for n, x in p.items() if x.kind is x.POSITIONAL_OR_KEYWORD] == pref
+    p = inspect.signature(gdn.kernel_prefill_hip).parameters
+    assert [n for n, x in p.items() if x.kind is x.POSITIONAL_OR_KEYWORD] == (
+        pref + ["output", "new_state"])
 
 
 @pytest.mark.parametrize("scale,expect", [
