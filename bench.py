@@ -365,6 +365,77 @@ def traffic_floor(device, iters: int):
     return out
 
 
+# Prefill workloads: name -> (sequence lengths, H, HV).  The reference's
+# prefill workload 0 is one 6-token sequence (findings/research.md:1029).
+PREFILL_CONFIGS = {
+    "prefill_qk4_v8_1x6": ([6], 4, 8),
+    "prefill_qk4_v8_1x16384": ([16384], 4, 8),
+    "prefill_qk4_v8_16x1024": ([1024] * 16, 4, 8),
+    "prefill_qk16_v32_1x8192": ([8192], 16, 32),
+    "prefill_qk16_v32_64x512": ([512] * 64, 16, 32),
+}
+# Algorithmic flops of the chunkwise prefill per (64-token chunk, v-head):
+# K K^T and Q K^T (2 x 64x64x128), W and U (2 x 64x64x128), Delta = U - W S,
+# Q S and K^T Delta (3 x 64x128x128), P Delta (64x64x128); multiply-adds x 2.
+PREFILL_FLOP_PER_CHUNK_HEAD = 2 * (4 * 64 * 64 * 128 + 3 * 64 * 128 * 128 + 64 * 64 * 128)
+
+
+def prefill_bytes(lens, H, HV) -> int:
+    """Unique HBM bytes of one prefill: q, k, v, output, a, b per token,
+    state read and written per sequence, A_log, dt_bias, cu_seqlens."""
+    L, N = sum(lens), len(lens)
+    return (L * (2 * H * 128 * 2 + 2 * HV * 128 * 2 + 2 * HV * 2)
+            + N * HV * 128 * 128 * 4 * 2 + 2 * HV * 4 + (N + 1) * 4)
+
+
+def prefill_bench(device, iters: int = 20):
+    """Per prefill workload: median time of the whole prefill (its three
+    launches) from HIP event markers on the launch stream, algorithmic
+    TFLOP/s and GB/s.  Inputs: unit-norm q/k rows (the model's
+    normalisation), the decode benchmark's other distributions."""
+    out = {}
+    for name, (lens, H, HV) in PREFILL_CONFIGS.items():
+        L, N = sum(lens), len(lens)
+        g = torch.Generator(device=device).manual_seed(17)
+        f = dict(device=device)
+        q = torch.randn(L, H, 128, generator=g, **f)
+        k = torch.randn(L, H, 128, generator=g, **f)
+        t = dict(q=(q / q.norm(dim=-1, keepdim=True)).to(torch.bfloat16),
+                 k=(k / k.norm(dim=-1, keepdim=True)).to(torch.bfloat16),
+                 v=torch.randn(L, HV, 128, generator=g, **f).to(torch.bfloat16),
+                 state=torch.randn(N, HV, 128, 128, generator=g, **f).mul_(0.05),
+                 A_log=torch.log(torch.rand(HV, generator=g, **f) * 15.0 + 1.0),
+                 a=torch.randn(L, HV, generator=g, **f).to(torch.bfloat16),
+                 dt_bias=torch.rand(HV, generator=g, **f) * 2.0 - 1.0,
+                 b=torch.randn(L, HV, generator=g, **f).to(torch.bfloat16),
+                 scale=1.0 / math.sqrt(128))
+        cu = torch.zeros(N + 1, dtype=torch.int32)
+        cu[1:] = torch.cumsum(torch.tensor(lens), 0)
+        t["cu_seqlens"] = cu.to(device)
+        t["output"] = torch.empty(L, HV, 128, dtype=torch.bfloat16, **f)
+        t["new_state"] = torch.empty_like(t["state"])
+        for _ in range(3):
+            gdn.kernel_prefill_hip(**t)
+        stream = torch.cuda.current_stream()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(iters)]
+        for a_, b_ in ev:
+            a_.record(stream)
+            gdn.kernel_prefill_hip(**t)
+            b_.record(stream)
+        torch.cuda.synchronize()
+        us = statistics.median(a_.elapsed_time(b_) * 1e3 for a_, b_ in ev)
+        chunks = sum((n + 63) // 64 for n in lens)
+        flop = chunks * HV * PREFILL_FLOP_PER_CHUNK_HEAD
+        nb = prefill_bytes(lens, H, HV)
+        out[name] = {"seqs": N, "tokens": L, "H": H, "HV": HV, "us": round(us, 2),
+                     "tflops": round(flop / (us * 1e-6) / 1e12, 2),
+                     "gbs": round(nb / (us * 1e-6) / 1e9, 1),
+                     "tokens_per_s": round(L / (us * 1e-6), 1)}
+        del t
+    return out
+
+
 def pmc_pass(device):
     """Short run for rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE): three
     plain 256 MiB copies (calibrate the counters against known bytes), then
@@ -399,6 +470,9 @@ def main():
     ap.add_argument("--iters", type=int, default=100,
                     help="launches per per-config kernel-time measurement")
     ap.add_argument("--pmc-pass", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="time the prefill workloads only and print them as JSON")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -412,6 +486,9 @@ def main():
     _lib.get_lib()
     if args.pmc_pass:
         pmc_pass(device)
+        return
+    if args.prefill_only:
+        print(json.dumps({"prefill": prefill_bench(device)}), flush=True)
         return
 
     log = lambda *a: print(*a, file=sys.stderr, flush=True)  # noqa: E731
@@ -474,6 +551,12 @@ def main():
         f"empty kernel {floor['empty_us']} us; B=256 state RMW {floor['b256_rmw_us']} us "
         f"({floor['b256_rmw_gbs']} GB/s)")
 
+    prefill = {}
+    if not args.no_prefill:
+        prefill = prefill_bench(device)
+        for name, r in prefill.items():
+            log(f"[bench] {name}: {r['us']} us, {r['tflops']} TFLOP/s, {r['gbs']} GB/s")
+
     serving = b1_serving(device)
     log(f"[bench] B=1 serving, {serving['layers']} layer steps: eager "
         f"{serving['eager_us_per_step']} us/step, HIP graph {serving['graph_us_per_step']} us/step")
@@ -526,6 +609,7 @@ def main():
         },
         "cpu_baseline": cpu,
         "per_config": per_config,
+        "prefill": prefill,
     }
     print(json.dumps(line), flush=True)
 

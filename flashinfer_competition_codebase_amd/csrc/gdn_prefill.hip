@@ -27,7 +27,8 @@
 //      W and U (fp32 MFMA) -- into a workspace slot per (chunk, v-head).
 //   3. scan, grid (N, HV, 128/16): the sequential part, per sequence, v-head
 //      and 16-column slice of the state: Delta, O and S_C chunk after chunk
-//      (fp32 MFMA), the state slice kept in registers.
+//      (bf16 MFMA on hi/lo-split fp32 operands), the state slice kept in
+//      registers and the next chunk's operands loaded while this one runs.
 //
 // MFMA lane layouts (v_mfma_f32_16x16x4_f32, v_mfma_f32_16x16x16_bf16):
 // A[i][k] from lane i + 16 g, B[k][j] from lane j + 16 g (k = g for fp32,
@@ -54,26 +55,67 @@ constexpr float kL2Eps = 1e-6f;
 constexpr float kSoftplusThreshold = 20.0f;
 constexpr float kLn2 = 0.693147180559945309f;
 
-// Workspace slot of one (chunk, v-head), in floats.
-constexpr int kSlotW = 0;                          // W [64][128]
-constexpr int kSlotU = kSlotW + kChunk * kDim;     // U [64][128]
-constexpr int kSlotP = kSlotU + kChunk * kDim;     // scale * rq_i rk_j M_ij (Q K^T)_ij [64][64]
-constexpr int kSlotQs = kSlotP + kChunk * kChunk;  // scale * rq_i e^gamma_i [64]
-constexpr int kSlotKs = kSlotQs + kChunk;          // rk_i e^(gamma_C - gamma_i) [64]
-constexpr int kSlotGl = kSlotKs + kChunk;          // e^gamma_C [1], padded to 64
-constexpr int kSlotFloats = kSlotGl + 64;
+// Workspace slot of one (chunk, v-head), offsets in floats.  The scan's MFMA
+// A operands (W, P, K^T and a copy of Q) are stored in operand order: a
+// 16 x 16 block of an A operand is 64 lanes x 4 bf16 contiguous (lane =
+// row + 16 (col / 4), item = col % 4), so each scan load instruction reads
+// 512 contiguous bytes.  fp32 operands are split into a bf16 high and low
+// part (x ~ hi + lo to ~2^-16 relative).  U is stored in the MFMA result
+// order the scan consumes (per 16 x 16 block, lane-major 4 floats).
+constexpr int kBlk = 256;                             // bf16 per 16 x 16 operand block
+constexpr int kSlotWh = 0;                            // W hi: blocks (row blk 0..3, k blk 0..7)
+constexpr int kSlotWl = kSlotWh + 32 * kBlk / 2;      // W lo
+constexpr int kSlotU = kSlotWl + 32 * kBlk / 2;       // U: blocks (row blk 0..3, col blk 0..7)
+constexpr int kSlotPh = kSlotU + kChunk * kDim;       // P hi: blocks (row blk 0..3, j blk 0..3),
+constexpr int kSlotPl = kSlotPh + 16 * kBlk / 2;      //   P = scale rq_i rk_j M_ij (Q K^T)_ij; lo
+constexpr int kSlotQs = kSlotPl + 16 * kBlk / 2;      // scale * rq_i e^gamma_i [64]
+constexpr int kSlotKs = kSlotQs + kChunk;             // rk_i e^(gamma_C - gamma_i) [64]
+constexpr int kSlotGl = kSlotKs + kChunk;             // e^gamma_C [1], padded to 64
+constexpr int kSlotKt = kSlotGl + 64;                 // K^T: blocks (key blk 0..7, token blk 0..3)
+constexpr int kSlotQ = kSlotKt + 32 * kBlk / 2;       // Q: blocks (token blk 0..3, k blk 0..7)
+constexpr int kSlotFloats = kSlotQ + 32 * kBlk / 2;
 static_assert(kSlotFloats % 64 == 0, "slots stay 256-byte aligned");
+
+// Offset (bf16 units) of A-operand element (r, c) inside its 16 x 16 block.
+__host__ __device__ constexpr int blk_off(int r, int c) {
+  return ((r & 15) + 16 * ((c & 15) >> 2)) * 4 + (c & 3);
+}
 
 // LDS row strides (elements) chosen so MFMA operand reads spread over banks.
 constexpr int kBfStride = kDim + 8;       // bf16 rows of 128
 constexpr int kF64Stride = kChunk + 4;    // fp32 rows of 64
-constexpr int kF16Stride = kVT + 4;       // fp32 rows of 16
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 __device__ __forceinline__ uint16_t f32_to_bf16(float x) {
   return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));  // round to nearest even
+}
+
+// x ~ hi + lo with hi = bf16(x), lo = bf16(x - hi).
+__device__ __forceinline__ void split_bf16(float x, uint16_t& hi, uint16_t& lo) {
+  hi = f32_to_bf16(x);
+  lo = f32_to_bf16(x - bf16_to_f32(hi));
+}
+
+__device__ __forceinline__ void split4(const f32x4& x, s16x4& hi, s16x4& lo) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    uint16_t h, l;
+    split_bf16(x[e], h, l);
+    hi[e] = static_cast<short>(h);
+    lo[e] = static_cast<short>(l);
+  }
+}
+
+// Workgroup barrier that orders LDS only.  The waves of these kernels
+// exchange data through LDS alone, so global loads issued ahead of a barrier
+// (the next chunk's operands) stay in flight across it instead of being
+// drained as __syncthreads' all-memory fence would.
+__device__ __forceinline__ void block_sync_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 __device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) {
@@ -219,7 +261,7 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
     lds.gamma[lane] = g;
     lds.beta[lane] = beta;
   }
-  __syncthreads();
+  block_sync_lds();
 
   // Row scales of the L2-norm (1 when off): 4 threads per row.
   {
@@ -243,9 +285,10 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
       lds.rk[r] = p.l2norm ? __builtin_amdgcn_rsqf(sk + kL2Eps) : 1.0f;
     }
   }
-  __syncthreads();
+  block_sync_lds();
 
   float* slot = p.slots + (static_cast<size_t>(c) * p.HV + hv) * kSlotFloats;
+  uint16_t* slot16 = reinterpret_cast<uint16_t*>(slot);
   const int col = lane & 15;
   const int g4 = lane >> 4;
 
@@ -283,11 +326,15 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
         const float dec = j <= i ? __expf(gi - gj) : 0.0f;   // exponent <= 0
         const float a = j < i ? lds.beta[i] * dec * lds.rk[i] * rkj * kk[nj][e] : 0.0f;
         lds.A[i * kF64Stride + j] = a;
-        slot[kSlotP + i * kChunk + j] = p.scale * lds.rq[i] * rkj * dec * qk[nj][e];
+        uint16_t ph, pl;
+        split_bf16(p.scale * lds.rq[i] * rkj * dec * qk[nj][e], ph, pl);
+        const int po = (wave * 4 + nj) * kBlk + blk_off(i, j);
+        slot16[2 * kSlotPh + po] = ph;
+        slot16[2 * kSlotPl + po] = pl;
       }
     }
   }
-  __syncthreads();
+  block_sync_lds();
 
   // T = (I + A)^-1 by forward substitution, one column per lane of wave 0:
   // T[i][c] = delta_ic - sum_{j<i} A[i][j] T[j][c].
@@ -302,7 +349,7 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
       lds.T[i * kF64Stride + lane] = acc;
     }
   }
-  __syncthreads();
+  block_sync_lds();
 
   // W = T diag(beta e^gamma rk) K and U = T diag(beta) V, row block `wave`
   // (T is lower triangular: inner index j < 16 (wave + 1)), fp32 MFMA.
@@ -332,9 +379,13 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int i = wave * 16 + g4 * 4 + e;
-        slot[kSlotW + i * kDim + nj * 16 + col] = w[nj][e];
-        slot[kSlotU + i * kDim + nj * 16 + col] = u[nj][e];
+        uint16_t wh, wl;
+        split_bf16(w[nj][e], wh, wl);
+        const int wo = (wave * 8 + nj) * kBlk + blk_off(i, col);
+        slot16[2 * kSlotWh + wo] = wh;
+        slot16[2 * kSlotWl + wo] = wl;
       }
+      *reinterpret_cast<f32x4*>(slot + kSlotU + ((wave * 8 + nj) * 64 + lane) * 4) = u[nj];
     }
   }
 
@@ -346,17 +397,104 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
     slot[kSlotKs + lane] = lds.rk[lane] * __expf(gl - gi);
     slot[kSlotGl + lane] = __expf(gl);
   }
+
+  // K^T (A operand of the scan's state update: rows = key index, inner =
+  // token) and Q (A operand of Q S: rows = token, inner = key index), in
+  // operand order, 8 bytes per store; rows past the chunk's end are zero.
+  for (int idx = threadIdx.x; idx < kDim * (kChunk / 4); idx += kThreads) {
+    const int kc = idx >> 4;                 // key index 0..127
+    const int i0 = (idx & 15) * 4;           // first of 4 tokens
+    s16x4 v4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v4[e] = static_cast<short>(lds.K[(i0 + e) * kBfStride + kc]);
+    *reinterpret_cast<s16x4*>(slot16 + 2 * kSlotKt + ((kc >> 4) * 4 + (i0 >> 4)) * kBlk +
+                              blk_off(kc, i0)) = v4;
+  }
+  for (int idx = threadIdx.x; idx < kChunk * (kDim / 4); idx += kThreads) {
+    const int i = idx >> 5;                  // token 0..63
+    const int k0 = (idx & 31) * 4;           // first of 4 key indices
+    const s16x4 v4 = *reinterpret_cast<const s16x4*>(&lds.Q[i * kBfStride + k0]);
+    *reinterpret_cast<s16x4*>(slot16 + 2 * kSlotQ + ((i >> 4) * 8 + (k0 >> 4)) * kBlk +
+                              blk_off(i, k0)) = v4;
+  }
 }
 
 // ---------------------------------------------------------------------------
 // 3. sequential scan over the chunks of a sequence
 // ---------------------------------------------------------------------------
+// Every product is a bf16 MFMA (16x16x16); fp32 operands enter split into
+// hi + lo and a product x y is hi_x hi_y + hi_x lo_y + lo_x hi_y (the lo lo
+// term is ~2^-16 relative and dropped); q and k are bf16 already.  The state
+// slice and Delta are split once per chunk by the wave that owns them and
+// kept transposed in LDS, so every B operand is one 8-byte read.
+constexpr int kStStride = kDim + 8;     // S^T rows ([col][k]), bf16
+constexpr int kDtStride = kChunk + 8;   // Delta^T and K^T rows, bf16
+
 struct ScanLds {
-  uint16_t K[kChunk * kBfStride];     // K rows of the chunk
-  float S[kDim * kF16Stride];         // state slice S[k][v] at the chunk start
-  float D[kChunk * kF16Stride];       // Delta [64][16]
-  float ks[kChunk];
+  uint16_t Sh[kVT * kStStride];      // state slice^T at the chunk start, hi
+  uint16_t Sl[kVT * kStStride];      //   lo
+  uint16_t Dh[kVT * kDtStride];      // Delta^T [col][i], hi
+  uint16_t Dl[kVT * kDtStride];      //   lo
+  uint16_t Eh[kVT * kDtStride];      // (ks (.) Delta)^T, hi
+  uint16_t El[kVT * kDtStride];      //   lo
 };
+
+// Per-lane operands of one chunk, loaded ahead of use.
+struct ScanOps {
+  s16x4 wh[8], wl[8];   // W rows 16 wave + (lane % 16), k = 16 m + 4 g .. +3
+  s16x4 q[8];           // Q rows (the slot's copy), same k
+  s16x4 ph[4], pl[4];   // P rows, i = 16 m + 4 g .. +3
+  f32x4 u;              // U rows 16 wave + 4 g + e, column v0 + lane % 16
+  f32x4 qs, ks;         // row scales of the same rows
+  float gl;             // chunk decay e^gamma_C
+  s16x4 kt[2][4];       // K^T rows 32 wave + 16 t + lane % 16, tokens 16 m + 4 g .. +3
+};
+
+__device__ __forceinline__ s16x4 ld_s16x4(const uint16_t* ptr) {
+  return *reinterpret_cast<const s16x4*>(ptr);
+}
+
+// Loads of one chunk's operands from its workspace slot.  Every load is
+// unconditional and in straight-line code so that the compiler can count the
+// loads in flight and wait only for the ones a use needs (a load under a
+// branch makes it drain every outstanding load); all of them are 512-byte
+// (or 1 KiB) contiguous wave accesses in the slot's operand order.
+__device__ __forceinline__ void load_w_q_u(const float* slot, int vt, int wave, int lane,
+                                           int g4, ScanOps& o) {
+  const uint16_t* slot16 = reinterpret_cast<const uint16_t*>(slot);
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    const int bo = (wave * 8 + m) * kBlk + lane * 4;
+    o.wh[m] = ld_s16x4(slot16 + 2 * kSlotWh + bo);
+    o.wl[m] = ld_s16x4(slot16 + 2 * kSlotWl + bo);
+    o.q[m] = ld_s16x4(slot16 + 2 * kSlotQ + bo);
+  }
+  o.u = *reinterpret_cast<const f32x4*>(slot + kSlotU + ((wave * 8 + vt) * 64 + lane) * 4);
+  o.ks = *reinterpret_cast<const f32x4*>(slot + kSlotKs + wave * 16 + g4 * 4);
+}
+
+__device__ __forceinline__ void load_p_qs(const float* slot, int wave, int lane, int g4,
+                                          ScanOps& o) {
+  const uint16_t* slot16 = reinterpret_cast<const uint16_t*>(slot);
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int bo = (wave * 4 + m) * kBlk + lane * 4;
+    o.ph[m] = ld_s16x4(slot16 + 2 * kSlotPh + bo);
+    o.pl[m] = ld_s16x4(slot16 + 2 * kSlotPl + bo);
+  }
+  o.qs = *reinterpret_cast<const f32x4*>(slot + kSlotQs + wave * 16 + g4 * 4);
+  o.gl = slot[kSlotGl];
+}
+
+__device__ __forceinline__ void load_kt(const float* slot, int wave, int lane, ScanOps& o) {
+  const uint16_t* slot16 = reinterpret_cast<const uint16_t*>(slot);
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+      o.kt[t][m] = ld_s16x4(slot16 + 2 * kSlotKt + ((wave * 2 + t) * 4 + m) * kBlk + lane * 4);
+  }
+}
 
 __global__ __launch_bounds__(kThreads) void scan_kernel(Params p) {
   __shared__ ScanLds lds;
@@ -367,15 +505,13 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Params p) {
   const int wave = threadIdx.x >> 6;
   const int col = lane & 15;
   const int g4 = lane >> 4;
-  const int h = hv / p.ratio;
   int start, end;
   seq_range(p, s, start, end);
 
   // This wave's two 16-row tiles of the state slice: rows k = 32 wave + 16 t
-  // + 4 g4 + e, column v0 + col.  k-last storage: 4 consecutive k are one
-  // 16-byte vector.
+  // + 4 g4 + e, column v0 + col (k-last storage: 4 consecutive k are one
+  // 16-byte vector).
   const size_t head = static_cast<size_t>(s) * p.HV + hv;
-  float* ns_base = p.new_state + head * kDim * kDim + static_cast<size_t>(v0 + col) * kDim;
   f32x4 st[2];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
@@ -389,94 +525,122 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Params p) {
   // Chunk count from the slot offsets (never more than the range holds, and
   // never more slots than the workspace has, whatever cu_seqlens contains).
   const int nchunks = p.offs[s + 1] - p.offs[s];
+  const float* slot_base = p.slots + (static_cast<size_t>(p.offs[s]) * p.HV + hv) * kSlotFloats;
+  const size_t slot_step = static_cast<size_t>(p.HV) * kSlotFloats;
+
+  float* ns_base = p.new_state + head * kDim * kDim + static_cast<size_t>(v0 + col) * kDim;
+  if (nchunks <= 0) {                 // no tokens: zeros, as the reference
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      *reinterpret_cast<f32x4*>(ns_base + wave * 32 + t * 16 + g4 * 4) = f32x4{0, 0, 0, 0};
+    return;
+  }
+
+  ScanOps op;
+  load_kt(slot_base, wave, lane, op);
+  load_w_q_u(slot_base, blockIdx.z, wave, lane, g4, op);
+  load_p_qs(slot_base, wave, lane, g4, op);
+
   for (int ci = 0; ci < nchunks; ++ci) {
     const int t0 = start + ci * kChunk;
     const int n = min(kChunk, end - t0);
-    const float* slot = p.slots + (static_cast<size_t>(p.offs[s] + ci) * p.HV + hv) * kSlotFloats;
+    // operands of the next chunk, or of this one again after the last
+    const int cn = ci + 1 < nchunks ? ci + 1 : ci;
+    const float* slot_next = slot_base + cn * slot_step;
 
-    // state slice and K rows into LDS
+    // A. state slice (split) into LDS.  No barrier is needed before these
+    // writes: the previous chunk's reads of Sh / Sl (step B) precede its
+    // second barrier.
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        lds.S[(wave * 32 + t * 16 + g4 * 4 + e) * kF16Stride + col] = st[t][e];
+      s16x4 hi, lo;
+      split4(st[t], hi, lo);
+      const int k0 = wave * 32 + t * 16 + g4 * 4;
+      *reinterpret_cast<s16x4*>(&lds.Sh[col * kStStride + k0]) = hi;
+      *reinterpret_cast<s16x4*>(&lds.Sl[col * kStStride + k0]) = lo;
     }
-    stage_rows_bf16(lds.K, p.k + (static_cast<size_t>(t0) * p.H + h) * kDim,
-                    static_cast<size_t>(p.H) * kDim, n);
-    if (threadIdx.x < kChunk) lds.ks[threadIdx.x] = slot[kSlotKs + threadIdx.x];
-    __syncthreads();
+    block_sync_lds();
 
-    // Delta rows 16 wave .. +15 = U - W S;  O rows = Qs Q S (+ P Delta below)
-    const int ra = wave * 16 + col;                // A-operand row of this lane
-    const bool row_ok = ra < n;
-    const float qs = slot[kSlotQs + ra];
-    const uint16_t* qrow = p.q + ((static_cast<size_t>(t0) + (row_ok ? ra : 0)) * p.H + h) * kDim;
-    f32x4 ws = {0, 0, 0, 0};
-    f32x4 qsacc = {0, 0, 0, 0};
-#pragma unroll 4
-    for (int m = 0; m < kDim / 16; ++m) {
-      // inner index k = 16 m + 4 g4 + e for step e: one 16-byte W load and
-      // one 8-byte Q load per lane per m
+    // B. Delta rows 16 wave .. +15 = U - W S, and Q S for the output rows
+    // two accumulators per product halve the dependent MFMA chains
+    f32x4 ws0 = {0, 0, 0, 0}, ws1 = {0, 0, 0, 0};
+    f32x4 qs0 = {0, 0, 0, 0}, qs1 = {0, 0, 0, 0};
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
       const int kb = m * 16 + g4 * 4;
-      const f32x4 wv = *reinterpret_cast<const f32x4*>(slot + kSlotW + ra * kDim + kb);
-      u32x2 qv = {0u, 0u};
-      if (row_ok) qv = *reinterpret_cast<const u32x2*>(qrow + kb);
-      const float qf[4] = {bf16_to_f32(static_cast<uint16_t>(qv.x & 0xffffu)),
-                           bf16_to_f32(static_cast<uint16_t>(qv.x >> 16)),
-                           bf16_to_f32(static_cast<uint16_t>(qv.y & 0xffffu)),
-                           bf16_to_f32(static_cast<uint16_t>(qv.y >> 16))};
+      const s16x4 sh = ld_s16x4(&lds.Sh[col * kStStride + kb]);
+      const s16x4 sl = ld_s16x4(&lds.Sl[col * kStStride + kb]);
+      ws0 = mfma_bf16(op.wh[m], sh, ws0);
+      ws1 = mfma_bf16(op.wh[m], sl, ws1);
+      ws0 = mfma_bf16(op.wl[m], sh, ws0);
+      qs0 = mfma_bf16(op.q[m], sh, qs0);
+      qs1 = mfma_bf16(op.q[m], sl, qs1);
+    }
+    const f32x4 ws = ws0 + ws1;
+    const f32x4 qsum = qs0 + qs1;
+    {
+      f32x4 d, dk;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float sb = lds.S[(kb + e) * kF16Stride + col];
-        ws = mfma_f32(wv[e], sb, ws);
-        qsacc = mfma_f32(qs * qf[e], sb, qsacc);
+        d[e] = op.u[e] - ws[e];
+        dk[e] = op.ks[e] * d[e];
       }
+      s16x4 hi, lo;
+      const int i0 = wave * 16 + g4 * 4;
+      split4(d, hi, lo);
+      *reinterpret_cast<s16x4*>(&lds.Dh[col * kDtStride + i0]) = hi;
+      *reinterpret_cast<s16x4*>(&lds.Dl[col * kDtStride + i0]) = lo;
+      split4(dk, hi, lo);
+      *reinterpret_cast<s16x4*>(&lds.Eh[col * kDtStride + i0]) = hi;
+      *reinterpret_cast<s16x4*>(&lds.El[col * kDtStride + i0]) = lo;
     }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = wave * 16 + g4 * 4 + e;
-      lds.D[i * kF16Stride + col] = slot[kSlotU + i * kDim + v0 + col] - ws[e];
-    }
-    __syncthreads();
+    load_w_q_u(slot_next, blockIdx.z, wave, lane, g4, op);
+    block_sync_lds();
 
-    // O rows += P Delta; store
+    // C. output rows: qs (.) (Q S) + P Delta
     {
-      f32x4 o = qsacc;
-#pragma unroll 4
-      for (int m = 0; m < kChunk / 16; ++m) {
-        const int kb = m * 16 + g4 * 4;
-        const f32x4 pv = *reinterpret_cast<const f32x4*>(slot + kSlotP + ra * kChunk + kb);
+      f32x4 pd0 = {0, 0, 0, 0}, pd1 = {0, 0, 0, 0};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o = mfma_f32(pv[e], lds.D[(kb + e) * kF16Stride + col], o);
+      for (int m = 0; m < 4; ++m) {
+        const int ib = m * 16 + g4 * 4;
+        const s16x4 dh = ld_s16x4(&lds.Dh[col * kDtStride + ib]);
+        const s16x4 dl = ld_s16x4(&lds.Dl[col * kDtStride + ib]);
+        pd0 = mfma_bf16(op.ph[m], dh, pd0);
+        pd1 = mfma_bf16(op.ph[m], dl, pd1);
+        pd0 = mfma_bf16(op.pl[m], dh, pd0);
       }
+      const f32x4 pd = pd0 + pd1;
+      uint16_t ob[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ob[e] = f32_to_bf16(fmaf(op.qs[e], qsum[e], pd[e]));
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int i = wave * 16 + g4 * 4 + e;
-        if (i < n)
-          p.out[((static_cast<size_t>(t0) + i) * p.HV + hv) * kDim + v0 + col] = f32_to_bf16(o[e]);
+        if (i < n) p.out[((static_cast<size_t>(t0) + i) * p.HV + hv) * kDim + v0 + col] = ob[e];
       }
     }
 
-    // S rows 32 wave .. +31: S = e^gamma_C S + (ks (.) K)^T Delta
-    {
-      const float gl = slot[kSlotGl];
+    // D. state rows 32 wave .. +31: S = e^gamma_C S + K^T (ks (.) Delta)
+    const float gl = op.gl;
+    s16x4 kt[2][4];
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        f32x4 acc = st[t] * gl;
-        const int kr = wave * 32 + t * 16 + col;   // A-operand row (state row k)
-#pragma unroll 4
-        for (int m = 0; m < kChunk / 16; ++m) {
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int i = m * 16 + g4 * 4 + e;
-            const float ak = lds.ks[i] * bf16_to_f32(lds.K[i * kBfStride + kr]);
-            acc = mfma_f32(ak, lds.D[i * kF16Stride + col], acc);
-          }
-        }
-        st[t] = acc;
+      for (int m = 0; m < 4; ++m) kt[t][m] = op.kt[t][m];
+    load_p_qs(slot_next, wave, lane, g4, op);
+    load_kt(slot_next, wave, lane, op);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      f32x4 acc0 = st[t] * gl;
+      f32x4 acc1 = {0, 0, 0, 0};
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int ib = m * 16 + g4 * 4;
+        acc0 = mfma_bf16(kt[t][m], ld_s16x4(&lds.Eh[col * kDtStride + ib]), acc0);
+        acc1 = mfma_bf16(kt[t][m], ld_s16x4(&lds.El[col * kDtStride + ib]), acc1);
       }
+      st[t] = acc0 + acc1;
     }
-    __syncthreads();   // LDS is rewritten by the next chunk
   }
 
 #pragma unroll

@@ -39,7 +39,7 @@ def test_header_and_library_agree():
 
 def test_workspace_size_formula():
     lib = _lib.get_prefill_lib()
-    slot = (2 * 64 * 128 + 64 * 64 + 3 * 64) * 4            # W, U, P, row scales
+    slot = (2 * 64 * 128 + 64 * 64 + 3 * 64) * 4 + 2 * 128 * 64 * 2  # W U P scales K^T Q
     for L, N, HV in ((6, 1, 8), (16384, 1, 8), (1000, 37, 32), (0, 3, 8)):
         chunks = (L + 63) // 64 + N
         offs = ((N + 1) * 4 + 255) // 256 * 256
