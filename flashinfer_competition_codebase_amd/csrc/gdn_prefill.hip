@@ -23,8 +23,9 @@
 //      of every sequence (token ranges clamped to [0, L]).
 //   2. prep, grid (chunk slots, HV): everything that does not depend on the
 //      state, for all chunks at once -- gates and gamma, K K^T and Q K^T
-//      (bf16 MFMA: the inputs are bf16), T by forward substitution (fp32),
-//      W and U (fp32 MFMA) -- into a workspace slot per (chunk, v-head).
+//      (bf16 MFMA: the inputs are bf16), T by block recursion (fp32 MFMA),
+//      W and U (bf16 MFMA on hi/lo-split T) -- into a workspace slot per
+//      (chunk, v-head), in the order the scan's MFMAs read it.
 //   3. scan, grid (N, HV, 128/16): the sequential part, per sequence, v-head
 //      and 16-column slice of the state: Delta, O and S_C chunk after chunk
 //      (bf16 MFMA on hi/lo-split fp32 operands), the state slice kept in
@@ -216,17 +217,36 @@ __device__ __forceinline__ void stage_rows_bf16(uint16_t* dst, const uint16_t* b
 // ---------------------------------------------------------------------------
 // 2. per-chunk preparation
 // ---------------------------------------------------------------------------
+constexpr int kXStride = 32 + 4;          // fp32 rows of the 32-wide scratch
+
 struct PrepLds {
   uint16_t K[kChunk * kBfStride];
-  uint16_t Q[kChunk * kBfStride];
   uint16_t V[kChunk * kBfStride];
   float A[kChunk * kF64Stride];   // strict lower part of (I + A) minus I
   float T[kChunk * kF64Stride];   // (I + A)^-1
+  float X[32 * kXStride];         // block products of the inverse
   float gamma[kChunk];
   float beta[kChunk];
   float rq[kChunk];
   float rk[kChunk];
 };
+
+// 16 x 16 x 16 fp32 block product A[0:16, 0:16] B[0:16, 0:16] from LDS rows
+// of stride lda / ldb, as an MFMA result (lane (col, g) holds rows 4 g + e).
+__device__ __forceinline__ f32x4 mm16_f32(const float* A, int lda, const float* B, int ldb,
+                                          int col, int g4) {
+  f32x4 acc = {0, 0, 0, 0};
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+    acc = mfma_f32(A[col * lda + 4 * ks + g4], B[(4 * ks + g4) * ldb + col], acc);
+  return acc;
+}
+
+__device__ __forceinline__ void store16(float* D, int ldd, const f32x4& v, float sign, int col,
+                                        int g4) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) D[(4 * g4 + e) * ldd + col] = sign * v[e];
+}
 
 __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
   __shared__ PrepLds lds;
@@ -242,13 +262,42 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
   const int h = hv / p.ratio;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const int col = lane & 15;
+  const int g4 = lane >> 4;
+  float* slot = p.slots + (static_cast<size_t>(c) * p.HV + hv) * kSlotFloats;
+  uint16_t* slot16 = reinterpret_cast<uint16_t*>(slot);
 
   stage_rows_bf16(lds.K, p.k + (static_cast<size_t>(t0) * p.H + h) * kDim,
                   static_cast<size_t>(p.H) * kDim, n);
-  stage_rows_bf16(lds.Q, p.q + (static_cast<size_t>(t0) * p.H + h) * kDim,
-                  static_cast<size_t>(p.H) * kDim, n);
   stage_rows_bf16(lds.V, p.v + (static_cast<size_t>(t0) * p.HV + hv) * kDim,
                   static_cast<size_t>(p.HV) * kDim, n);
+  for (int idx = threadIdx.x; idx < kChunk * kF64Stride; idx += kThreads) lds.T[idx] = 0.0f;
+
+  // Q rows 16 wave + col straight into MFMA A-operand registers (k = 16 m +
+  // 4 g .. +3; rows past the chunk's end zero), which are also the scan's
+  // operand-ordered copy of Q; with the L2-norm, their row norms.
+  s16x4 qa[8];
+  {
+    const int ra = wave * 16 + col;
+    const bool row_ok = ra < n;
+    const uint16_t* qrow =
+        p.q + ((static_cast<size_t>(t0) + (row_ok ? ra : n - 1)) * p.H + h) * kDim;
+    float sq = 0.0f;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const s16x4 v = *reinterpret_cast<const s16x4*>(qrow + m * 16 + g4 * 4);
+      qa[m] = row_ok ? v : s16x4{0, 0, 0, 0};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x = bf16_to_f32(static_cast<uint16_t>(qa[m][e]));
+        sq = fmaf(x, x, sq);
+      }
+      *reinterpret_cast<s16x4*>(slot16 + 2 * kSlotQ + (wave * 8 + m) * kBlk + lane * 4) = qa[m];
+    }
+    sq += __shfl_xor(sq, 16, 64);
+    sq += __shfl_xor(sq, 32, 64);
+    if (g4 == 0) lds.rq[ra] = p.l2norm ? __builtin_amdgcn_rsqf(sq + kL2Eps) : 1.0f;
+  }
   if (wave == 0) {
     float logg = 0.0f, beta = 0.0f;                // padded rows: no decay, no update
     if (lane < n) token_gates(p, t0 + lane, hv, logg, beta);
@@ -263,34 +312,22 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
   }
   block_sync_lds();
 
-  // Row scales of the L2-norm (1 when off): 4 threads per row.
+  // K row scales of the L2-norm (1 when off): 4 threads per row.
   {
     const int r = threadIdx.x >> 2;
     const int part = threadIdx.x & 3;
-    float sq = 0.0f, sk = 0.0f;
+    float sk = 0.0f;
     if (p.l2norm) {
       for (int i = part * 32; i < part * 32 + 32; ++i) {
-        const float x = bf16_to_f32(lds.Q[r * kBfStride + i]);
         const float y = bf16_to_f32(lds.K[r * kBfStride + i]);
-        sq = fmaf(x, x, sq);
         sk = fmaf(y, y, sk);
       }
-      sq += __shfl_xor(sq, 1, 64);
       sk += __shfl_xor(sk, 1, 64);
-      sq += __shfl_xor(sq, 2, 64);
       sk += __shfl_xor(sk, 2, 64);
     }
-    if (part == 0) {
-      lds.rq[r] = p.l2norm ? __builtin_amdgcn_rsqf(sq + kL2Eps) : 1.0f;
-      lds.rk[r] = p.l2norm ? __builtin_amdgcn_rsqf(sk + kL2Eps) : 1.0f;
-    }
+    if (part == 0) lds.rk[r] = p.l2norm ? __builtin_amdgcn_rsqf(sk + kL2Eps) : 1.0f;
   }
   block_sync_lds();
-
-  float* slot = p.slots + (static_cast<size_t>(c) * p.HV + hv) * kSlotFloats;
-  uint16_t* slot16 = reinterpret_cast<uint16_t*>(slot);
-  const int col = lane & 15;
-  const int g4 = lane >> 4;
 
   // K K^T and Q K^T for row block `wave` (rows 16 wave .. +15), all 4 column
   // blocks; bf16 MFMA over the 128-long rows.
@@ -306,12 +343,11 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
     for (int ks = 0; ks < kDim / 16; ++ks) {
       const int kk0 = ks * 16 + g4 * 4;
       const s16x4 ak = *reinterpret_cast<const s16x4*>(&lds.K[ra * kBfStride + kk0]);
-      const s16x4 aq = *reinterpret_cast<const s16x4*>(&lds.Q[ra * kBfStride + kk0]);
 #pragma unroll
       for (int nj = 0; nj < 4; ++nj) {
         const s16x4 bk = *reinterpret_cast<const s16x4*>(&lds.K[(nj * 16 + col) * kBfStride + kk0]);
         kk[nj] = mfma_bf16(ak, bk, kk[nj]);
-        qk[nj] = mfma_bf16(aq, bk, qk[nj]);
+        qk[nj] = mfma_bf16(qa[ks], bk, qk[nj]);
       }
     }
 #pragma unroll
@@ -336,56 +372,124 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
   }
   block_sync_lds();
 
-  // T = (I + A)^-1 by forward substitution, one column per lane of wave 0:
-  // T[i][c] = delta_ic - sum_{j<i} A[i][j] T[j][c].
-  if (wave == 0) {
-    float tc[kChunk];
+  // T = (I + A)^-1 by block recursion on 16 x 16 blocks (A is strictly lower
+  // triangular, so T is unit lower triangular; the upper blocks stay zero):
+  // 1. each wave inverts one diagonal block by forward substitution (one
+  //    column per lane, two partial sums per dot product);
+  if (lane < 16) {
+    const int b0 = wave * 16;
+    float t[16];
 #pragma unroll
-    for (int i = 0; i < kChunk; ++i) {
-      float acc = (i == lane) ? 1.0f : 0.0f;
+    for (int r = 0; r < 16; ++r) {
+      float s0 = (r == lane) ? 1.0f : 0.0f, s1 = 0.0f;
 #pragma unroll
-      for (int j = 0; j < i; ++j) acc = fmaf(-lds.A[i * kF64Stride + j], tc[j], acc);
-      tc[i] = acc;
-      lds.T[i * kF64Stride + lane] = acc;
+      for (int j = 0; j < r; ++j) {
+        const float aij = lds.A[(b0 + r) * kF64Stride + b0 + j];
+        if (j & 1) s1 = fmaf(-aij, t[j], s1); else s0 = fmaf(-aij, t[j], s0);
+      }
+      t[r] = s0 + s1;
+      lds.T[(b0 + r) * kF64Stride + b0 + lane] = t[r];
     }
   }
   block_sync_lds();
-
-  // W = T diag(beta e^gamma rk) K and U = T diag(beta) V, row block `wave`
-  // (T is lower triangular: inner index j < 16 (wave + 1)), fp32 MFMA.
+  // 2. the 32 x 32 diagonal halves: T_10 = -T_11 A_10 T_00 (wave 0) and
+  //    T_32 = -T_33 A_32 T_22 (wave 1), through LDS within the wave;
+  if (wave < 2) {
+    const int b = wave * 32;
+    float* Xw = lds.X + wave * 16 * kXStride;
+    const f32x4 x = mm16_f32(&lds.A[(b + 16) * kF64Stride + b], kF64Stride,
+                             &lds.T[b * kF64Stride + b], kF64Stride, col, g4);
+    store16(Xw, kXStride, x, 1.0f, col, g4);
+    const f32x4 y = mm16_f32(&lds.T[(b + 16) * kF64Stride + b + 16], kF64Stride, Xw, kXStride,
+                             col, g4);
+    store16(&lds.T[(b + 16) * kF64Stride + b], kF64Stride, y, -1.0f, col, g4);
+  }
+  block_sync_lds();
+  // 3. the lower-left 32 x 32 quarter: T_BA = -T_B (A_BA T_A), one 16 x 16
+  //    tile per wave.
   {
-    const int ra = wave * 16 + col;
-    f32x4 w[8], u[8];
+    const int rb = wave >> 1, cb = wave & 1;
+    const float* Arow = &lds.A[(32 + 16 * rb) * kF64Stride];
+    const f32x4 x = mm16_f32(Arow, kF64Stride, &lds.T[16 * cb], kF64Stride, col, g4) +
+                    mm16_f32(Arow + 16, kF64Stride, &lds.T[16 * kF64Stride + 16 * cb],
+                             kF64Stride, col, g4);
+    store16(&lds.X[16 * rb * kXStride + 16 * cb], kXStride, x, 1.0f, col, g4);
+  }
+  block_sync_lds();
+  {
+    const int rb = wave >> 1, cb = wave & 1;
+    const float* Trow = &lds.T[(32 + 16 * rb) * kF64Stride + 32];
+    const f32x4 y = mm16_f32(Trow, kF64Stride, &lds.X[16 * cb], kXStride, col, g4) +
+                    mm16_f32(Trow + 16, kF64Stride, &lds.X[16 * kXStride + 16 * cb], kXStride,
+                             col, g4);
+    store16(&lds.T[(32 + 16 * rb) * kF64Stride + 16 * cb], kF64Stride, y, -1.0f, col, g4);
+  }
+  block_sync_lds();
+
+  // W = (T diag(beta e^gamma rk)) K and U = (T diag(beta)) V with bf16 MFMA:
+  // the scaled T is split into hi + lo, K and V are exact bf16.  Wave `wave`
+  // computes column tiles 2 wave and 2 wave + 1 for all row blocks (inner
+  // blocks kb <= rb: T is lower triangular).
+  {
+    f32x4 w[4][2], u[4][2];
 #pragma unroll
-    for (int nj = 0; nj < 8; ++nj) {
-      w[nj] = f32x4{0, 0, 0, 0};
-      u[nj] = f32x4{0, 0, 0, 0};
-    }
-    const int ksteps = 4 * (wave + 1);
-    for (int ks = 0; ks < ksteps; ++ks) {
-      const int j = ks * 4 + g4;
-      const float ta = lds.T[ra * kF64Stride + j];
-      const float xs = lds.beta[j] * __expf(lds.gamma[j]) * lds.rk[j];
-      const float ys = lds.beta[j];
+    for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-      for (int nj = 0; nj < 8; ++nj) {
-        const int cc = nj * 16 + col;
-        w[nj] = mfma_f32(ta, xs * bf16_to_f32(lds.K[j * kBfStride + cc]), w[nj]);
-        u[nj] = mfma_f32(ta, ys * bf16_to_f32(lds.V[j * kBfStride + cc]), u[nj]);
+      for (int q2 = 0; q2 < 2; ++q2) {
+        w[rb][q2] = f32x4{0, 0, 0, 0};
+        u[rb][q2] = f32x4{0, 0, 0, 0};
       }
-    }
 #pragma unroll
-    for (int nj = 0; nj < 8; ++nj) {
+    for (int kb = 0; kb < 4; ++kb) {
+      const int j0 = kb * 16 + g4 * 4;
+      s16x4 bk[2], bv[2];
+#pragma unroll
+      for (int q2 = 0; q2 < 2; ++q2) {
+        const int cc = (2 * wave + q2) * 16 + col;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          bk[q2][e] = static_cast<short>(lds.K[(j0 + e) * kBfStride + cc]);
+          bv[q2][e] = static_cast<short>(lds.V[(j0 + e) * kBfStride + cc]);
+        }
+      }
+      f32x4 xs, ys;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int i = wave * 16 + g4 * 4 + e;
-        uint16_t wh, wl;
-        split_bf16(w[nj][e], wh, wl);
-        const int wo = (wave * 8 + nj) * kBlk + blk_off(i, col);
-        slot16[2 * kSlotWh + wo] = wh;
-        slot16[2 * kSlotWl + wo] = wl;
+        const int j = j0 + e;
+        ys[e] = lds.beta[j];
+        xs[e] = ys[e] * __expf(lds.gamma[j]) * lds.rk[j];
       }
-      *reinterpret_cast<f32x4*>(slot + kSlotU + ((wave * 8 + nj) * 64 + lane) * 4) = u[nj];
+#pragma unroll
+      for (int rb = kb; rb < 4; ++rb) {
+        const f32x4 tv = *reinterpret_cast<const f32x4*>(&lds.T[(rb * 16 + col) * kF64Stride + j0]);
+        s16x4 awh, awl, auh, aul;
+        split4(tv * xs, awh, awl);
+        split4(tv * ys, auh, aul);
+#pragma unroll
+        for (int q2 = 0; q2 < 2; ++q2) {
+          w[rb][q2] = mfma_bf16(awh, bk[q2], w[rb][q2]);
+          w[rb][q2] = mfma_bf16(awl, bk[q2], w[rb][q2]);
+          u[rb][q2] = mfma_bf16(auh, bv[q2], u[rb][q2]);
+          u[rb][q2] = mfma_bf16(aul, bv[q2], u[rb][q2]);
+        }
+      }
+    }
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+      for (int q2 = 0; q2 < 2; ++q2) {
+        const int ct = 2 * wave + q2;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = rb * 16 + g4 * 4 + e;
+          uint16_t wh, wl;
+          split_bf16(w[rb][q2][e], wh, wl);
+          const int wo = (rb * 8 + ct) * kBlk + blk_off(i, col);
+          slot16[2 * kSlotWh + wo] = wh;
+          slot16[2 * kSlotWl + wo] = wl;
+        }
+        *reinterpret_cast<f32x4*>(slot + kSlotU + ((rb * 8 + ct) * 64 + lane) * 4) = u[rb][q2];
+      }
     }
   }
 
@@ -399,8 +503,8 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
   }
 
   // K^T (A operand of the scan's state update: rows = key index, inner =
-  // token) and Q (A operand of Q S: rows = token, inner = key index), in
-  // operand order, 8 bytes per store; rows past the chunk's end are zero.
+  // token), in operand order, 8 bytes per store; rows past the chunk's end
+  // are zero.
   for (int idx = threadIdx.x; idx < kDim * (kChunk / 4); idx += kThreads) {
     const int kc = idx >> 4;                 // key index 0..127
     const int i0 = (idx & 15) * 4;           // first of 4 tokens
@@ -409,13 +513,6 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
     for (int e = 0; e < 4; ++e) v4[e] = static_cast<short>(lds.K[(i0 + e) * kBfStride + kc]);
     *reinterpret_cast<s16x4*>(slot16 + 2 * kSlotKt + ((kc >> 4) * 4 + (i0 >> 4)) * kBlk +
                               blk_off(kc, i0)) = v4;
-  }
-  for (int idx = threadIdx.x; idx < kChunk * (kDim / 4); idx += kThreads) {
-    const int i = idx >> 5;                  // token 0..63
-    const int k0 = (idx & 31) * 4;           // first of 4 key indices
-    const s16x4 v4 = *reinterpret_cast<const s16x4*>(&lds.Q[i * kBfStride + k0]);
-    *reinterpret_cast<s16x4*>(slot16 + 2 * kSlotQ + ((i >> 4) * 8 + (k0 >> 4)) * kBlk +
-                              blk_off(i, k0)) = v4;
   }
 }
 
