@@ -26,8 +26,8 @@
 //      (bf16 MFMA: the inputs are bf16), T by block recursion (fp32 MFMA),
 //      W and U (bf16 MFMA on hi/lo-split T) -- into a workspace slot per
 //      (chunk, v-head), in the order the scan's MFMAs read it.
-//   3. scan, grid (N, HV, 128/16): the sequential part, per sequence, v-head
-//      and 16-column slice of the state: Delta, O and S_C chunk after chunk
+//   3. scan, one workgroup per (sequence, v-head, 16- or 32-column slice of
+//      the state), XCD-aware order: the sequential part, Delta, O and S_C chunk after chunk
 //      (bf16 MFMA on hi/lo-split fp32 operands), the state slice kept in
 //      registers and the next chunk's operands loaded while this one runs.
 //
@@ -51,7 +51,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kDim = 128;            // K == V == 128
 constexpr int kChunk = 64;           // tokens per chunk
 constexpr int kThreads = 256;        // 4 wavefronts
-constexpr int kVT = 16;              // state columns per scan workgroup
+constexpr long long kScanWideHeads = 256;  // N * HV from which the scan takes 32 columns
 constexpr float kL2Eps = 1e-6f;
 constexpr float kSoftplusThreshold = 20.0f;
 constexpr float kLn2 = 0.693147180559945309f;
@@ -329,14 +329,17 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
   }
   block_sync_lds();
 
-  // K K^T and Q K^T for row block `wave` (rows 16 wave .. +15), all 4 column
-  // blocks; bf16 MFMA over the 128-long rows.
+  // K K^T for row block `wave` (rows 16 wave .. +15) and (Q K^T)^T = K Q^T
+  // for column block `wave`, all 4 blocks of the other index; bf16 MFMA over
+  // the 128-long rows.  The transposed product leaves each lane holding 4
+  // consecutive j of one row i of P, which is the scan's A-operand order, so
+  // P goes out as one 8-byte store per lane.
   {
-    f32x4 kk[4], qk[4];
+    f32x4 kk[4], pt[4];
 #pragma unroll
     for (int nj = 0; nj < 4; ++nj) {
       kk[nj] = f32x4{0, 0, 0, 0};
-      qk[nj] = f32x4{0, 0, 0, 0};
+      pt[nj] = f32x4{0, 0, 0, 0};
     }
     const int ra = wave * 16 + col;
 #pragma unroll
@@ -347,9 +350,10 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
       for (int nj = 0; nj < 4; ++nj) {
         const s16x4 bk = *reinterpret_cast<const s16x4*>(&lds.K[(nj * 16 + col) * kBfStride + kk0]);
         kk[nj] = mfma_bf16(ak, bk, kk[nj]);
-        qk[nj] = mfma_bf16(qa[ks], bk, qk[nj]);
+        pt[nj] = mfma_bf16(bk, qa[ks], pt[nj]);
       }
     }
+    // A[i][j], i = 16 wave + 4 g + e, j = 16 nj + col (K K^T is symmetric)
 #pragma unroll
     for (int nj = 0; nj < 4; ++nj) {
       const int j = nj * 16 + col;
@@ -358,16 +362,28 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int i = wave * 16 + g4 * 4 + e;
-        const float gi = lds.gamma[i];
-        const float dec = j <= i ? __expf(gi - gj) : 0.0f;   // exponent <= 0
-        const float a = j < i ? lds.beta[i] * dec * lds.rk[i] * rkj * kk[nj][e] : 0.0f;
-        lds.A[i * kF64Stride + j] = a;
-        uint16_t ph, pl;
-        split_bf16(p.scale * lds.rq[i] * rkj * dec * qk[nj][e], ph, pl);
-        const int po = (wave * 4 + nj) * kBlk + blk_off(i, j);
-        slot16[2 * kSlotPh + po] = ph;
-        slot16[2 * kSlotPl + po] = pl;
+        const float dec = j < i ? __expf(lds.gamma[i] - gj) : 0.0f;   // exponent <= 0
+        lds.A[i * kF64Stride + j] = lds.beta[i] * dec * lds.rk[i] * rkj * kk[nj][e];
       }
+    }
+    // P[i][j], i = 16 wave + col, j = 16 nj + 4 g + e
+    const int i = wave * 16 + col;
+    const float gi = lds.gamma[i];
+    const float sqi = p.scale * lds.rq[i];
+#pragma unroll
+    for (int nj = 0; nj < 4; ++nj) {
+      f32x4 pv;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int j = nj * 16 + g4 * 4 + e;
+        const float dec = j <= i ? __expf(gi - lds.gamma[j]) : 0.0f;
+        pv[e] = sqi * lds.rk[j] * dec * pt[nj][e];
+      }
+      s16x4 hi, lo;
+      split4(pv, hi, lo);
+      const int bo = (wave * 4 + nj) * kBlk + lane * 4;
+      *reinterpret_cast<s16x4*>(slot16 + 2 * kSlotPh + bo) = hi;
+      *reinterpret_cast<s16x4*>(slot16 + 2 * kSlotPl + bo) = lo;
     }
   }
   block_sync_lds();
@@ -426,8 +442,10 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
   }
   block_sync_lds();
 
-  // W = (T diag(beta e^gamma rk)) K and U = (T diag(beta)) V with bf16 MFMA:
-  // the scaled T is split into hi + lo, K and V are exact bf16.  Wave `wave`
+  // W = (T diag(beta e^gamma rk)) K (computed transposed, as K^T (T diag)^T,
+  // so the result registers are in the scan's operand order) and U =
+  // (T diag(beta)) V with bf16 MFMA: the scaled T is split into hi + lo, K
+  // and V are exact bf16.  Wave `wave`
   // computes column tiles 2 wave and 2 wave + 1 for all row blocks (inner
   // blocks kb <= rb: T is lower triangular).
   {
@@ -467,27 +485,26 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
         split4(tv * ys, auh, aul);
 #pragma unroll
         for (int q2 = 0; q2 < 2; ++q2) {
-          w[rb][q2] = mfma_bf16(awh, bk[q2], w[rb][q2]);
-          w[rb][q2] = mfma_bf16(awl, bk[q2], w[rb][q2]);
+          // W^T tile (rows: key index, cols: token), U tile (rows: token)
+          w[rb][q2] = mfma_bf16(bk[q2], awh, w[rb][q2]);
+          w[rb][q2] = mfma_bf16(bk[q2], awl, w[rb][q2]);
           u[rb][q2] = mfma_bf16(auh, bv[q2], u[rb][q2]);
           u[rb][q2] = mfma_bf16(aul, bv[q2], u[rb][q2]);
         }
       }
     }
+    // Each lane of a W^T tile holds W[16 rb + col][16 ct + 4 g + e]: the
+    // scan's A-operand items of lane `lane` in block (rb, ct).
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
 #pragma unroll
       for (int q2 = 0; q2 < 2; ++q2) {
         const int ct = 2 * wave + q2;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int i = rb * 16 + g4 * 4 + e;
-          uint16_t wh, wl;
-          split_bf16(w[rb][q2][e], wh, wl);
-          const int wo = (rb * 8 + ct) * kBlk + blk_off(i, col);
-          slot16[2 * kSlotWh + wo] = wh;
-          slot16[2 * kSlotWl + wo] = wl;
-        }
+        s16x4 hi, lo;
+        split4(w[rb][q2], hi, lo);
+        const int bo = (rb * 8 + ct) * kBlk + lane * 4;
+        *reinterpret_cast<s16x4*>(slot16 + 2 * kSlotWh + bo) = hi;
+        *reinterpret_cast<s16x4*>(slot16 + 2 * kSlotWl + bo) = lo;
         *reinterpret_cast<f32x4*>(slot + kSlotU + ((rb * 8 + ct) * 64 + lane) * 4) = u[rb][q2];
       }
     }
@@ -527,21 +544,23 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
 constexpr int kStStride = kDim + 8;     // S^T rows ([col][k]), bf16
 constexpr int kDtStride = kChunk + 8;   // Delta^T and K^T rows, bf16
 
+template <int NT>   // 16-column tiles of the state slice per workgroup
 struct ScanLds {
-  uint16_t Sh[kVT * kStStride];      // state slice^T at the chunk start, hi
-  uint16_t Sl[kVT * kStStride];      //   lo
-  uint16_t Dh[kVT * kDtStride];      // Delta^T [col][i], hi
-  uint16_t Dl[kVT * kDtStride];      //   lo
-  uint16_t Eh[kVT * kDtStride];      // (ks (.) Delta)^T, hi
-  uint16_t El[kVT * kDtStride];      //   lo
+  uint16_t Sh[16 * NT * kStStride];      // state slice^T at the chunk start, hi
+  uint16_t Sl[16 * NT * kStStride];      //   lo
+  uint16_t Dh[16 * NT * kDtStride];      // Delta^T [col][i], hi
+  uint16_t Dl[16 * NT * kDtStride];      //   lo
+  uint16_t Eh[16 * NT * kDtStride];      // (ks (.) Delta)^T, hi
+  uint16_t El[16 * NT * kDtStride];      //   lo
 };
 
 // Per-lane operands of one chunk, loaded ahead of use.
+template <int NT>
 struct ScanOps {
   s16x4 wh[8], wl[8];   // W rows 16 wave + (lane % 16), k = 16 m + 4 g .. +3
   s16x4 q[8];           // Q rows (the slot's copy), same k
   s16x4 ph[4], pl[4];   // P rows, i = 16 m + 4 g .. +3
-  f32x4 u;              // U rows 16 wave + 4 g + e, column v0 + lane % 16
+  f32x4 u[NT];          // U rows 16 wave + 4 g + e, columns of the NT tiles
   f32x4 qs, ks;         // row scales of the same rows
   float gl;             // chunk decay e^gamma_C
   s16x4 kt[2][4];       // K^T rows 32 wave + 16 t + lane % 16, tokens 16 m + 4 g .. +3
@@ -556,8 +575,9 @@ __device__ __forceinline__ s16x4 ld_s16x4(const uint16_t* ptr) {
 // loads in flight and wait only for the ones a use needs (a load under a
 // branch makes it drain every outstanding load); all of them are 512-byte
 // (or 1 KiB) contiguous wave accesses in the slot's operand order.
-__device__ __forceinline__ void load_w_q_u(const float* slot, int vt, int wave, int lane,
-                                           int g4, ScanOps& o) {
+template <int NT>
+__device__ __forceinline__ void load_w_q_u(const float* slot, int tile0, int wave, int lane,
+                                           int g4, ScanOps<NT>& o) {
   const uint16_t* slot16 = reinterpret_cast<const uint16_t*>(slot);
 #pragma unroll
   for (int m = 0; m < 8; ++m) {
@@ -566,12 +586,16 @@ __device__ __forceinline__ void load_w_q_u(const float* slot, int vt, int wave, 
     o.wl[m] = ld_s16x4(slot16 + 2 * kSlotWl + bo);
     o.q[m] = ld_s16x4(slot16 + 2 * kSlotQ + bo);
   }
-  o.u = *reinterpret_cast<const f32x4*>(slot + kSlotU + ((wave * 8 + vt) * 64 + lane) * 4);
+#pragma unroll
+  for (int cq = 0; cq < NT; ++cq)
+    o.u[cq] = *reinterpret_cast<const f32x4*>(slot + kSlotU +
+                                              ((wave * 8 + tile0 + cq) * 64 + lane) * 4);
   o.ks = *reinterpret_cast<const f32x4*>(slot + kSlotKs + wave * 16 + g4 * 4);
 }
 
+template <int NT>
 __device__ __forceinline__ void load_p_qs(const float* slot, int wave, int lane, int g4,
-                                          ScanOps& o) {
+                                          ScanOps<NT>& o) {
   const uint16_t* slot16 = reinterpret_cast<const uint16_t*>(slot);
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
@@ -583,7 +607,8 @@ __device__ __forceinline__ void load_p_qs(const float* slot, int wave, int lane,
   o.gl = slot[kSlotGl];
 }
 
-__device__ __forceinline__ void load_kt(const float* slot, int wave, int lane, ScanOps& o) {
+template <int NT>
+__device__ __forceinline__ void load_kt(const float* slot, int wave, int lane, ScanOps<NT>& o) {
   const uint16_t* slot16 = reinterpret_cast<const uint16_t*>(slot);
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
@@ -593,11 +618,23 @@ __device__ __forceinline__ void load_kt(const float* slot, int wave, int lane, S
   }
 }
 
+// One-dimensional grid over (head group of 8, column tile, head in group):
+// workgroup b serves head 8 (b / (8 tiles)) + b % 8 and tile (b / 8) % tiles.
+// Workgroups are handed to the 8 XCDs round-robin by index, so every tile of
+// a head runs on the same XCD (b % 8 is fixed) and the tiles are dispatched
+// 8 apart -- together -- sharing that XCD's L2 copy of the chunk operands
+// they all read.  Heads past N * HV (padding to a multiple of 8) exit.
+template <int NT>
 __global__ __launch_bounds__(kThreads) void scan_kernel(Params p) {
-  __shared__ ScanLds lds;
-  const int s = blockIdx.x;
-  const int hv = blockIdx.y;
-  const int v0 = blockIdx.z * kVT;
+  __shared__ ScanLds<NT> lds;
+  constexpr int kTiles = 8 / NT;
+  const long long b = blockIdx.x;
+  const long long head_id = (b / (8 * kTiles)) * 8 + (b & 7);
+  if (head_id >= static_cast<long long>(p.N) * p.HV) return;   // uniform per workgroup
+  const int s = static_cast<int>(head_id / p.HV);
+  const int hv = static_cast<int>(head_id % p.HV);
+  const int tile0 = static_cast<int>((b >> 3) % kTiles) * NT;  // first 16-column tile
+  const int v0 = tile0 * 16;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int col = lane & 15;
@@ -605,37 +642,41 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Params p) {
   int start, end;
   seq_range(p, s, start, end);
 
-  // This wave's two 16-row tiles of the state slice: rows k = 32 wave + 16 t
-  // + 4 g4 + e, column v0 + col (k-last storage: 4 consecutive k are one
-  // 16-byte vector).
+  // This wave's state tiles: rows k = 32 wave + 16 t + 4 g4 + e, columns
+  // v0 + 16 cq + col (k-last storage: 4 consecutive k are one 16-byte vector).
   const size_t head = static_cast<size_t>(s) * p.HV + hv;
-  f32x4 st[2];
+  const float* st_in = p.state + head * kDim * kDim;
+  float* st_out = p.new_state + head * kDim * kDim;
+  f32x4 st[2][NT];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int kr = wave * 32 + t * 16 + g4 * 4;
-    st[t] = (p.state != nullptr && end > start)
-                ? *reinterpret_cast<const f32x4*>(p.state + head * kDim * kDim +
-                                                 static_cast<size_t>(v0 + col) * kDim + kr)
-                : f32x4{0, 0, 0, 0};
-  }
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int cq = 0; cq < NT; ++cq) {
+      const int kr = wave * 32 + t * 16 + g4 * 4;
+      st[t][cq] = (p.state != nullptr && end > start)
+                      ? *reinterpret_cast<const f32x4*>(
+                            st_in + static_cast<size_t>(v0 + cq * 16 + col) * kDim + kr)
+                      : f32x4{0, 0, 0, 0};
+    }
 
   // Chunk count from the slot offsets (never more than the range holds, and
   // never more slots than the workspace has, whatever cu_seqlens contains).
   const int nchunks = p.offs[s + 1] - p.offs[s];
-  const float* slot_base = p.slots + (static_cast<size_t>(p.offs[s]) * p.HV + hv) * kSlotFloats;
-  const size_t slot_step = static_cast<size_t>(p.HV) * kSlotFloats;
-
-  float* ns_base = p.new_state + head * kDim * kDim + static_cast<size_t>(v0 + col) * kDim;
   if (nchunks <= 0) {                 // no tokens: zeros, as the reference
 #pragma unroll
     for (int t = 0; t < 2; ++t)
-      *reinterpret_cast<f32x4*>(ns_base + wave * 32 + t * 16 + g4 * 4) = f32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int cq = 0; cq < NT; ++cq)
+        *reinterpret_cast<f32x4*>(st_out + static_cast<size_t>(v0 + cq * 16 + col) * kDim +
+                                  wave * 32 + t * 16 + g4 * 4) = f32x4{0, 0, 0, 0};
     return;
   }
+  const float* slot_base = p.slots + (static_cast<size_t>(p.offs[s]) * p.HV + hv) * kSlotFloats;
+  const size_t slot_step = static_cast<size_t>(p.HV) * kSlotFloats;
 
-  ScanOps op;
+  ScanOps<NT> op;
   load_kt(slot_base, wave, lane, op);
-  load_w_q_u(slot_base, blockIdx.z, wave, lane, g4, op);
+  load_w_q_u(slot_base, tile0, wave, lane, g4, op);
   load_p_qs(slot_base, wave, lane, g4, op);
 
   for (int ci = 0; ci < nchunks; ++ci) {
@@ -649,59 +690,71 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Params p) {
     // writes: the previous chunk's reads of Sh / Sl (step B) precede its
     // second barrier.
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      s16x4 hi, lo;
-      split4(st[t], hi, lo);
-      const int k0 = wave * 32 + t * 16 + g4 * 4;
-      *reinterpret_cast<s16x4*>(&lds.Sh[col * kStStride + k0]) = hi;
-      *reinterpret_cast<s16x4*>(&lds.Sl[col * kStStride + k0]) = lo;
-    }
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int cq = 0; cq < NT; ++cq) {
+        s16x4 hi, lo;
+        split4(st[t][cq], hi, lo);
+        const int so = (cq * 16 + col) * kStStride + wave * 32 + t * 16 + g4 * 4;
+        *reinterpret_cast<s16x4*>(&lds.Sh[so]) = hi;
+        *reinterpret_cast<s16x4*>(&lds.Sl[so]) = lo;
+      }
     block_sync_lds();
 
-    // B. Delta rows 16 wave .. +15 = U - W S, and Q S for the output rows
+    // B. Delta rows 16 wave .. +15 = U - W S, and Q S for the output rows;
     // two accumulators per product halve the dependent MFMA chains
-    f32x4 ws0 = {0, 0, 0, 0}, ws1 = {0, 0, 0, 0};
-    f32x4 qs0 = {0, 0, 0, 0}, qs1 = {0, 0, 0, 0};
+    f32x4 ws0[NT], ws1[NT], qs0[NT], qs1[NT];
+#pragma unroll
+    for (int cq = 0; cq < NT; ++cq) {
+      ws0[cq] = ws1[cq] = qs0[cq] = qs1[cq] = f32x4{0, 0, 0, 0};
+    }
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
       const int kb = m * 16 + g4 * 4;
-      const s16x4 sh = ld_s16x4(&lds.Sh[col * kStStride + kb]);
-      const s16x4 sl = ld_s16x4(&lds.Sl[col * kStStride + kb]);
-      ws0 = mfma_bf16(op.wh[m], sh, ws0);
-      ws1 = mfma_bf16(op.wh[m], sl, ws1);
-      ws0 = mfma_bf16(op.wl[m], sh, ws0);
-      qs0 = mfma_bf16(op.q[m], sh, qs0);
-      qs1 = mfma_bf16(op.q[m], sl, qs1);
+#pragma unroll
+      for (int cq = 0; cq < NT; ++cq) {
+        const int so = (cq * 16 + col) * kStStride + kb;
+        const s16x4 sh = ld_s16x4(&lds.Sh[so]);
+        const s16x4 sl = ld_s16x4(&lds.Sl[so]);
+        ws0[cq] = mfma_bf16(op.wh[m], sh, ws0[cq]);
+        ws1[cq] = mfma_bf16(op.wh[m], sl, ws1[cq]);
+        ws0[cq] = mfma_bf16(op.wl[m], sh, ws0[cq]);
+        qs0[cq] = mfma_bf16(op.q[m], sh, qs0[cq]);
+        qs1[cq] = mfma_bf16(op.q[m], sl, qs1[cq]);
+      }
     }
-    const f32x4 ws = ws0 + ws1;
-    const f32x4 qsum = qs0 + qs1;
-    {
+    f32x4 qsum[NT];
+#pragma unroll
+    for (int cq = 0; cq < NT; ++cq) {
+      const f32x4 ws = ws0[cq] + ws1[cq];
+      qsum[cq] = qs0[cq] + qs1[cq];
       f32x4 d, dk;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        d[e] = op.u[e] - ws[e];
+        d[e] = op.u[cq][e] - ws[e];
         dk[e] = op.ks[e] * d[e];
       }
       s16x4 hi, lo;
-      const int i0 = wave * 16 + g4 * 4;
+      const int dof = (cq * 16 + col) * kDtStride + wave * 16 + g4 * 4;
       split4(d, hi, lo);
-      *reinterpret_cast<s16x4*>(&lds.Dh[col * kDtStride + i0]) = hi;
-      *reinterpret_cast<s16x4*>(&lds.Dl[col * kDtStride + i0]) = lo;
+      *reinterpret_cast<s16x4*>(&lds.Dh[dof]) = hi;
+      *reinterpret_cast<s16x4*>(&lds.Dl[dof]) = lo;
       split4(dk, hi, lo);
-      *reinterpret_cast<s16x4*>(&lds.Eh[col * kDtStride + i0]) = hi;
-      *reinterpret_cast<s16x4*>(&lds.El[col * kDtStride + i0]) = lo;
+      *reinterpret_cast<s16x4*>(&lds.Eh[dof]) = hi;
+      *reinterpret_cast<s16x4*>(&lds.El[dof]) = lo;
     }
-    load_w_q_u(slot_next, blockIdx.z, wave, lane, g4, op);
+    load_w_q_u(slot_next, tile0, wave, lane, g4, op);
     block_sync_lds();
 
     // C. output rows: qs (.) (Q S) + P Delta
-    {
+#pragma unroll
+    for (int cq = 0; cq < NT; ++cq) {
       f32x4 pd0 = {0, 0, 0, 0}, pd1 = {0, 0, 0, 0};
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
-        const int ib = m * 16 + g4 * 4;
-        const s16x4 dh = ld_s16x4(&lds.Dh[col * kDtStride + ib]);
-        const s16x4 dl = ld_s16x4(&lds.Dl[col * kDtStride + ib]);
+        const int dof = (cq * 16 + col) * kDtStride + m * 16 + g4 * 4;
+        const s16x4 dh = ld_s16x4(&lds.Dh[dof]);
+        const s16x4 dl = ld_s16x4(&lds.Dl[dof]);
         pd0 = mfma_bf16(op.ph[m], dh, pd0);
         pd1 = mfma_bf16(op.ph[m], dl, pd1);
         pd0 = mfma_bf16(op.pl[m], dh, pd0);
@@ -709,11 +762,12 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Params p) {
       const f32x4 pd = pd0 + pd1;
       uint16_t ob[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) ob[e] = f32_to_bf16(fmaf(op.qs[e], qsum[e], pd[e]));
+      for (int e = 0; e < 4; ++e) ob[e] = f32_to_bf16(fmaf(op.qs[e], qsum[cq][e], pd[e]));
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int i = wave * 16 + g4 * 4 + e;
-        if (i < n) p.out[((static_cast<size_t>(t0) + i) * p.HV + hv) * kDim + v0 + col] = ob[e];
+        if (i < n)
+          p.out[((static_cast<size_t>(t0) + i) * p.HV + hv) * kDim + v0 + cq * 16 + col] = ob[e];
       }
     }
 
@@ -727,24 +781,27 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Params p) {
     load_p_qs(slot_next, wave, lane, g4, op);
     load_kt(slot_next, wave, lane, op);
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      f32x4 acc0 = st[t] * gl;
-      f32x4 acc1 = {0, 0, 0, 0};
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const int ib = m * 16 + g4 * 4;
-        acc0 = mfma_bf16(kt[t][m], ld_s16x4(&lds.Eh[col * kDtStride + ib]), acc0);
-        acc1 = mfma_bf16(kt[t][m], ld_s16x4(&lds.El[col * kDtStride + ib]), acc1);
+      for (int cq = 0; cq < NT; ++cq) {
+        f32x4 acc0 = st[t][cq] * gl;
+        f32x4 acc1 = {0, 0, 0, 0};
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const int eo = (cq * 16 + col) * kDtStride + m * 16 + g4 * 4;
+          acc0 = mfma_bf16(kt[t][m], ld_s16x4(&lds.Eh[eo]), acc0);
+          acc1 = mfma_bf16(kt[t][m], ld_s16x4(&lds.El[eo]), acc1);
+        }
+        st[t][cq] = acc0 + acc1;
       }
-      st[t] = acc0 + acc1;
-    }
   }
 
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int kr = wave * 32 + t * 16 + g4 * 4;
-    *reinterpret_cast<f32x4*>(ns_base + kr) = st[t];
-  }
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int cq = 0; cq < NT; ++cq)
+      *reinterpret_cast<f32x4*>(st_out + static_cast<size_t>(v0 + cq * 16 + col) * kDim +
+                                wave * 32 + t * 16 + g4 * 4) = st[t][cq];
 }
 
 bool aligned(const void* ptr, uintptr_t a) {
@@ -805,6 +862,8 @@ int gdn_prefill(const void* q, const void* k, const void* v, const float* state,
   }
   const long long slots = max_slots(total_seq_len, num_seqs);
   if (slots > 0x7fffffffLL || num_seqs > 0x7fffffff - 1) return hipErrorInvalidValue;
+  if ((static_cast<long long>(num_seqs) * HV + 7) / 8 * 64 > 0x7fffffffLL)   // scan grid
+    return hipErrorInvalidValue;
 
   Params p;
   p.q = static_cast<const uint16_t*>(q);
@@ -840,7 +899,17 @@ int gdn_prefill(const void* q, const void* k, const void* v, const float* state,
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(scan_kernel, dim3(num_seqs, HV, kDim / kVT), dim3(kThreads), 0, stream, p);
+  // Two 16-column tiles per workgroup once there are enough heads to fill
+  // the GPU with them (fewer redundant operand loads); one tile otherwise.
+  const long long heads = static_cast<long long>(num_seqs) * HV;
+  const long long groups = (heads + 7) / 8;
+  if (heads >= kScanWideHeads) {
+    hipLaunchKernelGGL(scan_kernel<2>, dim3(static_cast<unsigned>(groups * 8 * 4)),
+                       dim3(kThreads), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL(scan_kernel<1>, dim3(static_cast<unsigned>(groups * 8 * 8)),
+                       dim3(kThreads), 0, stream, p);
+  }
   return hipGetLastError();
 }
 
