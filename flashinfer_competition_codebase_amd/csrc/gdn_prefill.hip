@@ -19,8 +19,8 @@
 // per-row scale factors of the same products.
 //
 // Kernels (one stream, in order):
-//   1. chunk_offsets: one thread turns cu_seqlens into the first chunk slot
-//      of every sequence (token ranges clamped to [0, L]).
+//   1. chunk_offsets: one workgroup turns cu_seqlens into the first chunk
+//      slot of every sequence (token ranges clamped to [0, L]) by a scan.
 //   2. prep, grid (chunk slots, HV): everything that does not depend on the
 //      state, for all chunks at once -- gates and gamma, K K^T and Q K^T
 //      (bf16 MFMA: the inputs are bf16), T by block recursion (fp32 MFMA),
@@ -164,16 +164,41 @@ __device__ __forceinline__ void seq_range(const Params& p, int s, int& start, in
 // ---------------------------------------------------------------------------
 // 1. chunk slots per sequence
 // ---------------------------------------------------------------------------
-__global__ void chunk_offsets_kernel(Params p, int32_t* offs) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
-  long long acc = 0;
-  offs[0] = 0;
-  for (int s = 0; s < p.N; ++s) {
-    int start, end;
-    seq_range(p, s, start, end);
-    acc += (end - start + kChunk - 1) / kChunk;
-    if (acc > p.max_slots) acc = p.max_slots;  // cannot happen for clamped ranges
-    offs[s + 1] = static_cast<int32_t>(acc);
+// One workgroup of 256 threads: each thread counts one sequence's chunks, a
+// block-wide inclusive scan (wave scans through LDS) turns 256 counts into
+// offsets, and a running total carries from one group of 256 sequences to
+// the next.
+__global__ __launch_bounds__(kThreads) void chunk_offsets_kernel(Params p, int32_t* offs) {
+  __shared__ long long wave_sum[kThreads / 64];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  long long carry = 0;
+  if (threadIdx.x == 0) offs[0] = 0;
+  for (int base = 0; base < p.N; base += kThreads) {
+    const int s = base + threadIdx.x;
+    long long cnt = 0;
+    if (s < p.N) {
+      int start, end;
+      seq_range(p, s, start, end);
+      cnt = (end - start + kChunk - 1) / kChunk;
+    }
+    long long x = cnt;                         // inclusive scan within the wave
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const long long y = __shfl_up(x, d, 64);
+      if (lane >= d) x += y;
+    }
+    if (lane == 63) wave_sum[wave] = x;
+    __syncthreads();
+    long long before = carry;
+    for (int w = 0; w < wave; ++w) before += wave_sum[w];
+    long long total = carry;
+    for (int w = 0; w < kThreads / 64; ++w) total += wave_sum[w];
+    long long v = before + x;
+    if (v > p.max_slots) v = p.max_slots;      // cannot happen for clamped ranges
+    if (s < p.N) offs[s + 1] = static_cast<int32_t>(v);
+    carry = total;
+    __syncthreads();                           // wave_sum is rewritten next round
   }
 }
 
@@ -889,7 +914,7 @@ int gdn_prefill(const void* q, const void* k, const void* v, const float* state,
   p.max_slots = slots;
 
   hipStream_t stream = static_cast<hipStream_t>(hip_stream);
-  hipLaunchKernelGGL(chunk_offsets_kernel, dim3(1), dim3(64), 0, stream, p,
+  hipLaunchKernelGGL(chunk_offsets_kernel, dim3(1), dim3(kThreads), 0, stream, p,
                      static_cast<int32_t*>(workspace));
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;

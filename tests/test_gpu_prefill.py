@@ -139,3 +139,15 @@ def test_prefill_equals_chained_decode_steps(hip_device):
     assert bool(((out.float().cpu() - dec).abs() <= 1e-2 + 1e-2 * dec.abs()).all())
     ds = (st.cpu() - state.cpu()).abs()
     assert bool((ds <= 1e-3 * state.cpu().abs() + 1e-5).all()), ds.max()
+
+
+def test_more_than_256_sequences(hip_device):
+    """Chunk offsets are scanned 256 sequences at a time: 300 short sequences
+    (some empty) cross a group boundary."""
+    _announce("prefill 300 sequences")
+    g = torch.Generator().manual_seed(21)
+    lens = [int(x) for x in torch.randint(0, 12, (300,), generator=g)] + [70]
+    t = make_prefill_inputs(lens, 4, 8, seed=22)
+    out, st = gdn.prefill_run(**_dev(t, hip_device))
+    torch.cuda.synchronize()
+    _check(t, out, st, loop=False)
