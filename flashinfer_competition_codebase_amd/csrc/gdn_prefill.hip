@@ -20,7 +20,8 @@
 //
 // Kernels (one stream, in order):
 //   1. chunk_offsets: one workgroup turns cu_seqlens into the first chunk
-//      slot of every sequence (token ranges clamped to [0, L]) by a scan.
+//      slot of every sequence (token ranges clamped to [0, L]) by a scan,
+//      and writes each slot's sequence, first token and token count.
 //   2. prep, grid (chunk slots, HV): everything that does not depend on the
 //      state, for all chunks at once -- gates and gamma, K K^T and Q K^T
 //      (bf16 MFMA: the inputs are bf16), T by block recursion (fp32 MFMA),
@@ -47,6 +48,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kDim = 128;            // K == V == 128
 constexpr int kChunk = 64;           // tokens per chunk
@@ -139,6 +141,8 @@ struct Params {
   uint16_t* out;             // [L, HV, 128] bf16
   float* new_state;          // [N, HV, 128, 128] fp32 k-last
   const int32_t* offs;       // [N + 1] first chunk slot of each sequence (workspace)
+  const i32x4* slot_info;    // [max_slots] per chunk slot: sequence, first token, tokens
+                             // (0 past the last slot) (workspace)
   float* slots;              // [slots, HV, kSlotFloats] (workspace)
   float scale;
   int L;
@@ -167,9 +171,15 @@ __device__ __forceinline__ void seq_range(const Params& p, int s, int& start, in
 // One workgroup of 256 threads: each thread counts one sequence's chunks, a
 // block-wide inclusive scan (wave scans through LDS) turns 256 counts into
 // offsets, and a running total carries from one group of 256 sequences to
-// the next.
-__global__ __launch_bounds__(kThreads) void chunk_offsets_kernel(Params p, int32_t* offs) {
+// the next.  The group's offsets and token ranges then go to LDS, and the
+// threads fill the group's slots of the slot table, each finding its slot's
+// sequence by binary search there.  Slots past the last one get zero tokens.
+__global__ __launch_bounds__(kThreads) void chunk_offsets_kernel(Params p, int32_t* offs,
+                                                                 i32x4* slot_info) {
   __shared__ long long wave_sum[kThreads / 64];
+  __shared__ int32_t grp_offs[kThreads + 1];   // offs[base .. base + 256]
+  __shared__ int32_t grp_start[kThreads];
+  __shared__ int32_t grp_end[kThreads];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   long long carry = 0;
@@ -177,8 +187,8 @@ __global__ __launch_bounds__(kThreads) void chunk_offsets_kernel(Params p, int32
   for (int base = 0; base < p.N; base += kThreads) {
     const int s = base + threadIdx.x;
     long long cnt = 0;
+    int start = 0, end = 0;
     if (s < p.N) {
-      int start, end;
       seq_range(p, s, start, end);
       cnt = (end - start + kChunk - 1) / kChunk;
     }
@@ -195,22 +205,31 @@ __global__ __launch_bounds__(kThreads) void chunk_offsets_kernel(Params p, int32
     long long total = carry;
     for (int w = 0; w < kThreads / 64; ++w) total += wave_sum[w];
     long long v = before + x;
-    if (v > p.max_slots) v = p.max_slots;      // cannot happen for clamped ranges
+    if (v > p.max_slots) v = p.max_slots;      // only for overlapping ranges
+    if (total > p.max_slots) total = p.max_slots;
     if (s < p.N) offs[s + 1] = static_cast<int32_t>(v);
+    grp_offs[threadIdx.x + 1] = static_cast<int32_t>(v);
+    if (threadIdx.x == 0) grp_offs[0] = static_cast<int32_t>(carry);
+    grp_start[threadIdx.x] = start;
+    grp_end[threadIdx.x] = end;
     carry = total;
-    __syncthreads();                           // wave_sum is rewritten next round
+    __syncthreads();
+    // slots [grp_offs[0], grp_offs[256]) belong to this group's sequences;
+    // slot c's sequence is the largest j with grp_offs[j] <= c
+    for (int c = grp_offs[0] + threadIdx.x; c < grp_offs[kThreads]; c += kThreads) {
+      int lo = 0, hi = kThreads - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (grp_offs[mid] <= c) lo = mid; else hi = mid - 1;
+      }
+      const int t0 = grp_start[lo] + (c - grp_offs[lo]) * kChunk;
+      const int n = min(kChunk, grp_end[lo] - t0);
+      slot_info[c] = i32x4{base + lo, t0, n, 0};
+    }
+    __syncthreads();                           // LDS is rewritten next round
   }
-}
-
-// Sequence owning chunk slot c (offs non-decreasing, offs[0] = 0, c < offs[N]):
-// the largest s with offs[s] <= c.
-__device__ __forceinline__ int seq_of_slot(const int32_t* offs, int N, int c) {
-  int lo = 0, hi = N - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (offs[mid] <= c) lo = mid; else hi = mid - 1;
-  }
-  return lo;
+  for (long long c = carry + threadIdx.x; c < p.max_slots; c += kThreads)
+    slot_info[c] = i32x4{0, 0, 0, 0};
 }
 
 // Gates of token t, v-head hv: log-space decay and beta
@@ -223,19 +242,32 @@ __device__ __forceinline__ void token_gates(const Params& p, int t, int hv, floa
   beta = __builtin_amdgcn_rcpf(1.0f + __expf(-bf16_to_f32(p.b[static_cast<size_t>(t) * p.HV + hv])));
 }
 
-// Copy rows [0, n) of a [*, stride_rows, 128] bf16 tensor (row r at
-// base + r * row_step elements) into LDS rows of kBfStride, zero rows >= n.
-__device__ __forceinline__ void stage_rows_bf16(uint16_t* dst, const uint16_t* base,
-                                                size_t row_step, int n) {
-  // 64 rows x 16 pieces of 16 bytes; 256 threads x 4
-  for (int idx = threadIdx.x; idx < kChunk * 16; idx += kThreads) {
+// Rows [0, 64) of a [*, stride, 128] bf16 tensor (row r at base + r * step
+// elements) as 4 pieces of 16 bytes per thread.  Rows >= n read row n - 1
+// (n >= 1) so that every load is unconditional: issued together, waited on
+// once.  store_rows_bf16 writes them to LDS rows of kBfStride, zeroing rows
+// >= n.
+__device__ __forceinline__ void load_rows_bf16(u32x4 (&val)[4], const uint16_t* base,
+                                               size_t step, int n) {
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int idx = threadIdx.x + it * kThreads;
     const int r = idx >> 4;
-    const int c8 = (idx & 15) * 8;
-    u32x4 val = {0u, 0u, 0u, 0u};
-    if (r < n) val = *reinterpret_cast<const u32x4*>(base + static_cast<size_t>(r) * row_step + c8);
-    uint16_t* d = dst + r * kBfStride + c8;
-    *reinterpret_cast<u32x2*>(d) = u32x2{val.x, val.y};
-    *reinterpret_cast<u32x2*>(d + 4) = u32x2{val.z, val.w};
+    const int rr = r < n ? r : n - 1;
+    val[it] = *reinterpret_cast<const u32x4*>(base + static_cast<size_t>(rr) * step +
+                                              (idx & 15) * 8);
+  }
+}
+
+__device__ __forceinline__ void store_rows_bf16(uint16_t* dst, const u32x4 (&val)[4], int n) {
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int idx = threadIdx.x + it * kThreads;
+    const int r = idx >> 4;
+    const u32x4 x = r < n ? val[it] : u32x4{0u, 0u, 0u, 0u};
+    uint16_t* d = dst + r * kBfStride + (idx & 15) * 8;
+    *reinterpret_cast<u32x2*>(d) = u32x2{x.x, x.y};
+    *reinterpret_cast<u32x2*>(d + 4) = u32x2{x.z, x.w};
   }
 }
 
@@ -277,13 +309,10 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
   __shared__ PrepLds lds;
   const int c = blockIdx.x;
   const int hv = blockIdx.y;
-  const int nslots = p.offs[p.N];
-  if (c >= nslots) return;                         // uniform per workgroup
-  const int s = seq_of_slot(p.offs, p.N, c);
-  int start, end;
-  seq_range(p, s, start, end);
-  const int t0 = start + (c - p.offs[s]) * kChunk;
-  const int n = min(kChunk, end - t0);             // 1..64
+  const i32x4 info = p.slot_info[c];
+  const int t0 = info.y;
+  const int n = info.z;                            // 1..64, 0 past the last slot
+  if (n <= 0) return;                              // uniform per workgroup
   const int h = hv / p.ratio;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -292,26 +321,39 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
   float* slot = p.slots + (static_cast<size_t>(c) * p.HV + hv) * kSlotFloats;
   uint16_t* slot16 = reinterpret_cast<uint16_t*>(slot);
 
-  stage_rows_bf16(lds.K, p.k + (static_cast<size_t>(t0) * p.H + h) * kDim,
-                  static_cast<size_t>(p.H) * kDim, n);
-  stage_rows_bf16(lds.V, p.v + (static_cast<size_t>(t0) * p.HV + hv) * kDim,
-                  static_cast<size_t>(p.HV) * kDim, n);
-  for (int idx = threadIdx.x; idx < kChunk * kF64Stride; idx += kThreads) lds.T[idx] = 0.0f;
+  // Every input load of the chunk is issued before the first is waited on.
+  u32x4 kreg[4], vreg[4];
+  load_rows_bf16(kreg, p.k + (static_cast<size_t>(t0) * p.H + h) * kDim,
+                 static_cast<size_t>(p.H) * kDim, n);
+  load_rows_bf16(vreg, p.v + (static_cast<size_t>(t0) * p.HV + hv) * kDim,
+                 static_cast<size_t>(p.HV) * kDim, n);
 
   // Q rows 16 wave + col straight into MFMA A-operand registers (k = 16 m +
   // 4 g .. +3; rows past the chunk's end zero), which are also the scan's
   // operand-ordered copy of Q; with the L2-norm, their row norms.
   s16x4 qa[8];
+  const int ra = wave * 16 + col;
+  const bool row_ok = ra < n;
   {
-    const int ra = wave * 16 + col;
-    const bool row_ok = ra < n;
     const uint16_t* qrow =
         p.q + ((static_cast<size_t>(t0) + (row_ok ? ra : n - 1)) * p.H + h) * kDim;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) qa[m] = *reinterpret_cast<const s16x4*>(qrow + m * 16 + g4 * 4);
+  }
+  // Gates of token t0 + lane (every wave computes them, wave 0 keeps them);
+  // padded rows: no decay, no update.
+  float logg, beta;
+  token_gates(p, t0 + (lane < n ? lane : n - 1), hv, logg, beta);
+  if (lane >= n) logg = beta = 0.0f;
+
+  store_rows_bf16(lds.K, kreg, n);
+  store_rows_bf16(lds.V, vreg, n);
+  for (int idx = threadIdx.x; idx < kChunk * kF64Stride; idx += kThreads) lds.T[idx] = 0.0f;
+  {
     float sq = 0.0f;
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
-      const s16x4 v = *reinterpret_cast<const s16x4*>(qrow + m * 16 + g4 * 4);
-      qa[m] = row_ok ? v : s16x4{0, 0, 0, 0};
+      if (!row_ok) qa[m] = s16x4{0, 0, 0, 0};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float x = bf16_to_f32(static_cast<uint16_t>(qa[m][e]));
@@ -324,8 +366,6 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
     if (g4 == 0) lds.rq[ra] = p.l2norm ? __builtin_amdgcn_rsqf(sq + kL2Eps) : 1.0f;
   }
   if (wave == 0) {
-    float logg = 0.0f, beta = 0.0f;                // padded rows: no decay, no update
-    if (lane < n) token_gates(p, t0 + lane, hv, logg, beta);
     float g = logg;                                // inclusive scan over the chunk
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
@@ -837,10 +877,16 @@ size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
 long long max_slots(long long L, long long N) { return (L + kChunk - 1) / kChunk + N; }
 
+// Workspace: chunk offsets [N + 1] int32, slot table [max_slots] x 16 bytes,
+// then the slots [max_slots, HV, kSlotFloats] fp32; each part 256-byte aligned.
 size_t offsets_bytes(long long N) { return align256(static_cast<size_t>(N + 1) * sizeof(int32_t)); }
 
+size_t slot_info_bytes(long long L, long long N) {
+  return align256(static_cast<size_t>(max_slots(L, N)) * sizeof(i32x4));
+}
+
 size_t workspace_bytes(long long L, long long N, long long HV) {
-  return offsets_bytes(N) +
+  return offsets_bytes(N) + slot_info_bytes(L, N) +
          static_cast<size_t>(max_slots(L, N)) * HV * kSlotFloats * sizeof(float);
 }
 
@@ -902,8 +948,13 @@ int gdn_prefill(const void* q, const void* k, const void* v, const float* state,
   p.cu_seqlens = cu_seqlens;
   p.out = static_cast<uint16_t*>(output);
   p.new_state = new_state;
-  p.offs = static_cast<const int32_t*>(workspace);
-  p.slots = reinterpret_cast<float*>(static_cast<char*>(workspace) + offsets_bytes(num_seqs));
+  char* ws = static_cast<char*>(workspace);
+  int32_t* offs = reinterpret_cast<int32_t*>(ws);
+  i32x4* slot_info = reinterpret_cast<i32x4*>(ws + offsets_bytes(num_seqs));
+  p.offs = offs;
+  p.slot_info = slot_info;
+  p.slots = reinterpret_cast<float*>(ws + offsets_bytes(num_seqs) +
+                                     slot_info_bytes(total_seq_len, num_seqs));
   p.scale = scale;
   p.L = total_seq_len;
   p.N = num_seqs;
@@ -914,8 +965,8 @@ int gdn_prefill(const void* q, const void* k, const void* v, const float* state,
   p.max_slots = slots;
 
   hipStream_t stream = static_cast<hipStream_t>(hip_stream);
-  hipLaunchKernelGGL(chunk_offsets_kernel, dim3(1), dim3(kThreads), 0, stream, p,
-                     static_cast<int32_t*>(workspace));
+  hipLaunchKernelGGL(chunk_offsets_kernel, dim3(1), dim3(kThreads), 0, stream, p, offs,
+                     slot_info);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (slots > 0) {

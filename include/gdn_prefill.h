@@ -45,7 +45,8 @@ extern "C" {
 /*
  * Bytes of device workspace gdn_prefill needs for L total tokens, N
  * sequences and HV v-heads (per-chunk intermediates: about 113 KiB per 64
- * tokens per v-head, plus 64-token slack per sequence).  0 for invalid sizes.
+ * tokens per v-head, plus 64-token slack per sequence; a 16-byte table entry
+ * per chunk and 4 bytes per sequence).  0 for invalid sizes.
  * The reference's FLA path allocates its intermediates per call inside
  * chunk_gated_delta_rule (solution/triton/fla_prefill_code.py:1726-1776);
  * here the caller provides them.

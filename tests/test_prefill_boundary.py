@@ -43,7 +43,8 @@ def test_workspace_size_formula():
     for L, N, HV in ((6, 1, 8), (16384, 1, 8), (1000, 37, 32), (0, 3, 8)):
         chunks = (L + 63) // 64 + N
         offs = ((N + 1) * 4 + 255) // 256 * 256
-        assert lib.gdn_prefill_workspace_bytes(L, N, HV) == offs + chunks * HV * slot
+        table = (chunks * 16 + 255) // 256 * 256                         # per-chunk slot table
+        assert lib.gdn_prefill_workspace_bytes(L, N, HV) == offs + table + chunks * HV * slot
     assert lib.gdn_prefill_workspace_bytes(-1, 1, 8) == 0
     assert lib.gdn_prefill_workspace_bytes(1, 1, 0) == 0
 
