@@ -95,20 +95,24 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float x) {
   return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));  // round to nearest even
 }
 
-// x ~ hi + lo with hi = bf16(x), lo = bf16(x - hi).
-__device__ __forceinline__ void split_bf16(float x, uint16_t& hi, uint16_t& lo) {
-  hi = f32_to_bf16(x);
-  lo = f32_to_bf16(x - bf16_to_f32(hi));
+// Two floats to a packed bf16 pair (round to nearest even), element 0 in
+// the low half.  split4: x ~ hi + lo with hi = bf16(x), lo = bf16(x - hi).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
 }
 
 __device__ __forceinline__ void split4(const f32x4& x, s16x4& hi, s16x4& lo) {
+  u32x2 h, l;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    uint16_t h, l;
-    split_bf16(x[e], h, l);
-    hi[e] = static_cast<short>(h);
-    lo[e] = static_cast<short>(l);
+  for (int e = 0; e < 2; ++e) {
+    const float x0 = x[2 * e], x1 = x[2 * e + 1];
+    h[e] = pack_bf16x2(x0, x1);
+    l[e] = pack_bf16x2(x0 - __uint_as_float(h[e] << 16), x1 - __uint_as_float(h[e] & 0xffff0000u));
   }
+  hi = __builtin_bit_cast(s16x4, h);
+  lo = __builtin_bit_cast(s16x4, l);
 }
 
 // Workgroup barrier that orders LDS only.  The waves of these kernels
@@ -348,12 +352,20 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
 
   store_rows_bf16(lds.K, kreg, n);
   store_rows_bf16(lds.V, vreg, n);
-  for (int idx = threadIdx.x; idx < kChunk * kF64Stride; idx += kThreads) lds.T[idx] = 0.0f;
+  // T's upper blocks that the block recursion multiplies, T_01 and T_23, are
+  // zero; the diagonal and lower blocks are all written, the other upper
+  // blocks never read.
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int idx = threadIdx.x + it * kThreads;
+    const int o = 32 * (idx >> 8);
+    lds.T[(o + ((idx >> 4) & 15)) * kF64Stride + o + 16 + (idx & 15)] = 0.0f;
+  }
   {
     float sq = 0.0f;
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
-      if (!row_ok) qa[m] = s16x4{0, 0, 0, 0};
+      qa[m] = row_ok ? qa[m] : s16x4{0, 0, 0, 0};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float x = bf16_to_f32(static_cast<uint16_t>(qa[m][e]));
@@ -418,7 +430,14 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
         pt[nj] = mfma_bf16(bk, qa[ks], pt[nj]);
       }
     }
+    // Row and column factors, read once.  The decays are computed for every
+    // element with the exponent clamped to <= 0 (it is <= 0 wherever the
+    // element is kept: gamma does not increase) and the masks are selects.
     // A[i][j], i = 16 wave + 4 g + e, j = 16 nj + col (K K^T is symmetric)
+    const int ia = wave * 16 + g4 * 4;
+    const f32x4 gi4 = *reinterpret_cast<const f32x4*>(&lds.gamma[ia]);
+    const f32x4 bri4 = *reinterpret_cast<const f32x4*>(&lds.beta[ia]) *
+                       *reinterpret_cast<const f32x4*>(&lds.rk[ia]);
 #pragma unroll
     for (int nj = 0; nj < 4; ++nj) {
       const int j = nj * 16 + col;
@@ -426,9 +445,9 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
       const float rkj = lds.rk[j];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int i = wave * 16 + g4 * 4 + e;
-        const float dec = j < i ? __expf(lds.gamma[i] - gj) : 0.0f;   // exponent <= 0
-        lds.A[i * kF64Stride + j] = lds.beta[i] * dec * lds.rk[i] * rkj * kk[nj][e];
+        const float dec = __expf(fminf(gi4[e] - gj, 0.0f));
+        const float x = bri4[e] * rkj * dec * kk[nj][e];
+        lds.A[(ia + e) * kF64Stride + j] = j < ia + e ? x : 0.0f;
       }
     }
     // P[i][j], i = 16 wave + col, j = 16 nj + 4 g + e
@@ -437,12 +456,15 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
     const float sqi = p.scale * lds.rq[i];
 #pragma unroll
     for (int nj = 0; nj < 4; ++nj) {
+      const int j0 = nj * 16 + g4 * 4;
+      const f32x4 gj4 = *reinterpret_cast<const f32x4*>(&lds.gamma[j0]);
+      const f32x4 rkj4 = *reinterpret_cast<const f32x4*>(&lds.rk[j0]);
       f32x4 pv;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int j = nj * 16 + g4 * 4 + e;
-        const float dec = j <= i ? __expf(gi - lds.gamma[j]) : 0.0f;
-        pv[e] = sqi * lds.rk[j] * dec * pt[nj][e];
+        const float dec = __expf(fminf(gi - gj4[e], 0.0f));
+        const float x = sqi * rkj4[e] * dec * pt[nj][e];
+        pv[e] = j0 + e <= i ? x : 0.0f;
       }
       s16x4 hi, lo;
       split4(pv, hi, lo);
@@ -587,9 +609,11 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
   // K^T (A operand of the scan's state update: rows = key index, inner =
   // token), in operand order, 8 bytes per store; rows past the chunk's end
   // are zero.
-  for (int idx = threadIdx.x; idx < kDim * (kChunk / 4); idx += kThreads) {
-    const int kc = idx >> 4;                 // key index 0..127
-    const int i0 = (idx & 15) * 4;           // first of 4 tokens
+#pragma unroll
+  for (int it = 0; it < kDim * (kChunk / 4) / kThreads; ++it) {
+    const int idx = threadIdx.x + it * kThreads;
+    const int kc = idx & (kDim - 1);         // key index 0..127
+    const int i0 = (idx >> 7) * 4;           // first of 4 tokens
     s16x4 v4;
 #pragma unroll
     for (int e = 0; e < 4; ++e) v4[e] = static_cast<short>(lds.K[(i0 + e) * kBfStride + kc]);
