@@ -15,7 +15,7 @@ MFMA kernels of ``libgdn_prefill.so``.  There is no CPU or fallback path.
 entries that return their outputs instead of writing caller-allocated ones.
 """
 
-from .kernel import kernel_hip, kernel_hip_shaped, resolve_scale, run
+from .kernel import kernel_hip, kernel_hip_shaped, resolve_scale, run, run_dps
 from .prefill import kernel_prefill_hip, prefill_run
 
 ENTRY_POINTS = {
@@ -27,5 +27,5 @@ ENTRY_POINTS = {
 
 NO_DPS = {"hip-run", "prefill-hip-run"}
 
-__all__ = ["run", "kernel_hip", "kernel_hip_shaped", "resolve_scale", "prefill_run",
+__all__ = ["run", "run_dps", "kernel_hip", "kernel_hip_shaped", "resolve_scale", "prefill_run",
            "kernel_prefill_hip", "ENTRY_POINTS", "NO_DPS"]

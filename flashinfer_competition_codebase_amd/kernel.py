@@ -46,7 +46,7 @@ from . import _lib
 K_DIM = 128
 V_DIM = 128
 
-__all__ = ["run", "kernel_hip", "kernel_hip_shaped", "resolve_scale"]
+__all__ = ["run", "run_dps", "kernel_hip", "kernel_hip_shaped", "resolve_scale"]
 
 
 def resolve_scale(scale, K: int = K_DIM) -> float:
@@ -243,3 +243,8 @@ def run(q, k, v, state, A_log, a, dt_bias, b, scale, *, use_qk_l2norm: bool = Fa
     kernel_hip(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
                use_qk_l2norm=use_qk_l2norm)
     return output, new_state
+
+
+# The 11-argument DPS form under the name a definition's solution module
+# exposes beside ``run`` (new_state may be state itself).
+run_dps = kernel_hip

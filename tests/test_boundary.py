@@ -29,6 +29,7 @@ def test_signatures_match_reference_names():
     assert [n for n, x in p.items() if x.kind is x.POSITIONAL_OR_KEYWORD] == (
         REF_ARGS + ["output", "new_state"])
     assert gdn.ENTRY_POINTS["hip"] is gdn.kernel_hip
+    assert gdn.run_dps is gdn.kernel_hip
     assert gdn.ENTRY_POINTS["hip-run"] is gdn.run
     assert gdn.NO_DPS == {"hip-run", "prefill-hip-run"}
     # prefill: kernel_prefill_reference / kernel_prefill_fla_chunk argument names
