@@ -32,10 +32,15 @@
 //      (bf16 MFMA on hi/lo-split fp32 operands), the state slice kept in
 //      registers and the next chunk's operands loaded while this one runs.
 //
-// MFMA lane layouts (v_mfma_f32_16x16x4_f32, v_mfma_f32_16x16x16_bf16):
-// A[i][k] from lane i + 16 g, B[k][j] from lane j + 16 g (k = g for fp32,
-// k = 4 g + e for the bf16 x4 items), D[i][j] in lane j + 16 (i / 4),
-// register i % 4.
+// MFMA lane layouts (v_mfma_f32_16x16x4_f32, v_mfma_f32_16x16x32_bf16):
+// A[i][k] from lane i + 16 g, B[k][j] from lane j + 16 g (k = g for fp32;
+// for bf16 the lane's 8 items cover the 32-long k block), D[i][j] in lane
+// j + 16 (i / 4), register i % 4.  A bf16 product sums over its k block in
+// any order both operands share; here item e of lane group g stands for
+//   k = 16 (e / 4) + 4 g + e % 4,
+// so a lane's 8 items are the 4-element runs at k = 4 g and 16 + 4 g, the
+// runs a 16 x 16 MFMA result holds per lane -- results become operands
+// without exchanging data between lanes.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -46,6 +51,8 @@ namespace gdn_pf {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
@@ -59,30 +66,28 @@ constexpr float kSoftplusThreshold = 20.0f;
 constexpr float kLn2 = 0.693147180559945309f;
 
 // Workspace slot of one (chunk, v-head), offsets in floats.  The scan's MFMA
-// A operands (W, P, K^T and a copy of Q) are stored in operand order: a
-// 16 x 16 block of an A operand is 64 lanes x 4 bf16 contiguous (lane =
-// row + 16 (col / 4), item = col % 4), so each scan load instruction reads
-// 512 contiguous bytes.  fp32 operands are split into a bf16 high and low
-// part (x ~ hi + lo to ~2^-16 relative).  U is stored in the MFMA result
-// order the scan consumes (per 16 x 16 block, lane-major 4 floats).
-constexpr int kBlk = 256;                             // bf16 per 16 x 16 operand block
-constexpr int kSlotWh = 0;                            // W hi: blocks (row blk 0..3, k blk 0..7)
-constexpr int kSlotWl = kSlotWh + 32 * kBlk / 2;      // W lo
-constexpr int kSlotU = kSlotWl + 32 * kBlk / 2;       // U: blocks (row blk 0..3, col blk 0..7)
-constexpr int kSlotPh = kSlotU + kChunk * kDim;       // P hi: blocks (row blk 0..3, j blk 0..3),
-constexpr int kSlotPl = kSlotPh + 16 * kBlk / 2;      //   P = scale rq_i rk_j M_ij (Q K^T)_ij; lo
-constexpr int kSlotQs = kSlotPl + 16 * kBlk / 2;      // scale * rq_i e^gamma_i [64]
+// operands (W, P, K^T and a copy of Q) are stored in operand order: a
+// 16 x 32 block of an operand is 64 lanes x 8 bf16 contiguous (lane = row +
+// 16 g, items in the k order above), so each scan load instruction reads
+// 1 KiB contiguous.  fp32 operands are split into a bf16 high and low part
+// (x ~ hi + lo to ~2^-16 relative).  U is stored in the MFMA result order
+// the scan consumes (per 16 x 16 block, lane-major 4 floats).
+constexpr int kBlk = 512;                             // bf16 per 16 x 32 operand block
+constexpr int kSlotWh = 0;                            // W hi: blocks (row blk 0..3, k blk 0..3)
+constexpr int kSlotWl = kSlotWh + 16 * kBlk / 2;      // W lo
+constexpr int kSlotU = kSlotWl + 16 * kBlk / 2;       // U: blocks (row blk 0..3, col blk 0..7)
+constexpr int kSlotPh = kSlotU + kChunk * kDim;       // P hi: blocks (row blk 0..3, j blk 0..1),
+constexpr int kSlotPl = kSlotPh + 8 * kBlk / 2;       //   P = scale rq_i rk_j M_ij (Q K^T)_ij; lo
+constexpr int kSlotQs = kSlotPl + 8 * kBlk / 2;       // scale * rq_i e^gamma_i [64]
 constexpr int kSlotKs = kSlotQs + kChunk;             // rk_i e^(gamma_C - gamma_i) [64]
 constexpr int kSlotGl = kSlotKs + kChunk;             // e^gamma_C [1], padded to 64
-constexpr int kSlotKt = kSlotGl + 64;                 // K^T: blocks (key blk 0..7, token blk 0..3)
-constexpr int kSlotQ = kSlotKt + 32 * kBlk / 2;       // Q: blocks (token blk 0..3, k blk 0..7)
-constexpr int kSlotFloats = kSlotQ + 32 * kBlk / 2;
+constexpr int kSlotKt = kSlotGl + 64;                 // K^T: blocks (key blk 0..7, token blk 0..1)
+constexpr int kSlotQ = kSlotKt + 16 * kBlk / 2;       // Q: blocks (token blk 0..3, k blk 0..3)
+constexpr int kSlotFloats = kSlotQ + 16 * kBlk / 2;
 static_assert(kSlotFloats % 64 == 0, "slots stay 256-byte aligned");
 
-// Offset (bf16 units) of A-operand element (r, c) inside its 16 x 16 block.
-__host__ __device__ constexpr int blk_off(int r, int c) {
-  return ((r & 15) + 16 * ((c & 15) >> 2)) * 4 + (c & 3);
-}
+// k (0..31) of item e of lane group g inside a 32-long block.
+__host__ __device__ constexpr int k_of(int g, int e) { return 16 * (e >> 2) + 4 * g + (e & 3); }
 
 // LDS row strides (elements) chosen so MFMA operand reads spread over banks.
 constexpr int kBfStride = kDim + 8;       // bf16 rows of 128
@@ -90,9 +95,6 @@ constexpr int kF64Stride = kChunk + 4;    // fp32 rows of 64
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
-}
-__device__ __forceinline__ uint16_t f32_to_bf16(float x) {
-  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));  // round to nearest even
 }
 
 // Two floats to a packed bf16 pair (round to nearest even), element 0 in
@@ -128,8 +130,19 @@ __device__ __forceinline__ void block_sync_lds() {
 __device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
-__device__ __forceinline__ f32x4 mfma_bf16(s16x4 a, s16x4 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+__device__ __forceinline__ f32x4 mfma_bf16(s16x8 a, s16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ s16x8 cat(s16x4 a, s16x4 b) {
+  return s16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// Operand items of lane group g for k block kb of a bf16 row (k contiguous).
+__device__ __forceinline__ s16x8 frag(const uint16_t* row, int kb, int g) {
+  return cat(*reinterpret_cast<const s16x4*>(row + 32 * kb + 4 * g),
+             *reinterpret_cast<const s16x4*>(row + 32 * kb + 16 + 4 * g));
 }
 
 struct Params {
@@ -332,17 +345,17 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
   load_rows_bf16(vreg, p.v + (static_cast<size_t>(t0) * p.HV + hv) * kDim,
                  static_cast<size_t>(p.HV) * kDim, n);
 
-  // Q rows 16 wave + col straight into MFMA A-operand registers (k = 16 m +
-  // 4 g .. +3; rows past the chunk's end zero), which are also the scan's
+  // Q rows 16 wave + col straight into MFMA operand registers (k block m;
+  // rows past the chunk's end zero), which are also the scan's
   // operand-ordered copy of Q; with the L2-norm, their row norms.
-  s16x4 qa[8];
+  s16x8 qa[4];
   const int ra = wave * 16 + col;
   const bool row_ok = ra < n;
   {
     const uint16_t* qrow =
         p.q + ((static_cast<size_t>(t0) + (row_ok ? ra : n - 1)) * p.H + h) * kDim;
 #pragma unroll
-    for (int m = 0; m < 8; ++m) qa[m] = *reinterpret_cast<const s16x4*>(qrow + m * 16 + g4 * 4);
+    for (int m = 0; m < 4; ++m) qa[m] = frag(qrow, m, g4);
   }
   // Gates of token t0 + lane (every wave computes them, wave 0 keeps them);
   // padded rows: no decay, no update.
@@ -364,14 +377,14 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
   {
     float sq = 0.0f;
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      qa[m] = row_ok ? qa[m] : s16x4{0, 0, 0, 0};
+    for (int m = 0; m < 4; ++m) {
+      qa[m] = row_ok ? qa[m] : s16x8{0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
+      for (int e = 0; e < 8; ++e) {
         const float x = bf16_to_f32(static_cast<uint16_t>(qa[m][e]));
         sq = fmaf(x, x, sq);
       }
-      *reinterpret_cast<s16x4*>(slot16 + 2 * kSlotQ + (wave * 8 + m) * kBlk + lane * 4) = qa[m];
+      *reinterpret_cast<s16x8*>(slot16 + 2 * kSlotQ + (wave * 4 + m) * kBlk + lane * 8) = qa[m];
     }
     sq += __shfl_xor(sq, 16, 64);
     sq += __shfl_xor(sq, 32, 64);
@@ -409,8 +422,8 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
   // K K^T for row block `wave` (rows 16 wave .. +15) and (Q K^T)^T = K Q^T
   // for column block `wave`, all 4 blocks of the other index; bf16 MFMA over
   // the 128-long rows.  The transposed product leaves each lane holding 4
-  // consecutive j of one row i of P, which is the scan's A-operand order, so
-  // P goes out as one 8-byte store per lane.
+  // consecutive j of one row i of P, two of which make the scan's operand
+  // items, so P goes out as one 16-byte store per lane and k block.
   {
     f32x4 kk[4], pt[4];
 #pragma unroll
@@ -420,14 +433,13 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
     }
     const int ra = wave * 16 + col;
 #pragma unroll
-    for (int ks = 0; ks < kDim / 16; ++ks) {
-      const int kk0 = ks * 16 + g4 * 4;
-      const s16x4 ak = *reinterpret_cast<const s16x4*>(&lds.K[ra * kBfStride + kk0]);
+    for (int m = 0; m < kDim / 32; ++m) {
+      const s16x8 ak = frag(&lds.K[ra * kBfStride], m, g4);
 #pragma unroll
       for (int nj = 0; nj < 4; ++nj) {
-        const s16x4 bk = *reinterpret_cast<const s16x4*>(&lds.K[(nj * 16 + col) * kBfStride + kk0]);
+        const s16x8 bk = frag(&lds.K[(nj * 16 + col) * kBfStride], m, g4);
         kk[nj] = mfma_bf16(ak, bk, kk[nj]);
-        pt[nj] = mfma_bf16(bk, qa[ks], pt[nj]);
+        pt[nj] = mfma_bf16(bk, qa[m], pt[nj]);
       }
     }
     // Row and column factors, read once.  The decays are computed for every
@@ -455,22 +467,26 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
     const float gi = lds.gamma[i];
     const float sqi = p.scale * lds.rq[i];
 #pragma unroll
-    for (int nj = 0; nj < 4; ++nj) {
-      const int j0 = nj * 16 + g4 * 4;
-      const f32x4 gj4 = *reinterpret_cast<const f32x4*>(&lds.gamma[j0]);
-      const f32x4 rkj4 = *reinterpret_cast<const f32x4*>(&lds.rk[j0]);
-      f32x4 pv;
+    for (int jb = 0; jb < 2; ++jb) {
+      s16x4 hi[2], lo[2];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float dec = __expf(fminf(gi - gj4[e], 0.0f));
-        const float x = sqi * rkj4[e] * dec * pt[nj][e];
-        pv[e] = j0 + e <= i ? x : 0.0f;
+      for (int hf = 0; hf < 2; ++hf) {
+        const int nj = 2 * jb + hf;
+        const int j0 = nj * 16 + g4 * 4;
+        const f32x4 gj4 = *reinterpret_cast<const f32x4*>(&lds.gamma[j0]);
+        const f32x4 rkj4 = *reinterpret_cast<const f32x4*>(&lds.rk[j0]);
+        f32x4 pv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float dec = __expf(fminf(gi - gj4[e], 0.0f));
+          const float x = sqi * rkj4[e] * dec * pt[nj][e];
+          pv[e] = j0 + e <= i ? x : 0.0f;
+        }
+        split4(pv, hi[hf], lo[hf]);
       }
-      s16x4 hi, lo;
-      split4(pv, hi, lo);
-      const int bo = (wave * 4 + nj) * kBlk + lane * 4;
-      *reinterpret_cast<s16x4*>(slot16 + 2 * kSlotPh + bo) = hi;
-      *reinterpret_cast<s16x4*>(slot16 + 2 * kSlotPl + bo) = lo;
+      const int bo = (wave * 2 + jb) * kBlk + lane * 8;
+      *reinterpret_cast<s16x8*>(slot16 + 2 * kSlotPh + bo) = cat(hi[0], hi[1]);
+      *reinterpret_cast<s16x8*>(slot16 + 2 * kSlotPl + bo) = cat(lo[0], lo[1]);
     }
   }
   block_sync_lds();
@@ -531,10 +547,11 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
 
   // W = (T diag(beta e^gamma rk)) K (computed transposed, as K^T (T diag)^T,
   // so the result registers are in the scan's operand order) and U =
-  // (T diag(beta)) V with bf16 MFMA: the scaled T is split into hi + lo, K
-  // and V are exact bf16.  Wave `wave`
-  // computes column tiles 2 wave and 2 wave + 1 for all row blocks (inner
-  // blocks kb <= rb: T is lower triangular).
+  // (T diag(beta)) V with bf16 MFMA over 32-token blocks jb: the scaled T is
+  // split into hi + lo, K and V are exact bf16.  Wave `wave` computes column
+  // tiles 2 wave and 2 wave + 1 (one 32-wide k block of W) for all row
+  // blocks; T is lower triangular, so token block 1 only meets row blocks
+  // 2 and 3.
   {
     f32x4 w[4][2], u[4][2];
 #pragma unroll
@@ -545,31 +562,40 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
         u[rb][q2] = f32x4{0, 0, 0, 0};
       }
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const int j0 = kb * 16 + g4 * 4;
-      s16x4 bk[2], bv[2];
+    for (int jb = 0; jb < 2; ++jb) {
+      s16x8 bk[2], bv[2];
 #pragma unroll
       for (int q2 = 0; q2 < 2; ++q2) {
         const int cc = (2 * wave + q2) * 16 + col;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          bk[q2][e] = static_cast<short>(lds.K[(j0 + e) * kBfStride + cc]);
-          bv[q2][e] = static_cast<short>(lds.V[(j0 + e) * kBfStride + cc]);
+        for (int e = 0; e < 8; ++e) {
+          const int j = 32 * jb + k_of(g4, e);
+          bk[q2][e] = static_cast<short>(lds.K[j * kBfStride + cc]);
+          bv[q2][e] = static_cast<short>(lds.V[j * kBfStride + cc]);
         }
       }
-      f32x4 xs, ys;
+      f32x4 xs[2], ys[2];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int j = j0 + e;
-        ys[e] = lds.beta[j];
-        xs[e] = ys[e] * __expf(lds.gamma[j]) * lds.rk[j];
+      for (int hf = 0; hf < 2; ++hf) {
+        const int j0 = 32 * jb + 16 * hf + 4 * g4;
+        ys[hf] = *reinterpret_cast<const f32x4*>(&lds.beta[j0]);
+        const f32x4 gj = *reinterpret_cast<const f32x4*>(&lds.gamma[j0]);
+        const f32x4 rkj = *reinterpret_cast<const f32x4*>(&lds.rk[j0]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xs[hf][e] = ys[hf][e] * __expf(gj[e]) * rkj[e];
       }
 #pragma unroll
-      for (int rb = kb; rb < 4; ++rb) {
-        const f32x4 tv = *reinterpret_cast<const f32x4*>(&lds.T[(rb * 16 + col) * kF64Stride + j0]);
-        s16x4 awh, awl, auh, aul;
-        split4(tv * xs, awh, awl);
-        split4(tv * ys, auh, aul);
+      for (int rb = 2 * jb; rb < 4; ++rb) {
+        const float* trow = &lds.T[(rb * 16 + col) * kF64Stride + 32 * jb + 4 * g4];
+        s16x4 wh[2], wl[2], uh[2], ul[2];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const f32x4 tv = *reinterpret_cast<const f32x4*>(trow + 16 * hf);
+          split4(tv * xs[hf], wh[hf], wl[hf]);
+          split4(tv * ys[hf], uh[hf], ul[hf]);
+        }
+        const s16x8 awh = cat(wh[0], wh[1]), awl = cat(wl[0], wl[1]);
+        const s16x8 auh = cat(uh[0], uh[1]), aul = cat(ul[0], ul[1]);
 #pragma unroll
         for (int q2 = 0; q2 < 2; ++q2) {
           // W^T tile (rows: key index, cols: token), U tile (rows: token)
@@ -580,20 +606,21 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
         }
       }
     }
-    // Each lane of a W^T tile holds W[16 rb + col][16 ct + 4 g + e]: the
-    // scan's A-operand items of lane `lane` in block (rb, ct).
+    // Lane (col, g) of W^T tile (rb, 2 wave + q2) holds W[16 rb + col][32
+    // wave + 16 q2 + 4 g + e]: items 4 q2 + e of the scan's operand block
+    // (rb, wave).
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
+      s16x4 hi[2], lo[2];
 #pragma unroll
       for (int q2 = 0; q2 < 2; ++q2) {
-        const int ct = 2 * wave + q2;
-        s16x4 hi, lo;
-        split4(w[rb][q2], hi, lo);
-        const int bo = (rb * 8 + ct) * kBlk + lane * 4;
-        *reinterpret_cast<s16x4*>(slot16 + 2 * kSlotWh + bo) = hi;
-        *reinterpret_cast<s16x4*>(slot16 + 2 * kSlotWl + bo) = lo;
-        *reinterpret_cast<f32x4*>(slot + kSlotU + ((rb * 8 + ct) * 64 + lane) * 4) = u[rb][q2];
+        split4(w[rb][q2], hi[q2], lo[q2]);
+        *reinterpret_cast<f32x4*>(slot + kSlotU + ((rb * 8 + 2 * wave + q2) * 64 + lane) * 4) =
+            u[rb][q2];
       }
+      const int bo = (rb * 4 + wave) * kBlk + lane * 8;
+      *reinterpret_cast<s16x8*>(slot16 + 2 * kSlotWh + bo) = cat(hi[0], hi[1]);
+      *reinterpret_cast<s16x8*>(slot16 + 2 * kSlotWl + bo) = cat(lo[0], lo[1]);
     }
   }
 
@@ -606,26 +633,27 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
     slot[kSlotGl + lane] = __expf(gl);
   }
 
-  // K^T (A operand of the scan's state update: rows = key index, inner =
-  // token), in operand order, 8 bytes per store; rows past the chunk's end
-  // are zero.
+  // K^T (A operand of the scan's state update: rows = key index, k =
+  // token), in operand order, 16 bytes per store; rows past the chunk's end
+  // are zero.  A wave reads 64 consecutive keys of one token row at a time.
 #pragma unroll
-  for (int it = 0; it < kDim * (kChunk / 4) / kThreads; ++it) {
+  for (int it = 0; it < kDim * 8 / kThreads; ++it) {
     const int idx = threadIdx.x + it * kThreads;
     const int kc = idx & (kDim - 1);         // key index 0..127
-    const int i0 = (idx >> 7) * 4;           // first of 4 tokens
-    s16x4 v4;
+    const int jg = idx >> 7;                 // token block jb = jg / 4, lane group jg % 4
+    s16x8 v8;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v4[e] = static_cast<short>(lds.K[(i0 + e) * kBfStride + kc]);
-    *reinterpret_cast<s16x4*>(slot16 + 2 * kSlotKt + ((kc >> 4) * 4 + (i0 >> 4)) * kBlk +
-                              blk_off(kc, i0)) = v4;
+    for (int e = 0; e < 8; ++e)
+      v8[e] = static_cast<short>(lds.K[(32 * (jg >> 2) + k_of(jg & 3, e)) * kBfStride + kc]);
+    *reinterpret_cast<s16x8*>(slot16 + 2 * kSlotKt + ((kc >> 4) * 2 + (jg >> 2)) * kBlk +
+                              ((kc & 15) + 16 * (jg & 3)) * 8) = v8;
   }
 }
 
 // ---------------------------------------------------------------------------
 // 3. sequential scan over the chunks of a sequence
 // ---------------------------------------------------------------------------
-// Every product is a bf16 MFMA (16x16x16); fp32 operands enter split into
+// Every product is a bf16 MFMA (16x16x32); fp32 operands enter split into
 // hi + lo and a product x y is hi_x hi_y + hi_x lo_y + lo_x hi_y (the lo lo
 // term is ~2^-16 relative and dropped); q and k are bf16 already.  The state
 // slice and Delta are split once per chunk by the wave that owns them and
@@ -646,34 +674,35 @@ struct ScanLds {
 // Per-lane operands of one chunk, loaded ahead of use.
 template <int NT>
 struct ScanOps {
-  s16x4 wh[8], wl[8];   // W rows 16 wave + (lane % 16), k = 16 m + 4 g .. +3
-  s16x4 q[8];           // Q rows (the slot's copy), same k
-  s16x4 ph[4], pl[4];   // P rows, i = 16 m + 4 g .. +3
+  s16x8 wh[4], wl[4];   // W rows 16 wave + (lane % 16), k block m (keys)
+  s16x8 q[4];           // Q rows (the slot's copy), same k
+  s16x8 ph[2], pl[2];   // P rows 16 wave + (lane % 16), k block m (tokens)
   f32x4 u[NT];          // U rows 16 wave + 4 g + e, columns of the NT tiles
-  f32x4 qs, ks;         // row scales of the same rows
+  f32x4 ks;             // row scales of the same rows
+  float qs;             // output row scale of row 16 wave + (lane % 16)
   float gl;             // chunk decay e^gamma_C
-  s16x4 kt[2][4];       // K^T rows 32 wave + 16 t + lane % 16, tokens 16 m + 4 g .. +3
+  s16x8 kt[2][2];       // K^T rows 32 wave + 16 t + lane % 16, k block m (tokens)
 };
 
-__device__ __forceinline__ s16x4 ld_s16x4(const uint16_t* ptr) {
-  return *reinterpret_cast<const s16x4*>(ptr);
+__device__ __forceinline__ s16x8 ld_s16x8(const uint16_t* ptr) {
+  return *reinterpret_cast<const s16x8*>(ptr);
 }
 
 // Loads of one chunk's operands from its workspace slot.  Every load is
 // unconditional and in straight-line code so that the compiler can count the
 // loads in flight and wait only for the ones a use needs (a load under a
-// branch makes it drain every outstanding load); all of them are 512-byte
-// (or 1 KiB) contiguous wave accesses in the slot's operand order.
+// branch makes it drain every outstanding load); all of them are 1 KiB
+// contiguous wave accesses in the slot's operand order.
 template <int NT>
 __device__ __forceinline__ void load_w_q_u(const float* slot, int tile0, int wave, int lane,
                                            int g4, ScanOps<NT>& o) {
   const uint16_t* slot16 = reinterpret_cast<const uint16_t*>(slot);
 #pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    const int bo = (wave * 8 + m) * kBlk + lane * 4;
-    o.wh[m] = ld_s16x4(slot16 + 2 * kSlotWh + bo);
-    o.wl[m] = ld_s16x4(slot16 + 2 * kSlotWl + bo);
-    o.q[m] = ld_s16x4(slot16 + 2 * kSlotQ + bo);
+  for (int m = 0; m < 4; ++m) {
+    const int bo = (wave * 4 + m) * kBlk + lane * 8;
+    o.wh[m] = ld_s16x8(slot16 + 2 * kSlotWh + bo);
+    o.wl[m] = ld_s16x8(slot16 + 2 * kSlotWl + bo);
+    o.q[m] = ld_s16x8(slot16 + 2 * kSlotQ + bo);
   }
 #pragma unroll
   for (int cq = 0; cq < NT; ++cq)
@@ -683,16 +712,16 @@ __device__ __forceinline__ void load_w_q_u(const float* slot, int tile0, int wav
 }
 
 template <int NT>
-__device__ __forceinline__ void load_p_qs(const float* slot, int wave, int lane, int g4,
+__device__ __forceinline__ void load_p_qs(const float* slot, int wave, int lane,
                                           ScanOps<NT>& o) {
   const uint16_t* slot16 = reinterpret_cast<const uint16_t*>(slot);
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const int bo = (wave * 4 + m) * kBlk + lane * 4;
-    o.ph[m] = ld_s16x4(slot16 + 2 * kSlotPh + bo);
-    o.pl[m] = ld_s16x4(slot16 + 2 * kSlotPl + bo);
+  for (int m = 0; m < 2; ++m) {
+    const int bo = (wave * 2 + m) * kBlk + lane * 8;
+    o.ph[m] = ld_s16x8(slot16 + 2 * kSlotPh + bo);
+    o.pl[m] = ld_s16x8(slot16 + 2 * kSlotPl + bo);
   }
-  o.qs = *reinterpret_cast<const f32x4*>(slot + kSlotQs + wave * 16 + g4 * 4);
+  o.qs = slot[kSlotQs + wave * 16 + (lane & 15)];
   o.gl = slot[kSlotGl];
 }
 
@@ -702,8 +731,8 @@ __device__ __forceinline__ void load_kt(const float* slot, int wave, int lane, S
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
 #pragma unroll
-    for (int m = 0; m < 4; ++m)
-      o.kt[t][m] = ld_s16x4(slot16 + 2 * kSlotKt + ((wave * 2 + t) * 4 + m) * kBlk + lane * 4);
+    for (int m = 0; m < 2; ++m)
+      o.kt[t][m] = ld_s16x8(slot16 + 2 * kSlotKt + ((wave * 2 + t) * 2 + m) * kBlk + lane * 8);
   }
 }
 
@@ -766,7 +795,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Params p) {
   ScanOps<NT> op;
   load_kt(slot_base, wave, lane, op);
   load_w_q_u(slot_base, tile0, wave, lane, g4, op);
-  load_p_qs(slot_base, wave, lane, g4, op);
+  load_p_qs(slot_base, wave, lane, op);
 
   for (int ci = 0; ci < nchunks; ++ci) {
     const int t0 = start + ci * kChunk;
@@ -790,7 +819,8 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Params p) {
       }
     block_sync_lds();
 
-    // B. Delta rows 16 wave .. +15 = U - W S, and Q S for the output rows;
+    // B. Delta rows 16 wave .. +15 = U - W S, and (Q S)^T for the output
+    // rows (S^T Q^T: the state fragment is the A operand, Q the B operand);
     // two accumulators per product halve the dependent MFMA chains
     f32x4 ws0[NT], ws1[NT], qs0[NT], qs1[NT];
 #pragma unroll
@@ -798,21 +828,20 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Params p) {
       ws0[cq] = ws1[cq] = qs0[cq] = qs1[cq] = f32x4{0, 0, 0, 0};
     }
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      const int kb = m * 16 + g4 * 4;
+    for (int m = 0; m < 4; ++m) {
 #pragma unroll
       for (int cq = 0; cq < NT; ++cq) {
-        const int so = (cq * 16 + col) * kStStride + kb;
-        const s16x4 sh = ld_s16x4(&lds.Sh[so]);
-        const s16x4 sl = ld_s16x4(&lds.Sl[so]);
+        const int so = (cq * 16 + col) * kStStride;
+        const s16x8 sh = frag(&lds.Sh[so], m, g4);
+        const s16x8 sl = frag(&lds.Sl[so], m, g4);
         ws0[cq] = mfma_bf16(op.wh[m], sh, ws0[cq]);
         ws1[cq] = mfma_bf16(op.wh[m], sl, ws1[cq]);
         ws0[cq] = mfma_bf16(op.wl[m], sh, ws0[cq]);
-        qs0[cq] = mfma_bf16(op.q[m], sh, qs0[cq]);
-        qs1[cq] = mfma_bf16(op.q[m], sl, qs1[cq]);
+        qs0[cq] = mfma_bf16(sh, op.q[m], qs0[cq]);
+        qs1[cq] = mfma_bf16(sl, op.q[m], qs1[cq]);
       }
     }
-    f32x4 qsum[NT];
+    f32x4 qsum[NT];       // (Q S)^T: lane (row i, g) holds columns 4 g + e
 #pragma unroll
     for (int cq = 0; cq < NT; ++cq) {
       const f32x4 ws = ws0[cq] + ws1[cq];
@@ -835,39 +864,38 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Params p) {
     load_w_q_u(slot_next, tile0, wave, lane, g4, op);
     block_sync_lds();
 
-    // C. output rows: qs (.) (Q S) + P Delta
+    // C. output rows, transposed: qs (.) (Q S)^T + Delta^T P^T; lane (row
+    // i, g) ends with columns 4 g .. +3 of token row 16 wave + i, stored as
+    // one 8-byte piece
+    const int orow = wave * 16 + col;
 #pragma unroll
     for (int cq = 0; cq < NT; ++cq) {
       f32x4 pd0 = {0, 0, 0, 0}, pd1 = {0, 0, 0, 0};
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const int dof = (cq * 16 + col) * kDtStride + m * 16 + g4 * 4;
-        const s16x4 dh = ld_s16x4(&lds.Dh[dof]);
-        const s16x4 dl = ld_s16x4(&lds.Dl[dof]);
-        pd0 = mfma_bf16(op.ph[m], dh, pd0);
-        pd1 = mfma_bf16(op.ph[m], dl, pd1);
-        pd0 = mfma_bf16(op.pl[m], dh, pd0);
+      for (int m = 0; m < 2; ++m) {
+        const int dof = (cq * 16 + col) * kDtStride;
+        const s16x8 dh = frag(&lds.Dh[dof], m, g4);
+        const s16x8 dl = frag(&lds.Dl[dof], m, g4);
+        pd0 = mfma_bf16(dh, op.ph[m], pd0);
+        pd1 = mfma_bf16(dl, op.ph[m], pd1);
+        pd0 = mfma_bf16(dh, op.pl[m], pd0);
       }
       const f32x4 pd = pd0 + pd1;
-      uint16_t ob[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) ob[e] = f32_to_bf16(fmaf(op.qs[e], qsum[cq][e], pd[e]));
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int i = wave * 16 + g4 * 4 + e;
-        if (i < n)
-          p.out[((static_cast<size_t>(t0) + i) * p.HV + hv) * kDim + v0 + cq * 16 + col] = ob[e];
-      }
+      const u32x2 ob = {pack_bf16x2(fmaf(op.qs, qsum[cq][0], pd[0]), fmaf(op.qs, qsum[cq][1], pd[1])),
+                        pack_bf16x2(fmaf(op.qs, qsum[cq][2], pd[2]), fmaf(op.qs, qsum[cq][3], pd[3]))};
+      if (orow < n)
+        *reinterpret_cast<u32x2*>(p.out + ((static_cast<size_t>(t0) + orow) * p.HV + hv) * kDim +
+                                  v0 + cq * 16 + g4 * 4) = ob;
     }
 
     // D. state rows 32 wave .. +31: S = e^gamma_C S + K^T (ks (.) Delta)
     const float gl = op.gl;
-    s16x4 kt[2][4];
+    s16x8 kt[2][2];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int m = 0; m < 4; ++m) kt[t][m] = op.kt[t][m];
-    load_p_qs(slot_next, wave, lane, g4, op);
+      for (int m = 0; m < 2; ++m) kt[t][m] = op.kt[t][m];
+    load_p_qs(slot_next, wave, lane, op);
     load_kt(slot_next, wave, lane, op);
 #pragma unroll
     for (int t = 0; t < 2; ++t)
@@ -876,10 +904,10 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Params p) {
         f32x4 acc0 = st[t][cq] * gl;
         f32x4 acc1 = {0, 0, 0, 0};
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          const int eo = (cq * 16 + col) * kDtStride + m * 16 + g4 * 4;
-          acc0 = mfma_bf16(kt[t][m], ld_s16x4(&lds.Eh[eo]), acc0);
-          acc1 = mfma_bf16(kt[t][m], ld_s16x4(&lds.El[eo]), acc1);
+        for (int m = 0; m < 2; ++m) {
+          const int eo = (cq * 16 + col) * kDtStride;
+          acc0 = mfma_bf16(kt[t][m], frag(&lds.Eh[eo], m, g4), acc0);
+          acc1 = mfma_bf16(kt[t][m], frag(&lds.El[eo], m, g4), acc1);
         }
         st[t][cq] = acc0 + acc1;
       }
