@@ -46,14 +46,14 @@ ABI_VERSION = 3
 
 _S = ctypes.c_size_t
 PREFILL_SIGNATURES = {
-    "gdn_prefill_workspace_bytes": (_S, [_I, _I, _I]),
+    "gdn_prefill_workspace_bytes": (_S, [_I, _I, _I, _I]),
     "gdn_prefill": (
         _I,
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P] + [_I] * 7 + [_P, _S, _P],
     ),
     "gdn_prefill_abi_version": (_I, []),
 }
-PREFILL_ABI_VERSION = 1
+PREFILL_ABI_VERSION = 2
 
 _lock = threading.Lock()
 _lib = None

@@ -81,10 +81,14 @@ constexpr int kSlotPl = kSlotPh + 8 * kBlk / 2;       //   P = scale rq_i rk_j M
 constexpr int kSlotQs = kSlotPl + 8 * kBlk / 2;       // scale * rq_i e^gamma_i [64]
 constexpr int kSlotKs = kSlotQs + kChunk;             // rk_i e^(gamma_C - gamma_i) [64]
 constexpr int kSlotGl = kSlotKs + kChunk;             // e^gamma_C [1], padded to 64
-constexpr int kSlotKt = kSlotGl + 64;                 // K^T: blocks (key blk 0..7, token blk 0..1)
-constexpr int kSlotQ = kSlotKt + 16 * kBlk / 2;       // Q: blocks (token blk 0..3, k blk 0..3)
-constexpr int kSlotFloats = kSlotQ + 16 * kBlk / 2;
+constexpr int kSlotFloats = kSlotGl + 64;
 static_assert(kSlotFloats % 64 == 0, "slots stay 256-byte aligned");
+// Slot of one (chunk, q/k head), shared by the v-heads of the group: K^T and
+// the copy of Q, written by the group's first v-head.
+constexpr int kQkSlotKt = 0;                          // K^T: blocks (key blk 0..7, token blk 0..1)
+constexpr int kQkSlotQ = kQkSlotKt + 16 * kBlk / 2;   // Q: blocks (token blk 0..3, k blk 0..3)
+constexpr int kQkSlotFloats = kQkSlotQ + 16 * kBlk / 2;
+static_assert(kQkSlotFloats % 64 == 0, "slots stay 256-byte aligned");
 
 // k (0..31) of item e of lane group g inside a 32-long block.
 __host__ __device__ constexpr int k_of(int g, int e) { return 16 * (e >> 2) + 4 * g + (e & 3); }
@@ -160,7 +164,8 @@ struct Params {
   const int32_t* offs;       // [N + 1] first chunk slot of each sequence (workspace)
   const i32x4* slot_info;    // [max_slots] per chunk slot: sequence, first token, tokens
                              // (0 past the last slot) (workspace)
-  float* slots;              // [slots, HV, kSlotFloats] (workspace)
+  float* slots;              // [max_slots, HV, kSlotFloats] (workspace)
+  float* qk_slots;           // [max_slots, H, kQkSlotFloats] (workspace)
   float scale;
   int L;
   int N;
@@ -337,6 +342,10 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
   const int g4 = lane >> 4;
   float* slot = p.slots + (static_cast<size_t>(c) * p.HV + hv) * kSlotFloats;
   uint16_t* slot16 = reinterpret_cast<uint16_t*>(slot);
+  // the group's first v-head writes the shared Q copy and K^T
+  const bool qk_writer = hv == h * p.ratio;
+  uint16_t* qk16 =
+      reinterpret_cast<uint16_t*>(p.qk_slots + (static_cast<size_t>(c) * p.H + h) * kQkSlotFloats);
 
   // Every input load of the chunk is issued before the first is waited on.
   u32x4 kreg[4], vreg[4];
@@ -384,7 +393,8 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
         const float x = bf16_to_f32(static_cast<uint16_t>(qa[m][e]));
         sq = fmaf(x, x, sq);
       }
-      *reinterpret_cast<s16x8*>(slot16 + 2 * kSlotQ + (wave * 4 + m) * kBlk + lane * 8) = qa[m];
+      if (qk_writer)
+        *reinterpret_cast<s16x8*>(qk16 + 2 * kQkSlotQ + (wave * 4 + m) * kBlk + lane * 8) = qa[m];
     }
     sq += __shfl_xor(sq, 16, 64);
     sq += __shfl_xor(sq, 32, 64);
@@ -636,6 +646,7 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
   // K^T (A operand of the scan's state update: rows = key index, k =
   // token), in operand order, 16 bytes per store; rows past the chunk's end
   // are zero.  A wave reads 64 consecutive keys of one token row at a time.
+  if (!qk_writer) return;                          // uniform per workgroup
 #pragma unroll
   for (int it = 0; it < kDim * 8 / kThreads; ++it) {
     const int idx = threadIdx.x + it * kThreads;
@@ -645,7 +656,7 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
 #pragma unroll
     for (int e = 0; e < 8; ++e)
       v8[e] = static_cast<short>(lds.K[(32 * (jg >> 2) + k_of(jg & 3, e)) * kBfStride + kc]);
-    *reinterpret_cast<s16x8*>(slot16 + 2 * kSlotKt + ((kc >> 4) * 2 + (jg >> 2)) * kBlk +
+    *reinterpret_cast<s16x8*>(qk16 + 2 * kQkSlotKt + ((kc >> 4) * 2 + (jg >> 2)) * kBlk +
                               ((kc & 15) + 16 * (jg & 3)) * 8) = v8;
   }
 }
@@ -694,15 +705,16 @@ __device__ __forceinline__ s16x8 ld_s16x8(const uint16_t* ptr) {
 // branch makes it drain every outstanding load); all of them are 1 KiB
 // contiguous wave accesses in the slot's operand order.
 template <int NT>
-__device__ __forceinline__ void load_w_q_u(const float* slot, int tile0, int wave, int lane,
-                                           int g4, ScanOps<NT>& o) {
+__device__ __forceinline__ void load_w_q_u(const float* slot, const float* qk, int tile0,
+                                           int wave, int lane, int g4, ScanOps<NT>& o) {
   const uint16_t* slot16 = reinterpret_cast<const uint16_t*>(slot);
+  const uint16_t* qk16 = reinterpret_cast<const uint16_t*>(qk);
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     const int bo = (wave * 4 + m) * kBlk + lane * 8;
     o.wh[m] = ld_s16x8(slot16 + 2 * kSlotWh + bo);
     o.wl[m] = ld_s16x8(slot16 + 2 * kSlotWl + bo);
-    o.q[m] = ld_s16x8(slot16 + 2 * kSlotQ + bo);
+    o.q[m] = ld_s16x8(qk16 + 2 * kQkSlotQ + bo);
   }
 #pragma unroll
   for (int cq = 0; cq < NT; ++cq)
@@ -726,13 +738,13 @@ __device__ __forceinline__ void load_p_qs(const float* slot, int wave, int lane,
 }
 
 template <int NT>
-__device__ __forceinline__ void load_kt(const float* slot, int wave, int lane, ScanOps<NT>& o) {
-  const uint16_t* slot16 = reinterpret_cast<const uint16_t*>(slot);
+__device__ __forceinline__ void load_kt(const float* qk, int wave, int lane, ScanOps<NT>& o) {
+  const uint16_t* qk16 = reinterpret_cast<const uint16_t*>(qk);
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
 #pragma unroll
     for (int m = 0; m < 2; ++m)
-      o.kt[t][m] = ld_s16x8(slot16 + 2 * kSlotKt + ((wave * 2 + t) * 2 + m) * kBlk + lane * 8);
+      o.kt[t][m] = ld_s16x8(qk16 + 2 * kQkSlotKt + ((wave * 2 + t) * 2 + m) * kBlk + lane * 8);
   }
 }
 
@@ -791,10 +803,13 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Params p) {
   }
   const float* slot_base = p.slots + (static_cast<size_t>(p.offs[s]) * p.HV + hv) * kSlotFloats;
   const size_t slot_step = static_cast<size_t>(p.HV) * kSlotFloats;
+  const float* qk_base =
+      p.qk_slots + (static_cast<size_t>(p.offs[s]) * p.H + hv / p.ratio) * kQkSlotFloats;
+  const size_t qk_step = static_cast<size_t>(p.H) * kQkSlotFloats;
 
   ScanOps<NT> op;
-  load_kt(slot_base, wave, lane, op);
-  load_w_q_u(slot_base, tile0, wave, lane, g4, op);
+  load_kt(qk_base, wave, lane, op);
+  load_w_q_u(slot_base, qk_base, tile0, wave, lane, g4, op);
   load_p_qs(slot_base, wave, lane, op);
 
   for (int ci = 0; ci < nchunks; ++ci) {
@@ -803,6 +818,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Params p) {
     // operands of the next chunk, or of this one again after the last
     const int cn = ci + 1 < nchunks ? ci + 1 : ci;
     const float* slot_next = slot_base + cn * slot_step;
+    const float* qk_next = qk_base + cn * qk_step;
 
     // A. state slice (split) into LDS.  No barrier is needed before these
     // writes: the previous chunk's reads of Sh / Sl (step B) precede its
@@ -861,7 +877,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Params p) {
       *reinterpret_cast<s16x4*>(&lds.Eh[dof]) = hi;
       *reinterpret_cast<s16x4*>(&lds.El[dof]) = lo;
     }
-    load_w_q_u(slot_next, tile0, wave, lane, g4, op);
+    load_w_q_u(slot_next, qk_next, tile0, wave, lane, g4, op);
     block_sync_lds();
 
     // C. output rows, transposed: qs (.) (Q S)^T + Delta^T P^T; lane (row
@@ -896,7 +912,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Params p) {
 #pragma unroll
       for (int m = 0; m < 2; ++m) kt[t][m] = op.kt[t][m];
     load_p_qs(slot_next, wave, lane, op);
-    load_kt(slot_next, wave, lane, op);
+    load_kt(qk_next, wave, lane, op);
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -930,16 +946,21 @@ size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 long long max_slots(long long L, long long N) { return (L + kChunk - 1) / kChunk + N; }
 
 // Workspace: chunk offsets [N + 1] int32, slot table [max_slots] x 16 bytes,
-// then the slots [max_slots, HV, kSlotFloats] fp32; each part 256-byte aligned.
+// the v-head slots [max_slots, HV, kSlotFloats] fp32, then the q/k-head
+// slots [max_slots, H, kQkSlotFloats]; each part 256-byte aligned.
 size_t offsets_bytes(long long N) { return align256(static_cast<size_t>(N + 1) * sizeof(int32_t)); }
 
 size_t slot_info_bytes(long long L, long long N) {
   return align256(static_cast<size_t>(max_slots(L, N)) * sizeof(i32x4));
 }
 
-size_t workspace_bytes(long long L, long long N, long long HV) {
-  return offsets_bytes(N) + slot_info_bytes(L, N) +
-         static_cast<size_t>(max_slots(L, N)) * HV * kSlotFloats * sizeof(float);
+size_t slots_bytes(long long L, long long N, long long HV) {
+  return static_cast<size_t>(max_slots(L, N)) * HV * kSlotFloats * sizeof(float);
+}
+
+size_t workspace_bytes(long long L, long long N, long long H, long long HV) {
+  return offsets_bytes(N) + slot_info_bytes(L, N) + slots_bytes(L, N, HV) +
+         static_cast<size_t>(max_slots(L, N)) * H * kQkSlotFloats * sizeof(float);
 }
 
 }  // namespace gdn_pf
@@ -948,9 +969,9 @@ using namespace gdn_pf;
 
 extern "C" {
 
-size_t gdn_prefill_workspace_bytes(int total_seq_len, int num_seqs, int HV) {
-  if (total_seq_len < 0 || num_seqs < 0 || HV <= 0) return 0;
-  return workspace_bytes(total_seq_len, num_seqs, HV);
+size_t gdn_prefill_workspace_bytes(int total_seq_len, int num_seqs, int H, int HV) {
+  if (total_seq_len < 0 || num_seqs < 0 || H <= 0 || HV <= 0 || HV % H != 0) return 0;
+  return workspace_bytes(total_seq_len, num_seqs, H, HV);
 }
 
 int gdn_prefill(const void* q, const void* k, const void* v, const float* state,
@@ -968,7 +989,7 @@ int gdn_prefill(const void* q, const void* k, const void* v, const float* state,
     return hipErrorInvalidValue;
   if (total_seq_len > 0 && (!q || !k || !v || !a || !b || !output))
     return hipErrorInvalidValue;
-  if (workspace_size < workspace_bytes(total_seq_len, num_seqs, HV)) return hipErrorInvalidValue;
+  if (workspace_size < workspace_bytes(total_seq_len, num_seqs, H, HV)) return hipErrorInvalidValue;
   if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(output, 16) ||
       !aligned(new_state, 16) || !aligned(state, 16) || !aligned(workspace, 256) ||
       !aligned(A_log, 4) || !aligned(dt_bias, 4) || !aligned(cu_seqlens, 4) ||
@@ -1007,6 +1028,8 @@ int gdn_prefill(const void* q, const void* k, const void* v, const float* state,
   p.slot_info = slot_info;
   p.slots = reinterpret_cast<float*>(ws + offsets_bytes(num_seqs) +
                                      slot_info_bytes(total_seq_len, num_seqs));
+  p.qk_slots = reinterpret_cast<float*>(reinterpret_cast<char*>(p.slots) +
+                                        slots_bytes(total_seq_len, num_seqs, HV));
   p.scale = scale;
   p.L = total_seq_len;
   p.N = num_seqs;
@@ -1041,6 +1064,6 @@ int gdn_prefill(const void* q, const void* k, const void* v, const float* state,
   return hipGetLastError();
 }
 
-int gdn_prefill_abi_version(void) { return 1; }
+int gdn_prefill_abi_version(void) { return 2; }
 
 }  // extern "C"

@@ -38,12 +38,12 @@ from .kernel import K_DIM, V_DIM, _expect, _overlap, resolve_scale
 __all__ = ["prefill_run", "kernel_prefill_hip", "workspace_bytes"]
 
 
-def workspace_bytes(total_seq_len: int, num_seqs: int, HV: int) -> int:
+def workspace_bytes(total_seq_len: int, num_seqs: int, H: int, HV: int) -> int:
     """Device workspace bytes a prefill of this size needs."""
     n = _lib.get_prefill_lib().gdn_prefill_workspace_bytes(int(total_seq_len), int(num_seqs),
-                                                          int(HV))
+                                                          int(H), int(HV))
     if n == 0:
-        raise ValueError(f"invalid prefill sizes L={total_seq_len}, N={num_seqs}, HV={HV}")
+        raise ValueError(f"invalid prefill sizes L={total_seq_len}, N={num_seqs}, H={H}, HV={HV}")
     return n
 
 
@@ -114,7 +114,7 @@ def kernel_prefill_hip(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, 
     if cu_seqlens.dtype != torch.int32:
         cu_seqlens = cu_seqlens.to(torch.int32)
     lib = _lib.get_prefill_lib()
-    ws_bytes = workspace_bytes(L, N, HV)
+    ws_bytes = workspace_bytes(L, N, H, HV)
     workspace = torch.empty(ws_bytes + 256, dtype=torch.uint8, device=q.device)
     ws_ptr = (workspace.data_ptr() + 255) & ~255
     stream = torch.cuda.current_stream(q.device).cuda_stream

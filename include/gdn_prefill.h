@@ -44,14 +44,15 @@ extern "C" {
 
 /*
  * Bytes of device workspace gdn_prefill needs for L total tokens, N
- * sequences and HV v-heads (per-chunk intermediates: about 113 KiB per 64
- * tokens per v-head, plus 64-token slack per sequence; a 16-byte table entry
- * per chunk and 4 bytes per sequence).  0 for invalid sizes.
+ * sequences, H q/k heads and HV v-heads (per-chunk intermediates: about
+ * 81 KiB per 64 tokens per v-head and 32 KiB per 64 tokens per q/k head,
+ * with 64-token slack per sequence; a 16-byte table entry per chunk and 4
+ * bytes per sequence).  0 for invalid sizes.
  * The reference's FLA path allocates its intermediates per call inside
  * chunk_gated_delta_rule (solution/triton/fla_prefill_code.py:1726-1776);
  * here the caller provides them.
  */
-size_t gdn_prefill_workspace_bytes(int total_seq_len, int num_seqs, int HV);
+size_t gdn_prefill_workspace_bytes(int total_seq_len, int num_seqs, int H, int HV);
 
 /*
  * One prefill over all sequences.  Replaces the reference's prefill entry
@@ -72,7 +73,7 @@ int gdn_prefill(const void* q, const void* k, const void* v, const float* state,
                 int use_qk_l2norm, void* workspace, size_t workspace_size,
                 void* hip_stream);
 
-/* ABI version of this header: 1. */
+/* ABI version of this header: 2 (1 had no H in gdn_prefill_workspace_bytes). */
 int gdn_prefill_abi_version(void);
 
 #ifdef __cplusplus

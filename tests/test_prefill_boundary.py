@@ -39,14 +39,18 @@ def test_header_and_library_agree():
 
 def test_workspace_size_formula():
     lib = _lib.get_prefill_lib()
-    slot = (2 * 64 * 128 + 64 * 64 + 3 * 64) * 4 + 2 * 128 * 64 * 2  # W U P scales K^T Q
-    for L, N, HV in ((6, 1, 8), (16384, 1, 8), (1000, 37, 32), (0, 3, 8)):
+    vslot = (2 * 64 * 128 + 64 * 64 + 3 * 64) * 4        # per v-head: W hi/lo, U, P hi/lo, scales
+    qkslot = 2 * 128 * 64 * 2                             # per q/k head: K^T, Q copy (bf16)
+    for L, N, H, HV in ((6, 1, 4, 8), (16384, 1, 4, 8), (1000, 37, 16, 32), (0, 3, 4, 8),
+                        (100, 2, 2, 2)):
         chunks = (L + 63) // 64 + N
         offs = ((N + 1) * 4 + 255) // 256 * 256
         table = (chunks * 16 + 255) // 256 * 256                         # per-chunk slot table
-        assert lib.gdn_prefill_workspace_bytes(L, N, HV) == offs + table + chunks * HV * slot
-    assert lib.gdn_prefill_workspace_bytes(-1, 1, 8) == 0
-    assert lib.gdn_prefill_workspace_bytes(1, 1, 0) == 0
+        assert lib.gdn_prefill_workspace_bytes(L, N, H, HV) == (
+            offs + table + chunks * HV * vslot + chunks * H * qkslot)
+    assert lib.gdn_prefill_workspace_bytes(-1, 1, 4, 8) == 0
+    assert lib.gdn_prefill_workspace_bytes(1, 1, 4, 0) == 0
+    assert lib.gdn_prefill_workspace_bytes(1, 1, 3, 8) == 0              # HV % H != 0
 
 
 def test_c_side_validation_rejects_before_launching():
