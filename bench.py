@@ -31,7 +31,13 @@ step's dirty lines: the steady state of serving.  Prints ONE JSON line:
   states) and on an empty kernel, so that the decode times read against the
   floor of their own traffic;
 * ``cpu_baseline``: the reference's PyTorch-eager step (the oracle's
-  loop-for-loop restatement) timed on this host's cores on a bounded sample.
+  loop-for-loop restatement) timed on this host's cores on a bounded sample;
+* ``prefill``: the variable-length prefill workloads, each with the whole
+  call's time and its three kernels' times (events the library records
+  between its launches); ``prefill_roofline``: the largest workload's
+  algorithmic FLOP rate against the bf16 MFMA peak and its preparation
+  kernel's HBM rate; ``prefill_cpu_baseline``: the reference's prefill loop
+  (the oracle) on a bounded sample, in tokens/s.
 
 Algorithmic bytes per step: state read + write (B*HV*128*128*4*2, half that
 for a bf16 state), and per token q and k (2*B*H*128*2), v (B*HV*128*2),
@@ -60,6 +66,7 @@ from flashinfer_competition_codebase_amd import _lib  # noqa: E402
 
 METRIC = ("GDN decode µs/step at B=1; achieved HBM GB/s (% of peak) at B=256")
 PEAK_HBM_GBS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0      # dense bf16 MFMA, MI355X
 TRAFFIC_SUMMARY = ROOT / "profiles" / "gdn_decode_b256_qk16v32_traffic.json"
 
 # name -> (B, H, HV, use_qk_l2norm)
@@ -124,6 +131,12 @@ class KernelStamps:
         if self.hip.hipEventSynchronize(self.stop[i]) != 0:
             raise RuntimeError("hipEventSynchronize failed")
         if self.hip.hipEventElapsedTime(ctypes.byref(ms), self.start[i], self.stop[i]) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value * 1e3
+
+    def between_us(self, a, b) -> float:
+        ms = ctypes.c_float()
+        if self.hip.hipEventElapsedTime(ctypes.byref(ms), a, b) != 0:
             raise RuntimeError("hipEventElapsedTime failed")
         return ms.value * 1e3
 
@@ -388,12 +401,83 @@ def prefill_bytes(lens, H, HV) -> int:
             + N * HV * 128 * 128 * 4 * 2 + 2 * HV * 4 + (N + 1) * 4)
 
 
+def prefill_workspace_bytes(lens, H, HV) -> int:
+    """Bytes the preparation kernel writes: a v-head slot per (chunk, v-head)
+    (W and P as bf16 hi/lo, U fp32, row scales) and a q/k-head slot per
+    (chunk, q/k head) (K^T and the Q copy, bf16)."""
+    chunks = sum((n + 63) // 64 for n in lens)
+    vslot = (2 * 64 * 128 + 64 * 64 + 3 * 64) * 4
+    qkslot = 2 * 128 * 64 * 2
+    return chunks * (HV * vslot + H * qkslot)
+
+
+PREFILL_ROOFLINE_WORKLOAD = "prefill_qk16_v32_64x512"
+
+
+def prefill_roofline(prefill: dict) -> dict:
+    """Roofline of the largest prefill workload: its algorithmic FLOP rate
+    over the whole prefill (kernel time) against the bf16 dense MFMA peak;
+    the preparation kernel's HBM bytes (inputs read + workspace written) per
+    its time against the HBM peak."""
+    r = prefill[PREFILL_ROOFLINE_WORKLOAD]
+    lens_h = PREFILL_CONFIGS[PREFILL_ROOFLINE_WORKLOAD]
+    lens, H, HV = lens_h
+    chunks = sum((n + 63) // 64 for n in lens)
+    flop = chunks * HV * PREFILL_FLOP_PER_CHUNK_HEAD
+    ku = r["kernel_us"]
+    achieved = flop / (ku["kernels"] * 1e-6) / 1e12
+    L = sum(lens)
+    prep_in = L * (2 * H * 128 * 2 + HV * 128 * 2 + 2 * HV * 2)
+    prep_bytes = prep_in + r["prep_workspace_bytes"]
+    prep_gbs = prep_bytes / (ku["prep"] * 1e-6) / 1e9
+    return {"workload": PREFILL_ROOFLINE_WORKLOAD, "bound": "mfma",
+            "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+            "kernel_us": ku,
+            "prep": {"hbm_bytes": prep_bytes, "gbs": round(prep_gbs, 1),
+                     "frac_of_hbm_peak": round(prep_gbs / PEAK_HBM_GBS, 4)}}
+
+
+def prefill_cpu_baseline(seconds: float, gpu_tokens_per_s: float | None):
+    """The reference's prefill loop (prefill_loop, a restatement of
+    solution/triton/prefill_kernel.py:85-183) on this host's cores, on a
+    bounded sample of the 16 x 1024 qk4_v8 workload: one 256-token sequence,
+    repeated until about ``seconds`` of CPU work; and the 6-token workload."""
+    from oracle.gdn_prefill_oracle import make_prefill_inputs, prefill_loop
+
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    torch.set_num_threads(threads)
+    t = make_prefill_inputs([256], 4, 8, seed=5)
+    prefill_loop(**t)                              # warmup
+    reps, elapsed = 0, 0.0
+    t0 = time.perf_counter()
+    while elapsed < seconds:
+        prefill_loop(**t)
+        reps += 1
+        elapsed = time.perf_counter() - t0
+    tps = 256 * reps / elapsed
+    t6 = make_prefill_inputs([6], 4, 8, seed=6)
+    w0 = []
+    for _ in range(5):
+        s_ = time.perf_counter()
+        prefill_loop(**t6)
+        w0.append((time.perf_counter() - s_) * 1e6)
+    return {"value": round(tps, 1), "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": (f"one 256-token sequence of the 16 x 1024 qk4_v8 workload, {reps} "
+                       f"prefills in {elapsed:.1f} s"),
+            "gpu_tokens_per_s_same_workload": gpu_tokens_per_s,
+            "workload0_1x6_us": round(statistics.median(w0), 1)}
+
+
 def prefill_bench(device, iters: int = 20):
-    """Per prefill workload: median time of the whole prefill (its three
-    launches) from HIP event markers on the launch stream, algorithmic
-    TFLOP/s and GB/s.  Inputs: unit-norm q/k rows (the model's
+    """Per prefill workload: median time of the whole prefill call from
+    torch events around it, and of each of its three kernels from HIP events
+    the library records between its launches (gdn_prefill_timed);
+    algorithmic TFLOP/s and GB/s.  Inputs: unit-norm q/k rows (the model's
     normalisation), the decode benchmark's other distributions."""
     out = {}
+    stamps = KernelStamps(2 * iters)              # 4 events per timed prefill
     for name, (lens, H, HV) in PREFILL_CONFIGS.items():
         L, N = sum(lens), len(lens)
         g = torch.Generator(device=device).manual_seed(17)
@@ -425,14 +509,28 @@ def prefill_bench(device, iters: int = 20):
             b_.record(stream)
         torch.cuda.synchronize()
         us = statistics.median(a_.elapsed_time(b_) * 1e3 for a_, b_ in ev)
+        parts = {"offsets": [], "prep": [], "scan": [], "kernels": []}
+        for i in range(iters):
+            e4 = [stamps.start[2 * i], stamps.stop[2 * i], stamps.start[2 * i + 1],
+                  stamps.stop[2 * i + 1]]
+            gdn.kernel_prefill_hip_timed(**t, events=e4)
+            torch.cuda.synchronize()
+            d = [stamps.between_us(e4[j], e4[j + 1]) for j in range(3)]
+            for key, val in zip(("offsets", "prep", "scan"), d):
+                parts[key].append(val)
+            parts["kernels"].append(sum(d))
+        med = {key: statistics.median(v) for key, v in parts.items()}
         chunks = sum((n + 63) // 64 for n in lens)
         flop = chunks * HV * PREFILL_FLOP_PER_CHUNK_HEAD
         nb = prefill_bytes(lens, H, HV)
         out[name] = {"seqs": N, "tokens": L, "H": H, "HV": HV, "us": round(us, 2),
+                     "kernel_us": {key: round(v, 2) for key, v in med.items()},
                      "tflops": round(flop / (us * 1e-6) / 1e12, 2),
                      "gbs": round(nb / (us * 1e-6) / 1e9, 1),
-                     "tokens_per_s": round(L / (us * 1e-6), 1)}
+                     "tokens_per_s": round(L / (us * 1e-6), 1),
+                     "prep_workspace_bytes": prefill_workspace_bytes(lens, H, HV)}
         del t
+    stamps.close()
     return out
 
 
@@ -465,6 +563,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="b256_qk16_v32_l2", choices=list(CONFIGS))
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--prefill-cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-per-config", action="store_true")
     ap.add_argument("--iters", type=int, default=100,
@@ -488,7 +587,8 @@ def main():
         pmc_pass(device)
         return
     if args.prefill_only:
-        print(json.dumps({"prefill": prefill_bench(device)}), flush=True)
+        pf = prefill_bench(device)
+        print(json.dumps({"prefill": pf, "prefill_roofline": prefill_roofline(pf)}), flush=True)
         return
 
     log = lambda *a: print(*a, file=sys.stderr, flush=True)  # noqa: E731
@@ -551,11 +651,13 @@ def main():
         f"empty kernel {floor['empty_us']} us; B=256 state RMW {floor['b256_rmw_us']} us "
         f"({floor['b256_rmw_gbs']} GB/s)")
 
-    prefill = {}
+    prefill, prefill_rl = {}, None
     if not args.no_prefill:
         prefill = prefill_bench(device)
         for name, r in prefill.items():
-            log(f"[bench] {name}: {r['us']} us, {r['tflops']} TFLOP/s, {r['gbs']} GB/s")
+            log(f"[bench] {name}: {r['us']} us, {r['tflops']} TFLOP/s, {r['gbs']} GB/s, "
+                f"kernels {r['kernel_us']}")
+        prefill_rl = prefill_roofline(prefill)
 
     serving = b1_serving(device)
     log(f"[bench] B=1 serving, {serving['layers']} layer steps: eager "
@@ -563,11 +665,16 @@ def main():
     ref_stream = reference_stream(device)
     log(f"[bench] reference stream: {ref_stream['gbs']:.0f} GB/s ({ref_stream['us']} us)")
 
-    cpu = None
+    cpu, prefill_cpu = None, None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(args.cpu_seconds)
         log(f"[bench] cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads "
             f"({cpu['sample']}); B=1 {cpu['b1_us_per_step']} us/step")
+        if prefill:
+            prefill_cpu = prefill_cpu_baseline(
+                args.prefill_cpu_seconds, prefill["prefill_qk4_v8_16x1024"]["tokens_per_s"])
+            log(f"[bench] prefill cpu baseline: {prefill_cpu['value']} tokens/s "
+                f"({prefill_cpu['sample']})")
 
     b1 = per_config.get("b1_qk16_v32_l2")
     line = {
@@ -610,6 +717,8 @@ def main():
         "cpu_baseline": cpu,
         "per_config": per_config,
         "prefill": prefill,
+        "prefill_roofline": prefill_rl,
+        "prefill_cpu_baseline": prefill_cpu,
     }
     print(json.dumps(line), flush=True)
 

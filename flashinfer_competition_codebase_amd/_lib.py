@@ -51,9 +51,13 @@ PREFILL_SIGNATURES = {
         _I,
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P] + [_I] * 7 + [_P, _S, _P],
     ),
+    "gdn_prefill_timed": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P] + [_I] * 7 + [_P, _S, _P, _P],
+    ),
     "gdn_prefill_abi_version": (_I, []),
 }
-PREFILL_ABI_VERSION = 2
+PREFILL_ABI_VERSION = 3
 
 _lock = threading.Lock()
 _lib = None

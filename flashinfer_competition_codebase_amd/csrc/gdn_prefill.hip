@@ -967,19 +967,12 @@ size_t workspace_bytes(long long L, long long N, long long H, long long HV) {
 
 using namespace gdn_pf;
 
-extern "C" {
-
-size_t gdn_prefill_workspace_bytes(int total_seq_len, int num_seqs, int H, int HV) {
-  if (total_seq_len < 0 || num_seqs < 0 || H <= 0 || HV <= 0 || HV % H != 0) return 0;
-  return workspace_bytes(total_seq_len, num_seqs, H, HV);
-}
-
-int gdn_prefill(const void* q, const void* k, const void* v, const float* state,
+static int prefill_impl(const void* q, const void* k, const void* v, const float* state,
                 const float* A_log, const void* a, const float* dt_bias, const void* b,
                 const int32_t* cu_seqlens, float scale, void* output, float* new_state,
                 int total_seq_len, int num_seqs, int H, int HV, int K, int V,
                 int use_qk_l2norm, void* workspace, size_t workspace_size,
-                void* hip_stream) {
+                void* hip_stream, void* const* events) {
   if (total_seq_len < 0 || num_seqs < 0 || H <= 0 || HV <= 0 || HV % H != 0)
     return hipErrorInvalidValue;
   if (K != kDim || V != kDim) return hipErrorInvalidValue;
@@ -1040,9 +1033,16 @@ int gdn_prefill(const void* q, const void* k, const void* v, const float* state,
   p.max_slots = slots;
 
   hipStream_t stream = static_cast<hipStream_t>(hip_stream);
+  // events[i] (optional) is recorded before launch i and events[3] after the last
+  auto mark = [&](int i) -> hipError_t {
+    return events ? hipEventRecord(static_cast<hipEvent_t>(events[i]), stream) : hipSuccess;
+  };
+  hipError_t e = mark(0);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL(chunk_offsets_kernel, dim3(1), dim3(kThreads), 0, stream, p, offs,
                      slot_info);
-  hipError_t e = hipGetLastError();
+  e = hipGetLastError();
+  if (e == hipSuccess) e = mark(1);
   if (e != hipSuccess) return e;
   if (slots > 0) {
     hipLaunchKernelGGL(prep_kernel, dim3(static_cast<unsigned>(slots), HV), dim3(kThreads), 0,
@@ -1050,6 +1050,8 @@ int gdn_prefill(const void* q, const void* k, const void* v, const float* state,
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
+  e = mark(2);
+  if (e != hipSuccess) return e;
   // Two 16-column tiles per workgroup once there are enough heads to fill
   // the GPU with them (fewer redundant operand loads); one tile otherwise.
   const long long heads = static_cast<long long>(num_seqs) * HV;
@@ -1061,9 +1063,43 @@ int gdn_prefill(const void* q, const void* k, const void* v, const float* state,
     hipLaunchKernelGGL(scan_kernel<1>, dim3(static_cast<unsigned>(groups * 8 * 8)),
                        dim3(kThreads), 0, stream, p);
   }
-  return hipGetLastError();
+  e = hipGetLastError();
+  if (e == hipSuccess) e = mark(3);
+  return e;
 }
 
-int gdn_prefill_abi_version(void) { return 2; }
+extern "C" {
+
+size_t gdn_prefill_workspace_bytes(int total_seq_len, int num_seqs, int H, int HV) {
+  if (total_seq_len < 0 || num_seqs < 0 || H <= 0 || HV <= 0 || HV % H != 0) return 0;
+  return workspace_bytes(total_seq_len, num_seqs, H, HV);
+}
+
+int gdn_prefill(const void* q, const void* k, const void* v, const float* state,
+                const float* A_log, const void* a, const float* dt_bias, const void* b,
+                const int32_t* cu_seqlens, float scale, void* output, float* new_state,
+                int total_seq_len, int num_seqs, int H, int HV, int K, int V,
+                int use_qk_l2norm, void* workspace, size_t workspace_size,
+                void* hip_stream) {
+  return prefill_impl(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output,
+                      new_state, total_seq_len, num_seqs, H, HV, K, V, use_qk_l2norm, workspace,
+                      workspace_size, hip_stream, nullptr);
+}
+
+int gdn_prefill_timed(const void* q, const void* k, const void* v, const float* state,
+                      const float* A_log, const void* a, const float* dt_bias, const void* b,
+                      const int32_t* cu_seqlens, float scale, void* output, float* new_state,
+                      int total_seq_len, int num_seqs, int H, int HV, int K, int V,
+                      int use_qk_l2norm, void* workspace, size_t workspace_size,
+                      void* hip_stream, void* const* events) {
+  if (events == nullptr) return hipErrorInvalidValue;
+  for (int i = 0; i < 4; ++i)
+    if (events[i] == nullptr) return hipErrorInvalidValue;
+  return prefill_impl(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output,
+                      new_state, total_seq_len, num_seqs, H, HV, K, V, use_qk_l2norm, workspace,
+                      workspace_size, hip_stream, events);
+}
+
+int gdn_prefill_abi_version(void) { return 3; }
 
 }  // extern "C"

@@ -30,12 +30,14 @@ off by default as in the reference's prefill (prefill_kernel.py:45).
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
 from .kernel import K_DIM, V_DIM, _expect, _overlap, resolve_scale
 
-__all__ = ["prefill_run", "kernel_prefill_hip", "workspace_bytes"]
+__all__ = ["prefill_run", "kernel_prefill_hip", "kernel_prefill_hip_timed", "workspace_bytes"]
 
 
 def workspace_bytes(total_seq_len: int, num_seqs: int, H: int, HV: int) -> int:
@@ -104,6 +106,25 @@ def kernel_prefill_hip(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, 
     """Destination-passing prefill (reference DPS form,
     solution/triton/prefill_kernel.py:10-58): writes ``output`` and
     ``new_state``; ``new_state is state`` updates in place."""
+    _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new_state,
+            use_qk_l2norm, None)
+
+
+@torch.no_grad()
+def kernel_prefill_hip_timed(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output,
+                             new_state, events, *, use_qk_l2norm: bool = False):
+    """``kernel_prefill_hip`` with four ``hipEvent_t`` handles (int or
+    ``ctypes.c_void_p``) recorded before the offsets, preparation and scan
+    launches and after the scan (``gdn_prefill_timed``); a measurement hook,
+    not part of the reference's interface."""
+    if len(events) != 4:
+        raise ValueError("events must be four hipEvent_t handles")
+    _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new_state,
+            use_qk_l2norm, events)
+
+
+def _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new_state,
+            use_qk_l2norm, events):
     if output is None or new_state is None:
         raise ValueError("kernel_prefill_hip needs preallocated output and new_state")
     L, N, H, HV = check_prefill_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens,
@@ -118,14 +139,20 @@ def kernel_prefill_hip(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, 
     workspace = torch.empty(ws_bytes + 256, dtype=torch.uint8, device=q.device)
     ws_ptr = (workspace.data_ptr() + 255) & ~255
     stream = torch.cuda.current_stream(q.device).cuda_stream
-    with torch.cuda.device(q.device):
-        code = lib.gdn_prefill(
-            q.data_ptr(), k.data_ptr(), v.data_ptr(),
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(),
             None if state is None else state.data_ptr(),
             A_log.data_ptr(), a.data_ptr(), dt_bias.data_ptr(), b.data_ptr(),
             cu_seqlens.data_ptr(), scale, output.data_ptr(), new_state.data_ptr(),
             L, N, H, HV, K_DIM, V_DIM, int(bool(use_qk_l2norm)), ws_ptr, ws_bytes, stream)
-    _lib.check(code, "gdn_prefill")
+    with torch.cuda.device(q.device):
+        if events is None:
+            code = lib.gdn_prefill(*args)
+        else:
+            handles = (ctypes.c_void_p * 4)(
+                *[e if isinstance(e, ctypes.c_void_p) else ctypes.c_void_p(int(e))
+                  for e in events])
+            code = lib.gdn_prefill_timed(*args, handles)
+    _lib.check(code, "gdn_prefill_timed" if events is not None else "gdn_prefill")
     # keep the workspace (and a converted cu_seqlens) alive until the kernels ran
     workspace.record_stream(torch.cuda.current_stream(q.device))
     cu_seqlens.record_stream(torch.cuda.current_stream(q.device))

@@ -73,7 +73,22 @@ int gdn_prefill(const void* q, const void* k, const void* v, const float* state,
                 int use_qk_l2norm, void* workspace, size_t workspace_size,
                 void* hip_stream);
 
-/* ABI version of this header: 2 (1 had no H in gdn_prefill_workspace_bytes). */
+/*
+ * Measurement hook, no counterpart in the reference: gdn_prefill with
+ * events[0..3] (hipEvent_t, all non-null) recorded on hip_stream before the
+ * offsets, preparation and scan launches and after the scan, so that
+ * hipEventElapsedTime gives each kernel's time.  Nothing is recorded when
+ * num_seqs is 0.
+ */
+int gdn_prefill_timed(const void* q, const void* k, const void* v, const float* state,
+                      const float* A_log, const void* a, const float* dt_bias, const void* b,
+                      const int32_t* cu_seqlens, float scale, void* output, float* new_state,
+                      int total_seq_len, int num_seqs, int H, int HV, int K, int V,
+                      int use_qk_l2norm, void* workspace, size_t workspace_size,
+                      void* hip_stream, void* const* events);
+
+/* ABI version of this header: 3 (2 had no gdn_prefill_timed; 1 had no H in
+ * gdn_prefill_workspace_bytes). */
 int gdn_prefill_abi_version(void);
 
 #ifdef __cplusplus

@@ -151,3 +151,33 @@ def test_more_than_256_sequences(hip_device):
     out, st = gdn.prefill_run(**_dev(t, hip_device))
     torch.cuda.synchronize()
     _check(t, out, st, loop=False)
+
+
+def test_timed_entry_matches_and_times_each_kernel(hip_device):
+    """gdn_prefill_timed: the same results as gdn_prefill, and its four events
+    bracket the three launches (each interval non-negative, the scan's
+    positive)."""
+    import ctypes
+    _announce("prefill timed entry")
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    evs = []
+    for _ in range(4):
+        e = ctypes.c_void_p()
+        assert hip.hipEventCreate(ctypes.byref(e)) == 0
+        evs.append(e)
+    try:
+        t = _dev(make_prefill_inputs([70, 10], 4, 8, seed=23), hip_device)
+        ref_o, ref_s = gdn.prefill_run(**t)
+        out, st = torch.empty_like(ref_o), torch.empty_like(ref_s)
+        gdn.kernel_prefill_hip_timed(**t, output=out, new_state=st, events=evs)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref_o) and torch.equal(st, ref_s)
+        ms = []
+        for i in range(3):
+            x = ctypes.c_float()
+            assert hip.hipEventElapsedTime(ctypes.byref(x), evs[i], evs[i + 1]) == 0
+            ms.append(x.value)
+        assert all(m >= 0.0 for m in ms) and ms[2] > 0.0, ms
+    finally:
+        for e in evs:
+            hip.hipEventDestroy(e)

@@ -28,7 +28,7 @@ def _header_functions():
 
 def test_header_and_library_agree():
     funcs = _header_functions()
-    assert set(funcs) == {"gdn_prefill_workspace_bytes", "gdn_prefill",
+    assert set(funcs) == {"gdn_prefill_workspace_bytes", "gdn_prefill", "gdn_prefill_timed",
                           "gdn_prefill_abi_version"}
     lib = _lib.get_prefill_lib()
     for name, nparams in funcs.items():
@@ -68,6 +68,12 @@ def test_c_side_validation_rejects_before_launching():
     assert call() == 1                        # null pointers
     if not torch.cuda.is_available():         # made-up pointers only where no device exists
         assert call(cu=0x1000, new_state=0x2000, ws=0x3000, ws_size=10) == 1   # short workspace
+    # the timed entry validates its events before anything else
+    assert lib.gdn_prefill_timed(*n, None, f, None, None, 6, 1, 4, 8, 128, 128, 0, None, 0, None,
+                                 None) == 1
+    ev = (ctypes.c_void_p * 4)(0x10, 0x20, None, 0x40)
+    assert lib.gdn_prefill_timed(*n, None, f, None, None, 6, 1, 4, 8, 128, 128, 0, None, 0, None,
+                                 ev) == 1
 
 
 def _cpu_inputs():
