@@ -296,19 +296,24 @@ __device__ __forceinline__ void store_rows_bf16(uint16_t* dst, const u32x4 (&val
 // ---------------------------------------------------------------------------
 // 2. per-chunk preparation
 // ---------------------------------------------------------------------------
-constexpr int kXStride = 32 + 4;          // fp32 rows of the 32-wide scratch
 
+// 52 KiB, so that three workgroups share a CU: A (dead once T is built) and
+// V (staged from registers after that) share storage, and the 32 x 32
+// scratch of the block recursion is T's upper-right quarter, which T never
+// uses (rows 0..31, columns 32..63).
 struct PrepLds {
   uint16_t K[kChunk * kBfStride];
-  uint16_t V[kChunk * kBfStride];
-  float A[kChunk * kF64Stride];   // strict lower part of (I + A) minus I
-  float T[kChunk * kF64Stride];   // (I + A)^-1
-  float X[32 * kXStride];         // block products of the inverse
+  union {
+    float A[kChunk * kF64Stride];     // strict lower part of (I + A) minus I
+    uint16_t V[kChunk * kBfStride];
+  };
+  float T[kChunk * kF64Stride];       // (I + A)^-1
   float gamma[kChunk];
   float beta[kChunk];
   float rq[kChunk];
   float rk[kChunk];
 };
+static_assert(sizeof(PrepLds) <= 160 * 1024 / 3, "three preparation workgroups per CU");
 
 // 16 x 16 x 16 fp32 block product A[0:16, 0:16] B[0:16, 0:16] from LDS rows
 // of stride lda / ldb, as an MFMA result (lane (col, g) holds rows 4 g + e).
@@ -327,7 +332,7 @@ __device__ __forceinline__ void store16(float* D, int ldd, const f32x4& v, float
   for (int e = 0; e < 4; ++e) D[(4 * g4 + e) * ldd + col] = sign * v[e];
 }
 
-__global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) void prep_kernel(Params p) {
   __shared__ PrepLds lds;
   const int c = blockIdx.x;
   const int hv = blockIdx.y;
@@ -372,8 +377,7 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
   token_gates(p, t0 + (lane < n ? lane : n - 1), hv, logg, beta);
   if (lane >= n) logg = beta = 0.0f;
 
-  store_rows_bf16(lds.K, kreg, n);
-  store_rows_bf16(lds.V, vreg, n);
+  store_rows_bf16(lds.K, kreg, n);       // V waits in registers until A is dead
   // T's upper blocks that the block recursion multiplies, T_01 and T_23, are
   // zero; the diagonal and lower blocks are all written, the other upper
   // blocks never read.
@@ -525,12 +529,12 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
   //    T_32 = -T_33 A_32 T_22 (wave 1), through LDS within the wave;
   if (wave < 2) {
     const int b = wave * 32;
-    float* Xw = lds.X + wave * 16 * kXStride;
+    float* Xw = &lds.T[32] + wave * 16 * kF64Stride;
     const f32x4 x = mm16_f32(&lds.A[(b + 16) * kF64Stride + b], kF64Stride,
                              &lds.T[b * kF64Stride + b], kF64Stride, col, g4);
-    store16(Xw, kXStride, x, 1.0f, col, g4);
-    const f32x4 y = mm16_f32(&lds.T[(b + 16) * kF64Stride + b + 16], kF64Stride, Xw, kXStride,
-                             col, g4);
+    store16(Xw, kF64Stride, x, 1.0f, col, g4);
+    const f32x4 y = mm16_f32(&lds.T[(b + 16) * kF64Stride + b + 16], kF64Stride, Xw,
+                             kF64Stride, col, g4);
     store16(&lds.T[(b + 16) * kF64Stride + b], kF64Stride, y, -1.0f, col, g4);
   }
   block_sync_lds();
@@ -542,14 +546,16 @@ __global__ __launch_bounds__(kThreads) void prep_kernel(Params p) {
     const f32x4 x = mm16_f32(Arow, kF64Stride, &lds.T[16 * cb], kF64Stride, col, g4) +
                     mm16_f32(Arow + 16, kF64Stride, &lds.T[16 * kF64Stride + 16 * cb],
                              kF64Stride, col, g4);
-    store16(&lds.X[16 * rb * kXStride + 16 * cb], kXStride, x, 1.0f, col, g4);
+    store16(&lds.T[16 * rb * kF64Stride + 32 + 16 * cb], kF64Stride, x, 1.0f, col, g4);
   }
   block_sync_lds();
+  store_rows_bf16(lds.V, vreg, n);       // A is dead: V takes its storage
   {
     const int rb = wave >> 1, cb = wave & 1;
     const float* Trow = &lds.T[(32 + 16 * rb) * kF64Stride + 32];
-    const f32x4 y = mm16_f32(Trow, kF64Stride, &lds.X[16 * cb], kXStride, col, g4) +
-                    mm16_f32(Trow + 16, kF64Stride, &lds.X[16 * kXStride + 16 * cb], kXStride,
+    const float* X = &lds.T[32];
+    const f32x4 y = mm16_f32(Trow, kF64Stride, &X[16 * cb], kF64Stride, col, g4) +
+                    mm16_f32(Trow + 16, kF64Stride, &X[16 * kF64Stride + 16 * cb], kF64Stride,
                              col, g4);
     store16(&lds.T[(32 + 16 * rb) * kF64Stride + 16 * cb], kF64Stride, y, -1.0f, col, g4);
   }
