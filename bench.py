@@ -470,6 +470,52 @@ def prefill_cpu_baseline(seconds: float, gpu_tokens_per_s: float | None):
             "workload0_1x6_us": round(statistics.median(w0), 1)}
 
 
+def prefill_inputs(name: str, device) -> dict:
+    """DPS arguments of one prefill workload, seeded on the device."""
+    lens, H, HV = PREFILL_CONFIGS[name]
+    L, N = sum(lens), len(lens)
+    g = torch.Generator(device=device).manual_seed(17)
+    f = dict(device=device)
+    q = torch.randn(L, H, 128, generator=g, **f)
+    k = torch.randn(L, H, 128, generator=g, **f)
+    t = dict(q=(q / q.norm(dim=-1, keepdim=True)).to(torch.bfloat16),
+             k=(k / k.norm(dim=-1, keepdim=True)).to(torch.bfloat16),
+             v=torch.randn(L, HV, 128, generator=g, **f).to(torch.bfloat16),
+             state=torch.randn(N, HV, 128, 128, generator=g, **f).mul_(0.05),
+             A_log=torch.log(torch.rand(HV, generator=g, **f) * 15.0 + 1.0),
+             a=torch.randn(L, HV, generator=g, **f).to(torch.bfloat16),
+             dt_bias=torch.rand(HV, generator=g, **f) * 2.0 - 1.0,
+             b=torch.randn(L, HV, generator=g, **f).to(torch.bfloat16),
+             scale=1.0 / math.sqrt(128))
+    cu = torch.zeros(N + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(torch.tensor(lens), 0)
+    t["cu_seqlens"] = cu.to(device)
+    t["output"] = torch.empty(L, HV, 128, dtype=torch.bfloat16, **f)
+    t["new_state"] = torch.empty_like(t["state"])
+    return t
+
+
+def pmc_prefill(device):
+    """Short run for rocprofv3 counter passes over the prefill: three plain
+    256 MiB copies (calibrate FETCH_SIZE / WRITE_SIZE against known bytes),
+    then three prefills each of the 1 x 16384 qk4_v8 and 64 x 512 qk16_v32
+    workloads."""
+    n = 256 * 1024 * 1024 // 4
+    src = torch.randn(n, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    for name in ("prefill_qk4_v8_1x16384", "prefill_qk16_v32_64x512"):
+        t = prefill_inputs(name, device)
+        for _ in range(3):
+            gdn.kernel_prefill_hip(**t)
+        torch.cuda.synchronize()
+        del t
+    print(json.dumps({"pmc_prefill": "done", "copy_bytes": n * 4}), flush=True)
+
+
 def prefill_bench(device, iters: int = 20):
     """Per prefill workload: median time of the whole prefill call from
     torch events around it, and of each of its three kernels from HIP events
@@ -480,24 +526,7 @@ def prefill_bench(device, iters: int = 20):
     stamps = KernelStamps(2 * iters)              # 4 events per timed prefill
     for name, (lens, H, HV) in PREFILL_CONFIGS.items():
         L, N = sum(lens), len(lens)
-        g = torch.Generator(device=device).manual_seed(17)
-        f = dict(device=device)
-        q = torch.randn(L, H, 128, generator=g, **f)
-        k = torch.randn(L, H, 128, generator=g, **f)
-        t = dict(q=(q / q.norm(dim=-1, keepdim=True)).to(torch.bfloat16),
-                 k=(k / k.norm(dim=-1, keepdim=True)).to(torch.bfloat16),
-                 v=torch.randn(L, HV, 128, generator=g, **f).to(torch.bfloat16),
-                 state=torch.randn(N, HV, 128, 128, generator=g, **f).mul_(0.05),
-                 A_log=torch.log(torch.rand(HV, generator=g, **f) * 15.0 + 1.0),
-                 a=torch.randn(L, HV, generator=g, **f).to(torch.bfloat16),
-                 dt_bias=torch.rand(HV, generator=g, **f) * 2.0 - 1.0,
-                 b=torch.randn(L, HV, generator=g, **f).to(torch.bfloat16),
-                 scale=1.0 / math.sqrt(128))
-        cu = torch.zeros(N + 1, dtype=torch.int32)
-        cu[1:] = torch.cumsum(torch.tensor(lens), 0)
-        t["cu_seqlens"] = cu.to(device)
-        t["output"] = torch.empty(L, HV, 128, dtype=torch.bfloat16, **f)
-        t["new_state"] = torch.empty_like(t["state"])
+        t = prefill_inputs(name, device)
         for _ in range(3):
             gdn.kernel_prefill_hip(**t)
         stream = torch.cuda.current_stream()
@@ -569,6 +598,8 @@ def main():
     ap.add_argument("--iters", type=int, default=100,
                     help="launches per per-config kernel-time measurement")
     ap.add_argument("--pmc-pass", action="store_true")
+    ap.add_argument("--pmc-prefill", action="store_true",
+                    help="short prefill run for rocprofv3 counter passes")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--prefill-only", action="store_true",
                     help="time the prefill workloads only and print them as JSON")
@@ -585,6 +616,9 @@ def main():
     _lib.get_lib()
     if args.pmc_pass:
         pmc_pass(device)
+        return
+    if args.pmc_prefill:
+        pmc_prefill(device)
         return
     if args.prefill_only:
         pf = prefill_bench(device)
