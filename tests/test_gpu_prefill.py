@@ -181,3 +181,75 @@ def test_timed_entry_matches_and_times_each_kernel(hip_device):
     finally:
         for e in evs:
             hip.hipEventDestroy(e)
+
+
+def test_two_thousand_short_sequences(hip_device):
+    """2000 sequences of 1..8 tokens: eight groups of the offsets scan, one
+    partial chunk each."""
+    _announce("prefill 2000 short sequences")
+    g = torch.Generator().manual_seed(31)
+    lens = [int(x) for x in torch.randint(1, 9, (2000,), generator=g)]
+    t = make_prefill_inputs(lens, 4, 8, seed=32)
+    out, st = gdn.prefill_run(**_dev(t, hip_device))
+    torch.cuda.synchronize()
+    _check(t, out, st, loop=False)
+
+
+def _device_prefill_inputs(lens, H, HV, device, seed):
+    """Benchmark-style inputs generated on the device (unit-norm q/k rows)."""
+    L, N = sum(lens), len(lens)
+    g = torch.Generator(device=device).manual_seed(seed)
+    f = dict(device=device)
+    q = torch.randn(L, H, 128, generator=g, **f)
+    k = torch.randn(L, H, 128, generator=g, **f)
+    cu = torch.zeros(N + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(torch.tensor(lens), 0)
+    return dict(q=(q / q.norm(dim=-1, keepdim=True)).to(torch.bfloat16),
+                k=(k / k.norm(dim=-1, keepdim=True)).to(torch.bfloat16),
+                v=torch.randn(L, HV, 128, generator=g, **f).to(torch.bfloat16),
+                state=torch.randn(N, HV, 128, 128, generator=g, **f).mul_(0.05),
+                A_log=torch.log(torch.rand(HV, generator=g, **f) * 15.0 + 1.0),
+                a=torch.randn(L, HV, generator=g, **f).to(torch.bfloat16),
+                dt_bias=torch.rand(HV, generator=g, **f) * 2.0 - 1.0,
+                b=torch.randn(L, HV, generator=g, **f).to(torch.bfloat16),
+                cu_seqlens=cu.to(device), scale=None)
+
+
+@pytest.mark.parametrize("lens,H,HV,cut", [
+    ([1024] * 16, 16, 32, 389),       # 16 x 1024 at qk16_v32, cut off the chunk grid
+    ([512] * 64, 16, 32, 200),        # the 64 x 512 qk16_v32 bench workload
+    ([16384], 4, 8, 8000),            # the 1 x 16384 qk4_v8 bench workload
+])
+def test_split_sequences_compose_at_full_size(lens, H, HV, cut, hip_device):
+    """Size-independent property of the recurrence: prefilling every sequence
+    in two parts, the second starting from the first part's state, gives the
+    one-shot prefill.  The parts put chunk boundaries elsewhere, so the two
+    runs round differently; they must agree to the bars each meets against
+    the float64 oracle: outputs within 2 bf16 ulps + 1e-5, states within
+    1e-3 relative + 1e-5 per element and 1e-4 in relative Frobenius norm."""
+    _announce(f"prefill split property lens={lens[0]}x{len(lens)} H={H} HV={HV} cut={cut}")
+    t = _device_prefill_inputs(lens, H, HV, hip_device, seed=41)
+    out, st = gdn.prefill_run(**t)
+    cu = t["cu_seqlens"].cpu().tolist()
+    idx1 = torch.cat([torch.arange(cu[s], cu[s] + cut) for s in range(len(lens))]).to(hip_device)
+    idx2 = torch.cat([torch.arange(cu[s] + cut, cu[s + 1]) for s in range(len(lens))]).to(hip_device)
+
+    def part(idx, n_tok, state):
+        cu_p = torch.arange(0, n_tok * len(lens) + 1, n_tok, dtype=torch.int32, device=hip_device)
+        return gdn.prefill_run(q=t["q"][idx], k=t["k"][idx], v=t["v"][idx], state=state,
+                               A_log=t["A_log"], a=t["a"][idx], dt_bias=t["dt_bias"],
+                               b=t["b"][idx], cu_seqlens=cu_p, scale=None)
+
+    o1, s1 = part(idx1, cut, t["state"])
+    o2, s2 = part(idx2, lens[0] - cut, s1)
+    torch.cuda.synchronize()
+    split_out = torch.empty_like(out)
+    split_out[idx1] = o1
+    split_out[idx2] = o2
+    ref = out.float()
+    d_out = (split_out.float() - ref).abs()
+    assert bool((d_out <= 2.0 ** -7 * ref.abs() + 1e-5).all()), d_out.max()
+    d_st = (s2 - st).abs()
+    assert bool((d_st <= 1e-3 * st.abs() + 1e-5).all()), d_st.max()
+    rel = (torch.linalg.vector_norm(s2 - st) / torch.linalg.vector_norm(st)).item()
+    assert rel <= 1e-4, rel
