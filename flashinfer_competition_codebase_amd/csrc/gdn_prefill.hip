@@ -21,7 +21,8 @@
 // Kernels (one stream, in order):
 //   1. chunk_offsets: one workgroup turns cu_seqlens into the first chunk
 //      slot of every sequence (token ranges clamped to [0, L]) by a scan,
-//      and writes each slot's sequence, first token and token count.
+//      and writes each slot's sequence, first token and token count.  With
+//      one sequence it is not launched: chunk c is slot c.
 //   2. prep, grid (chunk slots, HV): everything that does not depend on the
 //      state, for all chunks at once -- gates and gamma, K K^T and Q K^T
 //      (bf16 MFMA: the inputs are bf16), T by block recursion (fp32 MFMA),
@@ -173,6 +174,7 @@ struct Params {
   int HV;
   int ratio;                 // HV / H
   int l2norm;
+  int single;                // one sequence: chunk c is slot c (no offsets kernel)
   long long max_slots;       // slots the workspace holds
 };
 
@@ -336,9 +338,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
   __shared__ PrepLds lds;
   const int c = blockIdx.x;
   const int hv = blockIdx.y;
-  const i32x4 info = p.slot_info[c];
-  const int t0 = info.y;
-  const int n = info.z;                            // 1..64, 0 past the last slot
+  int t0, n;                                       // n: 1..64, 0 past the last slot
+  if (p.single) {
+    int start, end;
+    seq_range(p, 0, start, end);
+    t0 = start + c * kChunk;
+    n = min(kChunk, end - t0);
+  } else {
+    const i32x4 info = p.slot_info[c];
+    t0 = info.y;
+    n = info.z;
+  }
   if (n <= 0) return;                              // uniform per workgroup
   const int h = hv / p.ratio;
   const int lane = threadIdx.x & 63;
@@ -797,7 +807,8 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Params p) {
 
   // Chunk count from the slot offsets (never more than the range holds, and
   // never more slots than the workspace has, whatever cu_seqlens contains).
-  const int nchunks = p.offs[s + 1] - p.offs[s];
+  const int slot0 = p.single ? 0 : p.offs[s];
+  const int nchunks = p.single ? (end - start + kChunk - 1) / kChunk : p.offs[s + 1] - slot0;
   if (nchunks <= 0) {                 // no tokens: zeros, as the reference
 #pragma unroll
     for (int t = 0; t < 2; ++t)
@@ -807,10 +818,10 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Params p) {
                                   wave * 32 + t * 16 + g4 * 4) = f32x4{0, 0, 0, 0};
     return;
   }
-  const float* slot_base = p.slots + (static_cast<size_t>(p.offs[s]) * p.HV + hv) * kSlotFloats;
+  const float* slot_base = p.slots + (static_cast<size_t>(slot0) * p.HV + hv) * kSlotFloats;
   const size_t slot_step = static_cast<size_t>(p.HV) * kSlotFloats;
   const float* qk_base =
-      p.qk_slots + (static_cast<size_t>(p.offs[s]) * p.H + hv / p.ratio) * kQkSlotFloats;
+      p.qk_slots + (static_cast<size_t>(slot0) * p.H + hv / p.ratio) * kQkSlotFloats;
   const size_t qk_step = static_cast<size_t>(p.H) * kQkSlotFloats;
 
   ScanOps<NT> op;
@@ -1036,6 +1047,7 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
   p.HV = HV;
   p.ratio = HV / H;
   p.l2norm = use_qk_l2norm != 0;
+  p.single = num_seqs == 1;
   p.max_slots = slots;
 
   hipStream_t stream = static_cast<hipStream_t>(hip_stream);
@@ -1045,8 +1057,9 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
   };
   hipError_t e = mark(0);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(chunk_offsets_kernel, dim3(1), dim3(kThreads), 0, stream, p, offs,
-                     slot_info);
+  if (!p.single)
+    hipLaunchKernelGGL(chunk_offsets_kernel, dim3(1), dim3(kThreads), 0, stream, p, offs,
+                       slot_info);
   e = hipGetLastError();
   if (e == hipSuccess) e = mark(1);
   if (e != hipSuccess) return e;
