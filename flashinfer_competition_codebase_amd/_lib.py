@@ -114,6 +114,21 @@ def get_prefill_lib() -> ctypes.CDLL:
     return _prefill_lib
 
 
+_raw_stream = None
+
+
+def current_stream(device_index: int) -> int:
+    """Raw ``hipStream_t`` of torch's current stream on ``device_index``
+    (torch's raw accessor where it has one: the public ``current_stream``
+    builds a Stream object per call)."""
+    global _raw_stream
+    if _raw_stream is None:
+        import torch
+        _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None) or (
+            lambda i: torch.cuda.current_stream(i).cuda_stream)
+    return _raw_stream(device_index)
+
+
 def error_string(code: int) -> str:
     text = get_lib().gdn_decode_error_string(int(code))
     return text.decode() if text else f"error {code}"

@@ -72,7 +72,7 @@ def _expect(t, name: str, dtype: torch.dtype, shape: tuple) -> None:
         raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
     if t.dtype != dtype:
         raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
-    if tuple(t.shape) != shape:
+    if t.shape != shape:                      # torch.Size compares with a tuple
         raise ValueError(f"{name} must have shape {shape}, got {tuple(t.shape)}")
     if not t.is_contiguous():
         raise ValueError(f"{name} must be contiguous")
@@ -130,20 +130,25 @@ def check_inputs(q, k, v, state, A_log, a, dt_bias, b, output=None, new_state=No
     if new_state is not None:
         _expect_state(new_state, "new_state", (B, HV, V, K),
                       None if state is None else state.dtype)
-    tensors = [q, k, v, A_log, a, dt_bias, b]
-    tensors += [t for t in (state, output, new_state) if t is not None]
-    dev = q.device
-    for t in tensors:
-        if t.device != dev:
-            raise ValueError(f"all tensors must be on one device, got {dev} and {t.device}")
-    if dev.type != "cuda":
-        raise ValueError(
-            f"the GDN decode kernel runs on a HIP device; got tensors on {dev}"
-        )
+    _same_hip_device(q, (k, v, A_log, a, dt_bias, b, state, output, new_state),
+                     "the GDN decode kernel")
     if state is not None and new_state is not None and new_state is not state:
         if new_state.data_ptr() != state.data_ptr() and _overlap(new_state, state):
             raise ValueError("new_state must be state itself or not overlap it")
     return B, T, H, HV
+
+
+def _same_hip_device(first: torch.Tensor, others, what: str) -> int:
+    """Device index of ``first``; raises unless every tensor of ``others``
+    (None entries skipped) is on that device and it is a HIP device."""
+    idx = first.get_device()                  # -1 off the GPU (cpu, meta, ...)
+    for t in others:
+        if t is not None and (t.get_device() != idx or (idx < 0 and t.device != first.device)):
+            raise ValueError(f"all tensors must be on one device, got {first.device} and "
+                             f"{t.device}")
+    if idx < 0 or first.device.type != "cuda":
+        raise ValueError(f"{what} runs on a HIP device; got tensors on {first.device}")
+    return idx
 
 
 def _overlap(x: torch.Tensor, y: torch.Tensor) -> bool:
@@ -152,15 +157,34 @@ def _overlap(x: torch.Tensor, y: torch.Tensor) -> bool:
     return x0 < y0 + yn and y0 < x0 + xn
 
 
+class _NoSwitch:
+    def __enter__(self):
+        return None
+
+    def __exit__(self, *exc):
+        return False
+
+
+_NO_SWITCH = _NoSwitch()
+
+
+def _on_device(idx: int):
+    """Context that makes device ``idx`` current for a launch; a no-op when
+    it already is."""
+    return _NO_SWITCH if torch.cuda.current_device() == idx else torch.cuda.device(idx)
+
+
 def _launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
             B, T, H, HV, use_qk_l2norm, shape=None):
     lib = _lib.get_lib()
-    stream = torch.cuda.current_stream(q.device).cuda_stream
+    idx = q.get_device()
+    stream = _lib.current_stream(idx)
     ptrs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), state.data_ptr(),
             A_log.data_ptr(), a.data_ptr(), dt_bias.data_ptr(), b.data_ptr())
     l2 = int(bool(use_qk_l2norm))
     bf16 = int(state.dtype == torch.bfloat16)
-    with torch.cuda.device(q.device):
+    # the launch goes to the inputs' device (switched to only when another is current)
+    with _on_device(idx):
         if shape is not None:
             ns, waves, policy, start_event, stop_event = shape
             code = lib.gdn_decode_step_shaped(
@@ -180,7 +204,6 @@ def _launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
             _lib.check(code, "gdn_decode_steps")
 
 
-@torch.no_grad()
 def kernel_hip(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
                *, use_qk_l2norm: bool = False):
     """Destination-passing decode step (reference DPS form,
@@ -195,7 +218,8 @@ def kernel_hip(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
     B, T, H, HV = check_inputs(q, k, v, state, A_log, a, dt_bias, b, output, new_state)
     scale = resolve_scale(scale, q.shape[-1])
     if state is None:
-        new_state.zero_()
+        with torch.no_grad():
+            new_state.zero_()
         state = new_state
     if B == 0:
         return None

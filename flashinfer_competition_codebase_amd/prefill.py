@@ -35,7 +35,7 @@ import ctypes
 import torch
 
 from . import _lib
-from .kernel import K_DIM, V_DIM, _expect, _overlap, resolve_scale
+from .kernel import K_DIM, V_DIM, _expect, _on_device, _overlap, _same_hip_device, resolve_scale
 
 __all__ = ["prefill_run", "kernel_prefill_hip", "kernel_prefill_hip_timed", "workspace_bytes"]
 
@@ -86,14 +86,8 @@ def check_prefill_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, outpu
         _expect(output, "output", torch.bfloat16, (L, HV, V))
     if new_state is not None:
         _expect(new_state, "new_state", torch.float32, (N, HV, V, K))
-    tensors = [q, k, v, A_log, a, dt_bias, b, cu_seqlens]
-    tensors += [t for t in (state, output, new_state) if t is not None]
-    dev = q.device
-    for t in tensors:
-        if t.device != dev:
-            raise ValueError(f"all tensors must be on one device, got {dev} and {t.device}")
-    if dev.type != "cuda":
-        raise ValueError(f"the GDN prefill kernels run on a HIP device; got tensors on {dev}")
+    _same_hip_device(q, (k, v, A_log, a, dt_bias, b, cu_seqlens, state, output, new_state),
+                     "the GDN prefill")
     if state is not None and new_state is not None and new_state is not state:
         if new_state.data_ptr() != state.data_ptr() and _overlap(new_state, state):
             raise ValueError("new_state must be state itself or not overlap it")
@@ -138,13 +132,14 @@ def _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new
     ws_bytes = workspace_bytes(L, N, H, HV)
     workspace = torch.empty(ws_bytes + 256, dtype=torch.uint8, device=q.device)
     ws_ptr = (workspace.data_ptr() + 255) & ~255
-    stream = torch.cuda.current_stream(q.device).cuda_stream
+    idx = q.get_device()
+    stream = _lib.current_stream(idx)
     args = (q.data_ptr(), k.data_ptr(), v.data_ptr(),
             None if state is None else state.data_ptr(),
             A_log.data_ptr(), a.data_ptr(), dt_bias.data_ptr(), b.data_ptr(),
             cu_seqlens.data_ptr(), scale, output.data_ptr(), new_state.data_ptr(),
             L, N, H, HV, K_DIM, V_DIM, int(bool(use_qk_l2norm)), ws_ptr, ws_bytes, stream)
-    with torch.cuda.device(q.device):
+    with _on_device(idx):
         if events is None:
             code = lib.gdn_prefill(*args)
         else:
