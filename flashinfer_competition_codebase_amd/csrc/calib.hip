@@ -33,7 +33,8 @@ __global__ __launch_bounds__(kThreads) void rmw(float* buf, float c) {
              threadIdx.x;
   f32x4 v[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = NT ? __builtin_nontemporal_load(p + i * kThreads) : p[i * kThreads];
+  for (int i = 0; i < 4; ++i)
+    v[i] = NT ? __builtin_nontemporal_load(p + i * kThreads) : p[i * kThreads];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     v[i] *= c;

@@ -23,15 +23,18 @@
 //      slot of every sequence (token ranges clamped to [0, L]) by a scan,
 //      and writes each slot's sequence, first token and token count.  With
 //      one sequence it is not launched: chunk c is slot c.
-//   2. prep, grid (chunk slots, HV): everything that does not depend on the
-//      state, for all chunks at once -- gates and gamma, K K^T and Q K^T
-//      (bf16 MFMA: the inputs are bf16), T by block recursion (fp32 MFMA),
-//      W and U (bf16 MFMA on hi/lo-split T) -- into a workspace slot per
-//      (chunk, v-head), in the order the scan's MFMAs read it.
+//   2. prep, grid (chunk slots, HV), three workgroups per CU: everything
+//      that does not depend on the state, for all chunks at once -- gates
+//      and gamma, K K^T and Q K^T (bf16 MFMA: the inputs are bf16), T by
+//      block recursion (fp32 MFMA), W and U (bf16 MFMA on hi/lo-split T) --
+//      into a workspace slot per (chunk, v-head), and K^T and a copy of Q
+//      into one per (chunk, q/k head), in the order the scan's MFMAs read
+//      them.
 //   3. scan, one workgroup per (sequence, v-head, 16- or 32-column slice of
-//      the state), XCD-aware order: the sequential part, Delta, O and S_C chunk after chunk
-//      (bf16 MFMA on hi/lo-split fp32 operands), the state slice kept in
-//      registers and the next chunk's operands loaded while this one runs.
+//      the state), XCD-aware order: the sequential part, Delta, O and S_C
+//      chunk after chunk (bf16 MFMA on hi/lo-split fp32 operands), the state
+//      slice kept in registers and the next chunk's operands loaded while
+//      this one runs.
 //
 // MFMA lane layouts (v_mfma_f32_16x16x4_f32, v_mfma_f32_16x16x32_bf16):
 // A[i][k] from lane i + 16 g, B[k][j] from lane j + 16 g (k = g for fp32;
@@ -263,7 +266,8 @@ __device__ __forceinline__ void token_gates(const Params& p, int t, int hv, floa
   const float x = bf16_to_f32(p.a[static_cast<size_t>(t) * p.HV + hv]) + p.dt_bias[hv];
   const float sp = x > kSoftplusThreshold ? x : __builtin_amdgcn_logf(1.0f + __expf(x)) * kLn2;
   logg = -__expf(p.A_log[hv]) * sp;
-  beta = __builtin_amdgcn_rcpf(1.0f + __expf(-bf16_to_f32(p.b[static_cast<size_t>(t) * p.HV + hv])));
+  const float bb = bf16_to_f32(p.b[static_cast<size_t>(t) * p.HV + hv]);
+  beta = __builtin_amdgcn_rcpf(1.0f + __expf(-bb));
 }
 
 // Rows [0, 64) of a [*, stride, 128] bf16 tensor (row r at base + r * step
@@ -334,7 +338,8 @@ __device__ __forceinline__ void store16(float* D, int ldd, const f32x4& v, float
   for (int e = 0; e < 4; ++e) D[(4 * g4 + e) * ldd + col] = sign * v[e];
 }
 
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) void prep_kernel(Params p) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3)))
+void prep_kernel(Params p) {
   __shared__ PrepLds lds;
   const int c = blockIdx.x;
   const int hv = blockIdx.y;
@@ -914,8 +919,9 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Params p) {
         pd0 = mfma_bf16(dh, op.pl[m], pd0);
       }
       const f32x4 pd = pd0 + pd1;
-      const u32x2 ob = {pack_bf16x2(fmaf(op.qs, qsum[cq][0], pd[0]), fmaf(op.qs, qsum[cq][1], pd[1])),
-                        pack_bf16x2(fmaf(op.qs, qsum[cq][2], pd[2]), fmaf(op.qs, qsum[cq][3], pd[3]))};
+      const float qsc = op.qs;
+      const u32x2 ob = {pack_bf16x2(fmaf(qsc, qsum[cq][0], pd[0]), fmaf(qsc, qsum[cq][1], pd[1])),
+                        pack_bf16x2(fmaf(qsc, qsum[cq][2], pd[2]), fmaf(qsc, qsum[cq][3], pd[3]))};
       if (orow < n)
         *reinterpret_cast<u32x2*>(p.out + ((static_cast<size_t>(t0) + orow) * p.HV + hv) * kDim +
                                   v0 + cq * 16 + g4 * 4) = ob;

@@ -231,8 +231,9 @@ def test_split_sequences_compose_at_full_size(lens, H, HV, cut, hip_device):
     t = _device_prefill_inputs(lens, H, HV, hip_device, seed=41)
     out, st = gdn.prefill_run(**t)
     cu = t["cu_seqlens"].cpu().tolist()
-    idx1 = torch.cat([torch.arange(cu[s], cu[s] + cut) for s in range(len(lens))]).to(hip_device)
-    idx2 = torch.cat([torch.arange(cu[s] + cut, cu[s + 1]) for s in range(len(lens))]).to(hip_device)
+    seqs = range(len(lens))
+    idx1 = torch.cat([torch.arange(cu[s], cu[s] + cut) for s in seqs]).to(hip_device)
+    idx2 = torch.cat([torch.arange(cu[s] + cut, cu[s + 1]) for s in seqs]).to(hip_device)
 
     def part(idx, n_tok, state):
         cu_p = torch.arange(0, n_tok * len(lens) + 1, n_tok, dtype=torch.int32, device=hip_device)
