@@ -65,6 +65,10 @@ def _check(t, out, st, l2=False, loop=True):
     ([130, 3], 2, 2),
     ([100], 1, 4),
     ([200, 129], 16, 32),
+    ([90, 17], 2, 6),                 # GVA ratio 3, heads not a multiple of 8
+    ([77], 1, 1),                     # one head
+    ([40, 64, 3], 3, 12),             # odd q/k head count, ratio 4
+    ([66], 8, 64),                    # 64 v-heads
 ])
 def test_prefill_matches_the_oracle(seqlens, H, HV, hip_device):
     _announce(f"prefill seqlens={seqlens} H={H} HV={HV}")
