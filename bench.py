@@ -68,6 +68,7 @@ METRIC = ("GDN decode µs/step at B=1; achieved HBM GB/s (% of peak) at B=256")
 PEAK_HBM_GBS = 8000.0
 PEAK_BF16_TFLOPS = 2500.0      # dense bf16 MFMA, MI355X
 TRAFFIC_SUMMARY = ROOT / "profiles" / "gdn_decode_b256_qk16v32_traffic.json"
+PREFILL_TRAFFIC_SUMMARY = ROOT / "profiles" / "gdn_prefill_traffic.json"
 
 # name -> (B, H, HV, use_qk_l2norm)
 CONFIGS = {
@@ -414,11 +415,24 @@ def prefill_workspace_bytes(lens, H, HV) -> int:
 PREFILL_ROOFLINE_WORKLOAD = "prefill_qk16_v32_64x512"
 
 
+def _prefill_traffic() -> dict | None:
+    """Measured HBM bytes per launch of the 64 x 512 qk16_v32 prefill kernels
+    (rocprofv3 FETCH_SIZE / WRITE_SIZE, calibrated on a copy of known size),
+    from the committed counter summary."""
+    try:
+        k = json.loads(PREFILL_TRAFFIC_SUMMARY.read_text())["kernels"]
+        return {"prep": k["prep_64x512_qk16_v32"]["traffic_bytes_per_launch"],
+                "scan": k["scan_64x512_qk16_v32"]["traffic_bytes_per_launch"]}
+    except (OSError, ValueError, KeyError):
+        return None
+
+
 def prefill_roofline(prefill: dict) -> dict:
     """Roofline of the largest prefill workload: its algorithmic FLOP rate
     over the whole prefill (kernel time) against the bf16 dense MFMA peak;
     the preparation kernel's HBM bytes (inputs read + workspace written) per
-    its time against the HBM peak."""
+    its time against the HBM peak; ``traffic``: measured HBM bytes of prep +
+    scan per prefill and the HBM rate they make over the kernels' times."""
     r = prefill[PREFILL_ROOFLINE_WORKLOAD]
     lens_h = PREFILL_CONFIGS[PREFILL_ROOFLINE_WORKLOAD]
     lens, H, HV = lens_h
@@ -430,9 +444,17 @@ def prefill_roofline(prefill: dict) -> dict:
     prep_in = L * (2 * H * 128 * 2 + HV * 128 * 2 + 2 * HV * 2)
     prep_bytes = prep_in + r["prep_workspace_bytes"]
     prep_gbs = prep_bytes / (ku["prep"] * 1e-6) / 1e9
+    tr = _prefill_traffic()
+    traffic = None
+    if tr is not None:
+        total = tr["prep"] + tr["scan"]
+        gbs = total / ((ku["prep"] + ku["scan"]) * 1e-6) / 1e9
+        traffic = {"bytes": total, "prep_bytes": tr["prep"], "scan_bytes": tr["scan"],
+                   "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
+                   "source": str(PREFILL_TRAFFIC_SUMMARY.relative_to(ROOT))}
     return {"workload": PREFILL_ROOFLINE_WORKLOAD, "bound": "mfma",
             "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
             "kernel_us": ku,
             "prep": {"hbm_bytes": prep_bytes, "gbs": round(prep_gbs, 1),
                      "frac_of_hbm_peak": round(prep_gbs / PEAK_HBM_GBS, 4)}}
