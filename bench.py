@@ -18,18 +18,27 @@ step's dirty lines: the steady state of serving.  Prints ONE JSON line:
   around every timed launch on the launch stream, against MI355X's 8 TB/s;
   ``traffic`` is the measured HBM bytes per launch from the committed
   rocprofv3 counter summary, when there is one;
-* ``b1``: kernel time per step at B=1 (qk16_v32, L2-norm), stamped by the
-  kernel dispatch itself (the analogue of the reference's CUPTI timings);
+* ``b1``: kernel time per step at B=1 (qk16_v32, L2-norm) from a rocprofv3
+  kernel trace (the analogue of the reference's CUPTI timings): a child
+  process, started under ``rocprofv3 --kernel-trace`` before this process
+  touches the GPU, launches every per-config shape through the product
+  entry point, and its dispatches are attributed back to the shapes;
 * ``per_config``: kernel times for every benchmark shape and for the
   reference's qk4_v8 definition at its workload batch sizes, plus bf16-state
   and multi-token (T = 2, 4) steps, in three regimes: steady (as above),
   warm (one state, repeatedly: cache-resident below 256 MiB) and cold (a
   1 GiB read evicts the caches just before the launch; the launch's own
-  writes may still be in cache when it ends);
-* ``b1.floor_same_timer``: the same timer on reference kernels that move
-  only the state bytes (an in-place read-modify-write of the B=1 and B=256
-  states) and on an empty kernel, so that the decode times read against the
-  floor of their own traffic;
+  writes may still be in cache when it ends); ``us_*`` from events the
+  kernel dispatch stamps (hipExtLaunchKernelGGL: ~2.5 us of their own
+  overhead, so only meaningful above ~10 us), ``trace_us_*`` from the
+  kernel trace;
+* ``b1.floor_kernel_trace`` and ``b1.stamped.floor_same_timer``: each timer
+  on reference kernels that move only the state bytes (an in-place
+  read-modify-write of the B=1 state, and of the B=256 state under the
+  stamped events) and on an empty kernel, so that the decode times read
+  against the floor of their own traffic; ``b1.serving``: host-inclusive
+  time per step of 48 back-to-back B=1 steps, eager and replayed from a
+  HIP graph;
 * ``cpu_baseline``: the reference's PyTorch-eager step (the oracle's
   loop-for-loop restatement) timed on this host's cores on a bounded sample;
 * ``prefill``: the variable-length prefill workloads, each with the whole
@@ -47,12 +56,16 @@ output (B*HV*128*2), a and b (2*B*HV*2); A_log and dt_bias (2*HV*4).
 from __future__ import annotations
 
 import argparse
+import csv
 import ctypes
 import json
 import math
 import os
+import shutil
 import statistics
+import subprocess
 import sys
+import tempfile
 import time
 from pathlib import Path
 
@@ -183,6 +196,143 @@ def kernel_times_us(t, l2, iters, *, mode, flush=None):
         return d[len(states):] if mode == "steady" else d
     finally:
         stamps.close()
+
+
+def per_config_shapes():
+    """(name, B, H, HV, use_qk_l2norm, T, state dtype) of every per-config
+    shape: the benchmark configs, the reference's qk4_v8 definition at its
+    workload batch sizes, bf16-state and multi-token steps."""
+    f32, bf16 = torch.float32, torch.bfloat16
+    shapes = [(n, *c, 1, f32) for n, c in CONFIGS.items()]
+    shapes += [(f"qk4_v8_b{bb}", bb, 4, 8, False, 1, f32) for bb in REF_BATCHES]
+    shapes += [(f"{n}_bf16_state", *CONFIGS[n], 1, bf16)
+               for n in ("b1_qk16_v32_l2", "b8_qk16_v32_l2", "b256_qk16_v32_l2")]
+    shapes += [(f"{n}_t{tt}", *CONFIGS[n], tt, f32)
+               for n in ("b1_qk16_v32_l2", "b256_qk16_v32_l2") for tt in (2, 4)]
+    return shapes
+
+
+# Kernel-name substrings in the trace: the decode kernel and the floor
+# kernels of libgdn_calib.so.
+TRACE_DECODE = "gdn_decode_k128"
+TRACE_RMW = "gdn_calib::rmw"
+TRACE_EMPTY = "gdn_calib::empty"
+TRACE_WARMUP = 5
+
+
+def trace_child(device, manifest_path: str, iters: int) -> None:
+    """The launches the kernel-trace leg records (run by ``kernel_trace_leg``
+    under rocprofv3).  Per shape: warmup launches, steady launches rotating
+    over layer states, then cold launches each right after a 1 GiB read, all
+    through the product entry point ``kernel_hip``; then the floor kernels
+    (the B=1 state's in-place read-modify-write, steady, and an empty kernel
+    on the B=1 decode grid).  Writes the launch counts, in launch order, to
+    ``manifest_path``."""
+    flush = torch.ones(1 << 28, device=device)
+    manifest = []
+    for name, b_, h_, hv_, l2_, t_, sd_ in per_config_shapes():
+        tc = make_device_inputs(b_, h_, hv_, device, seed=7, T=t_, state_dtype=sd_)
+        for _ in range(TRACE_WARMUP):
+            gdn.kernel_hip(**tc, use_qk_l2norm=l2_)
+        states = layer_states(tc["state"])
+        n_steady = max(iters, 2 * len(states))
+        for i in range(n_steady):
+            s_ = states[i % len(states)]
+            gdn.kernel_hip(**{**tc, "state": s_, "new_state": s_}, use_qk_l2norm=l2_)
+        for _ in range(iters):
+            flush.sum()
+            gdn.kernel_hip(**tc, use_qk_l2norm=l2_)
+        torch.cuda.synchronize()
+        # steady: the first pass over the states is still warm from setup
+        manifest.append({"name": name, "warmup": TRACE_WARMUP, "steady": n_steady,
+                         "steady_skip": len(states), "cold": iters})
+        print(f"[trace] {name}: {TRACE_WARMUP} + {n_steady} + {iters} launches",
+              file=sys.stderr, flush=True)
+        del tc, states
+    cal = Calib()
+    bufs = layer_states(torch.zeros(32 * 128 * 128, device=device))
+    n_rmw = max(iters, 2 * len(bufs))
+    for i in range(n_rmw):
+        cal.rmw(bufs[i % len(bufs)], None, None)
+    _, _, _, b1_blocks = _lib.launch_shape(1, 32)
+    for _ in range(iters):
+        cal.empty(b1_blocks, None, None)
+    torch.cuda.synchronize()
+    floor = {"rmw": n_rmw, "rmw_skip": len(bufs), "empty": iters, "empty_blocks": b1_blocks}
+    Path(manifest_path).write_text(json.dumps({"decode": manifest, "floor": floor}))
+
+
+def attribute_kernel_trace(trace_csv, manifest: dict) -> dict:
+    """Median kernel-trace duration (µs) per shape and regime: the decode
+    dispatches of the trace, in start order, are the launches the manifest
+    lists, in launch order."""
+    rows = {TRACE_DECODE: [], TRACE_RMW: [], TRACE_EMPTY: []}
+    with open(trace_csv) as f:
+        for r in csv.DictReader(f):
+            for key, lst in rows.items():
+                if key in r["Kernel_Name"]:
+                    lst.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
+    for lst in rows.values():
+        lst.sort()
+    dec = rows[TRACE_DECODE]
+    need = sum(m["warmup"] + m["steady"] + m["cold"] for m in manifest["decode"])
+    if len(dec) != need:
+        raise ValueError(f"{len(dec)} decode dispatches in the trace, {need} launched")
+
+    def med(span):
+        return round(statistics.median((e - s) / 1e3 for s, e in span), 3)
+
+    shapes, i = {}, 0
+    for m in manifest["decode"]:
+        i += m["warmup"]
+        steady = dec[i + m["steady_skip"]: i + m["steady"]]
+        i += m["steady"]
+        cold = dec[i: i + m["cold"]]
+        i += m["cold"]
+        shapes[m["name"]] = {"steady": med(steady), "cold": med(cold),
+                             "n_steady": len(steady), "n_cold": len(cold)}
+    fl = manifest["floor"]
+    floor = None
+    if len(rows[TRACE_RMW]) == fl["rmw"] and len(rows[TRACE_EMPTY]) == fl["empty"]:
+        floor = {"b1_rmw_us": med(rows[TRACE_RMW][fl["rmw_skip"]:]),
+                 "empty_us": med(rows[TRACE_EMPTY]), "empty_blocks": fl["empty_blocks"]}
+    return {"shapes": shapes, "floor": floor}
+
+
+def kernel_trace_leg(iters: int, timeout_s: float = 300.0) -> dict:
+    """rocprofv3 kernel-trace medians of the decode kernel per shape (steady
+    and cold) and of the floor kernels: ``trace_child`` run as a separate
+    program under ``rocprofv3 --kernel-trace``.  Called before this process
+    initialises the GPU; skipped when this process itself runs under
+    rocprofv3 (which sets ROCPROF_OUTPUT_PATH for the program it profiles)."""
+    if "ROCPROF_OUTPUT_PATH" in os.environ:
+        return {"skipped": "bench.py runs under rocprofv3"}
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        return {"skipped": "rocprofv3 not on PATH"}
+    with tempfile.TemporaryDirectory(prefix="gdn_trace_", dir="/tmp") as d:
+        manifest = os.path.join(d, "manifest.json")
+        cmd = [exe, "--kernel-trace", "--output-format", "csv", "-d", d, "-o", "trace", "--",
+               sys.executable, str(ROOT / "bench.py"), "--trace-child", manifest,
+               "--iters", str(iters)]
+        sys.stderr.flush()
+        try:
+            # the child's output goes to stderr: stdout carries only the JSON line
+            proc = subprocess.run(cmd, cwd="/tmp", env=dict(os.environ, TMPDIR="/tmp"),
+                                  stdout=sys.stderr, stderr=sys.stderr, timeout=timeout_s)
+        except subprocess.TimeoutExpired:
+            return {"skipped": f"traced run exceeded {timeout_s:.0f} s"}
+        traces = sorted(Path(d).rglob("*kernel_trace.csv"))
+        # rocprofv3 may end with a signal after the program has finished and
+        # its output is whole: the manifest and the trace decide.
+        if not os.path.exists(manifest) or not traces:
+            return {"skipped": f"traced run exited {proc.returncode} without a trace"}
+        try:
+            res = attribute_kernel_trace(traces[0], json.loads(Path(manifest).read_text()))
+        except (OSError, ValueError, KeyError) as e:
+            return {"skipped": f"trace not attributable: {e}"}
+    res["timer"] = "rocprofv3 --kernel-trace, median per shape and regime"
+    return res
 
 
 def timed_steps(t, l2, steps, states):
@@ -625,6 +775,10 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--prefill-only", action="store_true",
                     help="time the prefill workloads only and print them as JSON")
+    ap.add_argument("--no-kernel-trace", action="store_true",
+                    help="skip the rocprofv3 kernel-trace leg")
+    ap.add_argument("--trace-child", metavar="MANIFEST",
+                    help="(internal) the launches the kernel-trace leg records")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -633,9 +787,21 @@ def main():
               file=sys.stderr)
         sys.exit(1)
 
+    log = lambda *a: print(*a, file=sys.stderr, flush=True)  # noqa: E731
+    trace = None
+    if not (args.trace_child or args.no_kernel_trace or args.no_per_config or args.pmc_pass
+            or args.pmc_prefill or args.prefill_only):
+        # before this process touches the GPU: the traced run is its own program
+        log("[bench] kernel-trace leg: every per-config shape under rocprofv3")
+        trace = kernel_trace_leg(args.iters)
+        log(f"[bench] kernel-trace leg: {trace.get('skipped', 'done')}")
+
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
     _lib.get_lib()
+    if args.trace_child:
+        trace_child(device, args.trace_child, args.iters)
+        return
     if args.pmc_pass:
         pmc_pass(device)
         return
@@ -647,7 +813,6 @@ def main():
         print(json.dumps({"prefill": pf, "prefill_roofline": prefill_roofline(pf)}), flush=True)
         return
 
-    log = lambda *a: print(*a, file=sys.stderr, flush=True)  # noqa: E731
     B, H, HV, l2 = CONFIGS[args.config]
     nbytes = step_bytes(B, H, HV)
     t = make_device_inputs(B, H, HV, device, seed=1003)
@@ -672,15 +837,10 @@ def main():
 
     flush = torch.ones(1 << 28, device=device)     # 1 GiB > 32 MiB L2 + 256 MiB MALL
     per_config = {}
+    traced = (trace or {}).get("shapes", {})
     if not args.no_per_config:
-        f32, bf16 = torch.float32, torch.bfloat16
-        shapes = [(n, *c, 1, f32) for n, c in CONFIGS.items()]
-        shapes += [(f"qk4_v8_b{bb}", bb, 4, 8, False, 1, f32) for bb in REF_BATCHES]
-        shapes += [(f"{n}_bf16_state", *CONFIGS[n], 1, bf16)
-                   for n in ("b1_qk16_v32_l2", "b8_qk16_v32_l2", "b256_qk16_v32_l2")]
-        shapes += [(f"{n}_t{tt}", *CONFIGS[n], tt, f32)
-                   for n in ("b1_qk16_v32_l2", "b256_qk16_v32_l2") for tt in (2, 4)]
-        for name, b_, h_, hv_, l2_, t_, sd_ in shapes:
+        bf16 = torch.bfloat16
+        for name, b_, h_, hv_, l2_, t_, sd_ in per_config_shapes():
             tc = make_device_inputs(b_, h_, hv_, device, seed=7, T=t_, state_dtype=sd_)
             for _ in range(5):
                 gdn.kernel_hip(**tc, use_qk_l2norm=l2_)
@@ -698,8 +858,15 @@ def main():
                 "steady_hbm_gbs": round(nb / (sm * 1e-6) / 1e9, 1),
                 "steady_frac_of_peak": round(nb / (sm * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
             }
+            tr = traced.get(name)
+            if tr is not None:
+                per_config[name].update({
+                    "trace_us_steady": tr["steady"], "trace_us_cold": tr["cold"],
+                    "trace_steady_hbm_gbs": round(nb / (tr["steady"] * 1e-6) / 1e9, 1)})
             log(f"[bench] {name}: steady {sm:.2f} us ({per_config[name]['steady_hbm_gbs']:.0f}"
-                f" GB/s), warm {med['warm']:.2f} us, cold {med['cold']:.2f} us")
+                f" GB/s), warm {med['warm']:.2f} us, cold {med['cold']:.2f} us"
+                + (f"; kernel trace steady {tr['steady']:.2f} us, cold {tr['cold']:.2f} us"
+                   if tr is not None else ""))
             del tc
 
     floor = traffic_floor(device, args.iters)
@@ -733,6 +900,22 @@ def main():
                 f"({prefill_cpu['sample']})")
 
     b1 = per_config.get("b1_qk16_v32_l2")
+    b1_line = {"target_us": 3.0}
+    if b1 and "trace_us_steady" in b1:
+        b1_line.update({"us_per_step": b1["trace_us_steady"],
+                        "us_per_step_cold": b1["trace_us_cold"],
+                        "timer": trace["timer"], "floor_kernel_trace": trace["floor"]})
+    else:
+        b1_line.update({"us_per_step": None,
+                        "kernel_trace": (trace or {}).get("skipped", "not run")})
+    if b1:
+        b1_line["stamped"] = {"us_steady": b1["us_steady"], "us_warm": b1["us_warm"],
+                              "us_cold": b1["us_cold"],
+                              "timer": "kernel-stamped HIP events (hipExtLaunchKernelGGL)",
+                              "floor_same_timer": floor}
+    else:
+        b1_line["stamped"] = {"floor_same_timer": floor}
+    b1_line["serving"] = serving
     line = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -755,11 +938,7 @@ def main():
             "launch": {"rows_per_lane_group": ns, "waves_per_block": waves,
                        "cache_policy": policy, "blocks": blocks},
         },
-        "b1": ({"us_per_step_steady": b1["us_steady"], "us_per_step_warm": b1["us_warm"],
-                "us_per_step_cold": b1["us_cold"],
-                "timer": "kernel-stamped HIP events (hipExtLaunchKernelGGL)",
-                "floor_same_timer": floor, "serving": serving}
-               if b1 else {"floor_same_timer": floor, "serving": serving}),
+        "b1": b1_line,
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 1),

@@ -295,20 +295,30 @@ __device__ __forceinline__ void load_token(const Params& p, int bi, int t, int h
   in.v = load_bf16_run<NS>(p.v + (bt * p.HV + hv) * kDim + row0);
 }
 
-// One token of the recurrence on the NS rows a lane group holds:
-// decay, delta rule, rank-1 update (in s) and outputs o (reference
-// kernel.py:73-75, 101-113).
+// Per-head quantities of one token, from its small inputs only (gates, the
+// q/k scales, k.q): they do not depend on the state, so they are computed
+// while the state is still in flight.
+template <int NS>
+struct TokenHead {
+  float qf[8];      // this lane's raw q elements
+  float kf[8];      // this lane's raw k elements
+  float vrow[NS];   // v of the lane group's rows
+  float g;          // decay factor
+  float beta;
+  float kscale;     // 1 / |k| (L2-norm) or 1
+  float kq;         // k_hat . q'
+  float gk;         // g * kscale
+  float gq;         // g * qscale
+};
+
 template <int NS, bool L2NORM>
-__device__ __forceinline__ void token_update(float (&s)[NS][8], const TokenIn<NS>& in,
-                                             float A_log, float dt_bias, float scale,
-                                             float (&o)[NS]) {
+__device__ __forceinline__ void token_head(const TokenIn<NS>& in, float A_log, float dt_bias,
+                                           float scale, TokenHead<NS>& h) {
   float g, beta;
   gates(bf16_bits_to_f32(in.a_bits), dt_bias, A_log, bf16_bits_to_f32(in.b_bits), g, beta);
-
-  float qf[8], kf[8], vrow[NS];
-  unpack_bf16x8(in.q, qf);
-  unpack_bf16x8(in.k, kf);
-  unpack_bf16_run<NS>(in.v, vrow);
+  unpack_bf16x8(in.q, h.qf);
+  unpack_bf16x8(in.k, h.kf);
+  unpack_bf16_run<NS>(in.v, h.vrow);
 
   // Per-head reductions on the raw values: |q|^2, |k|^2 (L2-norm only) and
   // k.q.  The normalised, scaled vectors q' = qscale*q and k_hat = kscale*k
@@ -320,9 +330,9 @@ __device__ __forceinline__ void token_update(float (&s)[NS][8], const TokenIn<NS
     float hs[3] = {0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      hs[0] = fmaf(qf[i], qf[i], hs[0]);
-      hs[1] = fmaf(kf[i], kf[i], hs[1]);
-      hs[2] = fmaf(qf[i], kf[i], hs[2]);
+      hs[0] = fmaf(h.qf[i], h.qf[i], hs[0]);
+      hs[1] = fmaf(h.kf[i], h.kf[i], hs[1]);
+      hs[2] = fmaf(h.qf[i], h.kf[i], hs[2]);
     }
     row16_sum<3>(hs);
     // |x|^2 + eps >= eps is a normal number: the raw v_rsq_f32 suffices.
@@ -332,14 +342,24 @@ __device__ __forceinline__ void token_update(float (&s)[NS][8], const TokenIn<NS
   } else {
     float hs[1] = {0.0f};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) hs[0] = fmaf(qf[i], kf[i], hs[0]);
+    for (int i = 0; i < 8; ++i) hs[0] = fmaf(h.qf[i], h.kf[i], hs[0]);
     row16_sum<1>(hs);
     kq_raw = hs[0];
   }
-  const float kq = kq_raw * (qscale * kscale);  // k_hat . q'
-  const float gk = g * kscale;
-  const float gq = g * qscale;
+  h.g = g;
+  h.beta = beta;
+  h.kscale = kscale;
+  h.kq = kq_raw * (qscale * kscale);
+  h.gk = g * kscale;
+  h.gq = g * qscale;
+}
 
+// One token of the recurrence on the NS rows a lane group holds: decay,
+// delta rule, rank-1 update (in s) and outputs o (reference
+// kernel.py:73-75, 101-113).
+template <int NS>
+__device__ __forceinline__ void token_rows(float (&s)[NS][8], const TokenHead<NS>& h,
+                                           float (&o)[NS]) {
   // Per-row reductions k.S and q.S on the undecayed state.
   float red[2 * NS];
 #pragma unroll
@@ -347,8 +367,8 @@ __device__ __forceinline__ void token_update(float (&s)[NS][8], const TokenIn<NS
     float ak = 0.0f, aq = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      ak = fmaf(s[n][i], kf[i], ak);
-      aq = fmaf(s[n][i], qf[i], aq);
+      ak = fmaf(s[n][i], h.kf[i], ak);
+      aq = fmaf(s[n][i], h.qf[i], aq);
     }
     red[2 * n] = ak;
     red[2 * n + 1] = aq;
@@ -357,12 +377,12 @@ __device__ __forceinline__ void token_update(float (&s)[NS][8], const TokenIn<NS
 
 #pragma unroll
   for (int n = 0; n < NS; ++n) {
-    const float old_v = gk * red[2 * n];            // k_hat . (g S)
-    const float d = beta * (vrow[n] - old_v);       // beta * (v - old_v)
-    o[n] = fmaf(d, kq, gq * red[2 * n + 1]);        // q' . S_new
-    const float dk = d * kscale;                    // S_new = g S + d (x) k_hat
+    const float old_v = h.gk * red[2 * n];          // k_hat . (g S)
+    const float d = h.beta * (h.vrow[n] - old_v);   // beta * (v - old_v)
+    o[n] = fmaf(d, h.kq, h.gq * red[2 * n + 1]);    // q' . S_new
+    const float dk = d * h.kscale;                  // S_new = g S + d (x) k_hat
 #pragma unroll
-    for (int i = 0; i < 8; ++i) s[n][i] = fmaf(dk, kf[i], g * s[n][i]);
+    for (int i = 0; i < 8; ++i) s[n][i] = fmaf(dk, h.kf[i], h.g * s[n][i]);
   }
 }
 
@@ -376,15 +396,16 @@ __device__ __forceinline__ void token_update(float (&s)[NS][8], const TokenIn<NS
 // (b, hv) head per workgroup.
 //
 // The arguments are scalars rather than one struct so that the first 14
-// dwords (every pointer and size the first loads need) are preloaded into
+// dwords -- every pointer and size the first loads need: six pointers, H and
+// HV/H packed into one dword (16 bits each) and T -- are preloaded into
 // SGPRs by the dispatcher (-amdgpu-kernarg-preload-count): the state stream
 // then starts without waiting for a kernarg memory read.  The remaining
 // arguments are read while the first loads are in flight.
 template <int NS, int WAVES, bool L2NORM, int POLICY, bool BF16, bool MULTI>
 __global__ __launch_bounds__(64 * WAVES) void gdn_decode_k128(
     const void* state, const uint16_t* q, const uint16_t* k, const uint16_t* v,
-    const uint16_t* a, const uint16_t* b, int H, int ratio, const float* A_log_p,
-    const float* dt_bias_p, uint16_t* out, void* new_state, float scale, int T_arg) {
+    const uint16_t* a, const uint16_t* b, unsigned h_ratio, int T_arg, const float* A_log_p,
+    const float* dt_bias_p, uint16_t* out, void* new_state, float scale) {
   Params p;
   p.state = state;
   p.q = q;
@@ -398,9 +419,9 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_decode_k128(
   p.new_state = new_state;
   p.scale = scale;
   p.T = MULTI ? T_arg : 1;
-  p.H = H;
-  p.ratio = ratio;
-  p.HV = H * ratio;
+  p.H = static_cast<int>(h_ratio & 0xffffu);
+  p.ratio = static_cast<int>(h_ratio >> 16);
+  p.HV = p.H * p.ratio;
   constexpr int kRowsPerWave = kLaneGroups * NS;
   constexpr int kRowsPerBlock = kRowsPerWave * WAVES;
   constexpr int kTiles = kDim / kRowsPerBlock;
@@ -421,10 +442,11 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_decode_k128(
   const int T = p.T;
 
   // Issue every global load before any arithmetic.  Loads retire in issue
-  // order, so the small per-head operands (gate scalars, q, k, v) go first:
-  // their math then overlaps the state stream instead of waiting behind it.
-  const float A_log = p.A_log[hv];
-  const float dt_bias = p.dt_bias[hv];
+  // order, so the small per-token operands (a, b, q, k, v) go first: their
+  // math then overlaps the state stream instead of waiting behind it.  Both
+  // bursts use only preloaded arguments; A_log and dt_bias (whose pointers
+  // are not preloaded) are read after them, so no wave waits on a kernarg
+  // memory read before its state loads are in flight.
   TokenIn<NS> cur;
   load_token<NS, BF16>(p, bi, 0, hq, hv, row0, j, cur);
   __builtin_amdgcn_sched_barrier(0);
@@ -433,6 +455,15 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_decode_k128(
   RowRaw<BF16> raw[NS];
 #pragma unroll
   for (int n = 0; n < NS; ++n) raw[n] = load_row<BF16, POLICY>(p.state, row_base + n, j);
+  __builtin_amdgcn_sched_barrier(0);
+  const float A_log = p.A_log[hv];
+  const float dt_bias = p.dt_bias[hv];
+  __builtin_amdgcn_sched_barrier(0);  // both reads in flight before either is used
+
+  // The first token's per-head math waits only on the small loads: keep it
+  // ahead of everything that waits on the state.
+  TokenHead<NS> h;
+  token_head<NS, L2NORM>(cur, A_log, dt_bias, p.scale, h);
   __builtin_amdgcn_sched_barrier(0);
 
   float s[NS][8];
@@ -445,18 +476,25 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_decode_k128(
       if (t + 1 < T) load_token<NS, BF16>(p, bi, t + 1, hq, hv, row0, j, nxt);  // prefetch
     }
     float o[NS];
-    token_update<NS, L2NORM>(s, cur, A_log, dt_bias, p.scale, o);
+    token_rows<NS>(s, h, o);
+    if constexpr (!MULTI) {
+      // The state write-back is the kernel's tail: issue it before the output.
+#pragma unroll
+      for (int n = 0; n < NS; ++n) store_row<BF16, POLICY>(p.new_state, row_base + n, j, s[n]);
+    }
     if (j == 0) {
       const size_t out_row = ((static_cast<size_t>(bi) * T + t) * p.HV + hv) * kDim + row0;
       store_bf16_run<NS>(p.out + out_row, o);
     }
     if constexpr (MULTI) {
-      if (t + 1 < T) cur = nxt;
+      if (t + 1 < T) token_head<NS, L2NORM>(nxt, A_log, dt_bias, p.scale, h);
     }
   }
 
+  if constexpr (MULTI) {
 #pragma unroll
-  for (int n = 0; n < NS; ++n) store_row<BF16, POLICY>(p.new_state, row_base + n, j, s[n]);
+    for (int n = 0; n < NS; ++n) store_row<BF16, POLICY>(p.new_state, row_base + n, j, s[n]);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -487,13 +525,15 @@ hipError_t launch_one(bool l2, const Params& p, unsigned nb, const Launch& l) {
   const dim3 block(64 * W);
   auto* kern = l2 ? gdn_decode_k128<NS, W, true, POL, BF16, MULTI>
                   : gdn_decode_k128<NS, W, false, POL, BF16, MULTI>;
+  // H and HV/H are each below 2^16 (checked by the caller).
+  const unsigned h_ratio = static_cast<unsigned>(p.H) | (static_cast<unsigned>(p.ratio) << 16);
   if (l.start || l.stop) {
     hipExtLaunchKernelGGL(kern, grid, block, 0, l.stream, l.start, l.stop, 0, p.state, p.q,
-                          p.k, p.v, p.a, p.b, p.H, p.ratio, p.A_log, p.dt_bias, p.out,
-                          p.new_state, p.scale, p.T);
+                          p.k, p.v, p.a, p.b, h_ratio, p.T, p.A_log, p.dt_bias, p.out,
+                          p.new_state, p.scale);
   } else {
-    hipLaunchKernelGGL(kern, grid, block, 0, l.stream, p.state, p.q, p.k, p.v, p.a, p.b, p.H,
-                       p.ratio, p.A_log, p.dt_bias, p.out, p.new_state, p.scale, p.T);
+    hipLaunchKernelGGL(kern, grid, block, 0, l.stream, p.state, p.q, p.k, p.v, p.a, p.b,
+                       h_ratio, p.T, p.A_log, p.dt_bias, p.out, p.new_state, p.scale);
   }
   return hipGetLastError();
 }
@@ -617,6 +657,7 @@ int steps_impl(const void* q, const void* k, const void* v, const void* state,
                int policy, void* start_event, void* stop_event, void* hip_stream) {
   if (B < 0 || T < 1 || H <= 0 || HV <= 0 || HV % H != 0) return hipErrorInvalidValue;
   if (H > 65535) return hipErrorInvalidValue;  // grid y
+  if (HV / H > 65535) return hipErrorInvalidValue;  // packed with H into 32 bits
   if (K != kDim || V != kDim) return hipErrorInvalidValue;
   if (state_bf16 != 0 && state_bf16 != 1) return hipErrorInvalidValue;
   const Variant var{use_qk_l2norm != 0, state_bf16 != 0, T > 1};
