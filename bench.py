@@ -18,11 +18,16 @@ step's dirty lines: the steady state of serving.  Prints ONE JSON line:
   around every timed launch on the launch stream, against MI355X's 8 TB/s;
   ``traffic`` is the measured HBM bytes per launch from the committed
   rocprofv3 counter summary, when there is one;
-* ``b1``: kernel time per step at B=1 (qk16_v32, L2-norm) from a rocprofv3
-  kernel trace (the analogue of the reference's CUPTI timings): a child
-  process, started under ``rocprofv3 --kernel-trace`` before this process
-  touches the GPU, launches every per-config shape through the product
-  entry point, and its dispatches are attributed back to the shapes;
+* ``b1``: time per decode step at B=1 (qk16_v32, L2-norm).  ``us_per_step``:
+  steps back to back from a HIP graph, one per layer state (>= 1 GiB of
+  states, so every step reads its state from HBM), HIP events around the
+  replays: kernel plus launch gap per step, with the GPU never idle as in a
+  model's decode loop.  ``kernel_trace``: rocprofv3 kernel-trace durations
+  (the analogue of the reference's CUPTI timings) of isolated launches ~12 us
+  apart and right after a 1 GiB read: a child process, started under
+  ``rocprofv3 --kernel-trace`` before this process touches the GPU,
+  launches every per-config shape through the product entry point, and its
+  dispatches are attributed back to the shapes;
 * ``per_config``: kernel times for every benchmark shape and for the
   reference's qk4_v8 definition at its workload batch sizes, plus bf16-state
   and multi-token (T = 2, 4) steps, in three regimes: steady (as above),
@@ -32,7 +37,7 @@ step's dirty lines: the steady state of serving.  Prints ONE JSON line:
   kernel dispatch stamps (hipExtLaunchKernelGGL: ~2.5 us of their own
   overhead, so only meaningful above ~10 us), ``trace_us_*`` from the
   kernel trace;
-* ``b1.floor_kernel_trace`` and ``b1.stamped.floor_same_timer``: each timer
+* ``b1.kernel_trace.floor`` and ``b1.stamped.floor_same_timer``: each timer
   on reference kernels that move only the state bytes (an in-place
   read-modify-write of the B=1 state, and of the B=256 state under the
   stamped events) and on an empty kernel, so that the decode times read
@@ -443,6 +448,43 @@ def b1_serving(device, layers: int = 48, reps: int = 20):
         res[f"{name}_us_per_step"] = round(statistics.median(per), 2)
     res["layers"] = layers
     return res
+
+
+def b1_back_to_back(device, reps: int = 20):
+    """Time per decode step at B=1 qk16_v32 (L2-norm) when steps run back to
+    back with the GPU never idle, as in a model's decode loop: one HIP graph
+    of one step per layer state (``layer_states``: >= 1 GiB in total, so
+    every step reads a state that is no longer cached), replayed; HIP events
+    on the replay stream around each replay.  Per step: kernel plus the gap
+    to the next kernel, an upper bound on the kernel's duration."""
+    t = make_device_inputs(1, 16, 32, device, seed=12)
+    states = layer_states(t["state"])
+    views = [{**t, "state": s_, "new_state": s_} for s_ in states]
+
+    def steps():
+        for v_ in views:
+            gdn.kernel_hip(**v_, use_qk_l2norm=True)
+
+    steps()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        steps()
+    torch.cuda.synchronize()
+    for _ in range(2):
+        graph.replay()
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(reps)]
+    for a_, b_ in ev:
+        a_.record(stream)
+        graph.replay()
+        b_.record(stream)
+    torch.cuda.synchronize()
+    per = statistics.median(a_.elapsed_time(b_) * 1e3 for a_, b_ in ev) / len(views)
+    del graph
+    return {"us_per_step": round(per, 3), "steps_per_replay": len(views),
+            "state_bytes_rotated": len(views) * states[0].numel() * 4}
 
 
 def reference_stream(device, iters: int = 20):
@@ -885,6 +927,9 @@ def main():
     serving = b1_serving(device)
     log(f"[bench] B=1 serving, {serving['layers']} layer steps: eager "
         f"{serving['eager_us_per_step']} us/step, HIP graph {serving['graph_us_per_step']} us/step")
+    b2b = b1_back_to_back(device)
+    log(f"[bench] B=1 back to back over {b2b['steps_per_replay']} layer states "
+        f"({b2b['state_bytes_rotated'] >> 20} MiB): {b2b['us_per_step']} us/step")
     ref_stream = reference_stream(device)
     log(f"[bench] reference stream: {ref_stream['gbs']:.0f} GB/s ({ref_stream['us']} us)")
 
@@ -900,14 +945,20 @@ def main():
                 f"({prefill_cpu['sample']})")
 
     b1 = per_config.get("b1_qk16_v32_l2")
-    b1_line = {"target_us": 3.0}
+    b1_line = {"target_us": 3.0, "us_per_step": b2b["us_per_step"],
+               "timer": ("HIP events around replays of a HIP graph of back-to-back steps, "
+                         "one per layer state (>= 1 GiB of states: every step reads its "
+                         "state from HBM); per step = kernel + gap to the next kernel"),
+               "back_to_back": b2b}
     if b1 and "trace_us_steady" in b1:
-        b1_line.update({"us_per_step": b1["trace_us_steady"],
-                        "us_per_step_cold": b1["trace_us_cold"],
-                        "timer": trace["timer"], "floor_kernel_trace": trace["floor"]})
+        b1_line["kernel_trace"] = {
+            "us_isolated": b1["trace_us_steady"], "us_after_flush": b1["trace_us_cold"],
+            "floor": trace["floor"],
+            "timer": (trace["timer"] + "; launches ~12 us apart from Python (the GPU idles "
+                      "between them), rotating over >= 1 GiB of states; after_flush: right "
+                      "after a 1 GiB read")}
     else:
-        b1_line.update({"us_per_step": None,
-                        "kernel_trace": (trace or {}).get("skipped", "not run")})
+        b1_line["kernel_trace"] = {"skipped": (trace or {}).get("skipped", "not run")}
     if b1:
         b1_line["stamped"] = {"us_steady": b1["us_steady"], "us_warm": b1["us_warm"],
                               "us_cold": b1["us_cold"],
