@@ -1,4 +1,5 @@
-"""flashinfer-bench-style evaluation of the decode entry points on MI355X.
+"""flashinfer-bench-style evaluation of the decode and prefill entry points on
+MI355X.
 
 The reference evaluates a solution with flashinfer-bench over the contest's
 workloads of a definition (scripts/run_local.py:31-98): for each workload it
@@ -15,6 +16,12 @@ external to the reference, CLAUDE.md:164-168):
 * ``contest_decode_workloads()``: the 54 ``gdn_decode_qk4_v8_d128_k_last``
   workloads, batch sizes 1 x10, 4 x8, 8 x7, 16 x7, 32 x7, 48 x7, 64 x8
   (CLAUDE.md:139-140), each with its own seed;
+* ``prefill_workloads()``: a seeded mix of 20 ``gdn_prefill_qk4_v8_d128_k_last``
+  workloads (variable-length sequences packed with ``cu_seqlens``): the
+  reference's workload 0 (one 6-token sequence, findings/research.md:1029),
+  single sequences of 1 to 16384 tokens, uniform and ragged batches and
+  empty sequences.  The contest's 100 prefill workloads are not recorded in
+  the reference (CLAUDE.md:159), so the mix is this package's own;
 * ``evaluate(fn, workloads, ...)``: correctness against a caller-supplied
   reference (a value-returning ``ref(**inputs) -> (output, new_state)``, the
   role the definition's ``reference`` plays) and timing in the reference's
@@ -24,20 +31,27 @@ external to the reference, CLAUDE.md:164-168):
   old ``do_bench``) and "trace" (kernel durations from a rocprofv3 kernel
   trace of the run, the CUPTI tier: ``evaluate`` writes a manifest of its
   calls and ``attribute_trace`` assigns the trace's dispatches to them);
-* speedups against the reference's published per-batch B200 kernel times
-  (CUPTI medians of fla-recurrent and of the FlashInfer baseline,
-  CLAUDE.md:229-238); the contest's own speedup is against the definition's
-  reference on the same GPU, which is not available here.
+* speedups against the reference's published B200 kernel times: per batch
+  size for the decode (CUPTI medians of fla-recurrent and of the FlashInfer
+  baseline, CLAUDE.md:229-238), and for prefill workload 0 (CUPTI medians of
+  FLA's chunkwise prefill and of the FlashInfer baseline, CLAUDE.md:333-337);
+  the contest's own speedup is against the definition's reference on the
+  same GPU, which is not available here.
 
 Command line (arguments as scripts/shared.py:93-142):
 
     python -m flashinfer_competition_codebase_amd.harness run --algo hip [-n N]
+        [--definition gdn_prefill_qk4_v8_d128_k_last --algo prefill-hip]
         [--workload-id PREFIX] [--iterations 100] [--num-trials 5] [--tier event]
         [--manifest calls.json] [--json results.json]
     rocprofv3 --kernel-trace --output-format csv -d out -o run -- python3 -m \\
         flashinfer_competition_codebase_amd.harness run --manifest calls.json
     python -m flashinfer_competition_codebase_amd.harness attribute \\
-        --trace out/run_kernel_trace.csv --manifest calls.json
+        --trace out/run_kernel_trace.csv --manifest calls.json [--definition ...]
+
+In the trace tier a prefill call is its chunk-offsets (several sequences),
+preparation and scan dispatches, timed from the first one's start to the
+last one's end.
 """
 
 from __future__ import annotations
@@ -56,6 +70,8 @@ from typing import Callable, Optional
 import torch
 
 DECODE_DEFINITION = "gdn_decode_qk4_v8_d128_k_last"
+PREFILL_DEFINITION = "gdn_prefill_qk4_v8_d128_k_last"
+DEFINITIONS = (DECODE_DEFINITION, PREFILL_DEFINITION)
 
 # Batch sizes of the contest's 54 decode workloads and how many of each
 # (CLAUDE.md:139-140).
@@ -69,6 +85,17 @@ B200_CUPTI_US = {
     "fi-b200": {1: 3.36, 4: 3.65, 8: 4.22, 16: 5.31, 32: 7.71, 48: 10.50, 64: 12.74},
 }
 BASELINE_LABELS = {"fla-b200": "B200 fla-recurrent", "fi-b200": "B200 FlashInfer"}
+
+# Published B200 times (CUPTI medians, µs) of the qk4_v8 prefill definition's
+# workload 0, CLAUDE.md:333-337 (findings/research.md:1075-1080): FLA's
+# chunkwise prefill and the FlashInfer baseline.  No other prefill workload
+# has a published time.
+PREFILL_WORKLOAD0_LENS = (6,)
+B200_PREFILL_US = {"fla-b200": 1536.0, "fi-b200": 185.0}
+PREFILL_BASELINE_LABELS = {"fla-b200": "B200 fla-chunk", "fi-b200": "B200 FlashInfer"}
+
+# Kernel-name substrings of the dispatches one call makes, per definition.
+TRACE_KERNELS = {DECODE_DEFINITION: "gdn_decode", PREFILL_DEFINITION: "gdn_pf::"}
 
 ATOL = 1e-2
 RTOL = 1e-2
@@ -97,6 +124,81 @@ def contest_decode_workloads() -> list:
     return out
 
 
+@dataclass(frozen=True)
+class PrefillWorkload:
+    """One prefill workload: sequence lengths (packed with cu_seqlens), head
+    counts, seed and the L2-norm option."""
+    uuid: str
+    lens: tuple
+    H: int = 4
+    HV: int = 8
+    seed: int = 0
+    use_qk_l2norm: bool = False
+
+    @property
+    def L(self) -> int:
+        return sum(self.lens)
+
+    @property
+    def N(self) -> int:
+        return len(self.lens)
+
+    @property
+    def B(self) -> int:               # sequences: the batch of a prefill
+        return self.N
+
+    @property
+    def dispatches(self) -> int:      # kernels one prefill call launches
+        return 2 if self.N == 1 else 3
+
+
+def prefill_workloads() -> list:
+    """A seeded mix of 20 qk4_v8 prefill workloads: the reference's workload 0
+    (one 6-token sequence), single sequences across the chunk boundaries and
+    up to 16384 tokens, uniform and ragged batches, and empty sequences."""
+    g = torch.Generator().manual_seed(4242)
+
+    def ragged(n, hi):
+        return tuple(int(x) for x in torch.randint(1, hi + 1, (n,), generator=g))
+
+    mixes = [
+        (6,), (1,), (64,), (65,), (127,), (512,), (1000,), (2048,), (4096,), (8192,),
+        (16384,), (100, 200, 300, 400), (128,) * 8, (256,) * 16, (1024,) * 16,
+        (512,) * 32, (64,) * 64, ragged(24, 2048), ragged(8, 8192), (0, 17, 0, 300),
+    ]
+    return [PrefillWorkload(uuid=f"prefill-w{i:02d}", lens=lens, seed=20_000 + i)
+            for i, lens in enumerate(mixes)]
+
+
+def make_prefill_inputs(w: PrefillWorkload, device) -> dict:
+    """Seeded inputs of prefill workload ``w`` on ``device``: q and k rows of
+    unit norm (a model normalises them; unnormalised N(0, 1) keys make the
+    delta rule diverge over long sequences), v, a, b ~ N(0, 1) bf16; state
+    ~ N(0, 0.05^2) fp32; A_log = log U[1, 16]; dt_bias ~ U[-1, 1];
+    cu_seqlens int32; scale = 1/sqrt(128).  Drawn on the CPU."""
+    g = torch.Generator().manual_seed(w.seed)
+    K = V = 128
+    L, N = w.L, w.N
+    q = torch.randn(L, w.H, K, generator=g)
+    k = torch.randn(L, w.H, K, generator=g)
+    cu = torch.zeros(N + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(torch.tensor(w.lens, dtype=torch.int64), 0).to(torch.int32)
+    t = dict(
+        q=(q / q.norm(dim=-1, keepdim=True)).to(torch.bfloat16),
+        k=(k / k.norm(dim=-1, keepdim=True)).to(torch.bfloat16),
+        v=torch.randn(L, w.HV, V, generator=g).to(torch.bfloat16),
+        state=torch.randn(N, w.HV, V, K, generator=g) * 0.05,
+        A_log=torch.log(torch.rand(w.HV, generator=g) * 15.0 + 1.0),
+        a=torch.randn(L, w.HV, generator=g).to(torch.bfloat16),
+        dt_bias=torch.rand(w.HV, generator=g) * 2.0 - 1.0,
+        b=torch.randn(L, w.HV, generator=g).to(torch.bfloat16),
+        cu_seqlens=cu,
+    )
+    t = {n: x.to(device) for n, x in t.items()}
+    t["scale"] = 1.0 / math.sqrt(K)
+    return t
+
+
 def make_inputs(w: Workload, device) -> dict:
     """Seeded inputs of workload ``w`` on ``device`` with the benchmark's
     distributions: q, k, v, a, b ~ N(0, 1) bf16; state ~ N(0, 0.05^2) fp32;
@@ -120,7 +222,16 @@ def make_inputs(w: Workload, device) -> dict:
 
 
 def _dps_outputs(inputs: dict) -> dict:
-    """Caller-allocated outputs of the DPS form (scripts/profile_proton.py:106-110)."""
+    """Caller-allocated outputs of the DPS form (scripts/profile_proton.py:106-110):
+    decode ``output [B, T, HV, V]``, ``new_state [B, HV, V, K]``; prefill
+    ``output [L, HV, V]``, ``new_state [N, HV, V, K]``."""
+    if "cu_seqlens" in inputs:
+        L, HV, V = inputs["v"].shape
+        K = inputs["q"].shape[-1]
+        N = inputs["cu_seqlens"].numel() - 1
+        dev = inputs["q"].device
+        return dict(output=torch.empty(L, HV, V, dtype=torch.bfloat16, device=dev),
+                    new_state=torch.empty(N, HV, V, K, dtype=torch.float32, device=dev))
     B, T, HV, V = inputs["v"].shape
     K = inputs["q"].shape[-1]
     dev = inputs["q"].device
@@ -147,7 +258,8 @@ def compare(out, ref, atol: float = ATOL, rtol: float = RTOL):
 
 @dataclass
 class Result:
-    """One workload's evaluation (scripts/run_local.py:79-96 fields)."""
+    """One workload's evaluation (scripts/run_local.py:79-96 fields); ``B`` is
+    the batch (sequences of a prefill)."""
     uuid: str
     B: int
     status: str
@@ -161,17 +273,33 @@ class Result:
 
 class Manifest:
     """The ordered list of solution calls of a run, for ``attribute_trace``:
-    each call is (workload uuid, phase) with phase "check", "warmup" or
-    "timed"."""
+    each call is (workload uuid, phase, dispatches) with phase "check",
+    "warmup" or "timed" and the number of kernel dispatches the call makes."""
 
     def __init__(self):
         self.calls = []
 
-    def add(self, uuid: str, phase: str) -> None:
-        self.calls.append([uuid, phase])
+    def add(self, uuid: str, phase: str, dispatches: int = 1) -> None:
+        self.calls.append([uuid, phase, dispatches])
 
     def write(self, path) -> None:
         Path(path).write_text(json.dumps({"calls": self.calls}))
+
+
+def baseline_us(w, baseline: Optional[str]) -> Optional[float]:
+    """The published B200 time the speedup of workload ``w`` is taken
+    against, or None: the decode per batch size at the qk4_v8 shape (T = 1),
+    the prefill for the reference's workload 0 only."""
+    if not baseline:
+        return None
+    if isinstance(w, PrefillWorkload):
+        if tuple(w.lens) == PREFILL_WORKLOAD0_LENS and (w.H, w.HV) == (4, 8):
+            return B200_PREFILL_US.get(baseline)
+        return None
+    table = B200_CUPTI_US.get(baseline)
+    if table and w.B in table and w.T == 1 and (w.H, w.HV) == (4, 8):
+        return table[w.B]
+    return None
 
 
 def _call(fn, dps: bool, inputs: dict, outputs: dict):
@@ -186,7 +314,8 @@ def evaluate(fn: Callable, workloads, *, dps: bool = True, reference: Optional[C
              num_trials: int = 5, tier: str = "event", flush: str = "read",
              clone: bool = True, manifest: Optional[Manifest] = None,
              baseline: str = "fla-b200", log=None) -> list:
-    """Evaluate entry point ``fn`` on each workload.
+    """Evaluate entry point ``fn`` on each workload (``Workload`` for the
+    decode definition, ``PrefillWorkload`` for the prefill definition).
 
     ``dps``: ``fn`` is destination-passing (writes ``output`` and
     ``new_state``) or value-returning (returns them), the two forms of
@@ -213,18 +342,20 @@ def evaluate(fn: Callable, workloads, *, dps: bool = True, reference: Optional[C
     if flush != "none":
         flush_buf = torch.empty(FLUSH_BYTES // 4, dtype=torch.float32, device=device)
         flush_buf.fill_(1.0)
-    table = B200_CUPTI_US.get(baseline) if baseline else None
     results = []
     for w in workloads:
-        base = make_inputs(w, device)
+        prefill = isinstance(w, PrefillWorkload)
+        base = make_prefill_inputs(w, device) if prefill else make_inputs(w, device)
+        nd = w.dispatches if prefill else 1
         if log:
-            log(f"[harness] {w.uuid}: B={w.B} H={w.H} HV={w.HV} T={w.T}")
+            log(f"[harness] {w.uuid}: " + (f"N={w.N} L={w.L} H={w.H} HV={w.HV}" if prefill
+                                           else f"B={w.B} H={w.H} HV={w.HV} T={w.T}"))
         # correctness on one call with pristine inputs
         inputs = {n: (x.clone() if isinstance(x, torch.Tensor) else x) for n, x in base.items()}
         outputs = _dps_outputs(inputs) if dps else {}
         try:
             if manifest is not None:
-                manifest.add(w.uuid, "check")
+                manifest.add(w.uuid, "check", nd)
             out, new_state = _call(fn, dps, inputs, outputs)
             torch.cuda.synchronize(device)
         except Exception as exc:  # noqa: BLE001 - reported as the workload's status
@@ -253,7 +384,7 @@ def evaluate(fn: Callable, workloads, *, dps: bool = True, reference: Optional[C
                             for n, x in base.items()}
                     outs = _dps_outputs(args) if dps else {}
                 if manifest is not None:
-                    manifest.add(w.uuid, "timed" if timed else "warmup")
+                    manifest.add(w.uuid, "timed" if timed else "warmup", nd)
                 if tier == "event":
                     ev0 = torch.cuda.Event(enable_timing=True)
                     ev1 = torch.cuda.Event(enable_timing=True)
@@ -275,8 +406,9 @@ def evaluate(fn: Callable, workloads, *, dps: bool = True, reference: Optional[C
         res.timings_us = times
         res.latency_us = statistics.fmean(times)
         res.latency_median_us = statistics.median(times)
-        if table and w.B in table and w.T == 1 and (w.H, w.HV) == (4, 8):
-            res.speedup = table[w.B] / res.latency_us
+        ref_us = baseline_us(w, baseline)
+        if ref_us is not None:
+            res.speedup = ref_us / res.latency_us
         results.append(res)
     return results
 
@@ -291,32 +423,37 @@ def attribute_trace(trace_csv, manifest_calls, *, kernel_substring: str = "gdn_d
                     baseline: str = "fla-b200", workloads=None) -> list:
     """Kernel-trace tier: assign the dispatches of kernels whose name
     contains ``kernel_substring`` in a rocprofv3 ``kernel_trace.csv`` (in
-    start-time order) to the manifest's calls, one dispatch per call, and
-    return one Result per workload with the mean and median of its timed
-    calls' kernel durations.  Raises if the counts differ."""
+    start-time order) to the manifest's calls, each call taking as many
+    consecutive dispatches as it made, and return one Result per workload with
+    the mean and median of its timed calls' times (first dispatch's start to
+    last dispatch's end).  Raises if the counts differ."""
     rows = []
     with open(trace_csv) as f:
         for r in csv.DictReader(f):
             if kernel_substring in r["Kernel_Name"]:
                 rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
     rows.sort()
-    if len(rows) != len(manifest_calls):
+    counts = [int(c[2]) if len(c) > 2 else 1 for c in manifest_calls]
+    if len(rows) != sum(counts):
         raise ValueError(f"{len(rows)} '{kernel_substring}' dispatches in the trace but "
-                         f"{len(manifest_calls)} calls in the manifest")
+                         f"{sum(counts)} in the manifest's {len(manifest_calls)} calls")
     per = {}
-    for (start, end), (uuid, phase) in zip(rows, manifest_calls):
+    i = 0
+    for call, n in zip(manifest_calls, counts):
+        uuid, phase = call[0], call[1]
         if phase == "timed":
-            per.setdefault(uuid, []).append((end - start) / 1e3)
-    by_uuid = {w.uuid: w for w in (workloads or contest_decode_workloads())}
-    table = B200_CUPTI_US.get(baseline) if baseline else None
+            per.setdefault(uuid, []).append((rows[i + n - 1][1] - rows[i][0]) / 1e3)
+        i += n
+    by_uuid = {w.uuid: w for w in (workloads or contest_decode_workloads() + prefill_workloads())}
     out = []
     for uuid, d in per.items():
         w = by_uuid.get(uuid)
         B = w.B if w else -1
         res = Result(uuid, B, "TRACED", latency_us=statistics.fmean(d),
                      latency_median_us=statistics.median(d), timings_us=d)
-        if table and w is not None and w.B in table and w.T == 1 and (w.H, w.HV) == (4, 8):
-            res.speedup = table[w.B] / res.latency_us
+        ref_us = baseline_us(w, baseline) if w is not None else None
+        if ref_us is not None:
+            res.speedup = ref_us / res.latency_us
         out.append(res)
     return out
 
@@ -326,7 +463,8 @@ def print_results(results, definition: str = DECODE_DEFINITION, baseline: str = 
     """One line per workload in the layout of scripts/run_local.py:101-120,
     then the mean speedup."""
     file = file or sys.stdout
-    label = BASELINE_LABELS.get(baseline, baseline)
+    labels = PREFILL_BASELINE_LABELS if definition == PREFILL_DEFINITION else BASELINE_LABELS
+    label = labels.get(baseline, baseline)
     print(f"\n{definition}:", file=file)
     for r in results:
         line = f"  Workload {r.uuid}: {r.status}"
@@ -341,6 +479,12 @@ def print_results(results, definition: str = DECODE_DEFINITION, baseline: str = 
     if ms is not None:
         print(f"  mean speedup vs {label} over {sum(r.speedup is not None for r in results)} "
               f"workloads: {ms:.3f}x", file=file)
+
+
+def per_workload_summary(results) -> dict:
+    """Median latency (µs) per workload."""
+    return {r.uuid: round(r.latency_median_us, 3) for r in results
+            if r.latency_median_us is not None}
 
 
 def per_batch_summary(results) -> dict:
@@ -364,14 +508,15 @@ def _select(workloads, num_workloads: int, workload_id: Optional[str]):
 
 def _parser():
     ap = argparse.ArgumentParser(prog="python -m flashinfer_competition_codebase_amd.harness",
-                                 description="Evaluate the GDN decode entry points over the "
-                                             "contest workload mix")
+                                 description="Evaluate the GDN decode or prefill entry points "
+                                             "over a workload mix of the definition")
     sub = ap.add_subparsers(dest="cmd", required=True)
     r = sub.add_parser("run", help="check and time an entry point over the workloads")
     r.add_argument("--algo", default="hip", help="entry point name (ENTRY_POINTS)")
-    r.add_argument("--definition", default=DECODE_DEFINITION, choices=[DECODE_DEFINITION])
+    r.add_argument("--definition", default=DECODE_DEFINITION, choices=DEFINITIONS)
     r.add_argument("-n", "--num-workloads", type=int, default=0)
-    r.add_argument("--workload-id", default=None, help="workload name prefix, e.g. qk4v8-b16")
+    r.add_argument("--workload-id", default=None,
+                   help="workload name prefix, e.g. qk4v8-b16 or prefill-w0")
     r.add_argument("--iterations", type=int, default=100)
     r.add_argument("--num-trials", type=int, default=5)
     r.add_argument("--warmup", type=int, default=3)
@@ -386,6 +531,7 @@ def _parser():
     a = sub.add_parser("attribute", help="kernel-trace tier from a rocprofv3 trace of 'run'")
     a.add_argument("--trace", type=Path, required=True)
     a.add_argument("--manifest", type=Path, required=True)
+    a.add_argument("--definition", default=DECODE_DEFINITION, choices=DEFINITIONS)
     a.add_argument("--baseline", choices=sorted(B200_CUPTI_US), default="fla-b200")
     a.add_argument("--json", type=Path, default=None)
     return ap
@@ -395,29 +541,37 @@ def _dump(results, path, extra=None) -> None:
     doc = {"results": [{k: v for k, v in asdict(r).items() if k != "timings_us"}
                        for r in results],
            "mean_speedup": mean_speedup(results),
-           "per_batch_median_us": per_batch_summary(results)}
+           "per_batch_median_us": per_batch_summary(results),
+           "per_workload_median_us": per_workload_summary(results)}
     doc.update(extra or {})
     Path(path).write_text(json.dumps(doc, indent=1))
 
 
 def main(argv=None) -> int:
     args = _parser().parse_args(argv)
+    prefill = args.definition == PREFILL_DEFINITION
     if args.cmd == "attribute":
         calls = json.loads(args.manifest.read_text())["calls"]
-        results = attribute_trace(args.trace, calls, baseline=args.baseline)
-        print_results(results, baseline=args.baseline)
-        print(f"  per-batch median kernel time (µs): {per_batch_summary(results)}")
+        results = attribute_trace(args.trace, calls, baseline=args.baseline,
+                                  kernel_substring=TRACE_KERNELS[args.definition])
+        print_results(results, definition=args.definition, baseline=args.baseline)
+        if prefill:
+            print(f"  per-workload median kernel time (µs): {per_workload_summary(results)}")
+        else:
+            print(f"  per-batch median kernel time (µs): {per_batch_summary(results)}")
         if args.json:
-            _dump(results, args.json, {"tier": "trace", "baseline": args.baseline})
+            _dump(results, args.json, {"tier": "trace", "baseline": args.baseline,
+                                       "definition": args.definition})
         return 0
 
     from . import ENTRY_POINTS, NO_DPS
 
-    decode_algos = sorted(a for a in ENTRY_POINTS if not a.startswith("prefill"))
-    if args.algo not in decode_algos:
-        raise SystemExit(f"algo {args.algo!r} is not a decode entry point of this package; "
-                         f"available for {args.definition}: {decode_algos}")
-    workloads = _select(contest_decode_workloads(), args.num_workloads, args.workload_id)
+    algos = sorted(a for a in ENTRY_POINTS if a.startswith("prefill") == prefill)
+    if args.algo not in algos:
+        raise SystemExit(f"algo {args.algo!r} is not an entry point of this package for "
+                         f"{args.definition}; available: {algos}")
+    workloads = _select(prefill_workloads() if prefill else contest_decode_workloads(),
+                        args.num_workloads, args.workload_id)
     manifest = Manifest() if args.manifest else None
     print(f"Algorithm: {args.algo} ({'value-returning' if args.algo in NO_DPS else 'DPS'}), "
           f"{len(workloads)} workloads, tier {args.tier}, flush {args.flush}, "
@@ -428,14 +582,18 @@ def main(argv=None) -> int:
                        num_trials=args.num_trials, tier=args.tier, flush=args.flush,
                        clone=not args.no_clone, manifest=manifest, baseline=args.baseline,
                        log=lambda m: print(m, file=sys.stderr, flush=True))
-    print_results(results, baseline=args.baseline)
-    print(f"  per-batch median latency (µs, {args.tier} tier): {per_batch_summary(results)}")
+    print_results(results, definition=args.definition, baseline=args.baseline)
+    if prefill:
+        print(f"  per-workload median latency (µs, {args.tier} tier): "
+              f"{per_workload_summary(results)}")
+    else:
+        print(f"  per-batch median latency (µs, {args.tier} tier): {per_batch_summary(results)}")
     if manifest is not None:
         manifest.write(args.manifest)
     if args.json:
         _dump(results, args.json, {"tier": args.tier, "baseline": args.baseline,
                                    "algo": args.algo, "flush": args.flush,
-                                   "clone": not args.no_clone})
+                                   "clone": not args.no_clone, "definition": args.definition})
     return 0
 
 

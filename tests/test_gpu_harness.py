@@ -59,3 +59,24 @@ def test_a_wrong_solution_is_flagged(hip_device):
     res = harness.evaluate(no_decay, [w], reference=oracle_vec, device=hip_device, warmup=0,
                            iterations=1, num_trials=1, flush="none")
     assert res[0].status == "INCORRECT_NUMERICAL"
+
+
+def test_prefill_mix_short_workloads_pass(hip_device):
+    """The prefill definition through the harness: the short workloads of the
+    mix (including empty sequences), DPS and value-returning entries, checked
+    against the oracle's token loop."""
+    from oracle.gdn_prefill_oracle import prefill_loop
+
+    _announce("harness: prefill mix, short workloads, DPS and value-returning")
+    ws = [w for w in harness.prefill_workloads() if w.L <= 1000]
+    m = harness.Manifest()
+    res = harness.evaluate(gdn.kernel_prefill_hip, ws, dps=True, reference=prefill_loop,
+                           device=hip_device, warmup=1, iterations=2, num_trials=1, manifest=m)
+    assert [r.status for r in res] == ["PASSED"] * len(ws), [(r.uuid, r.status) for r in res]
+    assert len(m.calls) == len(ws) * 4
+    assert all(c[2] == (2 if w.N == 1 else 3) for w in ws for c in m.calls if c[0] == w.uuid)
+    assert res[0].speedup is not None and res[0].speedup > 0     # workload 0 vs B200
+    res2 = harness.evaluate(gdn.prefill_run, ws[:3], dps=False, reference=prefill_loop,
+                            device=hip_device, warmup=0, iterations=1, num_trials=1,
+                            tier="sync", flush="none")
+    assert [r.status for r in res2] == ["PASSED"] * 3

@@ -147,3 +147,110 @@ def test_evaluate_rejects_unknown_tier_and_flush():
         harness.evaluate(lambda **k: None, [], tier="cupti")
     with pytest.raises(ValueError):
         harness.evaluate(lambda **k: None, [], flush="l2")
+
+
+# --- prefill definition ---------------------------------------------------------
+
+def test_prefill_mix():
+    ws = harness.prefill_workloads()
+    assert len(ws) == 20
+    assert len({w.uuid for w in ws}) == 20 and len({w.seed for w in ws}) == 20
+    assert ws[0].lens == (6,)                        # the reference's workload 0
+    assert all((w.H, w.HV, w.use_qk_l2norm) == (4, 8, False) for w in ws)
+    assert any(0 in w.lens for w in ws)              # empty sequences
+    assert max(max(w.lens) for w in ws) == 16384   # longest single sequence
+    assert [w.dispatches for w in ws[:2]] == [2, 2]
+    assert all(w.dispatches == (2 if w.N == 1 else 3) for w in ws)
+    assert harness.prefill_workloads() == ws         # seeded: the same mix every time
+
+
+def test_prefill_inputs_are_seeded_and_shaped_like_the_definition():
+    w = harness.prefill_workloads()[11]              # lens 100, 200, 300, 400
+    t1 = harness.make_prefill_inputs(w, "cpu")
+    t2 = harness.make_prefill_inputs(w, "cpu")
+    for name in ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b", "cu_seqlens"):
+        assert torch.equal(t1[name], t2[name]), name
+    L, N = 1000, 4
+    assert t1["q"].shape == (L, 4, 128) and t1["q"].dtype == torch.bfloat16
+    assert t1["v"].shape == (L, 8, 128) and t1["a"].shape == (L, 8)
+    assert t1["state"].shape == (N, 8, 128, 128) and t1["state"].dtype == torch.float32
+    assert t1["cu_seqlens"].tolist() == [0, 100, 300, 600, 1000]
+    assert t1["cu_seqlens"].dtype == torch.int32
+    norms = t1["k"].float().norm(dim=-1)
+    assert bool(((norms - 1).abs() < 1e-2).all())   # unit rows up to bf16 rounding
+    outs = harness._dps_outputs(t1)
+    assert outs["output"].shape == (L, 8, 128) and outs["output"].dtype == torch.bfloat16
+    assert outs["new_state"].shape == (N, 8, 128, 128)
+
+
+def test_prefill_baseline_is_workload_0_only():
+    ws = harness.prefill_workloads()
+    assert harness.baseline_us(ws[0], "fla-b200") == 1536.0    # CLAUDE.md:333-337
+    assert harness.baseline_us(ws[0], "fi-b200") == 185.0
+    assert all(harness.baseline_us(w, "fi-b200") is None for w in ws[1:])
+    dec = harness.contest_decode_workloads()[0]
+    assert harness.baseline_us(dec, "fla-b200") == 2.46
+    assert harness.baseline_us(dec, None) is None
+
+
+def _prefill_trace_csv(tmp_path, calls):
+    """calls: list of lists of (start offset, duration) ns per dispatch."""
+    names = ["void gdn_pf::chunk_offsets_kernel(gdn_pf::Params, int*, int*)",
+             "void gdn_pf::prep_kernel(gdn_pf::Params)",
+             "void gdn_pf::scan_kernel<1>(gdn_pf::Params)"]
+    rows, t = [], 10_000
+    for disp in calls:
+        rows.append(("void at::native::reduce_kernel<512, 1>", t, t + 700))
+        t += 1000
+        for j, (off, dur) in enumerate(disp):
+            name = names[j + 3 - len(disp)]
+            rows.append((name, t + off, t + off + dur))
+        t += 100_000
+    rows.reverse()
+    path = tmp_path / "kernel_trace.csv"
+    with open(path, "w") as f:
+        f.write('"Kind","Kernel_Name","Start_Timestamp","End_Timestamp"\n')
+        for name, s, e in rows:
+            f.write(f'"KERNEL_DISPATCH","{name}",{s},{e}\n')
+    return path
+
+
+def test_prefill_trace_attribution_spans_the_calls_dispatches(tmp_path):
+    ws = harness.prefill_workloads()
+    w0, w11 = ws[0], ws[11]                          # one sequence (2), four (3 dispatches)
+    m = harness.Manifest()
+    calls = []
+    m.add(w0.uuid, "check", w0.dispatches); calls.append([(0, 5000), (6000, 4000)])
+    m.add(w0.uuid, "timed", w0.dispatches); calls.append([(0, 9000), (10_000, 6000)])
+    m.add(w11.uuid, "timed", w11.dispatches)
+    calls.append([(0, 3000), (4000, 20_000), (25_000, 30_000)])
+    path = _prefill_trace_csv(tmp_path, calls)
+    res = {r.uuid: r for r in harness.attribute_trace(path, m.calls, kernel_substring="gdn_pf::",
+                                                      baseline="fi-b200")}
+    assert res[w0.uuid].timings_us == [16.0]         # first start to last end
+    assert res[w11.uuid].timings_us == [55.0]
+    assert res[w0.uuid].speedup == pytest.approx(185.0 / 16.0)
+    assert res[w11.uuid].speedup is None
+    with pytest.raises(ValueError, match="dispatches"):
+        harness.attribute_trace(path, m.calls[:-1], kernel_substring="gdn_pf::")
+
+
+def test_cli_prefill_attribute(tmp_path, capsys):
+    ws = harness.prefill_workloads()
+    m = harness.Manifest()
+    m.add(ws[0].uuid, "timed", 2)
+    mpath = tmp_path / "calls.json"
+    m.write(mpath)
+    tpath = _prefill_trace_csv(tmp_path, [[(0, 10_000), (12_000, 8000)]])
+    assert harness.main(["attribute", "--trace", str(tpath), "--manifest", str(mpath),
+                         "--definition", harness.PREFILL_DEFINITION]) == 0
+    out = capsys.readouterr().out
+    assert "gdn_prefill_qk4_v8_d128_k_last:" in out
+    assert "Workload prefill-w00: TRACED | 20.000 µs | 76.80x vs B200 fla-chunk" in out
+
+
+def test_cli_rejects_an_entry_point_of_the_other_definition():
+    with pytest.raises(SystemExit, match="prefill-hip"):
+        harness.main(["run", "--algo", "hip", "--definition", harness.PREFILL_DEFINITION])
+    with pytest.raises(SystemExit, match="available"):
+        harness.main(["run", "--algo", "prefill-hip"])
