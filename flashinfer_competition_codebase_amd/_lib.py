@@ -55,9 +55,10 @@ PREFILL_SIGNATURES = {
         _I,
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P] + [_I] * 7 + [_P, _S, _P, _P],
     ),
+    "gdn_prefill_token_path_max_tokens": (_I, []),
     "gdn_prefill_abi_version": (_I, []),
 }
-PREFILL_ABI_VERSION = 3
+PREFILL_ABI_VERSION = 4
 
 _lock = threading.Lock()
 _lib = None

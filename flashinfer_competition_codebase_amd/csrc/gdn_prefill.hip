@@ -18,6 +18,13 @@
 // Every exponent is <= 0.  With the q/k L2-norm on, the row norms enter as
 // per-row scale factors of the same products.
 //
+// Prefills of at most kSmallTokens tokens in all (so every sequence is that
+// short) skip the chunkwise machinery: one launch of the decode kernel's
+// variable-length mode (gdn_decode_kernel.h) applies the recurrence token by
+// token with the state in registers, one workgroup per (sequence, v-head,
+// row tile), reading each sequence's token range from cu_seqlens on the
+// device.  Larger prefills run the chunkwise kernels.
+//
 // Kernels (one stream, in order):
 //   1. chunk_offsets: one workgroup turns cu_seqlens into the first chunk
 //      slot of every sequence (token ranges clamped to [0, L]) by a scan,
@@ -49,6 +56,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "gdn_decode_kernel.h"
 #include "gdn_prefill.h"
 
 namespace gdn_pf {
@@ -65,6 +73,10 @@ constexpr int kDim = 128;            // K == V == 128
 constexpr int kChunk = 64;           // tokens per chunk
 constexpr int kThreads = 256;        // 4 wavefronts
 constexpr long long kScanWideHeads = 256;  // N * HV from which the scan takes 32 columns
+// Total tokens up to which the token-by-token kernel runs the prefill: past
+// ~16 tokens per sequence the chunkwise kernels are faster (their cost is
+// ~15 us of preparation and scan latency; the token loop's ~0.6 us a token).
+constexpr int kSmallTokens = 16;
 constexpr float kL2Eps = 1e-6f;
 constexpr float kSoftplusThreshold = 20.0f;
 constexpr float kLn2 = 0.693147180559945309f;
@@ -990,6 +1002,43 @@ size_t workspace_bytes(long long L, long long N, long long H, long long HV) {
 
 using namespace gdn_pf;
 
+// One launch of the decode kernel's variable-length mode over the prefill's
+// packed inputs: grid (row tiles x v-heads of a q/k head, q/k heads,
+// sequences), one row per 16-lane group and one wave per workgroup for a few
+// heads, four waves for more.
+static hipError_t small_prefill(const void* q, const void* k, const void* v, const float* state,
+                                const float* A_log, const void* a, const float* dt_bias,
+                                const void* b, const int32_t* cu_seqlens, float scale,
+                                void* output, float* new_state, int L, int N, int H, int HV,
+                                bool l2, hipStream_t stream) {
+  constexpr int kNs = 1;
+  constexpr int kPolicy = gdn::kPolicyDefault;   // the next decode step re-reads the state
+  const unsigned ratio = static_cast<unsigned>(HV / H);
+  const unsigned h_ratio = static_cast<unsigned>(H) | (ratio << 16);
+  const auto* q16 = static_cast<const uint16_t*>(q);
+  const auto* k16 = static_cast<const uint16_t*>(k);
+  const auto* v16 = static_cast<const uint16_t*>(v);
+  const auto* a16 = static_cast<const uint16_t*>(a);
+  const auto* b16 = static_cast<const uint16_t*>(b);
+  auto* out16 = static_cast<uint16_t*>(output);
+  if (static_cast<long long>(N) * HV <= 16) {
+    constexpr int kW = 1;
+    const dim3 grid(ratio * (kDim / (gdn::kLaneGroups * kNs * kW)), H, N);
+    auto* kern = l2 ? gdn::gdn_decode_k128<kNs, kW, true, kPolicy, false, true, true>
+                    : gdn::gdn_decode_k128<kNs, kW, false, kPolicy, false, true, true>;
+    hipLaunchKernelGGL(kern, grid, dim3(64 * kW), 0, stream, state, q16, k16, v16, a16, b16,
+                       h_ratio, 0, A_log, dt_bias, out16, new_state, scale, cu_seqlens, L);
+  } else {
+    constexpr int kW = 4;
+    const dim3 grid(ratio * (kDim / (gdn::kLaneGroups * kNs * kW)), H, N);
+    auto* kern = l2 ? gdn::gdn_decode_k128<kNs, kW, true, kPolicy, false, true, true>
+                    : gdn::gdn_decode_k128<kNs, kW, false, kPolicy, false, true, true>;
+    hipLaunchKernelGGL(kern, grid, dim3(64 * kW), 0, stream, state, q16, k16, v16, a16, b16,
+                       h_ratio, 0, A_log, dt_bias, out16, new_state, scale, cu_seqlens, L);
+  }
+  return hipGetLastError();
+}
+
 static int prefill_impl(const void* q, const void* k, const void* v, const float* state,
                 const float* A_log, const void* a, const float* dt_bias, const void* b,
                 const int32_t* cu_seqlens, float scale, void* output, float* new_state,
@@ -1061,6 +1110,18 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
   auto mark = [&](int i) -> hipError_t {
     return events ? hipEventRecord(static_cast<hipEvent_t>(events[i]), stream) : hipSuccess;
   };
+  if (total_seq_len <= kSmallTokens && num_seqs <= 65535) {   // grid z
+    // token-by-token path: the three intervals of the timed form are the
+    // (empty) offsets and preparation steps and the one launch
+    hipError_t e = mark(0);
+    if (e == hipSuccess) e = mark(1);
+    if (e == hipSuccess) e = mark(2);
+    if (e != hipSuccess) return e;
+    e = small_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output,
+                      new_state, total_seq_len, num_seqs, H, HV, use_qk_l2norm != 0, stream);
+    if (e == hipSuccess) e = mark(3);
+    return e;
+  }
   hipError_t e = mark(0);
   if (e != hipSuccess) return e;
   if (!p.single)
@@ -1125,6 +1186,8 @@ int gdn_prefill_timed(const void* q, const void* k, const void* v, const float* 
                       workspace_size, hip_stream, events);
 }
 
-int gdn_prefill_abi_version(void) { return 3; }
+int gdn_prefill_token_path_max_tokens(void) { return kSmallTokens; }
+
+int gdn_prefill_abi_version(void) { return 4; }
 
 }  // extern "C"

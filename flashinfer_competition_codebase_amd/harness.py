@@ -50,8 +50,9 @@ Command line (arguments as scripts/shared.py:93-142):
         --trace out/run_kernel_trace.csv --manifest calls.json [--definition ...]
 
 In the trace tier a prefill call is its chunk-offsets (several sequences),
-preparation and scan dispatches, timed from the first one's start to the
-last one's end.
+preparation and scan dispatches -- or its one dispatch of the token-by-token
+kernel for a prefill of at most 16 tokens -- timed from the first one's
+start to the last one's end.
 """
 
 from __future__ import annotations
@@ -94,8 +95,11 @@ PREFILL_WORKLOAD0_LENS = (6,)
 B200_PREFILL_US = {"fla-b200": 1536.0, "fi-b200": 185.0}
 PREFILL_BASELINE_LABELS = {"fla-b200": "B200 fla-chunk", "fi-b200": "B200 FlashInfer"}
 
-# Kernel-name substrings of the dispatches one call makes, per definition.
-TRACE_KERNELS = {DECODE_DEFINITION: "gdn_decode", PREFILL_DEFINITION: "gdn_pf::"}
+# Kernel-name substrings of the dispatches one call makes, per definition (a
+# prefill of a few tokens is one launch of the decode kernel's
+# variable-length mode).
+TRACE_KERNELS = {DECODE_DEFINITION: ("gdn_decode",),
+                 PREFILL_DEFINITION: ("gdn_pf::", "gdn_decode_k128")}
 
 ATOL = 1e-2
 RTOL = 1e-2
@@ -149,7 +153,8 @@ class PrefillWorkload:
 
     @property
     def dispatches(self) -> int:      # kernels one prefill call launches
-        return 2 if self.N == 1 else 3
+        from .prefill import prefill_dispatches
+        return prefill_dispatches(self.L, self.N)
 
 
 def prefill_workloads() -> list:
@@ -419,23 +424,25 @@ def mean_speedup(results) -> Optional[float]:
     return statistics.fmean(s) if s else None
 
 
-def attribute_trace(trace_csv, manifest_calls, *, kernel_substring: str = "gdn_decode",
+def attribute_trace(trace_csv, manifest_calls, *, kernel_substring="gdn_decode",
                     baseline: str = "fla-b200", workloads=None) -> list:
     """Kernel-trace tier: assign the dispatches of kernels whose name
-    contains ``kernel_substring`` in a rocprofv3 ``kernel_trace.csv`` (in
+    contains ``kernel_substring`` (a string or a tuple of alternatives) in a
+    rocprofv3 ``kernel_trace.csv`` (in
     start-time order) to the manifest's calls, each call taking as many
     consecutive dispatches as it made, and return one Result per workload with
     the mean and median of its timed calls' times (first dispatch's start to
     last dispatch's end).  Raises if the counts differ."""
+    subs = (kernel_substring,) if isinstance(kernel_substring, str) else tuple(kernel_substring)
     rows = []
     with open(trace_csv) as f:
         for r in csv.DictReader(f):
-            if kernel_substring in r["Kernel_Name"]:
+            if any(x in r["Kernel_Name"] for x in subs):
                 rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
     rows.sort()
     counts = [int(c[2]) if len(c) > 2 else 1 for c in manifest_calls]
     if len(rows) != sum(counts):
-        raise ValueError(f"{len(rows)} '{kernel_substring}' dispatches in the trace but "
+        raise ValueError(f"{len(rows)} {'/'.join(subs)} dispatches in the trace but "
                          f"{sum(counts)} in the manifest's {len(manifest_calls)} calls")
     per = {}
     i = 0

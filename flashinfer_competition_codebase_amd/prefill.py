@@ -37,7 +37,8 @@ import torch
 from . import _lib
 from .kernel import K_DIM, V_DIM, _expect, _on_device, _overlap, _same_hip_device, resolve_scale
 
-__all__ = ["prefill_run", "kernel_prefill_hip", "kernel_prefill_hip_timed", "workspace_bytes"]
+__all__ = ["prefill_run", "kernel_prefill_hip", "kernel_prefill_hip_timed", "workspace_bytes",
+           "token_path_max_tokens", "prefill_dispatches"]
 
 
 def workspace_bytes(total_seq_len: int, num_seqs: int, H: int, HV: int) -> int:
@@ -47,6 +48,23 @@ def workspace_bytes(total_seq_len: int, num_seqs: int, H: int, HV: int) -> int:
     if n == 0:
         raise ValueError(f"invalid prefill sizes L={total_seq_len}, N={num_seqs}, H={H}, HV={HV}")
     return n
+
+
+def token_path_max_tokens() -> int:
+    """Total tokens up to which a prefill is one launch of the token-by-token
+    kernel instead of the chunkwise kernels."""
+    return int(_lib.get_prefill_lib().gdn_prefill_token_path_max_tokens())
+
+
+def prefill_dispatches(total_seq_len: int, num_seqs: int) -> int:
+    """Kernel dispatches of one prefill call: 1 on the token-by-token path,
+    else 2 for one sequence (preparation, scan) and 3 for several (the
+    chunk-offsets scan first); 0 for no sequences."""
+    if num_seqs <= 0:
+        return 0
+    if total_seq_len <= token_path_max_tokens() and num_seqs <= 65535:
+        return 1
+    return 2 if num_seqs == 1 else 3
 
 
 def check_prefill_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, output=None,

@@ -65,6 +65,9 @@ size_t gdn_prefill_workspace_bytes(int total_seq_len, int num_seqs, int H, int H
  * the caller, `scale` is already resolved (None/0 -> 1/sqrt(K) in the
  * Python caller), and bad arguments return an error instead of launching.
  * q, k, v, output, state and new_state must be 16-byte aligned.
+ * Launches one kernel when total_seq_len <= gdn_prefill_token_path_max_tokens()
+ * (and num_seqs <= 65535), else the chunkwise kernels (chunk offsets when
+ * num_seqs > 1, preparation, scan).
  */
 int gdn_prefill(const void* q, const void* k, const void* v, const float* state,
                 const float* A_log, const void* a, const float* dt_bias, const void* b,
@@ -77,8 +80,9 @@ int gdn_prefill(const void* q, const void* k, const void* v, const float* state,
  * Measurement hook, no counterpart in the reference: gdn_prefill with
  * events[0..3] (hipEvent_t, all non-null) recorded on hip_stream before the
  * offsets, preparation and scan launches and after the scan, so that
- * hipEventElapsedTime gives each kernel's time.  Nothing is recorded when
- * num_seqs is 0.
+ * hipEventElapsedTime gives each kernel's time.  On the token-by-token path
+ * events 0..2 are recorded back to back and its one launch lies between
+ * events 2 and 3.  Nothing is recorded when num_seqs is 0.
  */
 int gdn_prefill_timed(const void* q, const void* k, const void* v, const float* state,
                       const float* A_log, const void* a, const float* dt_bias, const void* b,
@@ -87,8 +91,17 @@ int gdn_prefill_timed(const void* q, const void* k, const void* v, const float* 
                       int use_qk_l2norm, void* workspace, size_t workspace_size,
                       void* hip_stream, void* const* events);
 
-/* ABI version of this header: 3 (2 had no gdn_prefill_timed; 1 had no H in
- * gdn_prefill_workspace_bytes). */
+/*
+ * Total tokens up to which gdn_prefill runs the token-by-token path: one
+ * launch in which each workgroup applies the recurrence to its sequence's
+ * tokens with its slice of the state in registers (no sequence is longer
+ * than the total).  No counterpart in the reference; for callers that count
+ * dispatches or time the two paths.
+ */
+int gdn_prefill_token_path_max_tokens(void);
+
+/* ABI version of this header: 4 (3 had no gdn_prefill_token_path_max_tokens;
+ * 2 had no gdn_prefill_timed; 1 had no H in gdn_prefill_workspace_bytes). */
 int gdn_prefill_abi_version(void);
 
 #ifdef __cplusplus

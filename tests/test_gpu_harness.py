@@ -74,7 +74,7 @@ def test_prefill_mix_short_workloads_pass(hip_device):
                            device=hip_device, warmup=1, iterations=2, num_trials=1, manifest=m)
     assert [r.status for r in res] == ["PASSED"] * len(ws), [(r.uuid, r.status) for r in res]
     assert len(m.calls) == len(ws) * 4
-    assert all(c[2] == (2 if w.N == 1 else 3) for w in ws for c in m.calls if c[0] == w.uuid)
+    assert all(c[2] == w.dispatches for w in ws for c in m.calls if c[0] == w.uuid)
     assert res[0].speedup is not None and res[0].speedup > 0     # workload 0 vs B200
     res2 = harness.evaluate(gdn.prefill_run, ws[:3], dps=False, reference=prefill_loop,
                             device=hip_device, warmup=0, iterations=1, num_trials=1,

@@ -258,3 +258,73 @@ def test_split_sequences_compose_at_full_size(lens, H, HV, cut, hip_device):
     assert bool((d_st <= 1e-3 * st.abs() + 1e-5).all()), d_st.max()
     rel = (torch.linalg.vector_norm(s2 - st) / torch.linalg.vector_norm(st)).item()
     assert rel <= 1e-4, rel
+
+
+# --- prefills of at most 16 tokens: the decode kernel's variable-length mode ----
+
+@pytest.mark.parametrize("seqlens,H,HV,l2,with_state", [
+    ([16], 4, 8, False, True),            # the largest token-by-token prefill
+    ([5, 0, 11], 4, 8, False, True),      # an empty sequence among them
+    ([1] * 16, 4, 8, False, True),        # sixteen one-token sequences
+    ([3, 9], 2, 8, True, True),           # GVA ratio 4, q/k L2-norm
+    ([8, 8], 16, 32, False, False),       # qk16_v32, no initial state
+    ([6], 1, 1, False, True),             # one head
+])
+def test_small_prefill_token_path(seqlens, H, HV, l2, with_state, hip_device):
+    _announce(f"small prefill seqlens={seqlens} H={H} HV={HV} l2={l2} state={with_state}")
+    t = make_prefill_inputs(seqlens, H, HV, seed=40 + sum(seqlens) + H, with_state=with_state)
+    out, st = gdn.prefill_run(**_dev(t, hip_device), use_qk_l2norm=l2)
+    torch.cuda.synchronize()
+    assert out.shape == (sum(seqlens), HV, 128) and st.shape == (len(seqlens), HV, 128, 128)
+    _check(t, out, st, l2=l2)
+
+
+def test_small_and_chunkwise_paths_agree(hip_device):
+    """16 tokens run token by token; the same sequence followed by a 1-token
+    one (17 tokens in all) runs chunkwise: the first sequence's results agree
+    within the output and state bars."""
+    _announce("small prefill vs chunkwise")
+    t = make_prefill_inputs([16, 1], 4, 8, seed=51)
+    out17, st17 = gdn.prefill_run(**_dev(t, hip_device))
+    t16 = {**t, "q": t["q"][:16], "k": t["k"][:16], "v": t["v"][:16], "a": t["a"][:16],
+           "b": t["b"][:16], "state": t["state"][:1], "cu_seqlens": t["cu_seqlens"][:2]}
+    out16, st16 = gdn.prefill_run(**_dev(t16, hip_device))
+    torch.cuda.synchronize()
+    o16, o17 = out16.float().cpu(), out17[:16].float().cpu()
+    assert bool(((o16 - o17).abs() <= 2.0 ** -7 * o17.abs() + 1e-5).all())
+    s16, s17 = st16.cpu(), st17[:1].cpu()
+    assert bool(((s16 - s17).abs() <= 1e-3 * s17.abs() + 1e-5).all())
+
+
+def test_small_prefill_in_place_and_timed(hip_device):
+    """Token path: in place equals out of place bitwise; the timed entry's
+    first two intervals are empty steps and the third the one launch."""
+    import ctypes
+    _announce("small prefill in place / timed")
+    t = _dev(make_prefill_inputs([7, 4], 4, 8, seed=52), hip_device)
+    ref_o, ref_s = gdn.prefill_run(**t)
+    state = t["state"].clone()
+    out = torch.empty_like(ref_o)
+    gdn.kernel_prefill_hip(**{**t, "state": state}, output=out, new_state=state)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref_o) and torch.equal(state, ref_s)
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    evs = []
+    for _ in range(4):
+        e = ctypes.c_void_p()
+        assert hip.hipEventCreate(ctypes.byref(e)) == 0
+        evs.append(e)
+    try:
+        out2, st2 = torch.empty_like(ref_o), torch.empty_like(ref_s)
+        gdn.kernel_prefill_hip_timed(**t, output=out2, new_state=st2, events=evs)
+        torch.cuda.synchronize()
+        assert torch.equal(out2, ref_o) and torch.equal(st2, ref_s)
+        ms = []
+        for i in range(3):
+            x = ctypes.c_float()
+            assert hip.hipEventElapsedTime(ctypes.byref(x), evs[i], evs[i + 1]) == 0
+            ms.append(x.value)
+        assert all(m >= 0.0 for m in ms) and ms[2] > 0.0, ms
+    finally:
+        for e in evs:
+            hip.hipEventDestroy(e)

@@ -159,8 +159,8 @@ def test_prefill_mix():
     assert all((w.H, w.HV, w.use_qk_l2norm) == (4, 8, False) for w in ws)
     assert any(0 in w.lens for w in ws)              # empty sequences
     assert max(max(w.lens) for w in ws) == 16384   # longest single sequence
-    assert [w.dispatches for w in ws[:2]] == [2, 2]
-    assert all(w.dispatches == (2 if w.N == 1 else 3) for w in ws)
+    assert [w.dispatches for w in ws[:3]] == [1, 1, 2]   # 6 and 1 tokens: the token path
+    assert all(w.dispatches == (1 if w.L <= 16 else 2 if w.N == 1 else 3) for w in ws)
     assert harness.prefill_workloads() == ws         # seeded: the same mix every time
 
 
@@ -194,16 +194,18 @@ def test_prefill_baseline_is_workload_0_only():
 
 
 def _prefill_trace_csv(tmp_path, calls):
-    """calls: list of lists of (start offset, duration) ns per dispatch."""
+    """calls: list of lists of (start offset, duration) ns per dispatch; a
+    one-dispatch call is the token-by-token kernel."""
     names = ["void gdn_pf::chunk_offsets_kernel(gdn_pf::Params, int*, int*)",
              "void gdn_pf::prep_kernel(gdn_pf::Params)",
              "void gdn_pf::scan_kernel<1>(gdn_pf::Params)"]
+    token = "void gdn::gdn_decode_k128<1, 1, false, 0, false, true, true>(void const*)"
     rows, t = [], 10_000
     for disp in calls:
         rows.append(("void at::native::reduce_kernel<512, 1>", t, t + 700))
         t += 1000
         for j, (off, dur) in enumerate(disp):
-            name = names[j + 3 - len(disp)]
+            name = token if len(disp) == 1 else names[j + 3 - len(disp)]
             rows.append((name, t + off, t + off + dur))
         t += 100_000
     rows.reverse()
@@ -217,31 +219,35 @@ def _prefill_trace_csv(tmp_path, calls):
 
 def test_prefill_trace_attribution_spans_the_calls_dispatches(tmp_path):
     ws = harness.prefill_workloads()
-    w0, w11 = ws[0], ws[11]                          # one sequence (2), four (3 dispatches)
+    w0, w2, w11 = ws[0], ws[2], ws[11]               # 1, 2 and 3 dispatches per call
+    assert (w0.dispatches, w2.dispatches, w11.dispatches) == (1, 2, 3)
     m = harness.Manifest()
     calls = []
-    m.add(w0.uuid, "check", w0.dispatches); calls.append([(0, 5000), (6000, 4000)])
-    m.add(w0.uuid, "timed", w0.dispatches); calls.append([(0, 9000), (10_000, 6000)])
+    m.add(w0.uuid, "check", w0.dispatches); calls.append([(0, 5000)])
+    m.add(w0.uuid, "timed", w0.dispatches); calls.append([(0, 4000)])
+    m.add(w2.uuid, "timed", w2.dispatches); calls.append([(0, 9000), (10_000, 6000)])
     m.add(w11.uuid, "timed", w11.dispatches)
     calls.append([(0, 3000), (4000, 20_000), (25_000, 30_000)])
     path = _prefill_trace_csv(tmp_path, calls)
-    res = {r.uuid: r for r in harness.attribute_trace(path, m.calls, kernel_substring="gdn_pf::",
+    subs = harness.TRACE_KERNELS[harness.PREFILL_DEFINITION]
+    res = {r.uuid: r for r in harness.attribute_trace(path, m.calls, kernel_substring=subs,
                                                       baseline="fi-b200")}
-    assert res[w0.uuid].timings_us == [16.0]         # first start to last end
+    assert res[w0.uuid].timings_us == [4.0]
+    assert res[w2.uuid].timings_us == [16.0]         # first start to last end
     assert res[w11.uuid].timings_us == [55.0]
-    assert res[w0.uuid].speedup == pytest.approx(185.0 / 16.0)
-    assert res[w11.uuid].speedup is None
+    assert res[w0.uuid].speedup == pytest.approx(185.0 / 4.0)
+    assert res[w2.uuid].speedup is None
     with pytest.raises(ValueError, match="dispatches"):
-        harness.attribute_trace(path, m.calls[:-1], kernel_substring="gdn_pf::")
+        harness.attribute_trace(path, m.calls[:-1], kernel_substring=subs)
 
 
 def test_cli_prefill_attribute(tmp_path, capsys):
     ws = harness.prefill_workloads()
     m = harness.Manifest()
-    m.add(ws[0].uuid, "timed", 2)
+    m.add(ws[0].uuid, "timed", 1)
     mpath = tmp_path / "calls.json"
     m.write(mpath)
-    tpath = _prefill_trace_csv(tmp_path, [[(0, 10_000), (12_000, 8000)]])
+    tpath = _prefill_trace_csv(tmp_path, [[(0, 20_000)]])
     assert harness.main(["attribute", "--trace", str(tpath), "--manifest", str(mpath),
                          "--definition", harness.PREFILL_DEFINITION]) == 0
     out = capsys.readouterr().out
@@ -254,3 +260,14 @@ def test_cli_rejects_an_entry_point_of_the_other_definition():
         harness.main(["run", "--algo", "hip", "--definition", harness.PREFILL_DEFINITION])
     with pytest.raises(SystemExit, match="available"):
         harness.main(["run", "--algo", "prefill-hip"])
+
+
+def test_prefill_dispatch_count_follows_the_token_path_threshold():
+    from flashinfer_competition_codebase_amd.prefill import (prefill_dispatches,
+                                                            token_path_max_tokens)
+    m = token_path_max_tokens()
+    assert m == 16
+    assert prefill_dispatches(m, 1) == 1 and prefill_dispatches(0, 5) == 1
+    assert prefill_dispatches(m + 1, 1) == 2 and prefill_dispatches(m + 1, 2) == 3
+    assert prefill_dispatches(m, 70_000) == 3            # past the grid's z limit
+    assert prefill_dispatches(100, 0) == 0
