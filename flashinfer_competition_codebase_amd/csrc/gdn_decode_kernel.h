@@ -450,6 +450,20 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_decode_k128(
 #pragma unroll
     for (int n = 0; n < NS; ++n) raw[n] = load_row<BF16, POLICY>(p.state, row_base + n, j);
   }
+  // Variable-length (small prefill: one wave of few rows per head, latency
+  // bound): the inputs of the next kDepth = 3 tokens are in flight while a
+  // token is applied, so each load has two iterations to arrive; token
+  // indices are clamped to the last token, so every load is unconditional
+  // (the clamped repeats are never used).  The decode's multi-token kernels
+  // prefetch one token ahead: at large batches deeper prefetch costs
+  // registers and load slots (B=256 T=2: 170 -> 202 us), and at small ones
+  // their per-token time is the token's instruction chain, not the load.
+  constexpr int kDepth = VARLEN ? 3 : 1;
+  TokenIn<NS> pre1, pre2;                     // tokens 1 and 2 (kDepth == 3)
+  if constexpr (kDepth == 3) {
+    load_token<NS, BF16>(p, tok0 + (T > 1 ? 1 : 0), hq, hv, row0, j, pre1);
+    load_token<NS, BF16>(p, tok0 + (T > 2 ? 2 : T - 1), hq, hv, row0, j, pre2);
+  }
   __builtin_amdgcn_sched_barrier(0);
   const float A_log = p.A_log[hv];
   const float dt_bias = p.dt_bias[hv];
@@ -473,9 +487,12 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_decode_k128(
   }
 
   for (int t = 0; t < T; ++t) {
-    TokenIn<NS> nxt;
-    if constexpr (MULTI) {
-      if (t + 1 < T) load_token<NS, BF16>(p, tok0 + t + 1, hq, hv, row0, j, nxt);  // prefetch
+    TokenIn<NS> nxt;                          // token t + kDepth
+    if constexpr (kDepth == 3) {
+      const int ta = t + kDepth < T ? t + kDepth : T - 1;
+      load_token<NS, BF16>(p, tok0 + ta, hq, hv, row0, j, nxt);
+    } else if constexpr (MULTI) {
+      if (t + 1 < T) load_token<NS, BF16>(p, tok0 + t + 1, hq, hv, row0, j, nxt);
     }
     float o[NS];
     token_rows<NS>(s, h, o);
@@ -488,7 +505,11 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_decode_k128(
       const size_t out_row = ((tok0 + t) * p.HV + hv) * kDim + row0;
       store_bf16_run<NS>(p.out + out_row, o);
     }
-    if constexpr (MULTI) {
+    if constexpr (kDepth == 3) {              // token t + 1 (unused after the last)
+      token_head<NS, L2NORM>(pre1, A_log, dt_bias, p.scale, h);
+      pre1 = pre2;
+      pre2 = nxt;
+    } else if constexpr (MULTI) {
       if (t + 1 < T) token_head<NS, L2NORM>(nxt, A_log, dt_bias, p.scale, h);
     }
   }
