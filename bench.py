@@ -214,6 +214,12 @@ def per_config_shapes():
                for n in ("b1_qk16_v32_l2", "b8_qk16_v32_l2", "b256_qk16_v32_l2")]
     shapes += [(f"{n}_t{tt}", *CONFIGS[n], tt, f32)
                for n in ("b1_qk16_v32_l2", "b256_qk16_v32_l2") for tt in (2, 4)]
+    # the shapes of FlashInfer's published decode tables (bf16 state at T = 1..4,
+    # fp32 state, up to B = 512; findings/fi-gdn-decode-kernel.md:26-60)
+    shapes += [(f"{n}_bf16_state_t{tt}", *CONFIGS[n], tt, bf16)
+               for n in ("b1_qk16_v32_l2", "b256_qk16_v32_l2") for tt in (2, 4)]
+    shapes += [("b512_qk16_v32_l2", 512, 16, 32, True, 1, f32),
+               ("b512_qk16_v32_l2_bf16_state", 512, 16, 32, True, 1, bf16)]
     return shapes
 
 
