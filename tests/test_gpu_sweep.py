@@ -1,0 +1,196 @@
+"""Seeded random sweeps of the decode step and the prefill on MI355X against
+the oracle, across the options the named tests take one at a time: batch,
+tokens per sequence, q/k heads and GVA ratio, fp32 / bf16 / no initial
+state, the q/k L2-norm, the entry form (DPS in place, DPS out of place,
+value-returning), the scale's forms and, for the prefill, ragged sequence
+lengths with empty sequences on either side of the 16-token path switch.
+
+Bars are those of the named tests (tests/gdn_cases.py, test_gpu_tokens.py,
+test_gpu_prefill.py): outputs within 1e-2 atol/rtol of the oracle's bf16
+output and one bf16 ulp of float64; bf16 states within one bf16 ulp of the
+oracle's bf16 state and the round-to-nearest of the float64 state; fp32
+states within 1e-3 relative of the float64 state element by element, with
+the absolute floor 1e-5 scaled by the head's largest magnitude when that
+exceeds 1 (raw N(0,1) keys, |k|^2 ~ 128, multiply a state's k-component by
+~|1 - 128 beta| per token, so after a few tokens entries of 1e3-1e4 make
+one fp32 rounding ~1e-3 and an entry that cancels to near zero cannot meet
+a fixed 1e-5), and within 1e-3 in relative Frobenius norm.
+"""
+
+from __future__ import annotations
+
+import math
+import random
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import flashinfer_competition_codebase_amd as gdn
+from flashinfer_competition_codebase_amd import _lib
+from oracle.gdn_decode_oracle import make_inputs, oracle_loop, oracle_tokens, oracle_vec
+from oracle.gdn_prefill_oracle import make_prefill_inputs, prefill_chunked_fp64, prefill_loop
+from tests.gdn_cases import assert_output_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _announce(case):
+    sys.stdout.write(f"[gpu case] {case}\n")
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _libraries_present():
+    _lib.get_lib()
+    _lib.get_prefill_lib()
+
+
+def _dev(t, device):
+    return {n: (x.to(device) if isinstance(x, torch.Tensor) else x) for n, x in t.items()}
+
+
+def _assert_fp32_state(st, s64):
+    sd = st.double()
+    ref = torch.as_tensor(np.asarray(s64), dtype=torch.float64)
+    scale = ref.abs().amax(dim=(-1, -2), keepdim=True).clamp_min(1.0)   # per head
+    diff = (sd - ref).abs()
+    bad = diff > 1e-3 * ref.abs() + 1e-5 * scale
+    assert not bool(bad.any()), (f"{int(bad.sum())} state elements off, max diff "
+                                 f"{diff.max().item():.3e} (head scale {scale.max().item():.3e})")
+    rel = (diff.norm() / ref.norm().clamp_min(1e-30)).item()
+    assert rel <= 1e-3, rel
+
+
+def _decode_cases(n=48, seed=20261202):
+    rng = random.Random(seed)
+    cases = []
+    for i in range(n):
+        H = rng.choice([1, 2, 3, 4, 6, 8, 16])
+        ratio = rng.choice([1, 2, 3, 4, 8])
+        while H * ratio > 64:
+            ratio //= 2
+        cases.append(dict(
+            i=i, B=rng.randint(1, 40), T=rng.choice([1, 1, 1, 2, 3, 5]), H=H, HV=H * ratio,
+            state=rng.choices(["fp32", "bf16", "none"], weights=[6, 3, 2])[0],
+            l2=rng.random() < 0.5, form=rng.choice(["inplace", "outofplace", "run"]),
+            scale=rng.choice(["none", "zero", "float", "tensor"]),
+            gates_bhv=rng.random() < 0.3, seed=30_000 + i))
+    return cases
+
+
+def _case_id(c):
+    return (f"{c['i']:02d}-B{c['B']}-T{c['T']}-qk{c['H']}v{c['HV']}-{c['state']}-"
+            f"{'l2' if c['l2'] else 'raw'}-{c['form']}")
+
+
+def _scale_arg(kind, K=128):
+    return {"none": None, "zero": 0, "float": 1.0 / math.sqrt(K),
+            "tensor": torch.tensor(1.0 / math.sqrt(K))}[kind]
+
+
+@pytest.mark.parametrize("c", _decode_cases(), ids=_case_id)
+def test_decode_sweep(c, hip_device):
+    _announce(f"decode sweep {_case_id(c)}")
+    B, T, H, HV, l2 = c["B"], c["T"], c["H"], c["HV"], c["l2"]
+    gate_shape = "bhv" if (c["gates_bhv"] and T == 1) else "b1hv"
+    t = make_inputs(B, H, HV, seed=c["seed"], T=T, gate_shape=gate_shape)
+    state_dtype = {"fp32": torch.float32, "bf16": torch.bfloat16, "none": None}[c["state"]]
+    if state_dtype is None:
+        t["state"] = None
+    elif state_dtype == torch.bfloat16:
+        t["state"] = t["state"].to(torch.bfloat16)
+    t["scale"] = _scale_arg(c["scale"])
+    td = _dev(t, hip_device)
+
+    if c["form"] == "run":
+        out, st = gdn.run(**td, use_qk_l2norm=l2)
+        if td["state"] is not None:                 # value-returning: state untouched
+            assert torch.equal(td["state"].cpu(), t["state"])
+    else:
+        out = torch.empty(B, T, HV, 128, dtype=torch.bfloat16, device=hip_device)
+        sd = torch.float32 if state_dtype is None else state_dtype
+        if c["form"] == "inplace" and td["state"] is not None:
+            st = td["state"]
+        else:
+            st = torch.empty(B, HV, 128, 128, dtype=sd, device=hip_device)
+        gdn.kernel_hip(**td, output=out, new_state=st, use_qk_l2norm=l2)
+    torch.cuda.synchronize()
+
+    tf = {**t, "state": None if t["state"] is None else t["state"].float(),
+          "a": t["a"].view(B, T, HV), "b": t["b"].view(B, T, HV)}  # [B, HV] gates at T=1
+    step = oracle_loop if B * HV <= 128 else oracle_vec
+    ref_o, ref_s = oracle_tokens(step, **tf, use_qk_l2norm=l2,
+                                 state_dtype=state_dtype or torch.float32)
+
+    def vec64(*args, **kw):
+        return oracle_vec(*args, **kw, output_fp32=True, dtype=torch.float64)
+
+    o64, s64 = oracle_tokens(vec64, **tf, use_qk_l2norm=l2, state_dtype=None)
+    assert out.shape == (B, T, HV, 128)
+    assert_output_close(out.cpu(), ref_o, tight_ref64=o64, what="output")
+    if state_dtype == torch.bfloat16:
+        assert st.dtype == torch.bfloat16
+        sc = st.cpu().double()
+        d_ref = (sc - ref_s.double()).abs()
+        assert bool((d_ref <= 2.0 ** -7 * ref_s.double().abs() + 1e-6).all())
+        assert bool(((sc - s64).abs() <= 2.0 ** -8 * s64.abs() + 1e-6).all())
+    else:
+        assert st.dtype == torch.float32
+        _assert_fp32_state(st.cpu(), s64)
+
+
+def _prefill_cases(n=24, seed=77001):
+    rng = random.Random(seed)
+    cases = []
+    for i in range(n):
+        N = rng.randint(1, 12)
+        small = rng.random() < 0.3                    # total <= 16: the token path
+        if small:
+            lens = [rng.randint(0, 4) for _ in range(N)]
+            while sum(lens) > 16:
+                lens[rng.randrange(N)] = 0
+        else:
+            lens = [rng.choice([0, rng.randint(1, 20), rng.randint(20, 140)]) for _ in range(N)]
+            if sum(lens) <= 16:
+                lens[0] += 17
+        H = rng.choice([1, 2, 4, 8])
+        cases.append(dict(i=i, lens=lens, H=H, HV=H * rng.choice([1, 2, 4]),
+                          l2=rng.random() < 0.4, with_state=rng.random() < 0.8,
+                          inplace=rng.random() < 0.5, seed=40_000 + i))
+    return cases
+
+
+def _pf_id(c):
+    return f"{c['i']:02d}-N{len(c['lens'])}-L{sum(c['lens'])}-qk{c['H']}v{c['HV']}"
+
+
+@pytest.mark.parametrize("c", _prefill_cases(), ids=_pf_id)
+def test_prefill_sweep(c, hip_device):
+    _announce(f"prefill sweep {_pf_id(c)} lens={c['lens']}")
+    lens, H, HV, l2 = c["lens"], c["H"], c["HV"], c["l2"]
+    t = make_prefill_inputs(lens, H, HV, seed=c["seed"], with_state=c["with_state"])
+    td = _dev(t, hip_device)
+    L, N = sum(lens), len(lens)
+    if c["inplace"] and td["state"] is not None:
+        out = torch.empty(L, HV, 128, dtype=torch.bfloat16, device=hip_device)
+        st = td["state"]
+        gdn.kernel_prefill_hip(**td, output=out, new_state=st, use_qk_l2norm=l2)
+    else:
+        out, st = gdn.prefill_run(**td, use_qk_l2norm=l2)
+    torch.cuda.synchronize()
+    out, st = out.cpu(), st.cpu()
+    o64, s64 = prefill_chunked_fp64(**t, use_qk_l2norm=l2)
+    of = out.double().numpy()
+    assert np.all(np.isfinite(of))
+    assert np.all(np.abs(of - o64) <= 2.0 ** -7 * np.abs(o64) + 1e-5)
+    if L <= 400:
+        ref_o, _ = prefill_loop(**t, use_qk_l2norm=l2)
+        dl = (out.float() - ref_o.float()).abs()
+        assert bool((dl <= 1e-2 + 1e-2 * ref_o.float().abs()).all())
+    sd = st.double().numpy()
+    assert np.all(np.abs(sd - s64) <= 1e-3 * np.abs(s64) + 1e-5)
+    for s, n in enumerate(lens):                      # empty sequences: zero state
+        if n == 0:
+            assert torch.count_nonzero(st[s]) == 0
