@@ -18,8 +18,8 @@
 // Every exponent is <= 0.  With the q/k L2-norm on, the row norms enter as
 // per-row scale factors of the same products.
 //
-// Prefills of at most kSmallTokens tokens in all (so every sequence is that
-// short) skip the chunkwise machinery: one launch of the decode kernel's
+// Prefills of at most kSmallTokens (32) tokens in all (so every sequence is
+// that short) skip the chunkwise machinery: one launch of the decode kernel's
 // variable-length mode (gdn_decode_kernel.h) applies the recurrence token by
 // token with the state in registers, one workgroup per (sequence, v-head,
 // row tile), reading each sequence's token range from cu_seqlens on the
@@ -73,10 +73,14 @@ constexpr int kDim = 128;            // K == V == 128
 constexpr int kChunk = 64;           // tokens per chunk
 constexpr int kThreads = 256;        // 4 wavefronts
 constexpr long long kScanWideHeads = 256;  // N * HV from which the scan takes 32 columns
-// Total tokens up to which the token-by-token kernel runs the prefill: past
-// ~16 tokens per sequence the chunkwise kernels are faster (their cost is
-// ~15 us of preparation and scan latency; the token loop's ~0.6 us a token).
-constexpr int kSmallTokens = 16;
+// Total tokens up to which the token-by-token kernel runs the prefill (so no
+// sequence is longer).  Measured (kernel trace, one sequence): the token loop
+// costs ~3.5 us plus ~0.3 us a token, the chunkwise kernels ~15-20 us from
+// 17 to 128 tokens; they cross near 36-40 tokens (qk4_v8 and qk16_v32).
+// Several short sequences favour the token path far more (4 x 16 tokens:
+// 8.9 against 22.7 us), but past 32 tokens in all the longest sequence is
+// not known on the host.
+constexpr int kSmallTokens = 32;
 constexpr float kL2Eps = 1e-6f;
 constexpr float kSoftplusThreshold = 20.0f;
 constexpr float kLn2 = 0.693147180559945309f;

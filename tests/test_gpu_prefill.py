@@ -260,10 +260,11 @@ def test_split_sequences_compose_at_full_size(lens, H, HV, cut, hip_device):
     assert rel <= 1e-4, rel
 
 
-# --- prefills of at most 16 tokens: the decode kernel's variable-length mode ----
+# --- prefills of at most 32 tokens: the decode kernel's variable-length mode ----
 
 @pytest.mark.parametrize("seqlens,H,HV,l2,with_state", [
-    ([16], 4, 8, False, True),            # the largest token-by-token prefill
+    ([32], 4, 8, False, True),            # the largest token-by-token prefill
+    ([16], 4, 8, False, True),
     ([5, 0, 11], 4, 8, False, True),      # an empty sequence among them
     ([1] * 16, 4, 8, False, True),        # sixteen one-token sequences
     ([3, 9], 2, 8, True, True),           # GVA ratio 4, q/k L2-norm
@@ -280,20 +281,21 @@ def test_small_prefill_token_path(seqlens, H, HV, l2, with_state, hip_device):
 
 
 def test_small_and_chunkwise_paths_agree(hip_device):
-    """16 tokens run token by token; the same sequence followed by a 1-token
-    one (17 tokens in all) runs chunkwise: the first sequence's results agree
+    """32 tokens run token by token; the same sequence followed by a 1-token
+    one (33 tokens in all) runs chunkwise: the first sequence's results agree
     within the output and state bars."""
     _announce("small prefill vs chunkwise")
-    t = make_prefill_inputs([16, 1], 4, 8, seed=51)
-    out17, st17 = gdn.prefill_run(**_dev(t, hip_device))
-    t16 = {**t, "q": t["q"][:16], "k": t["k"][:16], "v": t["v"][:16], "a": t["a"][:16],
-           "b": t["b"][:16], "state": t["state"][:1], "cu_seqlens": t["cu_seqlens"][:2]}
-    out16, st16 = gdn.prefill_run(**_dev(t16, hip_device))
+    n = gdn.prefill.token_path_max_tokens()
+    t = make_prefill_inputs([n, 1], 4, 8, seed=51)
+    out_c, st_c = gdn.prefill_run(**_dev(t, hip_device))
+    t_tok = {**t, "q": t["q"][:n], "k": t["k"][:n], "v": t["v"][:n], "a": t["a"][:n],
+             "b": t["b"][:n], "state": t["state"][:1], "cu_seqlens": t["cu_seqlens"][:2]}
+    out_t, st_t = gdn.prefill_run(**_dev(t_tok, hip_device))
     torch.cuda.synchronize()
-    o16, o17 = out16.float().cpu(), out17[:16].float().cpu()
-    assert bool(((o16 - o17).abs() <= 2.0 ** -7 * o17.abs() + 1e-5).all())
-    s16, s17 = st16.cpu(), st17[:1].cpu()
-    assert bool(((s16 - s17).abs() <= 1e-3 * s17.abs() + 1e-5).all())
+    o_t, o_c = out_t.float().cpu(), out_c[:n].float().cpu()
+    assert bool(((o_t - o_c).abs() <= 2.0 ** -7 * o_c.abs() + 1e-5).all())
+    s_t, s_c = st_t.cpu(), st_c[:1].cpu()
+    assert bool(((s_t - s_c).abs() <= 1e-3 * s_c.abs() + 1e-5).all())
 
 
 def test_small_prefill_in_place_and_timed(hip_device):

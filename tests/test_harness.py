@@ -160,7 +160,9 @@ def test_prefill_mix():
     assert any(0 in w.lens for w in ws)              # empty sequences
     assert max(max(w.lens) for w in ws) == 16384   # longest single sequence
     assert [w.dispatches for w in ws[:3]] == [1, 1, 2]   # 6 and 1 tokens: the token path
-    assert all(w.dispatches == (1 if w.L <= 16 else 2 if w.N == 1 else 3) for w in ws)
+    from flashinfer_competition_codebase_amd.prefill import token_path_max_tokens
+    small = token_path_max_tokens()
+    assert all(w.dispatches == (1 if w.L <= small else 2 if w.N == 1 else 3) for w in ws)
     assert harness.prefill_workloads() == ws         # seeded: the same mix every time
 
 
@@ -266,7 +268,7 @@ def test_prefill_dispatch_count_follows_the_token_path_threshold():
     from flashinfer_competition_codebase_amd.prefill import (prefill_dispatches,
                                                             token_path_max_tokens)
     m = token_path_max_tokens()
-    assert m == 16
+    assert m == 32
     assert prefill_dispatches(m, 1) == 1 and prefill_dispatches(0, 5) == 1
     assert prefill_dispatches(m + 1, 1) == 2 and prefill_dispatches(m + 1, 2) == 3
     assert prefill_dispatches(m, 70_000) == 3            # past the grid's z limit
