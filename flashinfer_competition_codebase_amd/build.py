@@ -34,6 +34,11 @@ PREFILL_PATH = PKG_DIR / "libgdn_prefill.so"
 # library -> source
 LIBRARIES = {LIB_PATH: CSRC, PREFILL_PATH: PREFILL_SRC, CALIB_PATH: CALIB_SRC}
 OFFLOAD_ARCH = "gfx950"
+# Per-library extra flags.  The prefill's MFMA results go to VGPRs (the
+# VALU work that follows every product then reads them without a
+# v_accvgpr_read copy; in the scan loop those copies were a quarter of the
+# VALU instructions).
+EXTRA_FLAGS = {PREFILL_PATH: ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 KERNARG_PRELOAD_ARGS = int(os.environ.get("GDN_KERNARG_PRELOAD_ARGS", "8"))
 
 
@@ -48,7 +53,8 @@ def hipcc_path() -> str:
     return found
 
 
-def compile_command(out: Path = LIB_PATH, src: Path = CSRC) -> list[str]:
+def compile_command(out: Path = LIB_PATH, src: Path = CSRC,
+                    extra: list[str] | None = None) -> list[str]:
     return [
         hipcc_path(),
         f"--offload-arch={OFFLOAD_ARCH}",
@@ -62,6 +68,7 @@ def compile_command(out: Path = LIB_PATH, src: Path = CSRC) -> list[str]:
         # sizes its first loads need) are preloaded into SGPRs at dispatch.
         "-mllvm", f"-amdgpu-kernarg-preload-count={KERNARG_PRELOAD_ARGS}",
         "-Wall",
+        *(extra or []),
         f"-I{INCLUDE_DIR}",
         str(src),
         "-o", str(out),
@@ -74,7 +81,7 @@ def build(verbose: bool = False) -> Path:
     jobs = []
     for lib, src in LIBRARIES.items():
         tmp = lib.with_suffix(".so.tmp")
-        cmd = compile_command(tmp, src)
+        cmd = compile_command(tmp, src, EXTRA_FLAGS.get(lib))
         if verbose:
             print(" ".join(cmd), flush=True)
         jobs.append((lib, tmp, subprocess.Popen(cmd, stdout=subprocess.PIPE,
