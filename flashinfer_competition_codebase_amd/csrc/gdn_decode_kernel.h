@@ -281,18 +281,16 @@ struct TokenHead {
   float gq;         // g * qscale
 };
 
+// The per-head quantities of one token from its q, k, v and its gates.
+// Per-head reductions on the raw values: |q|^2, |k|^2 (L2-norm only) and
+// k.q.  The normalised, scaled vectors q' = qscale*q and k_hat = kscale*k are
+// never formed: their scales multiply the reduced dots instead.
 template <int NS, bool L2NORM>
-__device__ __forceinline__ void token_head(const TokenIn<NS>& in, float A_log, float dt_bias,
-                                           float scale, TokenHead<NS>& h) {
-  float g, beta;
-  gates(bf16_bits_to_f32(in.a_bits), dt_bias, A_log, bf16_bits_to_f32(in.b_bits), g, beta);
-  unpack_bf16x8(in.q, h.qf);
-  unpack_bf16x8(in.k, h.kf);
-  unpack_bf16_run<NS>(in.v, h.vrow);
-
-  // Per-head reductions on the raw values: |q|^2, |k|^2 (L2-norm only) and
-  // k.q.  The normalised, scaled vectors q' = qscale*q and k_hat = kscale*k
-  // are never formed: their scales multiply the reduced dots instead.
+__device__ __forceinline__ void head_of(u32x4 qbits, u32x4 kbits, const Bf16Run<NS>& vbits,
+                                        float g, float beta, float scale, TokenHead<NS>& h) {
+  unpack_bf16x8(qbits, h.qf);
+  unpack_bf16x8(kbits, h.kf);
+  unpack_bf16_run<NS>(vbits, h.vrow);
   float qscale = scale;
   float kscale = 1.0f;
   float kq_raw;
@@ -322,6 +320,80 @@ __device__ __forceinline__ void token_head(const TokenIn<NS>& in, float A_log, f
   h.kq = kq_raw * (qscale * kscale);
   h.gk = g * kscale;
   h.gq = g * qscale;
+}
+
+template <int NS, bool L2NORM>
+__device__ __forceinline__ void token_head(const TokenIn<NS>& in, float A_log, float dt_bias,
+                                           float scale, TokenHead<NS>& h) {
+  float g, beta;
+  gates(bf16_bits_to_f32(in.a_bits), dt_bias, A_log, bf16_bits_to_f32(in.b_bits), g, beta);
+  unpack_bf16x8(in.q, h.qf);
+  unpack_bf16x8(in.k, h.kf);
+  unpack_bf16_run<NS>(in.v, h.vrow);
+  float qscale = scale;
+  float kscale = 1.0f;
+  float kq_raw;
+  if constexpr (L2NORM) {
+    float hs[3] = {0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      hs[0] = fmaf(h.qf[i], h.qf[i], hs[0]);
+      hs[1] = fmaf(h.kf[i], h.kf[i], hs[1]);
+      hs[2] = fmaf(h.qf[i], h.kf[i], hs[2]);
+    }
+    row16_sum<3>(hs);
+    qscale *= __builtin_amdgcn_rsqf(hs[0] + kL2Eps);
+    kscale = __builtin_amdgcn_rsqf(hs[1] + kL2Eps);
+    kq_raw = hs[2];
+  } else {
+    float hs[1] = {0.0f};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) hs[0] = fmaf(h.qf[i], h.kf[i], hs[0]);
+    row16_sum<1>(hs);
+    kq_raw = hs[0];
+  }
+  h.g = g;
+  h.beta = beta;
+  h.kscale = kscale;
+  h.kq = kq_raw * (qscale * kscale);
+  h.gk = g * kscale;
+  h.gq = g * qscale;
+}
+
+// Multi-token inputs of one token (its gates come from the per-lane table).
+template <int NS>
+struct TokenQkv {
+  u32x4 q;
+  u32x4 k;
+  Bf16Run<NS> v;
+};
+
+template <int NS, bool BF16>
+__device__ __forceinline__ void load_qkv(const Params& p, size_t bt, int hq, int hv, int row0,
+                                         int j, TokenQkv<NS>& in) {
+  const size_t qk = (bt * p.H + hq) * kDim;
+  in.q = load_lane_bf16x8<BF16>(p.q + qk, j);
+  in.k = load_lane_bf16x8<BF16>(p.k + qk, j);
+  in.v = load_bf16_run<NS>(p.v + (bt * p.HV + hv) * kDim + row0);
+}
+
+// Gate table of the multi-token loop: lane l holds the gates of token
+// base + l of the sequence (the last token past the end), so each token's
+// gates are two lane reads instead of their transcendental chain.
+__device__ __forceinline__ float lane_value(float x, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l));
+}
+
+struct GateBits {
+  uint16_t a;
+  uint16_t b;
+};
+
+__device__ __forceinline__ GateBits load_gate_bits(const Params& p, size_t tok0, int base, int T,
+                                                   int hv, int lane) {
+  const int tl = base + lane < T ? base + lane : T - 1;
+  const size_t bt = (tok0 + tl) * p.HV + hv;
+  return GateBits{p.a[bt], p.b[bt]};
 }
 
 // One token of the recurrence on the NS rows a lane group holds: decay,
@@ -374,8 +446,14 @@ __device__ __forceinline__ void token_rows(float (&s)[NS][8], const TokenHead<NS
 // SGPRs by the dispatcher (-amdgpu-kernarg-preload-count): the state stream
 // then starts without waiting for a kernarg memory read.  The remaining
 // arguments are read while the first loads are in flight.
+//
+// The fp32-state multi-token kernels with 2 rows per lane group (launched
+// for T = 2 at 65-128 and above 768 heads, for T >= 3 at 65-256 heads) are
+// held at 6 waves per SIMD: at their ~71 VGPRs the compiler would allow 7,
+// which measured 2.3% slower than 6 at B=256 T=2 (qk16_v32).
 template <int NS, int WAVES, bool L2NORM, int POLICY, bool BF16, bool MULTI, bool VARLEN>
-__global__ __launch_bounds__(64 * WAVES) void gdn_decode_k128(
+__global__ __launch_bounds__(64 * WAVES)
+__attribute__((amdgpu_waves_per_eu(1, (MULTI && !BF16 && NS == 2) ? 6 : 8))) void gdn_decode_k128(
     const void* state, const uint16_t* q, const uint16_t* k, const uint16_t* v,
     const uint16_t* a, const uint16_t* b, unsigned h_ratio, int T_arg, const float* A_log_p,
     const float* dt_bias_p, uint16_t* out, void* new_state, float scale,
@@ -441,80 +519,141 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_decode_k128(
   // bursts use only preloaded arguments; A_log and dt_bias (whose pointers
   // are not preloaded) are read after them, so no wave waits on a kernarg
   // memory read before its state loads are in flight.
-  TokenIn<NS> cur;
-  load_token<NS, BF16>(p, tok0, hq, hv, row0, j, cur);
-  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (!MULTI) {
+    TokenIn<NS> cur;
+    load_token<NS, BF16>(p, tok0, hq, hv, row0, j, cur);
+    __builtin_amdgcn_sched_barrier(0);
 
-  RowRaw<BF16> raw[NS];
-  if (has_state) {
-#pragma unroll
-    for (int n = 0; n < NS; ++n) raw[n] = load_row<BF16, POLICY>(p.state, row_base + n, j);
-  }
-  // Variable-length (small prefill: one wave of few rows per head, latency
-  // bound): the inputs of the next kDepth = 3 tokens are in flight while a
-  // token is applied, so each load has two iterations to arrive; token
-  // indices are clamped to the last token, so every load is unconditional
-  // (the clamped repeats are never used).  The decode's multi-token kernels
-  // prefetch one token ahead: at large batches deeper prefetch costs
-  // registers and load slots (B=256 T=2: 170 -> 202 us), and at small ones
-  // their per-token time is the token's instruction chain, not the load.
-  constexpr int kDepth = VARLEN ? 3 : 1;
-  TokenIn<NS> pre1, pre2;                     // tokens 1 and 2 (kDepth == 3)
-  if constexpr (kDepth == 3) {
-    load_token<NS, BF16>(p, tok0 + (T > 1 ? 1 : 0), hq, hv, row0, j, pre1);
-    load_token<NS, BF16>(p, tok0 + (T > 2 ? 2 : T - 1), hq, hv, row0, j, pre2);
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  const float A_log = p.A_log[hv];
-  const float dt_bias = p.dt_bias[hv];
-  __builtin_amdgcn_sched_barrier(0);  // both reads in flight before either is used
-
-  // The first token's per-head math waits only on the small loads: keep it
-  // ahead of everything that waits on the state.
-  TokenHead<NS> h;
-  token_head<NS, L2NORM>(cur, A_log, dt_bias, p.scale, h);
-  __builtin_amdgcn_sched_barrier(0);
-
-  float s[NS][8];
-#pragma unroll
-  for (int n = 0; n < NS; ++n) {
+    RowRaw<BF16> raw[NS];
     if (has_state) {
-      unpack_row<BF16>(raw[n], s[n]);
-    } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) s[n][i] = 0.0f;
+      for (int n = 0; n < NS; ++n) raw[n] = load_row<BF16, POLICY>(p.state, row_base + n, j);
     }
-  }
+    __builtin_amdgcn_sched_barrier(0);
+    const float A_log = p.A_log[hv];
+    const float dt_bias = p.dt_bias[hv];
+    __builtin_amdgcn_sched_barrier(0);  // both reads in flight before either is used
 
-  for (int t = 0; t < T; ++t) {
-    TokenIn<NS> nxt;                          // token t + kDepth
-    if constexpr (kDepth == 3) {
-      const int ta = t + kDepth < T ? t + kDepth : T - 1;
-      load_token<NS, BF16>(p, tok0 + ta, hq, hv, row0, j, nxt);
-    } else if constexpr (MULTI) {
-      if (t + 1 < T) load_token<NS, BF16>(p, tok0 + t + 1, hq, hv, row0, j, nxt);
+    // The per-head math waits only on the small loads: keep it ahead of
+    // everything that waits on the state.
+    TokenHead<NS> h;
+    token_head<NS, L2NORM>(cur, A_log, dt_bias, p.scale, h);
+    __builtin_amdgcn_sched_barrier(0);
+
+    float s[NS][8];
+#pragma unroll
+    for (int n = 0; n < NS; ++n) {
+      if (has_state) {
+        unpack_row<BF16>(raw[n], s[n]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s[n][i] = 0.0f;
+      }
     }
-    float o[NS];
-    token_rows<NS>(s, h, o);
-    if constexpr (!MULTI) {
+    for (int t = 0; t < T; ++t) {
+      float o[NS];
+      token_rows<NS>(s, h, o);
       // The state write-back is the kernel's tail: issue it before the output.
 #pragma unroll
       for (int n = 0; n < NS; ++n) store_row<BF16, POLICY>(p.new_state, row_base + n, j, s[n]);
+      if (j == 0) {
+        const size_t out_row = ((tok0 + t) * p.HV + hv) * kDim + row0;
+        store_bf16_run<NS>(p.out + out_row, o);
+      }
     }
-    if (j == 0) {
-      const size_t out_row = ((tok0 + t) * p.HV + hv) * kDim + row0;
-      store_bf16_run<NS>(p.out + out_row, o);
-    }
-    if constexpr (kDepth == 3) {              // token t + 1 (unused after the last)
-      token_head<NS, L2NORM>(pre1, A_log, dt_bias, p.scale, h);
-      pre1 = pre2;
-      pre2 = nxt;
-    } else if constexpr (MULTI) {
-      if (t + 1 < T) token_head<NS, L2NORM>(nxt, A_log, dt_bias, p.scale, h);
-    }
-  }
+  } else {
+    // Multi-token: the state stays in registers across the tokens.  Each
+    // lane computes the gates of one token (lane l: token l, tokens 64 and
+    // on in further batches of 64) once, and every token reads its two
+    // from that table, so a token's instructions are its q/k/v work and the
+    // row updates only: with one wave per SIMD, as in small batches and
+    // small prefills, a token costs about 4 cycles per instruction.
+    TokenQkv<NS> in0;
+    load_qkv<NS, BF16>(p, tok0, hq, hv, row0, j, in0);
+    GateBits gb = load_gate_bits(p, tok0, 0, T, hv, lane);
+    __builtin_amdgcn_sched_barrier(0);
 
-  if constexpr (MULTI) {
+    RowRaw<BF16> raw[NS];
+    if (has_state) {
+#pragma unroll
+      for (int n = 0; n < NS; ++n) raw[n] = load_row<BF16, POLICY>(p.state, row_base + n, j);
+    }
+    // Variable-length (small prefill: one wave of few rows per head, latency
+    // bound): the inputs of the next kDepth = 3 tokens are in flight while a
+    // token is applied, so each load has two tokens' time to arrive; token
+    // indices are clamped to the last token, so every load is unconditional
+    // (the clamped repeats are never used), and the three input buffers are
+    // refilled in place by a loop body unrolled three times.  The decode's
+    // multi-token kernels prefetch one token ahead: at large batches deeper
+    // prefetch costs registers and load slots (B=256 T=2: 170 -> 202 us),
+    // and at small ones it measured no better.
+    constexpr int kDepth = VARLEN ? 3 : 1;
+    TokenQkv<NS> in1, in2;                    // tokens 1 and 2 (kDepth == 3)
+    if constexpr (kDepth == 3) {
+      load_qkv<NS, BF16>(p, tok0 + (T > 1 ? 1 : 0), hq, hv, row0, j, in1);
+      load_qkv<NS, BF16>(p, tok0 + (T > 2 ? 2 : T - 1), hq, hv, row0, j, in2);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const float A_log = p.A_log[hv];
+    const float dt_bias = p.dt_bias[hv];
+    __builtin_amdgcn_sched_barrier(0);
+
+    float gl, bl;                             // gates of token base + lane
+    gates(bf16_bits_to_f32(gb.a), dt_bias, A_log, bf16_bits_to_f32(gb.b), gl, bl);
+    TokenHead<NS> h;
+    head_of<NS, L2NORM>(in0.q, in0.k, in0.v, lane_value(gl, 0), lane_value(bl, 0), p.scale, h);
+    __builtin_amdgcn_sched_barrier(0);
+
+    float s[NS][8];
+#pragma unroll
+    for (int n = 0; n < NS; ++n) {
+      if (has_state) {
+        unpack_row<BF16>(raw[n], s[n]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s[n][i] = 0.0f;
+      }
+    }
+
+    // Per-head quantities of token tt >= 1 (uniform) from its inputs.
+    auto head_at = [&](const TokenQkv<NS>& in, int tt) {
+      if ((tt & 63) == 0) {                   // tokens tt .. tt + 63: a new gate batch
+        gb = load_gate_bits(p, tok0, tt, T, hv, lane);
+        gates(bf16_bits_to_f32(gb.a), dt_bias, A_log, bf16_bits_to_f32(gb.b), gl, bl);
+      }
+      head_of<NS, L2NORM>(in.q, in.k, in.v, lane_value(gl, tt & 63), lane_value(bl, tt & 63),
+                          p.scale, h);
+    };
+    // Token tt with the per-head quantities in h: rows and output.
+    auto apply = [&](int tt) {
+      float o[NS];
+      token_rows<NS>(s, h, o);
+      if (j == 0) store_bf16_run<NS>(p.out + ((tok0 + tt) * p.HV + hv) * kDim + row0, o);
+    };
+
+    if constexpr (kDepth == 3) {
+      for (int t = 0; t < T; t += 3) {
+        load_qkv<NS, BF16>(p, tok0 + (t + 3 < T ? t + 3 : T - 1), hq, hv, row0, j, in0);
+        apply(t);
+        if (t + 1 >= T) break;
+        head_at(in1, t + 1);
+        load_qkv<NS, BF16>(p, tok0 + (t + 4 < T ? t + 4 : T - 1), hq, hv, row0, j, in1);
+        apply(t + 1);
+        if (t + 2 >= T) break;
+        head_at(in2, t + 2);
+        load_qkv<NS, BF16>(p, tok0 + (t + 5 < T ? t + 5 : T - 1), hq, hv, row0, j, in2);
+        apply(t + 2);
+        if (t + 3 >= T) break;
+        head_at(in0, t + 3);
+      }
+    } else {
+      for (int t = 0; t < T; ++t) {
+        TokenQkv<NS> nxt;                     // token t + 1
+        if (t + 1 < T) load_qkv<NS, BF16>(p, tok0 + t + 1, hq, hv, row0, j, nxt);
+        apply(t);
+        if (t + 1 < T) head_at(nxt, t + 1);
+      }
+    }
 #pragma unroll
     for (int n = 0; n < NS; ++n) store_row<BF16, POLICY>(p.new_state, row_base + n, j, s[n]);
   }
