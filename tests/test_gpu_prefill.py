@@ -260,11 +260,13 @@ def test_split_sequences_compose_at_full_size(lens, H, HV, cut, hip_device):
     assert rel <= 1e-4, rel
 
 
-# --- prefills of at most 32 tokens: the decode kernel's variable-length mode ----
+# --- prefills of at most 48 tokens: the decode kernel's variable-length mode ----
 
 @pytest.mark.parametrize("seqlens,H,HV,l2,with_state", [
-    ([32], 4, 8, False, True),            # the largest token-by-token prefill
+    ([48], 4, 8, False, True),            # the largest token-by-token prefill
     ([16], 4, 8, False, True),
+    ([47, 1], 16, 32, True, True),        # 47 tokens: not a multiple of the 3-token loop body
+    ([12] * 4, 4, 8, False, True),
     ([5, 0, 11], 4, 8, False, True),      # an empty sequence among them
     ([1] * 16, 4, 8, False, True),        # sixteen one-token sequences
     ([3, 9], 2, 8, True, True),           # GVA ratio 4, q/k L2-norm
@@ -281,9 +283,9 @@ def test_small_prefill_token_path(seqlens, H, HV, l2, with_state, hip_device):
 
 
 def test_small_and_chunkwise_paths_agree(hip_device):
-    """32 tokens run token by token; the same sequence followed by a 1-token
-    one (33 tokens in all) runs chunkwise: the first sequence's results agree
-    within the output and state bars."""
+    """The largest token-by-token prefill (one sequence of as many tokens as
+    the path takes) and the same sequence followed by a 1-token one (one
+    token more in all: chunkwise) agree within the output and state bars."""
     _announce("small prefill vs chunkwise")
     n = gdn.prefill.token_path_max_tokens()
     t = make_prefill_inputs([n, 1], 4, 8, seed=51)

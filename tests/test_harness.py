@@ -268,7 +268,7 @@ def test_prefill_dispatch_count_follows_the_token_path_threshold():
     from flashinfer_competition_codebase_amd.prefill import (prefill_dispatches,
                                                             token_path_max_tokens)
     m = token_path_max_tokens()
-    assert m == 32
+    assert m == 48
     assert prefill_dispatches(m, 1) == 1 and prefill_dispatches(0, 5) == 1
     assert prefill_dispatches(m + 1, 1) == 2 and prefill_dispatches(m + 1, 2) == 3
     assert prefill_dispatches(m, 70_000) == 3            # past the grid's z limit
