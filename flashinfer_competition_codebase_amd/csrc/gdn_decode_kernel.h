@@ -538,6 +538,11 @@ __attribute__((amdgpu_waves_per_eu(1, (MULTI && !BF16 && NS == 2) ? 6 : 8))) voi
     // everything that waits on the state.
     TokenHead<NS> h;
     token_head<NS, L2NORM>(cur, A_log, dt_bias, p.scale, h);
+    // Its scalars are materialised here, ahead of the state: left alone, the
+    // compiler sinks the output's factors (scale, the q-norm, k.q) to their
+    // use after the state stores, which puts a kernel-argument read and a
+    // v_rsq_f32 between the state's arrival and the final output store.
+    asm volatile("" ::"v"(h.g), "v"(h.beta), "v"(h.kscale), "v"(h.kq), "v"(h.gk), "v"(h.gq));
     __builtin_amdgcn_sched_barrier(0);
 
     float s[NS][8];
