@@ -153,6 +153,33 @@ def test_all_launch_shapes_agree_bitwise(hip_device):
         assert torch.equal(st, ref_s), (ns, w, pol)
 
 
+def test_batch_beyond_one_launch(hip_device):
+    """B = 65600 one-head sequences: more than one launch's grid-z limit
+    (65535), so the host splits the batch into two launches.  Slices at the
+    start, across the split and at the end match separate small calls
+    bitwise (the per-row arithmetic does not depend on the launch shape)."""
+    _announce("B=65600 qk1_v1, two launches")
+    B, H, HV = 65600, 1, 1
+    g = torch.Generator(device=hip_device).manual_seed(4100)
+
+    def rn(*shape, scale=1.0, dtype=torch.bfloat16):
+        return (torch.randn(*shape, generator=g, device=hip_device) * scale).to(dtype)
+
+    t = dict(q=rn(B, 1, H, 128), k=rn(B, 1, H, 128), v=rn(B, 1, HV, 128),
+             state=rn(B, HV, 128, 128, scale=0.05, dtype=torch.float32),
+             A_log=torch.log(torch.rand(HV, generator=g, device=hip_device) * 15 + 1),
+             a=rn(B, HV), dt_bias=torch.rand(HV, generator=g, device=hip_device) * 2 - 1,
+             b=rn(B, HV), scale=None)
+    out, st = gdn.run(**t, use_qk_l2norm=True)
+    for lo, hi in ((0, 3), (65530, 65540), (B - 3, B)):
+        part = {n: (x[lo:hi].contiguous() if n in ("q", "k", "v", "state", "a", "b") else x)
+                for n, x in t.items()}
+        o2, s2 = gdn.run(**part, use_qk_l2norm=True)
+        torch.cuda.synchronize()
+        assert torch.equal(out[lo:hi], o2), (lo, hi)
+        assert torch.equal(st[lo:hi], s2), (lo, hi)
+
+
 def test_state_none_is_zero_state(hip_device):
     _announce("state=None")
     t = make_inputs(2, 16, 32, seed=4003)

@@ -157,6 +157,34 @@ def test_more_than_256_sequences(hip_device):
     _check(t, out, st, loop=False)
 
 
+def test_many_empty_sequences_past_the_token_paths_grid(hip_device):
+    """65600 one-head sequences, all but five empty, 40 tokens in all: few
+    enough tokens for the token-by-token path but more sequences than its
+    grid holds (65535), so the chunkwise kernels run, with 257 groups of 256
+    sequences in the offsets scan.  The five match the oracle; every empty
+    sequence gets a zero state."""
+    _announce("65600 sequences, 5 of 8 tokens, chunkwise")
+    N = 65600
+    picks = [0, 255, 256, 65535, N - 1]
+    small = make_prefill_inputs([8] * len(picks), 1, 1, seed=77)
+    lens = [0] * N
+    for i in picks:
+        lens[i] = 8
+    cu = torch.zeros(N + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(torch.tensor(lens, dtype=torch.int64), 0).to(torch.int32)
+    g = torch.Generator(device=hip_device).manual_seed(78)
+    state = torch.randn(N, 1, 128, 128, generator=g, device=hip_device) * 0.05
+    state[picks] = small["state"].to(hip_device)
+    big = {**_dev(small, hip_device), "state": state, "cu_seqlens": cu.to(hip_device)}
+    assert gdn.prefill.prefill_dispatches(40, N) == 3
+    out, st = gdn.prefill_run(**big)
+    sums = st.abs().sum(dim=(1, 2, 3))
+    torch.cuda.synchronize()
+    nonzero = torch.nonzero(sums).flatten().cpu().tolist()
+    assert nonzero == picks
+    _check(small, out, st[picks])
+
+
 def test_timed_entry_matches_and_times_each_kernel(hip_device):
     """gdn_prefill_timed: the same results as gdn_prefill, and its four events
     bracket the three launches (each interval non-negative, the scan's
