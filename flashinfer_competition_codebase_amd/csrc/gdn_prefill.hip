@@ -73,6 +73,19 @@ constexpr int kDim = 128;            // K == V == 128
 constexpr int kChunk = 64;           // tokens per chunk
 constexpr int kThreads = 256;        // 4 wavefronts
 constexpr long long kScanWideHeads = 256;  // N * HV from which the scan takes 32 columns
+// Batches whose chunk slots the kernels find themselves, without the offsets
+// kernel: at most kFewSeqs sequences and kFewPrepGroups preparation
+// workgroups (slots x v-heads).  Each workgroup then scans the batch's
+// sequence lengths in one wave, which costs more than the saved launch once
+// there are thousands of them (16 x 512 tokens at 16/32 heads, 4608
+// workgroups: 2% slower; 8 x 1024 at 4/8, 1088: 3% faster; 3 sequences of
+// 30-50 tokens: 18.7 -> 16.3 us).
+constexpr int kFewSeqs = 64;
+constexpr long long kFewPrepGroups = 2048;
+
+bool few_seqs(long long L, long long N, long long HV) {
+  return N > 1 && N <= kFewSeqs && ((L + kChunk - 1) / kChunk + N) * HV <= kFewPrepGroups;
+}
 // Total tokens up to which the token-by-token kernel runs the prefill (so no
 // sequence is longer).  Measured (kernel trace, one sequence): the token loop
 // costs ~3.5 us plus ~0.25 us a token, the chunkwise kernels ~15-17 us up to
@@ -195,6 +208,8 @@ struct Params {
   int ratio;                 // HV / H
   int l2norm;
   int single;                // one sequence: chunk c is slot c (no offsets kernel)
+  int few;                   // 2..kFewSeqs sequences: the kernels compute the chunk
+                             // slots from cu_seqlens (no offsets kernel)
   long long max_slots;       // slots the workspace holds
 };
 
@@ -207,6 +222,37 @@ __device__ __forceinline__ void seq_range(const Params& p, int s, int& start, in
   s1 = s1 < s0 ? s0 : (s1 > p.L ? p.L : s1);
   start = s0;
   end = s1;
+}
+
+// Chunk slots of a batch of at most 64 sequences, from cu_seqlens in one
+// wave (lane s: sequence s): the prefix the offsets kernel writes, held in
+// registers.  excl = slots of the sequences before s, incl = excl + its own,
+// both capped at the workspace's slots as there.  A sequence's chunk count
+// is at most 2^25 (ranges are clamped to [0, L], L < 2^31), so 64 of them
+// sum without overflow in 32 bits.
+struct FewSlots {
+  int start, end;          // this lane's sequence's token range (0, 0 past N)
+  long long excl, incl;
+};
+
+__device__ __forceinline__ FewSlots few_slots(const Params& p) {
+  const int lane = threadIdx.x & 63;
+  FewSlots f{0, 0, 0, 0};
+  unsigned cnt = 0;
+  if (lane < p.N) {
+    seq_range(p, lane, f.start, f.end);
+    cnt = static_cast<unsigned>(f.end - f.start + kChunk - 1) / kChunk;
+  }
+  unsigned x = cnt;                                // inclusive scan over the wave
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const unsigned y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
+  }
+  const long long incl = x, excl = static_cast<long long>(x) - cnt;
+  f.incl = incl < p.max_slots ? incl : p.max_slots;
+  f.excl = excl < p.max_slots ? excl : p.max_slots;
+  return f;
 }
 
 // ---------------------------------------------------------------------------
@@ -366,6 +412,18 @@ void prep_kernel(Params p) {
     seq_range(p, 0, start, end);
     t0 = start + c * kChunk;
     n = min(kChunk, end - t0);
+  } else if (p.few) {
+    // slot c belongs to the sequence whose slots [excl, incl) hold it
+    const FewSlots f = few_slots(p);
+    const unsigned long long own = __ballot(f.excl <= c && c < f.incl);
+    t0 = 0;
+    n = 0;
+    if (own != 0) {
+      const int s = __builtin_ctzll(own);
+      const long long first = __shfl(f.excl, s, 64);
+      t0 = __shfl(f.start, s, 64) + static_cast<int>(c - first) * kChunk;
+      n = min(kChunk, __shfl(f.end, s, 64) - t0);
+    }
   } else {
     const i32x4 info = p.slot_info[c];
     t0 = info.y;
@@ -829,8 +887,18 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Params p) {
 
   // Chunk count from the slot offsets (never more than the range holds, and
   // never more slots than the workspace has, whatever cu_seqlens contains).
-  const int slot0 = p.single ? 0 : p.offs[s];
-  const int nchunks = p.single ? (end - start + kChunk - 1) / kChunk : p.offs[s + 1] - slot0;
+  int slot0, nchunks;
+  if (p.single) {
+    slot0 = 0;
+    nchunks = (end - start + kChunk - 1) / kChunk;
+  } else if (p.few) {
+    const FewSlots f = few_slots(p);
+    slot0 = static_cast<int>(__shfl(f.excl, s, 64));
+    nchunks = static_cast<int>(__shfl(f.incl, s, 64)) - slot0;
+  } else {
+    slot0 = p.offs[s];
+    nchunks = p.offs[s + 1] - slot0;
+  }
   if (nchunks <= 0) {                 // no tokens: zeros, as the reference
 #pragma unroll
     for (int t = 0; t < 2; ++t)
@@ -1108,6 +1176,7 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
   p.ratio = HV / H;
   p.l2norm = use_qk_l2norm != 0;
   p.single = num_seqs == 1;
+  p.few = few_seqs(total_seq_len, num_seqs, HV);
   p.max_slots = slots;
 
   hipStream_t stream = static_cast<hipStream_t>(hip_stream);
@@ -1129,7 +1198,7 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
   }
   hipError_t e = mark(0);
   if (e != hipSuccess) return e;
-  if (!p.single)
+  if (!p.single && !p.few)
     hipLaunchKernelGGL(chunk_offsets_kernel, dim3(1), dim3(kThreads), 0, stream, p, offs,
                        slot_info);
   e = hipGetLastError();
@@ -1193,6 +1262,12 @@ int gdn_prefill_timed(const void* q, const void* k, const void* v, const float* 
 
 int gdn_prefill_token_path_max_tokens(void) { return kSmallTokens; }
 
-int gdn_prefill_abi_version(void) { return 4; }
+int gdn_prefill_dispatches(int total_seq_len, int num_seqs, int HV) {
+  if (num_seqs <= 0 || total_seq_len < 0 || HV <= 0) return 0;
+  if (total_seq_len <= kSmallTokens && num_seqs <= 65535) return 1;
+  return num_seqs == 1 || few_seqs(total_seq_len, num_seqs, HV) ? 2 : 3;
+}
+
+int gdn_prefill_abi_version(void) { return 5; }
 
 }  // extern "C"

@@ -154,7 +154,7 @@ class PrefillWorkload:
     @property
     def dispatches(self) -> int:      # kernels one prefill call launches
         from .prefill import prefill_dispatches
-        return prefill_dispatches(self.L, self.N)
+        return prefill_dispatches(self.L, self.N, self.HV)
 
 
 def prefill_workloads() -> list:

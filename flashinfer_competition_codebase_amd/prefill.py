@@ -56,15 +56,14 @@ def token_path_max_tokens() -> int:
     return int(_lib.get_prefill_lib().gdn_prefill_token_path_max_tokens())
 
 
-def prefill_dispatches(total_seq_len: int, num_seqs: int) -> int:
-    """Kernel dispatches of one prefill call: 1 on the token-by-token path,
-    else 2 for one sequence (preparation, scan) and 3 for several (the
-    chunk-offsets scan first); 0 for no sequences."""
-    if num_seqs <= 0:
-        return 0
-    if total_seq_len <= token_path_max_tokens() and num_seqs <= 65535:
-        return 1
-    return 2 if num_seqs == 1 else 3
+def prefill_dispatches(total_seq_len: int, num_seqs: int, HV: int) -> int:
+    """Kernel dispatches of one prefill call over HV v-heads, as the library
+    makes them: 1 on the token-by-token path, else 2 (preparation, scan) for
+    one sequence or a few small ones (at most 64, at most 2048 preparation
+    workgroups) and 3 (the chunk-offsets scan first) otherwise; 0 for no
+    sequences."""
+    return int(_lib.get_prefill_lib().gdn_prefill_dispatches(int(total_seq_len), int(num_seqs),
+                                                            int(HV)))
 
 
 def check_prefill_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, output=None,

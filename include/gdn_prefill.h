@@ -80,8 +80,10 @@ int gdn_prefill(const void* q, const void* k, const void* v, const float* state,
  * Measurement hook, no counterpart in the reference: gdn_prefill with
  * events[0..3] (hipEvent_t, all non-null) recorded on hip_stream before the
  * offsets, preparation and scan launches and after the scan, so that
- * hipEventElapsedTime gives each kernel's time.  On the token-by-token path
- * events 0..2 are recorded back to back and its one launch lies between
+ * hipEventElapsedTime gives each kernel's time.  Without an offsets launch
+ * (one sequence, or few: see gdn_prefill_dispatches) events 0 and 1 are
+ * recorded back to back; on the
+ * token-by-token path events 0..2 are, and its one launch lies between
  * events 2 and 3.  Nothing is recorded when num_seqs is 0.
  */
 int gdn_prefill_timed(const void* q, const void* k, const void* v, const float* state,
@@ -100,8 +102,19 @@ int gdn_prefill_timed(const void* q, const void* k, const void* v, const float* 
  */
 int gdn_prefill_token_path_max_tokens(void);
 
-/* ABI version of this header: 4 (3 had no gdn_prefill_token_path_max_tokens;
- * 2 had no gdn_prefill_timed; 1 had no H in gdn_prefill_workspace_bytes). */
+/*
+ * Kernel launches gdn_prefill makes for these sizes: 0 for no sequences, 1
+ * on the token-by-token path, 2 (preparation, scan) for one sequence or for
+ * at most 64 with at most 2048 preparation workgroups ((ceil(L / 64) + N) x
+ * HV; the kernels then find the chunk slots from cu_seqlens themselves), 3
+ * (the chunk-offsets scan first) otherwise.  No counterpart in the
+ * reference; for callers that attribute kernel traces to calls.
+ */
+int gdn_prefill_dispatches(int total_seq_len, int num_seqs, int HV);
+
+/* ABI version of this header: 5 (4 had no gdn_prefill_dispatches; 3 had no
+ * gdn_prefill_token_path_max_tokens; 2 had no gdn_prefill_timed; 1 had no H
+ * in gdn_prefill_workspace_bytes). */
 int gdn_prefill_abi_version(void);
 
 #ifdef __cplusplus

@@ -57,6 +57,9 @@ def _check(t, out, st, l2=False, loop=True):
 
 
 @pytest.mark.parametrize("seqlens,H,HV", [
+    ([70] + [1] * 63, 4, 8),          # 64 sequences: chunk slots found in the kernels
+    ([70] + [1] * 64, 4, 8),          # 65: the chunk-offsets scan
+    ([0, 130, 0, 0, 64, 1, 0], 2, 4), # empty sequences among few
     ([6], 4, 8),                      # the size of the reference's prefill workload 0
     ([1], 4, 8),
     ([64], 4, 8),
@@ -176,7 +179,7 @@ def test_many_empty_sequences_past_the_token_paths_grid(hip_device):
     state = torch.randn(N, 1, 128, 128, generator=g, device=hip_device) * 0.05
     state[picks] = small["state"].to(hip_device)
     big = {**_dev(small, hip_device), "state": state, "cu_seqlens": cu.to(hip_device)}
-    assert gdn.prefill.prefill_dispatches(40, N) == 3
+    assert gdn.prefill.prefill_dispatches(40, N, 1) == 3
     out, st = gdn.prefill_run(**big)
     sums = st.abs().sum(dim=(1, 2, 3))
     torch.cuda.synchronize()

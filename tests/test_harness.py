@@ -162,7 +162,8 @@ def test_prefill_mix():
     assert [w.dispatches for w in ws[:3]] == [1, 1, 2]   # 6 and 1 tokens: the token path
     from flashinfer_competition_codebase_amd.prefill import token_path_max_tokens
     small = token_path_max_tokens()
-    assert all(w.dispatches == (1 if w.L <= small else 2 if w.N == 1 else 3) for w in ws)
+    assert all(w.dispatches == (1 if w.L <= small else 2 if w.N == 1 or (
+        w.N <= 64 and ((w.L + 63) // 64 + w.N) * w.HV <= 2048) else 3) for w in ws)
     assert harness.prefill_workloads() == ws         # seeded: the same mix every time
 
 
@@ -221,7 +222,8 @@ def _prefill_trace_csv(tmp_path, calls):
 
 def test_prefill_trace_attribution_spans_the_calls_dispatches(tmp_path):
     ws = harness.prefill_workloads()
-    w0, w2, w11 = ws[0], ws[2], ws[11]               # 1, 2 and 3 dispatches per call
+    w0, w2 = ws[0], ws[2]                            # 1 and 2 dispatches per call
+    w11 = harness.PrefillWorkload(uuid="prefill-70x1", lens=(1,) * 70, seed=1)   # 3
     assert (w0.dispatches, w2.dispatches, w11.dispatches) == (1, 2, 3)
     m = harness.Manifest()
     calls = []
@@ -269,7 +271,12 @@ def test_prefill_dispatch_count_follows_the_token_path_threshold():
                                                             token_path_max_tokens)
     m = token_path_max_tokens()
     assert m == 48
-    assert prefill_dispatches(m, 1) == 1 and prefill_dispatches(0, 5) == 1
-    assert prefill_dispatches(m + 1, 1) == 2 and prefill_dispatches(m + 1, 2) == 3
-    assert prefill_dispatches(m, 70_000) == 3            # past the grid's z limit
-    assert prefill_dispatches(100, 0) == 0
+    assert prefill_dispatches(m, 1, 8) == 1 and prefill_dispatches(0, 5, 8) == 1
+    assert prefill_dispatches(m + 1, 1, 8) == 2 and prefill_dispatches(m + 1, 2, 8) == 2
+    assert prefill_dispatches(m + 1, 64, 8) == 2          # slots found in the kernels
+    assert prefill_dispatches(m + 1, 65, 8) == 3          # the chunk-offsets scan first
+    assert prefill_dispatches(8192, 8, 8) == 2            # (128 + 8) x 8 = 1088 workgroups
+    assert prefill_dispatches(8192, 16, 32) == 3          # (128 + 16) x 32 = 4608
+    assert prefill_dispatches(16384, 1, 32) == 2          # one sequence: never offsets
+    assert prefill_dispatches(m, 70_000, 8) == 3         # past the grid's z limit
+    assert prefill_dispatches(100, 0, 8) == 0

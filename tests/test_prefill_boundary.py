@@ -29,7 +29,8 @@ def _header_functions():
 def test_header_and_library_agree():
     funcs = _header_functions()
     assert set(funcs) == {"gdn_prefill_workspace_bytes", "gdn_prefill", "gdn_prefill_timed",
-                          "gdn_prefill_token_path_max_tokens", "gdn_prefill_abi_version"}
+                          "gdn_prefill_token_path_max_tokens", "gdn_prefill_dispatches",
+                          "gdn_prefill_abi_version"}
     lib = _lib.get_prefill_lib()
     for name, nparams in funcs.items():
         assert hasattr(lib, name)
