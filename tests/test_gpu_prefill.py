@@ -188,6 +188,31 @@ def test_many_empty_sequences_past_the_token_paths_grid(hip_device):
     _check(small, out, st[picks])
 
 
+@pytest.mark.parametrize("cu,L", [
+    ([0, 30, 5, 40, 100], 40),         # decreasing and past L; 40 tokens: the token path
+    ([0, 50, 10, 60, 200, 30], 60),    # the same at 60 tokens: chunkwise, slots in the kernels
+    ([0, 50] + [10, 60, 200, 30] * 20, 60),   # 81 sequences: the chunk-offsets scan
+])
+def test_malformed_cu_seqlens_stay_in_bounds(cu, L, hip_device):
+    """cu_seqlens that decrease or pass L: every kernel clamps each range to
+    [0, L] (and to start <= end), so the call completes with finite results;
+    the first sequence, a well-formed range, gets the state that a call with
+    it alone gives (bitwise: the same arithmetic on every path)."""
+    N = len(cu) - 1
+    _announce(f"malformed cu_seqlens N={N} L={L}")
+    t = make_prefill_inputs([L] + [0] * (N - 1), 4, 8, seed=91)
+    t["cu_seqlens"] = torch.tensor(cu, dtype=torch.int32)
+    out, st = gdn.prefill_run(**_dev(t, hip_device))
+    n0 = min(cu[1], L)
+    alone = {**t, "q": t["q"][:n0], "k": t["k"][:n0], "v": t["v"][:n0], "a": t["a"][:n0],
+             "b": t["b"][:n0], "state": t["state"][:1],
+             "cu_seqlens": torch.tensor([0, n0], dtype=torch.int32)}
+    _, st1 = gdn.prefill_run(**_dev(alone, hip_device))
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out.float()).all()) and bool(torch.isfinite(st).all())
+    assert torch.equal(st[:1], st1)
+
+
 def test_timed_entry_matches_and_times_each_kernel(hip_device):
     """gdn_prefill_timed: the same results as gdn_prefill, and its four events
     bracket the three launches (each interval non-negative, the scan's
