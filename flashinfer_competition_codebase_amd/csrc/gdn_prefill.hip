@@ -401,6 +401,10 @@ __device__ __forceinline__ void store16(float* D, int ldd, const f32x4& v, float
   for (int e = 0; e < 4; ++e) D[(4 * g4 + e) * ldd + col] = sign * v[e];
 }
 
+// FEW: the batch's chunk slots come from cu_seqlens in the kernel (few
+// sequences, no offsets kernel); a template flag, so that the kernels of the
+// other modes are compiled without that code.
+template <bool FEW>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3)))
 void prep_kernel(Params p) {
   __shared__ PrepLds lds;
@@ -412,7 +416,7 @@ void prep_kernel(Params p) {
     seq_range(p, 0, start, end);
     t0 = start + c * kChunk;
     n = min(kChunk, end - t0);
-  } else if (p.few) {
+  } else if (FEW) {
     // slot c belongs to the sequence whose slots [excl, incl) hold it
     const FewSlots f = few_slots(p);
     const unsigned long long own = __ballot(f.excl <= c && c < f.incl);
@@ -849,8 +853,9 @@ __device__ __forceinline__ void load_kt(const float* qk, int wave, int lane, Sca
 // Workgroups are handed to the 8 XCDs round-robin by index, so every tile of
 // a head runs on the same XCD (b % 8 is fixed) and the tiles are dispatched
 // 8 apart -- together -- sharing that XCD's L2 copy of the chunk operands
-// they all read.  Heads past N * HV (padding to a multiple of 8) exit.
-template <int NT>
+// they all read.  Heads past N * HV (padding to a multiple of 8) exit.  FEW
+// as for prep_kernel.
+template <int NT, bool FEW>
 __global__ __launch_bounds__(kThreads) void scan_kernel(Params p) {
   __shared__ ScanLds<NT> lds;
   constexpr int kTiles = 8 / NT;
@@ -891,7 +896,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Params p) {
   if (p.single) {
     slot0 = 0;
     nchunks = (end - start + kChunk - 1) / kChunk;
-  } else if (p.few) {
+  } else if (FEW) {
     const FewSlots f = few_slots(p);
     slot0 = static_cast<int>(__shfl(f.excl, s, 64));
     nchunks = static_cast<int>(__shfl(f.incl, s, 64)) - slot0;
@@ -1205,7 +1210,8 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
   if (e == hipSuccess) e = mark(1);
   if (e != hipSuccess) return e;
   if (slots > 0) {
-    hipLaunchKernelGGL(prep_kernel, dim3(static_cast<unsigned>(slots), HV), dim3(kThreads), 0,
+    auto* prep = p.few ? prep_kernel<true> : prep_kernel<false>;
+    hipLaunchKernelGGL(prep, dim3(static_cast<unsigned>(slots), HV), dim3(kThreads), 0,
                        stream, p);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -1217,11 +1223,13 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
   const long long heads = static_cast<long long>(num_seqs) * HV;
   const long long groups = (heads + 7) / 8;
   if (heads >= kScanWideHeads) {
-    hipLaunchKernelGGL(scan_kernel<2>, dim3(static_cast<unsigned>(groups * 8 * 4)),
-                       dim3(kThreads), 0, stream, p);
+    auto* scan = p.few ? scan_kernel<2, true> : scan_kernel<2, false>;
+    hipLaunchKernelGGL(scan, dim3(static_cast<unsigned>(groups * 8 * 4)), dim3(kThreads), 0,
+                       stream, p);
   } else {
-    hipLaunchKernelGGL(scan_kernel<1>, dim3(static_cast<unsigned>(groups * 8 * 8)),
-                       dim3(kThreads), 0, stream, p);
+    auto* scan = p.few ? scan_kernel<1, true> : scan_kernel<1, false>;
+    hipLaunchKernelGGL(scan, dim3(static_cast<unsigned>(groups * 8 * 8)), dim3(kThreads), 0,
+                       stream, p);
   }
   e = hipGetLastError();
   if (e == hipSuccess) e = mark(3);
