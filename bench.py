@@ -301,6 +301,8 @@ def attribute_kernel_trace(trace_csv, manifest: dict) -> dict:
         cold = dec[i: i + m["cold"]]
         i += m["cold"]
         shapes[m["name"]] = {"steady": med(steady), "cold": med(cold),
+                             "steady_avg": round(statistics.fmean(
+                                 (e - s) / 1e3 for s, e in steady), 3),
                              "n_steady": len(steady), "n_cold": len(cold)}
     fl = manifest["floor"]
     floor = None
@@ -348,22 +350,24 @@ def kernel_trace_leg(iters: int, timeout_s: float = 300.0) -> dict:
 
 def timed_steps(t, l2, steps, states):
     """Wall clock over ``steps`` back-to-back launches of the product entry
-    point, rotating over ``states``, plus HIP event markers around every
-    launch on the launch stream."""
+    point, rotating over ``states``, and the GPU time of the same region from
+    one pair of HIP events on the launch stream (torch's current stream, the
+    one ``kernel_hip`` launches on) around all of them: the average launch
+    duration, gaps between back-to-back launches included, with nothing
+    between the launches.  Returns (wall seconds, GPU µs per launch)."""
     stream = torch.cuda.current_stream()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
     views = [{**t, "state": s, "new_state": s} for s in states]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    start.record(stream)
     for i in range(steps):
-        starts[i].record(stream)
         gdn.kernel_hip(**views[i % len(views)], use_qk_l2norm=l2)
-        ends[i].record(stream)
+    stop.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    durs = [s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends)]
-    return wall, durs
+    return wall, start.elapsed_time(stop) * 1e3 / steps
 
 
 def cpu_baseline(seconds: float):
@@ -373,8 +377,8 @@ def cpu_baseline(seconds: float):
     rows, repeated until about ``seconds`` of CPU work."""
     from oracle.gdn_decode_oracle import make_inputs, oracle_loop
 
-    threads = max(1, min(16, len(os.sched_getaffinity(0))))
-    torch.set_num_threads(threads)
+    threads = host_threads()
+    torch.set_num_threads(threads["affinity_cores"])
     torch.set_float32_matmul_precision("highest")
     Bs = 8
     t = make_inputs(Bs, 16, 32, seed=1003)
@@ -397,11 +401,27 @@ def cpu_baseline(seconds: float):
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"B={Bs} of the B=256 qk16_v32 L2-norm workload ({Bs * 32} heads), "
-                   f"{reps} steps in {elapsed:.1f} s; {per_step * 1e3:.1f} ms/step"),
+        "sample": (f"a rate: B={Bs} of the B=256 qk16_v32 L2-norm workload ({Bs * 32} of its "
+                   f"8192 heads; the per-head loop makes the rate independent of B), "
+                   f"{reps} steps in {elapsed:.1f} s; {per_step * 1e3:.1f} ms per B={Bs} step, "
+                   f"{per_step * 32e3:.0f} ms per B=256 step at this rate"),
         "b1_us_per_step": round(statistics.median(b1), 1),
         "cpu": _cpu_model(),
+        "threads": {**threads, "torch_num_threads": torch.get_num_threads()},
     }
+
+
+def host_threads() -> dict:
+    """Host cores for the CPU baseline: every core of this process's
+    affinity mask (``torch.set_num_threads(len(os.sched_getaffinity(0)))``),
+    with the cgroup CPU quota recorded beside it when one is set."""
+    res = {"affinity_cores": len(os.sched_getaffinity(0)), "os_cpu_count": os.cpu_count()}
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        res["cgroup_cpu_quota"] = None if quota == "max" else round(int(quota) / int(period), 2)
+    except (OSError, ValueError):
+        pass
+    return res
 
 
 def _cpu_model() -> str:
@@ -414,13 +434,107 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-def _traffic():
-    if not TRAFFIC_SUMMARY.exists():
-        return None
+def decode_kernel_name(ns: int, waves: int, l2: bool, policy: int, bf16: bool = False,
+                       multi: bool = False) -> str:
+    """Name prefix of the decode kernel instantiation a launch shape runs,
+    as rocprofv3 reports it."""
+    b = lambda x: "true" if x else "false"  # noqa: E731
+    return (f"gdn::gdn_decode_k128<{ns}, {waves}, {b(l2)}, {policy}, {b(bf16)}, {b(multi)}, "
+            f"false>")
+
+
+DECODE_SOURCES = ("flashinfer_competition_codebase_amd/csrc/gdn_decode_kernel.h",
+                  "flashinfer_competition_codebase_amd/csrc/gdn_decode.hip",
+                  "flashinfer_competition_codebase_amd/build.py")
+PREFILL_SOURCES = ("flashinfer_competition_codebase_amd/csrc/gdn_prefill.hip",
+                   "flashinfer_competition_codebase_amd/csrc/gdn_decode_kernel.h",
+                   "flashinfer_competition_codebase_amd/build.py")
+
+
+def sources_sha(paths) -> str:
+    """SHA-256 (16 hex digits) over the given source files, in order: the
+    code a counter summary was measured on."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for rel in paths:
+        h.update(rel.encode())
+        h.update((ROOT / rel).read_bytes())
+    return h.hexdigest()[:16]
+
+
+def _traffic(kernel: str) -> tuple[int | None, str]:
+    """Measured HBM bytes per launch from the committed counter summary, if
+    it was measured on ``kernel`` (the instantiation the timed launches
+    run) built from the current sources; else None and the reason."""
     try:
-        return json.loads(TRAFFIC_SUMMARY.read_text()).get("traffic_bytes_per_launch")
-    except (OSError, ValueError):
-        return None
+        summary = json.loads(TRAFFIC_SUMMARY.read_text())
+    except (OSError, ValueError) as e:
+        return None, f"no counter summary: {e}"
+    measured = summary.get("kernel", "")
+    if not measured.startswith(kernel):
+        return None, f"counter summary measured {measured.split('(')[0]!r}, not {kernel!r}"
+    if summary.get("sources_sha") != sources_sha(DECODE_SOURCES):
+        return None, "counter summary measured other decode sources (sources_sha differs)"
+    return summary.get("traffic_bytes_per_launch"), str(TRAFFIC_SUMMARY.relative_to(ROOT))
+
+
+PMC_DECODE_COMMANDS = [
+    "cd /tmp && export TMPDIR=/tmp && timeout -s KILL 90 rocprofv3 --pmc FETCH_SIZE "
+    "--output-format csv -d $REPO/gpurun_out/pmc_fetch -o pmc -- python3 $REPO/bench.py --pmc-pass",
+    "cd /tmp && export TMPDIR=/tmp && timeout -s KILL 90 rocprofv3 --pmc WRITE_SIZE "
+    "--output-format csv -d $REPO/gpurun_out/pmc_write -o pmc -- python3 $REPO/bench.py --pmc-pass",
+    "python3 bench.py --summarize-pmc gpurun_out/pmc_fetch/pmc_counter_collection.csv "
+    "gpurun_out/pmc_write/pmc_counter_collection.csv",
+]
+PMC_COPY_BYTES = 256 * 1024 * 1024
+
+
+def summarize_pmc(fetch_csv: str, write_csv: str) -> dict:
+    """The committed counter summary of the B=256 qk16_v32 decode launches
+    of ``--pmc-pass`` (two rocprofv3 runs, FETCH_SIZE then WRITE_SIZE)."""
+    from flashinfer_competition_codebase_amd.rocprof import pmc_traffic
+
+    B, H, HV, l2 = CONFIGS["b256_qk16_v32_l2"]
+    ns, waves, policy, _ = _lib.launch_shape(B, HV)
+    res = pmc_traffic(fetch_csv, write_csv, decode_kernel_name(ns, waves, l2, policy),
+                      PMC_COPY_BYTES, copies=3, skip=2)
+    nbytes = step_bytes(B, H, HV)
+    return {"kernel": res.pop("kernel"), "sources_sha": sources_sha(DECODE_SOURCES),
+            "workload": ("B=256 qk16_v32 K=V=128 T=1, q/k L2-norm on, fp32 state updated in "
+                         "place, steps rotating over 2 layer states"),
+            "commands": PMC_DECODE_COMMANDS, **res,
+            "algorithmic_bytes_per_launch": nbytes,
+            "traffic_over_algorithmic": round(res["traffic_bytes_per_launch"] / nbytes, 4),
+            "note": ("Counter values are KiB per dispatch.  Each counter is scaled by what it "
+                     "reads for the three 256 MiB copies the run makes first (bytes = KiB * "
+                     "1024 / factor); the decode value is the median over the launches after "
+                     "the first two, whose states were still warm from setup.")}
+
+
+def roofline_line(kernel: str, nbytes: int, kavg: float, traced: dict | None,
+                  ref_stream: dict) -> dict:
+    """The ``roofline`` object: algorithmic bytes per launch over the average
+    launch duration of the timed region (HIP events around it), against the
+    8 TB/s HBM peak; ``traffic``: measured HBM bytes per launch from the
+    committed counter summary when it was measured on the same kernel
+    instantiation; ``trace``: the same shape's average and median kernel
+    duration in the kernel-trace leg (rocprofv3), steady regime."""
+    achieved = nbytes / (kavg * 1e-6) / 1e9
+    traffic, source = _traffic(kernel)
+    line = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+            "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
+            "traffic_source": source, "kernel": kernel, "algorithmic_bytes": nbytes,
+            "kernel_us_avg": round(kavg, 3),
+            "timer": "HIP events on the launch stream around the timed launches"}
+    if traced is not None and "steady_avg" in traced:
+        t_avg = traced["steady_avg"]
+        line["trace"] = {"avg_us": t_avg, "median_us": traced["steady"],
+                         "frac": round(nbytes / (t_avg * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+                         "launches": traced["n_steady"],
+                         "timer": "rocprofv3 --kernel-trace (the kernel-trace leg), steady"}
+    line["reference_stream"] = ref_stream
+    return line
 
 
 def b1_serving(device, layers: int = 48, reps: int = 20):
@@ -665,8 +779,7 @@ def prefill_cpu_baseline(seconds: float, gpu_tokens_per_s: float | None):
     repeated until about ``seconds`` of CPU work; and the 6-token workload."""
     from oracle.gdn_prefill_oracle import make_prefill_inputs, prefill_loop
 
-    threads = max(1, min(16, len(os.sched_getaffinity(0))))
-    torch.set_num_threads(threads)
+    torch.set_num_threads(host_threads()["affinity_cores"])
     t = make_prefill_inputs([256], 4, 8, seed=5)
     prefill_loop(**t)                              # warmup
     reps, elapsed = 0, 0.0
@@ -818,6 +931,8 @@ def main():
     ap.add_argument("--iters", type=int, default=100,
                     help="launches per per-config kernel-time measurement")
     ap.add_argument("--pmc-pass", action="store_true")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="write the decode counter summary from two --pmc-pass runs")
     ap.add_argument("--pmc-prefill", action="store_true",
                     help="short prefill run for rocprofv3 counter passes")
     ap.add_argument("--no-prefill", action="store_true")
@@ -836,6 +951,13 @@ def main():
         sys.exit(1)
 
     log = lambda *a: print(*a, file=sys.stderr, flush=True)  # noqa: E731
+    if args.summarize_pmc:
+        summary = summarize_pmc(*args.summarize_pmc)
+        TRAFFIC_SUMMARY.write_text(json.dumps(summary, indent=1) + "\n")
+        log(f"[bench] wrote {TRAFFIC_SUMMARY.relative_to(ROOT)}: "
+            f"{summary['traffic_bytes_per_launch']} B per launch "
+            f"({summary['traffic_over_algorithmic']}x algorithmic)")
+        return
     trace = None
     if not (args.trace_child or args.no_kernel_trace or args.no_per_config or args.pmc_pass
             or args.pmc_prefill or args.prefill_only):
@@ -873,15 +995,15 @@ def main():
         s_ = states[i % len(states)]
         gdn.kernel_hip(**{**t, "state": s_, "new_state": s_}, use_qk_l2norm=l2)
     torch.cuda.synchronize()
-    wall, durs = timed_steps(t, l2, args.steps, states)
+    wall, kavg = timed_steps(t, l2, args.steps, states)
     del states
     ms_per_step = wall * 1e3 / args.steps
     value = nbytes / (wall / args.steps) / 1e9
-    kavg = statistics.fmean(durs)
     achieved = nbytes / (kavg * 1e-6) / 1e9
+    kernel = decode_kernel_name(ns, waves, l2, policy)
     log(f"[bench] timed {args.steps} steps: {ms_per_step * 1e3:.2f} us/step wall, "
-        f"kernel avg {kavg:.2f} us (median {statistics.median(durs):.2f}), "
-        f"{achieved:.0f} GB/s = {achieved / PEAK_HBM_GBS:.1%} of peak")
+        f"{kavg:.2f} us/launch on the GPU (events around the region), "
+        f"{achieved:.0f} GB/s = {achieved / PEAK_HBM_GBS:.1%} of peak; kernel {kernel}")
 
     flush = torch.ones(1 << 28, device=device)     # 1 GiB > 32 MiB L2 + 256 MiB MALL
     per_config = {}
@@ -996,16 +1118,7 @@ def main():
                        "cache_policy": policy, "blocks": blocks},
         },
         "b1": b1_line,
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(achieved, 1),
-            "peak": PEAK_HBM_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": _traffic(),
-            "kernel_us_avg": round(kavg, 3),
-            "reference_stream": ref_stream,
-        },
+        "roofline": roofline_line(kernel, nbytes, kavg, traced.get(args.config), ref_stream),
         "cpu_baseline": cpu,
         "per_config": per_config,
         "prefill": prefill,

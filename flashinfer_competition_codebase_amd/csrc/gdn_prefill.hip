@@ -83,8 +83,17 @@ constexpr long long kScanWideHeads = 256;  // N * HV from which the scan takes 3
 constexpr int kFewSeqs = 64;
 constexpr long long kFewPrepGroups = 2048;
 
+// Chunk slots the workspace holds for L tokens in N sequences: every chunk
+// of a well-formed batch fits, sum(ceil(len_i / 64)) <= ceil(L / 64) + N, and
+// every chunk holds at least one token, so there are at most L of them.
+// For malformed cu_seqlens the kernels cap the slots they use at this count.
+long long max_slots(long long L, long long N) {
+  const long long by_seqs = (L + kChunk - 1) / kChunk + N;
+  return by_seqs < L ? by_seqs : L;
+}
+
 bool few_seqs(long long L, long long N, long long HV) {
-  return N > 1 && N <= kFewSeqs && ((L + kChunk - 1) / kChunk + N) * HV <= kFewPrepGroups;
+  return N > 1 && N <= kFewSeqs && max_slots(L, N) * HV <= kFewPrepGroups;
 }
 // Total tokens up to which the token-by-token kernel runs the prefill (so no
 // sequence is longer).  Measured (kernel trace, one sequence): the token loop
@@ -1055,8 +1064,6 @@ bool aligned(const void* ptr, uintptr_t a) {
 }
 
 size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
-
-long long max_slots(long long L, long long N) { return (L + kChunk - 1) / kChunk + N; }
 
 // Workspace: chunk offsets [N + 1] int32, slot table [max_slots] x 16 bytes,
 // the v-head slots [max_slots, HV, kSlotFloats] fp32, then the q/k-head

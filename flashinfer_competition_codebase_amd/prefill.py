@@ -177,9 +177,11 @@ def prefill_run(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, *,
     """Value-returning prefill with the reference's contract
     (``kernel_prefill_reference``, solution/triton/prefill_kernel.py:85-183):
     returns ``(output [L, HV, 128] bf16, new_state [N, HV, 128, 128] fp32)``;
-    ``state`` is not modified."""
+    ``state`` is not modified.  Tokens that no sequence covers (all of them
+    when N = 0, those past ``cu_seqlens[N]`` otherwise) get zero outputs, as
+    the reference's zero-initialised result (prefill_kernel.py:135-137)."""
     L, N, H, HV = check_prefill_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens)
-    output = torch.empty((L, HV, V_DIM), dtype=torch.bfloat16, device=q.device)
+    output = torch.zeros((L, HV, V_DIM), dtype=torch.bfloat16, device=q.device)
     new_state = torch.empty((N, HV, V_DIM, K_DIM), dtype=torch.float32, device=q.device)
     kernel_prefill_hip(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output,
                        new_state, use_qk_l2norm=use_qk_l2norm)

@@ -44,10 +44,11 @@ extern "C" {
 
 /*
  * Bytes of device workspace gdn_prefill needs for L total tokens, N
- * sequences, H q/k heads and HV v-heads (per-chunk intermediates: about
- * 81 KiB per 64 tokens per v-head and 32 KiB per 64 tokens per q/k head,
- * with 64-token slack per sequence; a 16-byte table entry per chunk and 4
- * bytes per sequence).  0 for invalid sizes.
+ * sequences, H q/k heads and HV v-heads: per-chunk intermediates (about
+ * 81 KiB per chunk per v-head and 32 KiB per chunk per q/k head, for
+ * min(ceil(L / 64) + N, L) chunks, the most a well-formed batch has), a
+ * 16-byte table entry per chunk and 4 bytes per sequence.  0 for invalid
+ * sizes.
  * The reference's FLA path allocates its intermediates per call inside
  * chunk_gated_delta_rule (solution/triton/fla_prefill_code.py:1726-1776);
  * here the caller provides them.
@@ -66,8 +67,8 @@ size_t gdn_prefill_workspace_bytes(int total_seq_len, int num_seqs, int H, int H
  * Python caller), and bad arguments return an error instead of launching.
  * q, k, v, output, state and new_state must be 16-byte aligned.
  * Launches one kernel when total_seq_len <= gdn_prefill_token_path_max_tokens()
- * (and num_seqs <= 65535), else the chunkwise kernels (chunk offsets when
- * num_seqs > 1, preparation, scan).
+ * (and num_seqs <= 65535), else the chunkwise kernels: the chunk-offsets
+ * scan (only when gdn_prefill_dispatches returns 3), preparation, scan.
  */
 int gdn_prefill(const void* q, const void* k, const void* v, const float* state,
                 const float* A_log, const void* a, const float* dt_bias, const void* b,
@@ -105,9 +106,9 @@ int gdn_prefill_token_path_max_tokens(void);
 /*
  * Kernel launches gdn_prefill makes for these sizes: 0 for no sequences, 1
  * on the token-by-token path, 2 (preparation, scan) for one sequence or for
- * at most 64 with at most 2048 preparation workgroups ((ceil(L / 64) + N) x
- * HV; the kernels then find the chunk slots from cu_seqlens themselves), 3
- * (the chunk-offsets scan first) otherwise.  No counterpart in the
+ * at most 64 with at most 2048 preparation workgroups (min(ceil(L / 64) + N,
+ * L) x HV; the kernels then find the chunk slots from cu_seqlens
+ * themselves), 3 (the chunk-offsets scan first) otherwise.  No counterpart in the
  * reference; for callers that attribute kernel traces to calls.
  */
 int gdn_prefill_dispatches(int total_seq_len, int num_seqs, int HV);

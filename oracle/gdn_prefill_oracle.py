@@ -106,67 +106,87 @@ def _np64(t):
     return t.detach().to(torch.float64).cpu().numpy()
 
 
+@torch.no_grad()
 def prefill_chunked_fp64(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, *,
                          chunk=64, use_qk_l2norm=False, eps=L2NORM_EPS, _mutation=None):
     """Float64 chunkwise restatement (the kernels' algebra, module docstring).
 
     Same arguments as ``prefill_loop``; chunks of ``chunk`` tokens start at
-    each sequence's first token.  Returns float64 arrays
-    ``(output [L, HV, V], new_state [N, HV, V, K])``.  ``_mutation`` plants a
-    named mistake (tests only: each must be caught by the pinning checks).
+    each sequence's first token.  Returns float64 NumPy arrays
+    ``(output [L, HV, V], new_state [N, HV, V, K])``.  Sequences of equal
+    length share their chunk grid, so they and all heads are evaluated
+    together as one batch (float64 CPU torch, batched BLAS products; v-head
+    ``h * r + j`` of q/k head h is index ``[h, j]`` of the [H, r] head axes).
+    T is not formed: W and U come from triangular solves with I + A.
+    ``_mutation`` plants a named mistake (tests only: each must be caught by
+    the pinning checks).
     """
-    qn, kn, vn = _np64(q), _np64(k), _np64(v)
+    f64 = dict(dtype=torch.float64)
+    qn, kn, vn = q.cpu().to(**f64), k.cpu().to(**f64), v.cpu().to(**f64)
     L, H, K = qn.shape
     HV, V = vn.shape[1], vn.shape[2]
     r = HV // H
     scale = resolve_scale(scale, K)
-    A_log_n, dt_n = _np64(A_log), _np64(dt_bias)
-    an, bn = _np64(a).reshape(L, HV), _np64(b).reshape(L, HV)
+    A_log_n, dt_n = A_log.cpu().to(**f64), dt_bias.cpu().to(**f64)
+    an, bn = a.cpu().to(**f64).reshape(L, HV), b.cpu().to(**f64).reshape(L, HV)
     x = an + dt_n[None, :]
-    sp = np.where(x > SOFTPLUS_THRESHOLD, x, np.log1p(np.exp(np.minimum(x, SOFTPLUS_THRESHOLD))))
-    logg = -np.exp(A_log_n)[None, :] * sp                         # [L, HV] log-space decay
-    beta = 1.0 / (1.0 + np.exp(-bn))
+    sp = torch.where(x > SOFTPLUS_THRESHOLD, x,
+                     torch.log1p(torch.exp(torch.clamp(x, max=SOFTPLUS_THRESHOLD))))
+    logg = (-torch.exp(A_log_n)[None, :] * sp).view(L, H, r)     # log-space decay
+    beta = (1.0 / (1.0 + torch.exp(-bn))).view(L, H, r)
+    vn = vn.view(L, H, r, V)
     if use_qk_l2norm:
-        qn = qn / np.sqrt((qn * qn).sum(-1, keepdims=True) + eps)
-        kn = kn / np.sqrt((kn * kn).sum(-1, keepdims=True) + eps)
+        qn = qn / torch.sqrt((qn * qn).sum(-1, keepdim=True) + eps)
+        kn = kn / torch.sqrt((kn * kn).sum(-1, keepdim=True) + eps)
     cu = [int(c) for c in cu_seqlens.tolist()]
     N = len(cu) - 1
-    out = np.zeros((L, HV, V))
-    S_out = np.zeros((N, HV, V, K))
-    S0_all = None if state is None else _np64(state)
+    out = torch.zeros(L, H, r, V, **f64)
+    S_out = torch.zeros(N, HV, V, K, **f64)
+    S0_all = None if state is None else state.cpu().to(**f64)
+    by_len = {}
     for s in range(N):
-        start, end = cu[s], cu[s + 1]
-        if end <= start:            # as prefill_loop: zero new_state
-            continue
-        for hv in range(HV):
-            h = hv // r
-            S = np.zeros((K, V)) if S0_all is None else S0_all[s, hv].T.copy()
-            for c0 in range(start, end, chunk):
-                c1 = min(c0 + chunk, end)
-                Kc, Qc, Vc = kn[c0:c1, h], qn[c0:c1, h], vn[c0:c1, hv]
-                bc = beta[c0:c1, hv]
-                gam = np.cumsum(logg[c0:c1, hv])
-                D = gam[:, None] - gam[None, :]
-                n = c1 - c0
-                lower = np.tril(np.ones((n, n)), -1).astype(bool)
-                causal = np.tril(np.ones((n, n))).astype(bool)
-                Gam = np.exp(np.where(causal, D, -np.inf))          # M, incl. diagonal
-                if _mutation == "M_without_diagonal":
-                    Gam = Gam * lower
-                A = np.where(lower, bc[:, None] * Gam * (Kc @ Kc.T), 0.0)
-                if _mutation == "A_transposed":
-                    A = A.T
-                T = np.linalg.inv(np.eye(n) + A)
-                wdecay = np.ones(n) if _mutation == "W_without_decay" else np.exp(gam)
-                W = T @ ((bc * wdecay)[:, None] * Kc)
-                U = T @ (bc[:, None] * Vc)
-                Delta = U - W @ S
-                out[c0:c1, hv] = scale * ((np.exp(gam)[:, None] * Qc) @ S
-                                          + ((Qc @ Kc.T) * Gam) @ Delta)
-                last = gam[-1] if _mutation != "state_decay_from_first" else gam[0]
-                S = np.exp(last) * S + (np.exp(gam[-1] - gam)[:, None] * Kc).T @ Delta
-            S_out[s, hv] = S.T
-    return out, S_out
+        if cu[s + 1] > cu[s]:       # empty sequences keep a zero new_state, as prefill_loop
+            by_len.setdefault(cu[s + 1] - cu[s], []).append(s)
+    neg_inf, zero = torch.tensor(-math.inf, **f64), torch.zeros((), **f64)
+    for n_tok, seqs in by_len.items():
+        starts = torch.tensor([cu[s] for s in seqs])
+        G = len(seqs)
+        # S: [G, H, r, K, V] (the k-last storage transposed)
+        S = (torch.zeros(G, H, r, K, V, **f64) if S0_all is None
+             else S0_all[seqs].view(G, H, r, V, K).transpose(3, 4).contiguous())
+        for c0 in range(0, n_tok, chunk):
+            c1 = min(c0 + chunk, n_tok)
+            n = c1 - c0
+            idx = starts[:, None] + torch.arange(c0, c1)[None, :]  # [G, n] token rows
+            Kc = kn[idx].permute(0, 2, 1, 3).unsqueeze(2)         # [G, H, 1, n, K]
+            Qc = qn[idx].permute(0, 2, 1, 3).unsqueeze(2)
+            Vc = vn[idx].permute(0, 2, 3, 1, 4)                   # [G, H, r, n, V]
+            bc = beta[idx].permute(0, 2, 3, 1)                    # [G, H, r, n]
+            gam = torch.cumsum(logg[idx], dim=1).permute(0, 2, 3, 1)
+            D = gam[..., :, None] - gam[..., None, :]
+            lower = torch.tril(torch.ones(n, n, dtype=torch.bool), -1)
+            causal = torch.tril(torch.ones(n, n, dtype=torch.bool))
+            Gam = torch.exp(torch.where(causal, D, neg_inf))      # M, incl. diagonal
+            if _mutation == "M_without_diagonal":
+                Gam = Gam * lower
+            A = torch.where(lower, bc[..., :, None] * Gam * (Kc @ Kc.transpose(-1, -2)), zero)
+            if _mutation == "A_transposed":
+                A = A.transpose(-1, -2)
+            IA = torch.eye(n, **f64) + A
+            wdecay = torch.ones_like(gam) if _mutation == "W_without_decay" else torch.exp(gam)
+            rhs = torch.cat([((bc * wdecay)[..., None] * Kc),
+                             (bc[..., None] * Vc)], dim=-1)       # [G, H, r, n, K + V]
+            WU = torch.linalg.solve_triangular(IA, rhs, upper=False)
+            W, U = WU[..., :K], WU[..., K:]
+            Delta = U - W @ S
+            o = scale * ((torch.exp(gam)[..., None] * Qc) @ S
+                         + ((Qc @ Kc.transpose(-1, -2)) * Gam) @ Delta)
+            out[idx] = o.permute(0, 3, 1, 2, 4)
+            last = gam[..., -1] if _mutation != "state_decay_from_first" else gam[..., 0]
+            S = (torch.exp(last)[..., None, None] * S
+                 + (torch.exp(gam[..., -1:] - gam)[..., None] * Kc).transpose(-1, -2) @ Delta)
+        S_out[seqs] = S.transpose(3, 4).reshape(G, HV, V, K)
+    return out.view(L, HV, V).numpy(), S_out.numpy()
 
 
 def make_prefill_inputs(seqlens, H, HV, *, seed, state_std=0.05, with_state=True, K=128,

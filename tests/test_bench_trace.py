@@ -74,3 +74,64 @@ def test_floor_omitted_when_counts_differ(tmp_path):
 def test_leg_skipped_under_rocprofv3(monkeypatch):
     monkeypatch.setenv("ROCPROF_OUTPUT_PATH", "/tmp")
     assert "skipped" in bench.kernel_trace_leg(10)
+
+
+def test_steady_average_beside_the_median(tmp_path):
+    p = tmp_path / "trace_kernel_trace.csv"
+    _write_trace(p, _spans())
+    x = bench.attribute_kernel_trace(p, MANIFEST)["shapes"]["x"]
+    assert x["steady_avg"] == 4.0            # (3000 + 5000) / 2 ns
+
+
+def _pmc_csv(path, counter, dispatches):
+    """dispatches: (kernel name, value) in order, one counter row each."""
+    fields = ["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"]
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=fields)
+        w.writeheader()
+        for i, (name, val) in enumerate(dispatches):
+            w.writerow({"Dispatch_Id": i + 1, "Kernel_Name": name, "Counter_Name": counter,
+                        "Counter_Value": val})
+
+
+def test_counter_summary_scales_by_the_calibration_copies(tmp_path):
+    """FETCH_SIZE reading half the copy's bytes doubles the kernel's fetch;
+    the first two launches are skipped; the summary names the kernel."""
+    from flashinfer_competition_codebase_amd.rocprof import pmc_traffic
+
+    copy = "__amd_rocclr_copyBuffer"
+    kern = "void gdn::gdn_decode_k128<2, 4, true, 1, false, false, false>(void const*)"
+    mib = 1024 * 1024
+    _pmc_csv(tmp_path / "f.csv", "FETCH_SIZE",
+             [(copy, 512.0)] * 3 + [(kern, 9999.0), (kern, 9999.0), (kern, 1000.0), (kern, 1002.0),
+                                    (kern, 1004.0), (copy, 7.0)])
+    _pmc_csv(tmp_path / "w.csv", "WRITE_SIZE",
+             [(copy, 1024.0)] * 3 + [(kern, 1.0), (kern, 1.0), (kern, 2048.0)] * 1
+             + [(kern, 2048.0), (kern, 2048.0)])
+    res = pmc_traffic(tmp_path / "f.csv", tmp_path / "w.csv",
+                      "gdn::gdn_decode_k128<2, 4, true, 1, false, false, false>", mib)
+    assert res["calibration"]["fetch_factor"] == 0.5
+    assert res["fetch_bytes_per_launch"] == 1002 * 1024 * 2
+    assert res["write_bytes_per_launch"] == 2048 * 1024
+    assert res["kernel"].startswith("gdn::gdn_decode_k128<2, 4, true, 1")
+
+
+def test_traffic_only_from_a_summary_of_the_timed_kernel(tmp_path, monkeypatch):
+    import json
+
+    kernel = bench.decode_kernel_name(2, 4, True, 1)
+    assert kernel == "gdn::gdn_decode_k128<2, 4, true, 1, false, false, false>"
+    path = tmp_path / "traffic.json"
+    monkeypatch.setattr(bench, "TRAFFIC_SUMMARY", path)
+    monkeypatch.setattr(bench, "ROOT", tmp_path)
+    for rel in bench.DECODE_SOURCES:
+        (tmp_path / rel).parent.mkdir(parents=True, exist_ok=True)
+        (tmp_path / rel).write_text(rel)
+    sha = bench.sources_sha(bench.DECODE_SOURCES)
+    path.write_text(json.dumps({"kernel": kernel + "(void const*)", "sources_sha": sha,
+                                "traffic_bytes_per_launch": 123}))
+    assert bench._traffic(kernel) == (123, "traffic.json")
+    assert bench._traffic(bench.decode_kernel_name(4, 4, True, 1))[0] is None
+    path.write_text(json.dumps({"kernel": kernel, "sources_sha": "0" * 16,
+                                "traffic_bytes_per_launch": 123}))
+    assert bench._traffic(kernel)[0] is None

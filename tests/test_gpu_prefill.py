@@ -92,6 +92,34 @@ def test_long_sequence_and_many_sequences(hip_device):
     _check(t, out, st, loop=False)
 
 
+@pytest.mark.parametrize("lens,H,HV,a_log_range", [
+    ([16384], 4, 8, None),            # the benchmark's prefill workloads, full size
+    ([1024] * 16, 4, 8, None),
+    ([8192], 16, 32, None),
+    ([512] * 64, 16, 32, None),
+    ([16384], 4, 8, (1e-3, 1e-2)),    # slow decay (g ~ 0.993-0.9993): a long memory
+])
+def test_bench_size_prefills_match_the_fp64_oracle(lens, H, HV, a_log_range, hip_device):
+    """The benchmark's prefill workloads at their full sizes against the
+    float64 chunked oracle, at the bars of every other prefill test: fp32
+    rounding carried through 128-256 chained chunk steps stays inside them.
+    With the benchmark's gates (A_log = log U[1, 16]) a token's decay is
+    e^-0.5 .. e^-11, so the state forgets within a few tokens; the last case
+    draws A_log = log U[1e-3, 1e-2], so the state carries ~1000 tokens of
+    history through 256 chunk steps and every step's rounding with it."""
+    _announce(f"prefill bench size lens={lens[0]}x{len(lens)} H={H} HV={HV} "
+              f"A_log range={a_log_range}")
+    t = make_prefill_inputs(lens, H, HV, seed=200 + len(lens) + H)
+    if a_log_range is not None:
+        lo, hi = a_log_range
+        g = torch.Generator().manual_seed(201)
+        t["A_log"] = torch.log(torch.rand(HV, generator=g) * (hi - lo) + lo)
+    out, st = gdn.prefill_run(**_dev(t, hip_device))
+    torch.cuda.synchronize()
+    do, ds = _check(t, out, st, loop=False)
+    _announce(f"  max |out - fp64| {do:.3e}, max |state - fp64| {ds:.3e}")
+
+
 def test_l2norm_and_no_state(hip_device):
     _announce("prefill l2norm, state=None, raw-scale q/k")
     t = make_prefill_inputs([40, 90], 4, 8, seed=12, with_state=False, unit_qk=False)
@@ -124,6 +152,25 @@ def test_empty_sequences_get_a_zero_state(hip_device):
     out0, st0 = gdn.prefill_run(**_dev(t0, hip_device))
     torch.cuda.synchronize()
     assert out0.shape == (0, 8, 128) and torch.count_nonzero(st0) == 0
+
+
+@pytest.mark.parametrize("cu,L", [([0], 7), ([0, 5], 10), ([0, 30, 70], 100)])
+def test_tokens_outside_every_sequence_get_zero_output(cu, L, hip_device):
+    """prefill_run's output for tokens that no sequence covers (no sequences
+    at all, or tokens past cu_seqlens[N]) is zero, as the reference's
+    zero-initialised result; the covered tokens match the oracle."""
+    _announce(f"prefill uncovered tokens cu={cu} L={L}")
+    N = len(cu) - 1
+    lens = [cu[i + 1] - cu[i] for i in range(N)] + [L - cu[-1]]
+    t = make_prefill_inputs(lens, 4, 8, seed=61)      # the last "sequence" is uncovered
+    t["cu_seqlens"] = torch.tensor(cu, dtype=torch.int32)
+    t["state"] = t["state"][:N].contiguous()
+    out, st = gdn.prefill_run(**_dev(t, hip_device))
+    torch.cuda.synchronize()
+    assert out.shape == (L, 8, 128) and st.shape == (N, 8, 128, 128)
+    assert torch.count_nonzero(out[cu[-1]:]) == 0
+    if N:
+        _check(t, out, st)
 
 
 def test_prefill_equals_chained_decode_steps(hip_device):

@@ -43,8 +43,8 @@ def test_workspace_size_formula():
     vslot = (2 * 64 * 128 + 64 * 64 + 3 * 64) * 4        # per v-head: W hi/lo, U, P hi/lo, scales
     qkslot = 2 * 128 * 64 * 2                             # per q/k head: K^T, Q copy (bf16)
     for L, N, H, HV in ((6, 1, 4, 8), (16384, 1, 4, 8), (1000, 37, 16, 32), (0, 3, 4, 8),
-                        (100, 2, 2, 2)):
-        chunks = (L + 63) // 64 + N
+                        (100, 2, 2, 2), (40, 65600, 1, 1), (3, 10, 4, 8)):
+        chunks = min((L + 63) // 64 + N, L)          # the most a well-formed batch has
         offs = ((N + 1) * 4 + 255) // 256 * 256
         table = (chunks * 16 + 255) // 256 * 256                         # per-chunk slot table
         assert lib.gdn_prefill_workspace_bytes(L, N, H, HV) == (
