@@ -16,7 +16,8 @@ entries that return their outputs instead of writing caller-allocated ones.
 """
 
 from .kernel import kernel_hip, kernel_hip_shaped, resolve_scale, run, run_dps
-from .prefill import kernel_prefill_hip, kernel_prefill_hip_timed, prefill_run
+from .prefill import (kernel_prefill_hip, kernel_prefill_hip_noalloc, kernel_prefill_hip_timed,
+                      prefill_run)
 
 ENTRY_POINTS = {
     "hip": kernel_hip,
@@ -28,4 +29,5 @@ ENTRY_POINTS = {
 NO_DPS = {"hip-run", "prefill-hip-run"}
 
 __all__ = ["run", "run_dps", "kernel_hip", "kernel_hip_shaped", "resolve_scale", "prefill_run",
-           "kernel_prefill_hip", "kernel_prefill_hip_timed", "ENTRY_POINTS", "NO_DPS"]
+           "kernel_prefill_hip", "kernel_prefill_hip_timed", "kernel_prefill_hip_noalloc",
+           "ENTRY_POINTS", "NO_DPS"]

@@ -55,11 +55,15 @@ PREFILL_SIGNATURES = {
         _I,
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P] + [_I] * 7 + [_P, _S, _P, _P],
     ),
+    "gdn_prefill_noalloc": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P] + [_I] * 7 + [_P],
+    ),
     "gdn_prefill_token_path_max_tokens": (_I, []),
     "gdn_prefill_dispatches": (_I, [_I, _I, _I]),
     "gdn_prefill_abi_version": (_I, []),
 }
-PREFILL_ABI_VERSION = 5
+PREFILL_ABI_VERSION = 6
 
 _lock = threading.Lock()
 _lib = None

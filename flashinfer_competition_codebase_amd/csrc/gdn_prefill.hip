@@ -56,6 +56,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "gdn_decode_kernel.h"
 #include "gdn_prefill.h"
 
@@ -1124,22 +1127,67 @@ static hipError_t small_prefill(const void* q, const void* k, const void* v, con
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Fixed workspace of gdn_prefill_noalloc: a file-scope device array, so each
+// GPU holds its own copy, at its own address, from the library's load on
+// that GPU until the process ends.  Host code never passes the array's name
+// to a kernel (on the host it is only a stand-in for the symbol): the
+// device address comes from hipGetSymbolAddress, once per device, with that
+// device current, and is cached per device.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchBytes = GDN_PREFILL_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::atomic<void*> g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mutex;
+
+// Device address of the current device's scratch array.
+static hipError_t current_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  void* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    ptr = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (ptr == nullptr) {
+      e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return e;
+      if (ptr == nullptr) return hipErrorInvalidSymbol;
+      g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
+  return hipSuccess;
+}
+
+// fixed_scratch: the workspace is the current device's scratch array
+// (workspace / workspace_size are ignored); sizes whose workspace exceeds it
+// return hipErrorOutOfMemory before anything is launched.
 static int prefill_impl(const void* q, const void* k, const void* v, const float* state,
                 const float* A_log, const void* a, const float* dt_bias, const void* b,
                 const int32_t* cu_seqlens, float scale, void* output, float* new_state,
                 int total_seq_len, int num_seqs, int H, int HV, int K, int V,
                 int use_qk_l2norm, void* workspace, size_t workspace_size,
-                void* hip_stream, void* const* events) {
+                void* hip_stream, void* const* events, bool fixed_scratch = false) {
   if (total_seq_len < 0 || num_seqs < 0 || H <= 0 || HV <= 0 || HV % H != 0)
     return hipErrorInvalidValue;
   if (K != kDim || V != kDim) return hipErrorInvalidValue;
   if (HV > 65535) return hipErrorInvalidValue;      // grid y
   if (num_seqs == 0) return hipSuccess;
-  if (!cu_seqlens || !A_log || !dt_bias || !new_state || !workspace)
+  if (!cu_seqlens || !A_log || !dt_bias || !new_state || (!workspace && !fixed_scratch))
     return hipErrorInvalidValue;
   if (total_seq_len > 0 && (!q || !k || !v || !a || !b || !output))
     return hipErrorInvalidValue;
-  if (workspace_size < workspace_bytes(total_seq_len, num_seqs, H, HV)) return hipErrorInvalidValue;
+  const size_t need = workspace_bytes(total_seq_len, num_seqs, H, HV);
+  if (fixed_scratch) {
+    if (need > kScratchBytes) return hipErrorOutOfMemory;
+    workspace = nullptr;                               // set once validation has passed
+  } else if (workspace_size < need) {
+    return hipErrorInvalidValue;
+  }
   if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(output, 16) ||
       !aligned(new_state, 16) || !aligned(state, 16) || !aligned(workspace, 256) ||
       !aligned(A_log, 4) || !aligned(dt_bias, 4) || !aligned(cu_seqlens, 4) ||
@@ -1158,6 +1206,10 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
   if (slots > 0x7fffffffLL || num_seqs > 0x7fffffff - 1) return hipErrorInvalidValue;
   if ((static_cast<long long>(num_seqs) * HV + 7) / 8 * 64 > 0x7fffffffLL)   // scan grid
     return hipErrorInvalidValue;
+  if (fixed_scratch) {
+    const hipError_t e = current_scratch(&workspace);
+    if (e != hipSuccess) return e;
+  }
 
   Params p;
   p.q = static_cast<const uint16_t*>(q);
@@ -1275,6 +1327,16 @@ int gdn_prefill_timed(const void* q, const void* k, const void* v, const float* 
                       workspace_size, hip_stream, events);
 }
 
+int gdn_prefill_noalloc(const void* q, const void* k, const void* v, const float* state,
+                        const float* A_log, const void* a, const float* dt_bias, const void* b,
+                        const int32_t* cu_seqlens, float scale, void* output, float* new_state,
+                        int total_seq_len, int num_seqs, int H, int HV, int K, int V,
+                        int use_qk_l2norm, void* hip_stream) {
+  return prefill_impl(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output,
+                      new_state, total_seq_len, num_seqs, H, HV, K, V, use_qk_l2norm, nullptr,
+                      0, hip_stream, nullptr, true);
+}
+
 int gdn_prefill_token_path_max_tokens(void) { return kSmallTokens; }
 
 int gdn_prefill_dispatches(int total_seq_len, int num_seqs, int HV) {
@@ -1283,6 +1345,6 @@ int gdn_prefill_dispatches(int total_seq_len, int num_seqs, int HV) {
   return num_seqs == 1 || few_seqs(total_seq_len, num_seqs, HV) ? 2 : 3;
 }
 
-int gdn_prefill_abi_version(void) { return 5; }
+int gdn_prefill_abi_version(void) { return 6; }
 
 }  // extern "C"

@@ -37,8 +37,12 @@ import torch
 from . import _lib
 from .kernel import K_DIM, V_DIM, _expect, _on_device, _overlap, _same_hip_device, resolve_scale
 
-__all__ = ["prefill_run", "kernel_prefill_hip", "kernel_prefill_hip_timed", "workspace_bytes",
-           "token_path_max_tokens", "prefill_dispatches"]
+__all__ = ["prefill_run", "kernel_prefill_hip", "kernel_prefill_hip_timed",
+           "kernel_prefill_hip_noalloc", "workspace_bytes", "token_path_max_tokens",
+           "prefill_dispatches", "NOALLOC_SCRATCH_BYTES"]
+
+# Size of the library's fixed per-GPU workspace (GDN_PREFILL_NOALLOC_SCRATCH_BYTES).
+NOALLOC_SCRATCH_BYTES = 128 << 20
 
 
 def workspace_bytes(total_seq_len: int, num_seqs: int, H: int, HV: int) -> int:
@@ -134,14 +138,46 @@ def kernel_prefill_hip_timed(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, s
             use_qk_l2norm, events)
 
 
+@torch.no_grad()
+def kernel_prefill_hip_noalloc(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output,
+                               new_state, *, use_qk_l2norm: bool = False):
+    """``kernel_prefill_hip`` that allocates nothing (``gdn_prefill_noalloc``):
+    the workspace is the library's fixed per-GPU array of
+    ``NOALLOC_SCRATCH_BYTES``, so the call can sit inside HIP graph capture
+    or a loop that must not allocate.  ``cu_seqlens`` must be int32 (no
+    conversion copy).  Raises ValueError when these sizes need a larger
+    workspace.  Calls that overlap on one GPU (different streams) race on
+    that workspace; calls on one stream are ordered.  No counterpart in the
+    reference."""
+    if cu_seqlens.dtype != torch.int32:
+        raise TypeError("kernel_prefill_hip_noalloc takes int32 cu_seqlens (no conversion copy)")
+    _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new_state,
+            use_qk_l2norm, None, noalloc=True)
+
+
 def _launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new_state,
-            use_qk_l2norm, events):
+            use_qk_l2norm, events, noalloc=False):
     if output is None or new_state is None:
         raise ValueError("kernel_prefill_hip needs preallocated output and new_state")
     L, N, H, HV = check_prefill_inputs(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens,
                                        output, new_state)
     scale = resolve_scale(scale, q.shape[-1])
     if N == 0:
+        return None
+    if noalloc:
+        need = workspace_bytes(L, N, H, HV)
+        if need > NOALLOC_SCRATCH_BYTES:
+            raise ValueError(f"prefill of L={L}, N={N}, H={H}, HV={HV} needs a {need}-byte "
+                             f"workspace; gdn_prefill_noalloc has {NOALLOC_SCRATCH_BYTES}")
+        idx = q.get_device()
+        with _on_device(idx):
+            code = _lib.get_prefill_lib().gdn_prefill_noalloc(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                None if state is None else state.data_ptr(), A_log.data_ptr(), a.data_ptr(),
+                dt_bias.data_ptr(), b.data_ptr(), cu_seqlens.data_ptr(), scale,
+                output.data_ptr(), new_state.data_ptr(), L, N, H, HV, K_DIM, V_DIM,
+                int(bool(use_qk_l2norm)), _lib.current_stream(idx))
+        _lib.check(code, "gdn_prefill_noalloc")
         return None
     if cu_seqlens.dtype != torch.int32:
         cu_seqlens = cu_seqlens.to(torch.int32)

@@ -94,6 +94,31 @@ int gdn_prefill_timed(const void* q, const void* k, const void* v, const float* 
                       int use_qk_l2norm, void* workspace, size_t workspace_size,
                       void* hip_stream, void* const* events);
 
+/* Bytes of the fixed per-GPU workspace gdn_prefill_noalloc uses: 128 MiB. */
+#define GDN_PREFILL_NOALLOC_SCRATCH_BYTES ((size_t)128 << 20)
+
+/*
+ * gdn_prefill without a caller-provided workspace and without allocating:
+ * the workspace is a fixed device array of GDN_PREFILL_NOALLOC_SCRATCH_BYTES
+ * in this library, one per GPU, held from the library's first use on that
+ * GPU until the process ends.  No counterpart in the reference (whose FLA
+ * path allocates its intermediates per call, fla_prefill_code.py:1726-1776):
+ * for callers that cannot allocate device memory -- code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation.
+ * Sizes whose workspace (gdn_prefill_workspace_bytes) exceeds the array
+ * return hipErrorOutOfMemory (2) before anything is launched; other
+ * arguments and results as gdn_prefill, on the current device's array.
+ * Every call on one GPU shares that array, and nothing in it needs to start
+ * at zero: calls on one stream run one after another, but calls that overlap
+ * on one GPU (different streams, or different host threads without
+ * ordering) race on it and give wrong results.
+ */
+int gdn_prefill_noalloc(const void* q, const void* k, const void* v, const float* state,
+                        const float* A_log, const void* a, const float* dt_bias, const void* b,
+                        const int32_t* cu_seqlens, float scale, void* output, float* new_state,
+                        int total_seq_len, int num_seqs, int H, int HV, int K, int V,
+                        int use_qk_l2norm, void* hip_stream);
+
 /*
  * Total tokens up to which gdn_prefill runs the token-by-token path: one
  * launch in which each workgroup applies the recurrence to its sequence's
@@ -113,9 +138,9 @@ int gdn_prefill_token_path_max_tokens(void);
  */
 int gdn_prefill_dispatches(int total_seq_len, int num_seqs, int HV);
 
-/* ABI version of this header: 5 (4 had no gdn_prefill_dispatches; 3 had no
- * gdn_prefill_token_path_max_tokens; 2 had no gdn_prefill_timed; 1 had no H
- * in gdn_prefill_workspace_bytes). */
+/* ABI version of this header: 6 (5 had no gdn_prefill_noalloc; 4 had no
+ * gdn_prefill_dispatches; 3 had no gdn_prefill_token_path_max_tokens; 2 had
+ * no gdn_prefill_timed; 1 had no H in gdn_prefill_workspace_bytes). */
 int gdn_prefill_abi_version(void);
 
 #ifdef __cplusplus

@@ -29,8 +29,8 @@ def _header_functions():
 def test_header_and_library_agree():
     funcs = _header_functions()
     assert set(funcs) == {"gdn_prefill_workspace_bytes", "gdn_prefill", "gdn_prefill_timed",
-                          "gdn_prefill_token_path_max_tokens", "gdn_prefill_dispatches",
-                          "gdn_prefill_abi_version"}
+                          "gdn_prefill_noalloc", "gdn_prefill_token_path_max_tokens",
+                          "gdn_prefill_dispatches", "gdn_prefill_abi_version"}
     lib = _lib.get_prefill_lib()
     for name, nparams in funcs.items():
         assert hasattr(lib, name)
@@ -75,6 +75,17 @@ def test_c_side_validation_rejects_before_launching():
     ev = (ctypes.c_void_p * 4)(0x10, 0x20, None, 0x40)
     assert lib.gdn_prefill_timed(*n, None, f, None, None, 6, 1, 4, 8, 128, 128, 0, None, 0, None,
                                  ev) == 1
+    # the no-allocation entry: the same validation, and sizes whose workspace
+    # exceeds its fixed array rejected with hipErrorOutOfMemory before any HIP call
+    assert lib.gdn_prefill_noalloc(*n, None, f, None, None, 6, 0, 4, 8, 128, 128, 0, None) == 0
+    assert lib.gdn_prefill_noalloc(*n, None, f, None, None, 6, 1, 4, 8, 64, 128, 0, None) == 1
+    assert lib.gdn_prefill_noalloc(*n, None, f, None, None, 6, 1, 4, 8, 128, 128, 0, None) == 1
+    if not torch.cuda.is_available():         # made-up pointers only where no device exists
+        fake = [0x10000 * (i + 1) for i in range(8)]
+        big = 1 << 20
+        assert lib.gdn_prefill_workspace_bytes(big, 1, 16, 32) > (128 << 20)
+        assert lib.gdn_prefill_noalloc(*fake, 0x90000, f, 0xa0000, 0xb0000, big, 1, 16, 32, 128,
+                                       128, 0, None) == 2
 
 
 def _cpu_inputs():
