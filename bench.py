@@ -539,16 +539,31 @@ def roofline_line(kernel: str, nbytes: int, kavg: float, traced: dict | None,
 
 def b1_serving(device, layers: int = 48, reps: int = 20):
     """Host-inclusive time per decode step at B=1 qk16_v32 (L2-norm) when a
-    model issues one step per GDN layer: eager Python calls of ``kernel_hip``
-    back to back, and the same ``layers`` steps captured once in a HIP graph
-    and replayed.  Wall clock per step, median over ``reps`` passes."""
+    model issues one step per GDN layer (``layers`` states, inputs shared),
+    wall clock from a synchronised GPU to the end of the last step, median
+    over ``reps`` passes, divided by ``layers``:
+
+    * ``eager``: a ``kernel_hip`` call per step (validation every call);
+    * ``plan``: a bound ``DecodePlan.run()`` per step;
+    * ``layers_run``: ``DecodeLayers.run()``, all steps from one native call;
+    * ``graph``: ``DecodeLayers.replay()``, one HIP graph of all steps;
+    * ``torch_graph``: the ``kernel_hip`` calls captured by torch.cuda.graph.
+    """
+    from flashinfer_competition_codebase_amd.serving import DecodeLayers
+
     t = make_device_inputs(1, 16, 32, device, seed=11)
     states = [t["state"]] + [t["state"].clone() for _ in range(layers - 1)]
     views = [{**t, "state": s_, "new_state": s_} for s_ in states]
+    bound = DecodeLayers(views, use_qk_l2norm=True)
+    bound.capture()
 
     def eager():
         for v_ in views:
             gdn.kernel_hip(**v_, use_qk_l2norm=True)
+
+    def plans():
+        for p_ in bound.plans:
+            p_.run()
 
     eager()
     torch.cuda.synchronize()
@@ -557,7 +572,9 @@ def b1_serving(device, layers: int = 48, reps: int = 20):
         eager()
     torch.cuda.synchronize()
     res = {}
-    for name, fn in (("eager", eager), ("graph", graph.replay)):
+    for name, fn in (("eager", eager), ("plan", plans), ("layers_run", bound.run),
+                     ("graph", bound.replay), ("torch_graph", graph.replay)):
+        fn()
         per = []
         for _ in range(reps):
             torch.cuda.synchronize()
@@ -566,7 +583,19 @@ def b1_serving(device, layers: int = 48, reps: int = 20):
             torch.cuda.synchronize()
             per.append((time.perf_counter() - t0) * 1e6 / layers)
         res[f"{name}_us_per_step"] = round(statistics.median(per), 2)
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(reps)]
+    for a_, b_ in ev:
+        a_.record(stream)
+        bound.replay()
+        b_.record(stream)
+    torch.cuda.synchronize()
+    res["graph_gpu_us_per_step"] = round(
+        statistics.median(a_.elapsed_time(b_) * 1e3 for a_, b_ in ev) / layers, 3)
     res["layers"] = layers
+    bound.close()
+    del graph
     return res
 
 
@@ -896,10 +925,11 @@ def prefill_bench(device, iters: int = 20):
     return out
 
 
-def pmc_pass(device):
-    """Short run for rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE): three
-    plain 256 MiB copies (calibrate the counters against known bytes), then
-    six B=256 qk16_v32 decode steps rotating over two layer states, as in the
+def pmc_pass(device, shape: str = "b256_qk16_v32_l2"):
+    """Short run for rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE, or
+    others): three plain 256 MiB copies (calibrate the byte counters against
+    known bytes), then six decode steps of one per-config shape (by default
+    the B=256 qk16_v32 headline) rotating over two layer states, as in the
     timed region."""
     n = 256 * 1024 * 1024 // 4
     src = torch.randn(n, device=device)
@@ -908,14 +938,21 @@ def pmc_pass(device):
         dst.copy_(src)
     torch.cuda.synchronize()
     del src, dst
-    t = make_device_inputs(256, 16, 32, device, seed=1003)
-    states = layer_states(t["state"])
+    shapes = {sh[0]: sh[1:] for sh in per_config_shapes()}
+    B, H, HV, l2, T, sd = shapes[shape]
+    t = make_device_inputs(B, H, HV, device, seed=1003, T=T, state_dtype=sd)
+    states = layer_states(t["state"])[:2]
     for i in range(6):
         s_ = states[i % len(states)]
-        gdn.kernel_hip(**{**t, "state": s_, "new_state": s_}, use_qk_l2norm=True)
+        gdn.kernel_hip(**{**t, "state": s_, "new_state": s_}, use_qk_l2norm=l2)
     torch.cuda.synchronize()
-    print(json.dumps({"pmc_pass": "done", "copy_bytes": n * 4,
-                      "decode_bytes": step_bytes(256, 16, 32)}), flush=True)
+    ns, waves, policy, _ = _lib.launch_shape(B, HV, T, sd == torch.bfloat16)
+    print(json.dumps({"pmc_pass": shape, "copy_bytes": n * 4,
+                      "kernel": decode_kernel_name(ns, waves, l2, policy, sd == torch.bfloat16,
+                                                   T > 1),
+                      "decode_bytes": step_bytes(B, H, HV, T=T,
+                                                 state_elem=t["state"].element_size())}),
+          flush=True)
 
 
 def main():
@@ -931,6 +968,8 @@ def main():
     ap.add_argument("--iters", type=int, default=100,
                     help="launches per per-config kernel-time measurement")
     ap.add_argument("--pmc-pass", action="store_true")
+    ap.add_argument("--pmc-shape", default="b256_qk16_v32_l2",
+                    help="per-config shape the --pmc-pass run launches")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="write the decode counter summary from two --pmc-pass runs")
     ap.add_argument("--pmc-prefill", action="store_true",
@@ -938,6 +977,8 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--prefill-only", action="store_true",
                     help="time the prefill workloads only and print them as JSON")
+    ap.add_argument("--serving-only", action="store_true",
+                    help="time the B=1 serving paths only and print them as JSON")
     ap.add_argument("--no-kernel-trace", action="store_true",
                     help="skip the rocprofv3 kernel-trace leg")
     ap.add_argument("--trace-child", metavar="MANIFEST",
@@ -960,7 +1001,7 @@ def main():
         return
     trace = None
     if not (args.trace_child or args.no_kernel_trace or args.no_per_config or args.pmc_pass
-            or args.pmc_prefill or args.prefill_only):
+            or args.pmc_prefill or args.prefill_only or args.serving_only):
         # before this process touches the GPU: the traced run is its own program
         log("[bench] kernel-trace leg: every per-config shape under rocprofv3")
         trace = kernel_trace_leg(args.iters)
@@ -973,10 +1014,14 @@ def main():
         trace_child(device, args.trace_child, args.iters)
         return
     if args.pmc_pass:
-        pmc_pass(device)
+        pmc_pass(device, args.pmc_shape)
         return
     if args.pmc_prefill:
         pmc_prefill(device)
+        return
+    if args.serving_only:
+        print(json.dumps({"b1_serving": b1_serving(device),
+                          "b1_back_to_back": b1_back_to_back(device)}), flush=True)
         return
     if args.prefill_only:
         pf = prefill_bench(device)
@@ -1053,8 +1098,9 @@ def main():
         prefill_rl = prefill_roofline(prefill)
 
     serving = b1_serving(device)
-    log(f"[bench] B=1 serving, {serving['layers']} layer steps: eager "
-        f"{serving['eager_us_per_step']} us/step, HIP graph {serving['graph_us_per_step']} us/step")
+    log(f"[bench] B=1 serving, {serving['layers']} layer steps (us/step, host wall): "
+        + ", ".join(f"{k[:-12]} {v}" for k, v in serving.items() if k.endswith("_us_per_step"))
+        + f"; graph on the GPU {serving['graph_gpu_us_per_step']} us/step")
     b2b = b1_back_to_back(device)
     log(f"[bench] B=1 back to back over {b2b['steps_per_replay']} layer states "
         f"({b2b['state_bytes_rotated'] >> 20} MiB): {b2b['us_per_step']} us/step")

@@ -16,6 +16,7 @@ entries that return their outputs instead of writing caller-allocated ones.
 """
 
 from .kernel import kernel_hip, kernel_hip_shaped, resolve_scale, run, run_dps
+from .serving import DecodeLayers, DecodePlan
 from .prefill import (kernel_prefill_hip, kernel_prefill_hip_noalloc, kernel_prefill_hip_timed,
                       prefill_run)
 
@@ -30,4 +31,4 @@ NO_DPS = {"hip-run", "prefill-hip-run"}
 
 __all__ = ["run", "run_dps", "kernel_hip", "kernel_hip_shaped", "resolve_scale", "prefill_run",
            "kernel_prefill_hip", "kernel_prefill_hip_timed", "kernel_prefill_hip_noalloc",
-           "ENTRY_POINTS", "NO_DPS"]
+           "DecodePlan", "DecodeLayers", "ENTRY_POINTS", "NO_DPS"]

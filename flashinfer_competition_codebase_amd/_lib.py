@@ -38,11 +38,20 @@ SIGNATURES = {
         [_I, _I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I),
          ctypes.POINTER(ctypes.c_longlong)],
     ),
+    "gdn_decode_plan_create": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P] + [_I] * 8 + [ctypes.POINTER(_P)],
+    ),
+    "gdn_decode_plan_run": (_I, [ctypes.POINTER(_P), _I, _P]),
+    "gdn_decode_plan_destroy": (None, [_P]),
+    "gdn_decode_graph_create": (_I, [ctypes.POINTER(_P), _I, ctypes.POINTER(_P)]),
+    "gdn_decode_graph_launch": (_I, [_P, _P]),
+    "gdn_decode_graph_destroy": (None, [_P]),
     "gdn_decode_error_string": (ctypes.c_char_p, [_I]),
     "gdn_decode_abi_version": (_I, []),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _S = ctypes.c_size_t
 PREFILL_SIGNATURES = {

@@ -42,6 +42,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <new>
+
 #include "gdn_decode.h"
 #include "gdn_decode_kernel.h"
 
@@ -202,73 +204,124 @@ void choose_shape(long long heads, bool bf16, int T, int* ns, int* waves, int* p
   }
 }
 
-int steps_impl(const void* q, const void* k, const void* v, const void* state,
-               const float* A_log, const void* a, const float* dt_bias, const void* b,
-               float scale, void* output, void* new_state, int B, int T, int H, int HV,
-               int K, int V, int state_bf16, int use_qk_l2norm, int ns, int waves,
-               int policy, void* start_event, void* stop_event, void* hip_stream) {
-  if (B < 0 || T < 1 || H <= 0 || HV <= 0 || HV % H != 0) return hipErrorInvalidValue;
-  if (H > 65535) return hipErrorInvalidValue;  // grid y
-  if (HV / H > 65535) return hipErrorInvalidValue;  // packed with H into 32 bits
-  if (K != kDim || V != kDim) return hipErrorInvalidValue;
-  if (state_bf16 != 0 && state_bf16 != 1) return hipErrorInvalidValue;
-  const Variant var{use_qk_l2norm != 0, state_bf16 != 0, T > 1};
-  if (!shape_supported(var, ns, waves, policy)) return hipErrorInvalidValue;
-  if (B == 0) return hipSuccess;
-  if (!q || !k || !v || !state || !A_log || !a || !dt_bias || !b || !output ||
-      !new_state)
+// Every argument of one decode call, with the launch shape resolved.
+struct StepArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* state;        // null: start from zeros
+  const float* A_log;
+  const void* a;
+  const float* dt_bias;
+  const void* b;
+  float scale;
+  void* output;
+  void* new_state;
+  int B, T, H, HV, K, V;
+  int state_bf16;
+  int use_qk_l2norm;
+  int ns, waves, policy;
+};
+
+// Kernel variant of a call: the multi-token loop for T > 1, and also for a
+// null state (it starts from zeros; the single-token kernel always reads one).
+Variant variant_of(const StepArgs& s) {
+  return Variant{s.use_qk_l2norm != 0, s.state_bf16 != 0, s.T > 1 || s.state == nullptr};
+}
+
+// Host-side validation of a call (no HIP call): sizes, launch shape, null
+// and misaligned pointers, partial overlap of state and new_state.
+hipError_t validate(const StepArgs& s) {
+  if (s.B < 0 || s.T < 1 || s.H <= 0 || s.HV <= 0 || s.HV % s.H != 0) return hipErrorInvalidValue;
+  if (s.H > 65535) return hipErrorInvalidValue;  // grid y
+  if (s.HV / s.H > 65535) return hipErrorInvalidValue;  // packed with H into 32 bits
+  if (s.K != kDim || s.V != kDim) return hipErrorInvalidValue;
+  if (s.state_bf16 != 0 && s.state_bf16 != 1) return hipErrorInvalidValue;
+  const Variant var = variant_of(s);
+  if (!shape_supported(var, s.ns, s.waves, s.policy)) return hipErrorInvalidValue;
+  if (s.B == 0) return hipSuccess;
+  if (!s.q || !s.k || !s.v || !s.A_log || !s.a || !s.dt_bias || !s.b || !s.output ||
+      !s.new_state)
     return hipErrorInvalidValue;
   // 16-byte state row slices, 8- or 16-byte q/k slices, up to 16-byte v/out runs.
-  if (!aligned(state, 16) || !aligned(new_state, 16) || !aligned(q, 16) ||
-      !aligned(k, 16) || !aligned(v, 16) || !aligned(output, 16) ||
-      !aligned(A_log, 4) || !aligned(dt_bias, 4) || !aligned(a, 2) ||
-      !aligned(b, 2))
+  if (!aligned(s.state, 16) || !aligned(s.new_state, 16) || !aligned(s.q, 16) ||
+      !aligned(s.k, 16) || !aligned(s.v, 16) || !aligned(s.output, 16) ||
+      !aligned(s.A_log, 4) || !aligned(s.dt_bias, 4) || !aligned(s.a, 2) || !aligned(s.b, 2))
     return hipErrorInvalidValue;
-  const size_t elem = state_bf16 ? 2 : 4;
-  const size_t state_bytes = static_cast<size_t>(B) * HV * kDim * kDim * elem;
-  if (new_state != state) {
-    const uintptr_t s0 = reinterpret_cast<uintptr_t>(state);
-    const uintptr_t d0 = reinterpret_cast<uintptr_t>(new_state);
+  const size_t elem = s.state_bf16 ? 2 : 4;
+  const size_t state_bytes = static_cast<size_t>(s.B) * s.HV * kDim * kDim * elem;
+  if (s.state != nullptr && s.new_state != s.state) {
+    const uintptr_t s0 = reinterpret_cast<uintptr_t>(s.state);
+    const uintptr_t d0 = reinterpret_cast<uintptr_t>(s.new_state);
     if (s0 < d0 + state_bytes && d0 < s0 + state_bytes)
       return hipErrorInvalidValue;  // partial overlap: only exact aliasing
   }
+  const long long tiles = kDim / (kLaneGroups * s.ns * s.waves);
+  const long long max_blocks = (1LL << 31) / (64LL * s.waves);
+  if (max_blocks / (tiles * s.HV) < 1) return hipErrorInvalidValue;
+  return hipSuccess;
+}
 
-  const long long tiles = kDim / (kLaneGroups * ns * waves);
-  const long long threads_per_block = 64LL * waves;
-  // Keep each launch's work-item count well inside 32 bits.
-  const long long max_blocks = (1LL << 31) / threads_per_block;
-  long long batches_per_launch = max_blocks / (tiles * HV);
+// The launches of a validated call on `stream`: one per group of at most
+// 65535 sequences (grid z) whose work-items fit in 32 bits.
+hipError_t launch(const StepArgs& s, hipStream_t stream, hipEvent_t start_event,
+                  hipEvent_t stop_event) {
+  if (s.B == 0) return hipSuccess;
+  const Variant var = variant_of(s);
+  const size_t elem = s.state_bf16 ? 2 : 4;
+  const long long tiles = kDim / (kLaneGroups * s.ns * s.waves);
+  const long long max_blocks = (1LL << 31) / (64LL * s.waves);
+  long long batches_per_launch = max_blocks / (tiles * s.HV);
   if (batches_per_launch > 65535) batches_per_launch = 65535;  // grid z limit
-  if (batches_per_launch < 1) return hipErrorInvalidValue;
 
   Params p;
-  p.A_log = A_log;
-  p.dt_bias = dt_bias;
-  p.scale = scale;
-  p.T = T;
-  p.H = H;
-  p.HV = HV;
-  p.ratio = HV / H;
-  for (long long b0 = 0; b0 < B; b0 += batches_per_launch) {
-    const long long nb = (B - b0) < batches_per_launch ? (B - b0) : batches_per_launch;
+  p.A_log = s.A_log;
+  p.dt_bias = s.dt_bias;
+  p.scale = s.scale;
+  p.T = s.T;
+  p.H = s.H;
+  p.HV = s.HV;
+  p.ratio = s.HV / s.H;
+  const long long T = s.T, H = s.H, HV = s.HV;
+  for (long long b0 = 0; b0 < s.B; b0 += batches_per_launch) {
+    const long long nb = (s.B - b0) < batches_per_launch ? (s.B - b0) : batches_per_launch;
     const long long bt0 = b0 * T;
-    p.q = static_cast<const uint16_t*>(q) + bt0 * H * kDim;
-    p.k = static_cast<const uint16_t*>(k) + bt0 * H * kDim;
-    p.v = static_cast<const uint16_t*>(v) + bt0 * HV * kDim;
-    p.state = static_cast<const char*>(state) + b0 * HV * kDim * kDim * elem;
-    p.a = static_cast<const uint16_t*>(a) + bt0 * HV;
-    p.b = static_cast<const uint16_t*>(b) + bt0 * HV;
-    p.out = static_cast<uint16_t*>(output) + bt0 * HV * kDim;
-    p.new_state = static_cast<char*>(new_state) + b0 * HV * kDim * kDim * elem;
+    p.q = static_cast<const uint16_t*>(s.q) + bt0 * H * kDim;
+    p.k = static_cast<const uint16_t*>(s.k) + bt0 * H * kDim;
+    p.v = static_cast<const uint16_t*>(s.v) + bt0 * HV * kDim;
+    p.state = s.state == nullptr
+                  ? nullptr
+                  : static_cast<const char*>(s.state) + b0 * HV * kDim * kDim * elem;
+    p.a = static_cast<const uint16_t*>(s.a) + bt0 * HV;
+    p.b = static_cast<const uint16_t*>(s.b) + bt0 * HV;
+    p.out = static_cast<uint16_t*>(s.output) + bt0 * HV * kDim;
+    p.new_state = static_cast<char*>(s.new_state) + b0 * HV * kDim * kDim * elem;
     // Start stamp on the first launch, stop stamp on the last.
     Launch l;
-    l.stream = static_cast<hipStream_t>(hip_stream);
-    l.start = b0 == 0 ? static_cast<hipEvent_t>(start_event) : nullptr;
-    l.stop = b0 + nb == B ? static_cast<hipEvent_t>(stop_event) : nullptr;
-    const hipError_t e = dispatch(var, ns, waves, policy, p, static_cast<unsigned>(nb), l);
+    l.stream = stream;
+    l.start = b0 == 0 ? start_event : nullptr;
+    l.stop = b0 + nb == s.B ? stop_event : nullptr;
+    const hipError_t e = dispatch(var, s.ns, s.waves, s.policy, p, static_cast<unsigned>(nb), l);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
+}
+
+StepArgs make_args(const void* q, const void* k, const void* v, const void* state,
+                   const float* A_log, const void* a, const float* dt_bias, const void* b,
+                   float scale, void* output, void* new_state, int B, int T, int H, int HV,
+                   int K, int V, int state_bf16, int use_qk_l2norm, int ns, int waves,
+                   int policy) {
+  return StepArgs{q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, B, T, H,
+                  HV, K, V, state_bf16, use_qk_l2norm, ns, waves, policy};
+}
+
+// The library's launch shape for a call (unchanged shape fields when B or
+// HV is invalid: validation rejects the call).
+void choose_args_shape(StepArgs& s) {
+  if (s.B < 0 || s.HV <= 0) return;
+  choose_shape(static_cast<long long>(s.B) * s.HV, s.state_bf16 != 0, s.T, &s.ns, &s.waves,
+               &s.policy);
 }
 
 }  // namespace gdn
@@ -291,12 +344,12 @@ int gdn_decode_steps(const void* q, const void* k, const void* v, const void* st
                      const void* b, float scale, void* output, void* new_state,
                      int B, int T, int H, int HV, int K, int V, int state_bf16,
                      int use_qk_l2norm, void* hip_stream) {
-  if (B < 0 || HV <= 0) return hipErrorInvalidValue;
-  int ns = 0, waves = 0, policy = 0;
-  choose_shape(static_cast<long long>(B) * HV, state_bf16 != 0, T, &ns, &waves, &policy);
-  return steps_impl(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, B, T,
-                    H, HV, K, V, state_bf16, use_qk_l2norm, ns, waves, policy, nullptr,
-                    nullptr, hip_stream);
+  StepArgs s = make_args(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, B, T,
+                         H, HV, K, V, state_bf16, use_qk_l2norm, 0, 0, 0);
+  choose_args_shape(s);
+  hipError_t e = validate(s);
+  if (e != hipSuccess) return e;
+  return launch(s, static_cast<hipStream_t>(hip_stream), nullptr, nullptr);
 }
 
 int gdn_decode_step_shaped(const void* q, const void* k, const void* v,
@@ -307,9 +360,13 @@ int gdn_decode_step_shaped(const void* q, const void* k, const void* v,
                            int use_qk_l2norm, int rows_per_lane_group,
                            int waves_per_block, int cache_policy,
                            void* start_event, void* stop_event, void* hip_stream) {
-  return steps_impl(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, B, T,
-                    H, HV, K, V, state_bf16, use_qk_l2norm, rows_per_lane_group,
-                    waves_per_block, cache_policy, start_event, stop_event, hip_stream);
+  const StepArgs s = make_args(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
+                               B, T, H, HV, K, V, state_bf16, use_qk_l2norm,
+                               rows_per_lane_group, waves_per_block, cache_policy);
+  hipError_t e = validate(s);
+  if (e != hipSuccess) return e;
+  return launch(s, static_cast<hipStream_t>(hip_stream), static_cast<hipEvent_t>(start_event),
+                static_cast<hipEvent_t>(stop_event));
 }
 
 int gdn_decode_launch_shape(int B, int T, int HV, int state_bf16,
@@ -327,10 +384,100 @@ int gdn_decode_launch_shape(int B, int T, int HV, int state_bf16,
   return hipSuccess;
 }
 
+// ---------------------------------------------------------------------------
+// Bound steps and their HIP graph (B = 1 serving: launch overhead).
+// ---------------------------------------------------------------------------
+
+struct gdn_decode_plan {
+  gdn::StepArgs args;
+};
+
+struct gdn_decode_graph {
+  hipGraphExec_t exec;
+};
+
+int gdn_decode_plan_create(const void* q, const void* k, const void* v, const void* state,
+                           const float* A_log, const void* a, const float* dt_bias,
+                           const void* b, float scale, void* output, void* new_state, int B,
+                           int T, int H, int HV, int K, int V, int state_bf16,
+                           int use_qk_l2norm, gdn_decode_plan** plan) {
+  if (plan == nullptr) return hipErrorInvalidValue;
+  *plan = nullptr;
+  StepArgs s = make_args(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, B, T,
+                         H, HV, K, V, state_bf16, use_qk_l2norm, 0, 0, 0);
+  choose_args_shape(s);
+  const hipError_t e = validate(s);
+  if (e != hipSuccess) return e;
+  gdn_decode_plan* p = new (std::nothrow) gdn_decode_plan{s};
+  if (p == nullptr) return hipErrorOutOfMemory;
+  *plan = p;
+  return hipSuccess;
+}
+
+int gdn_decode_plan_run(const gdn_decode_plan* const* plans, int n, void* hip_stream) {
+  if (n < 0 || (n > 0 && plans == nullptr)) return hipErrorInvalidValue;
+  for (int i = 0; i < n; ++i)
+    if (plans[i] == nullptr) return hipErrorInvalidValue;
+  const hipStream_t stream = static_cast<hipStream_t>(hip_stream);
+  for (int i = 0; i < n; ++i) {
+    const hipError_t e = launch(plans[i]->args, stream, nullptr, nullptr);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+void gdn_decode_plan_destroy(gdn_decode_plan* plan) { delete plan; }
+
+int gdn_decode_graph_create(const gdn_decode_plan* const* plans, int n,
+                            gdn_decode_graph** graph) {
+  if (graph == nullptr) return hipErrorInvalidValue;
+  *graph = nullptr;
+  if (n < 1 || plans == nullptr) return hipErrorInvalidValue;
+  for (int i = 0; i < n; ++i)
+    if (plans[i] == nullptr) return hipErrorInvalidValue;
+  // The launches are recorded from a private stream of the current device
+  // (default priority) in capture mode; the graph is instantiated once.
+  hipStream_t s = nullptr;
+  hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+  if (e != hipSuccess) return e;
+  e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+  hipError_t launch_error = hipSuccess;
+  if (e == hipSuccess) {
+    for (int i = 0; i < n && launch_error == hipSuccess; ++i)
+      launch_error = launch(plans[i]->args, s, nullptr, nullptr);
+    hipGraph_t g = nullptr;
+    e = hipStreamEndCapture(s, &g);   // always ends the capture, also after a failed launch
+    if (e == hipSuccess && launch_error != hipSuccess) e = launch_error;
+    hipGraphExec_t exec = nullptr;
+    if (e == hipSuccess) e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    if (g != nullptr) (void)hipGraphDestroy(g);
+    if (e == hipSuccess) {
+      *graph = new (std::nothrow) gdn_decode_graph{exec};
+      if (*graph == nullptr) {
+        (void)hipGraphExecDestroy(exec);
+        e = hipErrorOutOfMemory;
+      }
+    }
+  }
+  const hipError_t d = hipStreamDestroy(s);
+  return e != hipSuccess ? e : d;
+}
+
+int gdn_decode_graph_launch(const gdn_decode_graph* graph, void* hip_stream) {
+  if (graph == nullptr) return hipErrorInvalidValue;
+  return hipGraphLaunch(graph->exec, static_cast<hipStream_t>(hip_stream));
+}
+
+void gdn_decode_graph_destroy(gdn_decode_graph* graph) {
+  if (graph == nullptr) return;
+  (void)hipGraphExecDestroy(graph->exec);
+  delete graph;
+}
+
 const char* gdn_decode_error_string(int code) {
   return hipGetErrorString(static_cast<hipError_t>(code));
 }
 
-int gdn_decode_abi_version(void) { return 3; }
+int gdn_decode_abi_version(void) { return 4; }
 
 }  // extern "C"

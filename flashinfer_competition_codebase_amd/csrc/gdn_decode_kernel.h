@@ -279,6 +279,7 @@ struct TokenHead {
   float kq;         // k_hat . q'
   float gk;         // g * kscale
   float gq;         // g * qscale
+  float qscale;     // scale / |q| (L2-norm) or scale
 };
 
 // The per-head quantities of one token from its q, k, v and its gates.
@@ -320,6 +321,7 @@ __device__ __forceinline__ void head_of(u32x4 qbits, u32x4 kbits, const Bf16Run<
   h.kq = kq_raw * (qscale * kscale);
   h.gk = g * kscale;
   h.gq = g * qscale;
+  h.qscale = qscale;
 }
 
 template <int NS, bool L2NORM>
@@ -358,6 +360,7 @@ __device__ __forceinline__ void token_head(const TokenIn<NS>& in, float A_log, f
   h.kq = kq_raw * (qscale * kscale);
   h.gk = g * kscale;
   h.gq = g * qscale;
+  h.qscale = qscale;
 }
 
 // Multi-token inputs of one token (its gates come from the per-lane table).
@@ -428,6 +431,60 @@ __device__ __forceinline__ void token_rows(float (&s)[NS][8], const TokenHead<NS
   }
 }
 
+// Multi-token form of token_rows with the decay applied lazily.  The lane
+// group holds s = S / G, the state divided by the decay G accumulated since
+// the last fold (G = 1 at the first token), so a token's decay g costs no
+// per-element multiply: with Gn = G g,
+//   k_hat . (g S) = Gn kscale (k . s),   q' . S_new = Gn qscale (q . s) + d (k_hat . q')
+//   S_new = Gn s + d (x) k_hat  =  Gn (s + (d / Gn) (x) k_hat),
+// one FMA per element.  When Gn would fall below kLazyMinDecay (s would
+// grow past 2^40 times S, or g itself underflows to 0) the token first
+// folds all of it into s -- s = Gn s, after which the token is one with no
+// decay on that s (Gn = 1) -- a uniform branch, rare for any decay the
+// gates produce.  Only the rounding order differs from token_rows.
+constexpr float kLazyMinDecay = 0x1p-40f;
+
+template <int NS>
+__device__ __forceinline__ void token_rows_lazy(float (&s)[NS][8], const TokenHead<NS>& h,
+                                                float& G, float (&o)[NS]) {
+  float gn = G * h.g;                 // decay of S relative to s after this token
+  float gk = G * h.gk;                // Gn kscale
+  float gq = G * h.gq;                // Gn qscale
+  if (gn < kLazyMinDecay) {
+#pragma unroll
+    for (int n = 0; n < NS; ++n)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s[n][i] *= gn;
+    gn = 1.0f;
+    gk = h.kscale;
+    gq = h.qscale;
+  }
+  float red[2 * NS];
+#pragma unroll
+  for (int n = 0; n < NS; ++n) {
+    float ak = 0.0f, aq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      ak = fmaf(s[n][i], h.kf[i], ak);
+      aq = fmaf(s[n][i], h.qf[i], aq);
+    }
+    red[2 * n] = ak;
+    red[2 * n + 1] = aq;
+  }
+  row16_sum<2 * NS>(red);
+
+  const float c = h.kscale * __builtin_amdgcn_rcpf(gn);
+#pragma unroll
+  for (int n = 0; n < NS; ++n) {
+    const float d = h.beta * (h.vrow[n] - gk * red[2 * n]);   // beta * (v - k_hat . (g S))
+    o[n] = fmaf(d, h.kq, gq * red[2 * n + 1]);              // q' . S_new
+    const float dk = d * c;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s[n][i] = fmaf(dk, h.kf[i], s[n][i]);
+  }
+  G = gn;
+}
+
 // Block order: consecutive blocks -- which the dispatcher hands round-robin
 // to the 8 XCDs -- stream adjacent state rows.  Renumbering blocks so that
 // each XCD works on its own contiguous eighth (sharing q/k in that XCD's L2)
@@ -438,7 +495,8 @@ __device__ __forceinline__ void token_rows(float (&s)[NS][8], const TokenHead<NS
 // (b, hv) head per workgroup.  VARLEN (multi-token only): sequence b is the
 // token rows [cu_seqlens[b], cu_seqlens[b + 1]) of packed [L, H|HV, ...]
 // inputs (the prefill layout), clamped to [0, L]; a sequence with no tokens
-// gets a zero state, and a null state starts from zeros.
+// gets a zero state.  MULTI: a null state starts from zeros (the state
+// stream is then only written).
 //
 // The arguments are scalars rather than one struct so that the first 14
 // dwords -- every pointer and size the first loads need: six pointers, H and
@@ -511,7 +569,10 @@ __attribute__((amdgpu_waves_per_eu(1, (MULTI && !BF16 && NS == 2) ? 6 : 8))) voi
       return;
     }
   }
-  const bool has_state = !VARLEN || p.state != nullptr;
+  // A null state starts from zeros (uniform per launch).  The single-token
+  // kernel is never launched with one (the host runs the multi-token loop
+  // for T = 1 then), so its state loads stay unconditional.
+  const bool has_state = !MULTI || p.state != nullptr;
 
   // Issue every global load before any arithmetic.  Loads retire in issue
   // order, so the small per-token operands (a, b, q, k, v) go first: their
@@ -629,10 +690,12 @@ __attribute__((amdgpu_waves_per_eu(1, (MULTI && !BF16 && NS == 2) ? 6 : 8))) voi
       head_of<NS, L2NORM>(in.q, in.k, in.v, lane_value(gl, tt & 63), lane_value(bl, tt & 63),
                           p.scale, h);
     };
-    // Token tt with the per-head quantities in h: rows and output.
+    // Token tt with the per-head quantities in h: rows and output.  The
+    // state is held divided by the decay G not yet applied to it.
+    float G = 1.0f;
     auto apply = [&](int tt) {
       float o[NS];
-      token_rows<NS>(s, h, o);
+      token_rows_lazy<NS>(s, h, G, o);
       if (j == 0) store_bf16_run<NS>(p.out + ((tok0 + tt) * p.HV + hv) * kDim + row0, o);
     };
 
@@ -660,7 +723,11 @@ __attribute__((amdgpu_waves_per_eu(1, (MULTI && !BF16 && NS == 2) ? 6 : 8))) voi
       }
     }
 #pragma unroll
-    for (int n = 0; n < NS; ++n) store_row<BF16, POLICY>(p.new_state, row_base + n, j, s[n]);
+    for (int n = 0; n < NS; ++n) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s[n][i] *= G;        // the decay still held back
+      store_row<BF16, POLICY>(p.new_state, row_base + n, j, s[n]);
+    }
   }
 }
 

@@ -179,10 +179,11 @@ def _launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
     lib = _lib.get_lib()
     idx = q.get_device()
     stream = _lib.current_stream(idx)
-    ptrs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), state.data_ptr(),
+    ptrs = (q.data_ptr(), k.data_ptr(), v.data_ptr(),
+            None if state is None else state.data_ptr(),
             A_log.data_ptr(), a.data_ptr(), dt_bias.data_ptr(), b.data_ptr())
     l2 = int(bool(use_qk_l2norm))
-    bf16 = int(state.dtype == torch.bfloat16)
+    bf16 = int(new_state.dtype == torch.bfloat16)
     # the launch goes to the inputs' device (switched to only when another is current)
     with _on_device(idx):
         if shape is not None:
@@ -217,12 +218,9 @@ def kernel_hip(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
         raise ValueError("kernel_hip needs preallocated output and new_state")
     B, T, H, HV = check_inputs(q, k, v, state, A_log, a, dt_bias, b, output, new_state)
     scale = resolve_scale(scale, q.shape[-1])
-    if state is None:
-        with torch.no_grad():
-            new_state.zero_()
-        state = new_state
     if B == 0:
         return None
+    # state=None: the kernel starts from zeros and only writes new_state
     _launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
             B, T, H, HV, use_qk_l2norm)
     return None
@@ -239,9 +237,6 @@ def kernel_hip_shaped(q, k, v, state, A_log, a, dt_bias, b, scale, output,
     timestamps."""
     B, T, H, HV = check_inputs(q, k, v, state, A_log, a, dt_bias, b, output, new_state)
     scale = resolve_scale(scale, q.shape[-1])
-    if state is None:
-        new_state.zero_()
-        state = new_state
     if B == 0:
         return None
     _launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,

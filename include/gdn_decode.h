@@ -8,7 +8,8 @@
  *   q, k       [B, T, H,  K]   bf16   (K = 128)
  *   v          [B, T, HV, V]   bf16   (V = 128, HV % H == 0, GVA ratio HV/H)
  *   state      [B, HV, V, K]   fp32   "k-last": element (k, v) at v*K + k
- *                                     (bf16 with gdn_decode_steps' state_bf16)
+ *                                     (bf16 with gdn_decode_steps' state_bf16);
+ *                                     NULL starts every sequence from zeros
  *   A_log      [HV]            fp32
  *   a, b       [B, T, HV]      bf16   ([B, HV] is the same memory at T = 1)
  *   dt_bias    [HV]            fp32
@@ -87,8 +88,8 @@ int gdn_decode_steps(const void* q, const void* k, const void* v,
  * rows_per_lane_group and waves_per_block are each one of 1, 2, 4, 8 and
  * their product is at most 32.  cache_policy selects how the state stream
  * is accessed: 0 ordinary loads and stores, 1 nontemporal loads and stores,
- * 2 nontemporal stores only, 3 nontemporal loads only.  With T > 1 or a
- * bf16 state, cache_policy is 0 or 1.  start_event / stop_event (hipEvent_t, may be
+ * 2 nontemporal stores only, 3 nontemporal loads only.  With T > 1, a
+ * bf16 state or a NULL state, cache_policy is 0 or 1.  start_event / stop_event (hipEvent_t, may be
  * NULL) are stamped with the kernel's own start and end timestamps
  * (hipExtLaunchKernelGGL), so hipEventElapsedTime gives the kernel duration
  * without event-marker overhead.  Used for launch-shape sweeps and timing.
@@ -121,13 +122,57 @@ int gdn_decode_launch_shape(int B, int T, int HV, int state_bf16,
                             int* cache_policy, long long* num_blocks);
 
 /*
+ * A decode call bound once: gdn_decode_plan_create validates the arguments
+ * of gdn_decode_steps (the same pointers, sizes and flags) and resolves the
+ * launch shape, so that running it again is one launch per plan with no
+ * per-call checks.  The pointed-to buffers must stay allocated while the
+ * plan (or a graph built from it) is used; their contents may change
+ * between runs (the caller writes the next token's q, k, v, a and b into
+ * them).  gdn_decode_plan_run launches plans[0 .. n-1] in order on
+ * hip_stream.  gdn_decode_plan_create returns the codes gdn_decode_steps
+ * returns for the same arguments (hipErrorOutOfMemory if the host
+ * allocation fails) and sets *plan to NULL on error.
+ *
+ * The reference's B = 1 serving notes plan exactly this for its decode step
+ * (launch overhead dominating a ~3 us kernel, findings/potential-cuda-
+ * improvement.md:143-147,539): its entries validate and look up the stream
+ * on every call (solution/cuda/kernel.cu:405-443).
+ */
+typedef struct gdn_decode_plan gdn_decode_plan;
+
+int gdn_decode_plan_create(const void* q, const void* k, const void* v, const void* state,
+                           const float* A_log, const void* a, const float* dt_bias,
+                           const void* b, float scale, void* output, void* new_state,
+                           int B, int T, int H, int HV, int K, int V, int state_bf16,
+                           int use_qk_l2norm, gdn_decode_plan** plan);
+int gdn_decode_plan_run(const gdn_decode_plan* const* plans, int n, void* hip_stream);
+void gdn_decode_plan_destroy(gdn_decode_plan* plan);
+
+/*
+ * One HIP graph of the launches of plans[0 .. n-1] (n >= 1), in order,
+ * recorded by stream capture on a private stream of the current device and
+ * instantiated once; gdn_decode_graph_launch replays it on hip_stream (a
+ * stream of the same device), as one submission for all n steps (e.g. the
+ * GDN layers of a model's decode step).  The plans may be destroyed after
+ * gdn_decode_graph_create; their buffers may not.  The graph holds no
+ * memset nodes.  Counterpart of the CUDA-graph capture the reference's
+ * serving notes plan (findings/potential-cuda-improvement.md:143-147).
+ */
+typedef struct gdn_decode_graph gdn_decode_graph;
+
+int gdn_decode_graph_create(const gdn_decode_plan* const* plans, int n,
+                            gdn_decode_graph** graph);
+int gdn_decode_graph_launch(const gdn_decode_graph* graph, void* hip_stream);
+void gdn_decode_graph_destroy(gdn_decode_graph* graph);
+
+/*
  * Human-readable text for a return code of the functions above
  * (hipGetErrorString).  The reference has no error path
  * (solution/cuda/kernel.cu:216-252 never checks a launch).
  */
 const char* gdn_decode_error_string(int code);
 
-/* ABI version of this header: 3. */
+/* ABI version of this header: 4 (3 had no plans or graphs and no NULL state). */
 int gdn_decode_abi_version(void);
 
 #ifdef __cplusplus

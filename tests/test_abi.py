@@ -33,7 +33,10 @@ def header_functions() -> dict:
 def test_header_declares_the_abi():
     funcs = header_functions()
     assert set(funcs) == {"gdn_decode_step", "gdn_decode_steps", "gdn_decode_step_shaped",
-                          "gdn_decode_launch_shape", "gdn_decode_error_string",
+                          "gdn_decode_launch_shape", "gdn_decode_plan_create",
+                          "gdn_decode_plan_run", "gdn_decode_plan_destroy",
+                          "gdn_decode_graph_create", "gdn_decode_graph_launch",
+                          "gdn_decode_graph_destroy", "gdn_decode_error_string",
                           "gdn_decode_abi_version"}
 
 
@@ -99,10 +102,12 @@ def test_validation_rejects_bad_sizes_without_launching():
     nulls = [None] * 8
     f = ctypes.c_float(0.1)
 
-    def sh(T, bf16, ns, w, pol):
+    def sh(T, bf16, ns, w, pol, state=0x1000):
         # B = 0: a supported request returns 0 (nothing to launch), an
-        # unsupported one is rejected first
-        return shaped(*nulls, f, None, None, 0, T, 16, 32, 128, 128, bf16, 1, ns, w, pol,
+        # unsupported one is rejected first (nothing is dereferenced)
+        args = list(nulls)
+        args[3] = state
+        return shaped(*args, f, None, None, 0, T, 16, 32, 128, 128, bf16, 1, ns, w, pol,
                       None, None, None)
 
     assert sh(1, 0, 2, 4, 1) == 0     # the B=256 fp32 shape
@@ -114,6 +119,7 @@ def test_validation_rejects_bad_sizes_without_launching():
     assert sh(1, 0, 1, 1, 4) == 1     # unknown cache policy
     assert sh(2, 0, 2, 1, 3) == 1     # multi-token kernels take cache policy 0 or 1
     assert sh(1, 1, 2, 4, 2) == 1     # bf16-state kernels take cache policy 0 or 1
+    assert sh(1, 0, 2, 4, 3, state=None) == 1   # a null state runs the multi-token loop
     assert sh(0, 0, 2, 4, 1) == 1     # T < 1
     assert sh(1, 2, 2, 4, 1) == 1     # state_bf16 is 0 or 1
     steps = lib.gdn_decode_steps
@@ -131,3 +137,54 @@ def test_validation_rejects_misaligned_and_overlapping_state():
     lib = _lib.get_lib()
     assert _step(lib, ptr=0x100002) == 1                       # 2-byte aligned
     assert _step(lib, ptr=0x100000, new_state=0x100010) == 1   # partial overlap
+
+
+def test_plans_validate_once_and_run_without_checks():
+    """gdn_decode_plan_create applies gdn_decode_steps' validation (no HIP
+    call); an empty batch makes a plan whose runs launch nothing; plan_run
+    and graph_create reject null or empty plan lists before any HIP call."""
+    lib = _lib.get_lib()
+    nulls = [None] * 8
+    f = ctypes.c_float(0.1)
+    plan = ctypes.c_void_p(1234)
+    assert lib.gdn_decode_plan_create(*nulls, f, None, None, 1, 1, 16, 32, 128, 128, 0, 1,
+                                      ctypes.byref(plan)) == 1
+    assert plan.value is None                               # NULL on error
+    assert lib.gdn_decode_plan_create(*nulls, f, None, None, 1, 1, 16, 32, 64, 128, 0, 1,
+                                      ctypes.byref(plan)) == 1
+    assert lib.gdn_decode_plan_create(*nulls, f, None, None, 0, 1, 16, 32, 128, 128, 0, 1,
+                                      None) == 1
+    assert lib.gdn_decode_plan_create(*nulls, f, None, None, 0, 1, 16, 32, 128, 128, 0, 1,
+                                      ctypes.byref(plan)) == 0
+    assert plan.value is not None
+    arr = (ctypes.c_void_p * 2)(plan, plan)
+    assert lib.gdn_decode_plan_run(arr, 2, None) == 0        # B = 0: nothing to launch
+    assert lib.gdn_decode_plan_run(arr, 0, None) == 0
+    assert lib.gdn_decode_plan_run(None, 1, None) == 1
+    assert lib.gdn_decode_plan_run((ctypes.c_void_p * 1)(None), 1, None) == 1
+    graph = ctypes.c_void_p()
+    assert lib.gdn_decode_graph_create(arr, 0, ctypes.byref(graph)) == 1
+    assert lib.gdn_decode_graph_create((ctypes.c_void_p * 1)(None), 1, ctypes.byref(graph)) == 1
+    assert lib.gdn_decode_graph_launch(None, None) == 1
+    lib.gdn_decode_plan_destroy(plan)
+    lib.gdn_decode_plan_destroy(None)
+    lib.gdn_decode_graph_destroy(None)
+
+
+def test_serving_classes_need_a_hip_device():
+    from flashinfer_competition_codebase_amd.serving import DecodeLayers, DecodePlan
+    from oracle.gdn_decode_oracle import make_inputs
+
+    t = make_inputs(1, 4, 8, seed=1)
+    out = torch_empty_out(t)
+    with pytest.raises(ValueError, match="HIP device"):
+        DecodePlan(**t, output=out, new_state=t["state"])
+    with pytest.raises(ValueError):
+        DecodeLayers([])
+
+
+def torch_empty_out(t):
+    import torch
+
+    B, T, HV = t["v"].shape[0], t["v"].shape[1], t["v"].shape[2]
+    return torch.empty(B, T, HV, 128, dtype=torch.bfloat16)

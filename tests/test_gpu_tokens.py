@@ -84,9 +84,13 @@ def test_multi_token(B, H, HV, T, l2, hip_device):
 
 
 @pytest.mark.parametrize("B,H,HV,T", [(3, 16, 32, 4), (1, 4, 8, 70)])
-def test_multi_token_equals_chained_single_tokens_bitwise(B, H, HV, T, hip_device):
-    """One launch of T tokens gives the bits of T chained T=1 launches (at
-    T=70 across the refill of the per-lane gate table at token 64)."""
+def test_multi_token_agrees_with_chained_single_tokens(B, H, HV, T, hip_device):
+    """One launch of T tokens against T chained T=1 launches (at T=70 across
+    the refill of the per-lane gate table at token 64).  The multi-token loop
+    applies each token's decay lazily (the state held divided by the decay
+    not yet applied, one FMA per element per token), the single-token kernel
+    directly, so the two round differently: outputs agree within one bf16
+    ulp, states within 1e-5 relative + 1e-6."""
     _announce(f"multi-token vs chained B={B} H={H} HV={HV} T={T}")
     t = _dev(make_inputs(B, H, HV, seed=5100 + T, T=T), hip_device)
     out, st = gdn.run(**t, use_qk_l2norm=True)
@@ -102,8 +106,29 @@ def test_multi_token_equals_chained_single_tokens_bitwise(B, H, HV, T, hip_devic
                        new_state=state, use_qk_l2norm=True)
         outs.append(o)
     torch.cuda.synchronize()
-    assert torch.equal(torch.cat(outs, dim=1), out)
-    assert torch.equal(state, st)
+    chained = torch.cat(outs, dim=1).float()
+    d_out = (chained - out.float()).abs()
+    assert bool((d_out <= 2.0 ** -7 * out.float().abs() + 1e-6).all()), d_out.max()
+    d_st = (state - st).abs()
+    assert bool((d_st <= 1e-5 * st.abs() + 1e-6).all()), d_st.max()
+
+
+@pytest.mark.parametrize("A_log_value,T", [(4.0, 8), (60.0, 5)])
+def test_multi_token_extreme_decay(A_log_value, T, hip_device):
+    """Decays far below the lazy loop's limit (2^-40 accumulated): with
+    exp(A_log) = e^4 a token's decay is ~e^-40 .. e^-1, so the decay owed
+    passes the limit within a token or two and is folded into the state;
+    with e^60 every decay underflows to 0 in fp32 (g = 0: the state
+    restarts from the token's own update).  Against the oracle."""
+    _announce(f"multi-token extreme decay A_log={A_log_value} T={T}")
+    t = make_inputs(4, 16, 32, seed=5150 + T, T=T)
+    t["A_log"] = torch.full_like(t["A_log"], A_log_value)
+    out, new_state = gdn.run(**_dev(t, hip_device), use_qk_l2norm=True)
+    torch.cuda.synchronize()
+    ref_o, ref_s, o64, s64 = _oracle(t, True, torch.float32)
+    assert_output_close(out.cpu(), ref_o, tight_ref64=o64, what="output")
+    assert_state_close(new_state.cpu(), ref_s)
+    assert bool(torch.isfinite(new_state).all())
 
 
 @pytest.mark.parametrize("B,H,HV,T,l2", [
