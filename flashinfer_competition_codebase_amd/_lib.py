@@ -33,6 +33,11 @@ SIGNATURES = {
         _I,
         [_P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P] + [_I] * 11 + [_P, _P, _P],
     ),
+    "gdn_decode_step_stamped": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P] + [_I] * 8
+        + [ctypes.POINTER(ctypes.c_ulonglong), ctypes.c_longlong, _P],
+    ),
     "gdn_decode_launch_shape": (
         _I,
         [_I, _I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I),
@@ -51,7 +56,7 @@ SIGNATURES = {
     "gdn_decode_abi_version": (_I, []),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _S = ctypes.c_size_t
 PREFILL_SIGNATURES = {

@@ -384,6 +384,54 @@ int gdn_decode_launch_shape(int B, int T, int HV, int state_bf16,
   return hipSuccess;
 }
 
+int gdn_decode_step_stamped(const void* q, const void* k, const void* v, const float* state,
+                            const float* A_log, const void* a, const float* dt_bias,
+                            const void* b, float scale, void* output, float* new_state, int B,
+                            int H, int HV, int K, int V, int use_qk_l2norm,
+                            int rows_per_lane_group, int waves_per_block,
+                            unsigned long long* stamps, long long stamp_capacity,
+                            void* hip_stream) {
+  StepArgs s = make_args(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, B, 1,
+                         H, HV, K, V, 0, use_qk_l2norm, rows_per_lane_group, waves_per_block,
+                         kPolicyNtBoth);
+  hipError_t e = validate(s);
+  if (e != hipSuccess) return e;
+  if (state == nullptr || stamps == nullptr || B == 0 || B > 65535)
+    return hipErrorInvalidValue;
+  const int ns = rows_per_lane_group, w = waves_per_block;
+  const long long tiles = kDim / (kLaneGroups * ns * w);
+  const long long waves_total = static_cast<long long>(B) * HV * tiles * w;
+  if (stamp_capacity < waves_total * kStampsPerWave) return hipErrorInvalidValue;
+  const unsigned ratio = static_cast<unsigned>(HV / H);
+  const dim3 grid(ratio * static_cast<unsigned>(tiles), static_cast<unsigned>(H),
+                  static_cast<unsigned>(B));
+  const unsigned h_ratio = static_cast<unsigned>(H) | (ratio << 16);
+  const bool l2 = use_qk_l2norm != 0;
+  const hipStream_t stream = static_cast<hipStream_t>(hip_stream);
+  const int32_t* no_seqlens = nullptr;
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(64 * w), 0, stream, state,
+                       static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                       static_cast<const uint16_t*>(v), static_cast<const uint16_t*>(a),
+                       static_cast<const uint16_t*>(b), h_ratio, 1, A_log, dt_bias,
+                       static_cast<uint16_t*>(output), static_cast<void*>(new_state), scale,
+                       no_seqlens, 0, stamps);
+    return hipGetLastError();
+  };
+  // the single-token launch shapes of the library's table
+  if (ns == 1 && w == 1) return l2 ? go(gdn_decode_k128_stamped<1, 1, true>)
+                                   : go(gdn_decode_k128_stamped<1, 1, false>);
+  if (ns == 2 && w == 2) return l2 ? go(gdn_decode_k128_stamped<2, 2, true>)
+                                   : go(gdn_decode_k128_stamped<2, 2, false>);
+  if (ns == 4 && w == 1) return l2 ? go(gdn_decode_k128_stamped<4, 1, true>)
+                                   : go(gdn_decode_k128_stamped<4, 1, false>);
+  if (ns == 8 && w == 1) return l2 ? go(gdn_decode_k128_stamped<8, 1, true>)
+                                   : go(gdn_decode_k128_stamped<8, 1, false>);
+  if (ns == 2 && w == 4) return l2 ? go(gdn_decode_k128_stamped<2, 4, true>)
+                                   : go(gdn_decode_k128_stamped<2, 4, false>);
+  return hipErrorInvalidValue;
+}
+
 // ---------------------------------------------------------------------------
 // Bound steps and their HIP graph (B = 1 serving: launch overhead).
 // ---------------------------------------------------------------------------
@@ -478,6 +526,6 @@ const char* gdn_decode_error_string(int code) {
   return hipGetErrorString(static_cast<hipError_t>(code));
 }
 
-int gdn_decode_abi_version(void) { return 4; }
+int gdn_decode_abi_version(void) { return 5; }
 
 }  // extern "C"

@@ -509,14 +509,54 @@ __device__ __forceinline__ void token_rows_lazy(float (&s)[NS][8], const TokenHe
 // for T = 2 at 65-128 and above 768 heads, for T >= 3 at 65-256 heads) are
 // held at 6 waves per SIMD: at their ~71 VGPRs the compiler would allow 7,
 // which measured 2.3% slower than 6 at B=256 T=2 (qk16_v32).
-template <int NS, int WAVES, bool L2NORM, int POLICY, bool BF16, bool MULTI, bool VARLEN>
-__global__ __launch_bounds__(64 * WAVES)
-__attribute__((amdgpu_waves_per_eu(1, (MULTI && !BF16 && NS == 2) ? 6 : 8))) void gdn_decode_k128(
+// Phase stamps of the instrumented single-token kernel (STAMP): per wave,
+// in this order, the real-time clock at entry, the shader clock at entry,
+// after the state loads are issued, after the per-head math (the small
+// inputs have arrived), when the state has arrived, after the state stores
+// are issued, when every store has completed, and the real-time clock at
+// the end.
+constexpr int kStampsPerWave = 8;
+
+// Clock reads of the instrumented kernel: issued in program order (the
+// scheduling barriers), waited for only where the stamps are stored.
+__device__ __forceinline__ unsigned long long shader_clock() {
+  __builtin_amdgcn_sched_barrier(0);
+  const unsigned long long t = __builtin_amdgcn_s_memtime();
+  __builtin_amdgcn_sched_barrier(0);
+  return t;
+}
+
+__device__ __forceinline__ unsigned long long real_clock() {
+  __builtin_amdgcn_sched_barrier(0);
+  const unsigned long long t = __builtin_amdgcn_s_memrealtime();
+  __builtin_amdgcn_sched_barrier(0);
+  return t;
+}
+
+// A per-head value read through the scalar cache (hv is uniform per
+// workgroup): the read the compiler makes of A_log and dt_bias anyway, made
+// explicit so that no earlier side effect (the instrumented kernel's clock
+// reads count as one) turns it into a vector load queued behind the state
+// stream.
+__device__ __forceinline__ float scalar_read(const float* ptr) {
+  typedef const __attribute__((address_space(4))) float ConstantFloat;
+  return *(ConstantFloat*)ptr;  // generic -> constant address space: a C-style cast
+}
+
+template <int NS, int WAVES, bool L2NORM, int POLICY, bool BF16, bool MULTI, bool VARLEN,
+          bool STAMP>
+__device__ __forceinline__ void decode_body(
     const void* state, const uint16_t* q, const uint16_t* k, const uint16_t* v,
     const uint16_t* a, const uint16_t* b, unsigned h_ratio, int T_arg, const float* A_log_p,
     const float* dt_bias_p, uint16_t* out, void* new_state, float scale,
-    const int32_t* cu_seqlens, int total_tokens) {
+    const int32_t* cu_seqlens, int total_tokens, unsigned long long* stamps) {
   static_assert(MULTI || !VARLEN, "variable-length sequences run the multi-token loop");
+  static_assert(!STAMP || (!MULTI && !BF16), "phase stamps: the fp32 single-token kernel");
+  unsigned long long st[kStampsPerWave] = {};
+  if constexpr (STAMP) {
+    st[0] = real_clock();
+    st[1] = shader_clock();
+  }
   Params p;
   p.state = state;
   p.q = q;
@@ -591,9 +631,10 @@ __attribute__((amdgpu_waves_per_eu(1, (MULTI && !BF16 && NS == 2) ? 6 : 8))) voi
       for (int n = 0; n < NS; ++n) raw[n] = load_row<BF16, POLICY>(p.state, row_base + n, j);
     }
     __builtin_amdgcn_sched_barrier(0);
-    const float A_log = p.A_log[hv];
-    const float dt_bias = p.dt_bias[hv];
+    const float A_log = scalar_read(p.A_log + hv);
+    const float dt_bias = scalar_read(p.dt_bias + hv);
     __builtin_amdgcn_sched_barrier(0);  // both reads in flight before either is used
+    if constexpr (STAMP) st[2] = shader_clock();
 
     // The per-head math waits only on the small loads: keep it ahead of
     // everything that waits on the state.
@@ -605,6 +646,12 @@ __attribute__((amdgpu_waves_per_eu(1, (MULTI && !BF16 && NS == 2) ? 6 : 8))) voi
     // v_rsq_f32 between the state's arrival and the final output store.
     asm volatile("" ::"v"(h.g), "v"(h.beta), "v"(h.kscale), "v"(h.kq), "v"(h.gk), "v"(h.gq));
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (STAMP) {
+      st[3] = shader_clock();
+      // a use of the last state load's data: the wait for the whole state
+      asm volatile("" ::"v"(raw[NS - 1].c[1][3]));
+      st[4] = shader_clock();
+    }
 
     float s[NS][8];
 #pragma unroll
@@ -622,9 +669,22 @@ __attribute__((amdgpu_waves_per_eu(1, (MULTI && !BF16 && NS == 2) ? 6 : 8))) voi
       // The state write-back is the kernel's tail: issue it before the output.
 #pragma unroll
       for (int n = 0; n < NS; ++n) store_row<BF16, POLICY>(p.new_state, row_base + n, j, s[n]);
+      if constexpr (STAMP) st[5] = shader_clock();
       if (j == 0) {
         const size_t out_row = ((tok0 + t) * p.HV + hv) * kDim + row0;
         store_bf16_run<NS>(p.out + out_row, o);
+      }
+    }
+    if constexpr (STAMP) {
+      __builtin_amdgcn_s_waitcnt(0);   // every load and store of this wave complete
+      st[6] = shader_clock();
+      st[7] = real_clock();
+      if (lane == 0) {                 // one lane per wave: ordinary vector stores
+        const size_t blk = blockIdx.x + static_cast<size_t>(gridDim.x) *
+                                             (blockIdx.y + static_cast<size_t>(gridDim.y) * blockIdx.z);
+        unsigned long long* dst = stamps + (blk * WAVES + wave) * kStampsPerWave;
+#pragma unroll
+        for (int i = 0; i < kStampsPerWave; ++i) dst[i] = st[i];
       }
     }
   } else {
@@ -729,6 +789,33 @@ __attribute__((amdgpu_waves_per_eu(1, (MULTI && !BF16 && NS == 2) ? 6 : 8))) voi
       store_row<BF16, POLICY>(p.new_state, row_base + n, j, s[n]);
     }
   }
+}
+
+template <int NS, int WAVES, bool L2NORM, int POLICY, bool BF16, bool MULTI, bool VARLEN>
+__global__ __launch_bounds__(64 * WAVES)
+__attribute__((amdgpu_waves_per_eu(1, (MULTI && !BF16 && NS == 2) ? 6 : 8))) void gdn_decode_k128(
+    const void* state, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+    const uint16_t* a, const uint16_t* b, unsigned h_ratio, int T_arg, const float* A_log_p,
+    const float* dt_bias_p, uint16_t* out, void* new_state, float scale,
+    const int32_t* cu_seqlens, int total_tokens) {
+  decode_body<NS, WAVES, L2NORM, POLICY, BF16, MULTI, VARLEN, false>(
+      state, q, k, v, a, b, h_ratio, T_arg, A_log_p, dt_bias_p, out, new_state, scale,
+      cu_seqlens, total_tokens, nullptr);
+}
+
+// The fp32 single-token kernel with phase stamps (kStampsPerWave per wave,
+// written to `stamps`, indexed by linear block * WAVES + wave): a
+// measurement instrument, never launched by the decode entry points.
+template <int NS, int WAVES, bool L2NORM>
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 8)))
+void gdn_decode_k128_stamped(
+    const void* state, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+    const uint16_t* a, const uint16_t* b, unsigned h_ratio, int T_arg, const float* A_log_p,
+    const float* dt_bias_p, uint16_t* out, void* new_state, float scale,
+    const int32_t* cu_seqlens, int total_tokens, unsigned long long* stamps) {
+  decode_body<NS, WAVES, L2NORM, kPolicyNtBoth, false, false, false, true>(
+      state, q, k, v, a, b, h_ratio, T_arg, A_log_p, dt_bias_p, out, new_state, scale,
+      cu_seqlens, total_tokens, stamps);
 }
 
 }  // namespace gdn

@@ -109,6 +109,30 @@ int gdn_decode_step_shaped(const void* q, const void* k, const void* v,
                            void* hip_stream);
 
 /*
+ * Measurement instrument, no counterpart in the reference: one T = 1 step
+ * (fp32 state, not NULL; B <= 65535) through an instrumented copy of the
+ * single-token kernel with the given launch shape (rows_per_lane_group x
+ * waves_per_block one of 1x1, 2x2, 4x1, 8x1, 2x4; nontemporal state
+ * access) that also writes 8 clock stamps per wavefront to `stamps`
+ * (stamp_capacity entries, at least 8 per wavefront: the launch has
+ * B x HV x 128 / (4 x rows_per_lane_group) wavefronts; wavefront w of
+ * linear block i at entry 8 * (i * waves_per_block + w)): the real-time
+ * clock (100 MHz) at entry; the shader clock at entry, after the state
+ * loads are issued, after the per-head math (the small inputs arrived),
+ * when the state has arrived, after the state stores are issued, and when
+ * every store has completed; the real-time clock at the end.  The phases
+ * of the reference's clock64 instrumentation plan
+ * (findings/potential-cuda-improvement.md:457-496) on this kernel.
+ */
+int gdn_decode_step_stamped(const void* q, const void* k, const void* v, const float* state,
+                            const float* A_log, const void* a, const float* dt_bias,
+                            const void* b, float scale, void* output, float* new_state,
+                            int B, int H, int HV, int K, int V, int use_qk_l2norm,
+                            int rows_per_lane_group, int waves_per_block,
+                            unsigned long long* stamps, long long stamp_capacity,
+                            void* hip_stream);
+
+/*
  * Launch shape gdn_decode_steps would use for B sequences of T tokens over
  * HV v-heads with an fp32 (state_bf16 = 0) or bf16 (1) state: writes
  * rows_per_lane_group, waves_per_block, cache_policy and the workgroup
@@ -172,7 +196,8 @@ void gdn_decode_graph_destroy(gdn_decode_graph* graph);
  */
 const char* gdn_decode_error_string(int code);
 
-/* ABI version of this header: 4 (3 had no plans or graphs and no NULL state). */
+/* ABI version of this header: 5 (4 had no gdn_decode_step_stamped; 3 had no
+ * plans or graphs and no NULL state). */
 int gdn_decode_abi_version(void);
 
 #ifdef __cplusplus

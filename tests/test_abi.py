@@ -33,7 +33,7 @@ def header_functions() -> dict:
 def test_header_declares_the_abi():
     funcs = header_functions()
     assert set(funcs) == {"gdn_decode_step", "gdn_decode_steps", "gdn_decode_step_shaped",
-                          "gdn_decode_launch_shape", "gdn_decode_plan_create",
+                          "gdn_decode_launch_shape", "gdn_decode_step_stamped", "gdn_decode_plan_create",
                           "gdn_decode_plan_run", "gdn_decode_plan_destroy",
                           "gdn_decode_graph_create", "gdn_decode_graph_launch",
                           "gdn_decode_graph_destroy", "gdn_decode_error_string",
