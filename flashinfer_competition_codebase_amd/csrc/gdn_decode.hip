@@ -179,6 +179,12 @@ constexpr ShapeRow kShapeT3Plus[] = {
 constexpr ShapeRow kShapeBf16[] = {
     {16, 1, 2}, {32, 1, 4}, {64, 2, 4}, {128, 2, 2}, {256, 2, 1}, {384, 2, 4},
     {768, 4, 4}, {2048, 2, 4}, {-1, 4, 4}};
+// A bf16 state at T >= 3 is VALU-bound from a few hundred heads on: more
+// rows per lane group share each token's per-head work (kernel-stamped
+// sweep of every shape, lazy decay: 256 heads 8.48 -> 7.68 us, 2048 heads
+// 38.0 -> 33.0 us, 8192 heads 127.9 -> 117.3 us at T = 4).
+constexpr ShapeRow kShapeBf16T3Plus[] = {
+    {16, 1, 2}, {32, 1, 4}, {64, 2, 4}, {128, 2, 2}, {512, 4, 2}, {-1, 8, 1}};
 
 template <size_t N>
 void pick_row(const ShapeRow (&table)[N], long long heads, int* ns, int* waves) {
@@ -193,7 +199,9 @@ void pick_row(const ShapeRow (&table)[N], long long heads, int* ns, int* waves) 
 
 void choose_shape(long long heads, bool bf16, int T, int* ns, int* waves, int* policy) {
   *policy = kPolicyNtBoth;
-  if (bf16) {
+  if (bf16 && T >= 3) {
+    pick_row(kShapeBf16T3Plus, heads, ns, waves);
+  } else if (bf16) {
     pick_row(kShapeBf16, heads, ns, waves);
   } else if (T >= 3) {
     pick_row(kShapeT3Plus, heads, ns, waves);

@@ -353,3 +353,35 @@ def test_hip_graph_capture_and_replay(hip_device):
         torch.cuda.synchronize()
         assert torch.equal(out_g, out_e), step
         assert torch.equal(state_g, state_e), step
+
+
+@pytest.mark.parametrize("B,H,HV,l2", [(1, 16, 32, True), (1, 4, 8, False), (4, 4, 8, False)])
+def test_stamped_instrument_matches_the_kernel(B, H, HV, l2, hip_device):
+    """The instrumented single-token kernel (gdn_decode_step_stamped) computes
+    the product kernel's bits with the same launch shape, and every
+    wavefront's stamps are in order."""
+    import ctypes
+
+    _announce(f"stamped instrument B={B} H={H} HV={HV}")
+    t = _dev(make_inputs(B, H, HV, seed=4100 + B + H), hip_device)
+    ref_o, ref_s = gdn.run(**t, use_qk_l2norm=l2)
+    ns, waves, _, blocks = _lib.launch_shape(B, HV)
+    n = blocks * waves * 8
+    stamps = torch.zeros(n, dtype=torch.int64, device=hip_device)
+    out = torch.empty_like(ref_o)
+    st = t["state"].clone()
+    lib = _lib.get_lib()
+    code = lib.gdn_decode_step_stamped(
+        t["q"].data_ptr(), t["k"].data_ptr(), t["v"].data_ptr(), st.data_ptr(),
+        t["A_log"].data_ptr(), t["a"].data_ptr(), t["dt_bias"].data_ptr(), t["b"].data_ptr(),
+        t["scale"], out.data_ptr(), st.data_ptr(), B, H, HV, 128, 128, int(l2), ns, waves,
+        ctypes.cast(stamps.data_ptr(), ctypes.POINTER(ctypes.c_ulonglong)), n,
+        torch.cuda.current_stream().cuda_stream)
+    assert code == 0
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref_o) and torch.equal(st, ref_s)
+    s = stamps.view(-1, 8).cpu()
+    assert bool((s[:, 2:7] >= s[:, 1:6]).all()), "shader-clock stamps out of order"
+    assert bool((s[:, 7] >= s[:, 0]).all()) and bool((s[:, 1] > 0).all())
+    assert lib.gdn_decode_step_stamped(*[None] * 8, 0.1, None, None, B, H, HV, 128, 128, 0,
+                                       ns, waves, None, 0, None) == 1
