@@ -178,7 +178,22 @@ def regimes(device, n: int = 32, manifest_path: str | None = None) -> dict:
         print(f"[probe] {name}: {len(manifest[-1]['schedule'])} launches", file=sys.stderr,
               flush=True)
         del t
-    # an empty kernel on the B = 1 qk16_v32 grid in the same regimes: what a
+    # B = 1 qk16_v32 through other launch shapes (workgroup counts 1024 to 32)
+    from .kernel import kernel_hip_shaped
+
+    t = _inputs(1, 16, 32, device)
+    common = {k: t[k] for k in ("q", "k", "v", "A_log", "a", "dt_bias", "b", "output")}
+    for ns, waves in ((1, 1), (8, 1), (8, 4)):
+        def shaped(s, slot, ns=ns, waves=waves):
+            kernel_hip_shaped(**common, state=s, new_state=s, scale=1.0 / math.sqrt(128),
+                              use_qk_l2norm=True, rows_per_lane_group=ns,
+                              waves_per_block=waves, cache_policy=1)
+
+        _run_schedule(t, n, shaped, flush)
+        manifest.append({"shape": f"b1_qk16_v32_l2_shape_{ns}x{waves}",
+                         "schedule": [[r, m] for r, _, m in _regime_schedule(n)]})
+    del t
+    # an empty kernel of 8 to 1024 workgroups in the same regimes: what a
     # dispatch costs with no work in it
     from .build import CALIB_PATH
 
@@ -186,16 +201,16 @@ def regimes(device, n: int = 32, manifest_path: str | None = None) -> dict:
     cal.gdn_calib_empty.argtypes = [ctypes.c_longlong, ctypes.c_void_p, ctypes.c_void_p,
                                     ctypes.c_void_p]
     cal.gdn_calib_empty.restype = ctypes.c_int
-    blocks = _lib.launch_shape(1, 32)[3]
     t = {"states": [None]}
+    for blocks in (8, 256, 1024):
+        def empty(_s, _slot, blocks=blocks):
+            _lib.check(cal.gdn_calib_empty(blocks, None, None,
+                                           torch.cuda.current_stream().cuda_stream),
+                       "gdn_calib_empty")
 
-    def empty(_s, _slot):
-        _lib.check(cal.gdn_calib_empty(blocks, None, None, torch.cuda.current_stream().cuda_stream),
-                   "gdn_calib_empty")
-
-    _run_schedule(t, n, empty, flush)
-    manifest.append({"shape": "empty_kernel", "kernel": "gdn_calib::empty",
-                     "schedule": [[r, m] for r, _, m in _regime_schedule(n)]})
+        _run_schedule(t, n, empty, flush)
+        manifest.append({"shape": f"empty_kernel_{blocks}_blocks", "kernel": "gdn_calib::empty",
+                         "schedule": [[r, m] for r, _, m in _regime_schedule(n)]})
     doc = {"shapes": manifest}
     if manifest_path:
         with open(manifest_path, "w") as f:
