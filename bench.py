@@ -744,26 +744,64 @@ def prefill_bytes(lens, H, HV) -> int:
 
 
 def prefill_workspace_bytes(lens, H, HV) -> int:
-    """Bytes the preparation kernel writes: a v-head slot per (chunk, v-head)
-    (W and P as bf16 hi/lo, U fp32, row scales) and a q/k-head slot per
-    (chunk, q/k head) (K^T and the Q copy, bf16)."""
+    """Bytes the preparation kernel writes: a slot per (chunk, v-head), the
+    six lower 16 x 32 operand blocks of T diag(beta) and of P as bf16 hi/lo,
+    and four rows of 64 fp32 scales."""
     chunks = sum((n + 63) // 64 for n in lens)
-    vslot = (2 * 64 * 128 + 64 * 64 + 3 * 64) * 4
-    qkslot = 2 * 128 * 64 * 2
-    return chunks * (HV * vslot + H * qkslot)
+    vslot = 4 * 6 * 16 * 32 * 2 + 4 * 64 * 4
+    return chunks * HV * vslot
 
 
 PREFILL_ROOFLINE_WORKLOAD = "prefill_qk16_v32_64x512"
 
 
+PREFILL_PREP_KERNEL = "gdn_pf::prep_kernel<false>"
+PREFILL_SCAN_KERNEL = "gdn_pf::scan_kernel<false, false>"
+PMC_PREFILL_COMMANDS = [
+    "cd /tmp && export TMPDIR=/tmp && timeout -s KILL 90 rocprofv3 --pmc FETCH_SIZE "
+    "--output-format csv -d $REPO/gpurun_out/pmcp1 -o p -- python3 $REPO/bench.py --pmc-prefill",
+    "cd /tmp && export TMPDIR=/tmp && timeout -s KILL 90 rocprofv3 --pmc WRITE_SIZE "
+    "--output-format csv -d $REPO/gpurun_out/pmcp2 -o p -- python3 $REPO/bench.py --pmc-prefill",
+    "python3 bench.py --summarize-pmc-prefill gpurun_out/pmcp1/p_counter_collection.csv "
+    "gpurun_out/pmcp2/p_counter_collection.csv",
+]
+
+
+def summarize_pmc_prefill(fetch_csv: str, write_csv: str) -> dict:
+    """The committed counter summary of the 64 x 512 qk16_v32 prefills of
+    ``--pmc-prefill`` (two rocprofv3 runs, FETCH_SIZE then WRITE_SIZE): HBM
+    bytes per launch of the preparation and scan kernels."""
+    from flashinfer_competition_codebase_amd.rocprof import pmc_traffic
+
+    lens, H, HV = PREFILL_CONFIGS[PREFILL_ROOFLINE_WORKLOAD]
+    kernels = {}
+    for key, name in (("prep", PREFILL_PREP_KERNEL), ("scan", PREFILL_SCAN_KERNEL)):
+        kernels[key] = pmc_traffic(fetch_csv, write_csv, name, PMC_COPY_BYTES, copies=3, skip=1)
+    total = kernels["prep"]["traffic_bytes_per_launch"] + kernels["scan"]["traffic_bytes_per_launch"]
+    alg = prefill_bytes(lens, H, HV)
+    return {"workload": f"{PREFILL_ROOFLINE_WORKLOAD}: {len(lens)} x {lens[0]} tokens, "
+                        f"H={H} HV={HV}, 3 prefills (the first one skipped)",
+            "sources_sha": sources_sha(PREFILL_SOURCES), "commands": PMC_PREFILL_COMMANDS,
+            "kernels": kernels, "traffic_bytes_per_prefill": total,
+            "algorithmic_bytes_per_prefill": alg,
+            "workspace_bytes_written": prefill_workspace_bytes(lens, H, HV),
+            "traffic_over_algorithmic": round(total / alg, 4),
+            "note": ("Counter values are KiB per dispatch, each scaled by what it reads for "
+                     "the three 256 MiB copies the run makes first (bytes = KiB * 1024 / "
+                     "factor); per kernel the median over the prefills after the first.")}
+
+
 def _prefill_traffic() -> dict | None:
-    """Measured HBM bytes per launch of the 64 x 512 qk16_v32 prefill kernels
-    (rocprofv3 FETCH_SIZE / WRITE_SIZE, calibrated on a copy of known size),
-    from the committed counter summary."""
+    """Measured HBM bytes per launch of the 64 x 512 qk16_v32 prefill kernels,
+    from the committed counter summary when it was measured on the current
+    prefill sources; else None."""
     try:
-        k = json.loads(PREFILL_TRAFFIC_SUMMARY.read_text())["kernels"]
-        return {"prep": k["prep_64x512_qk16_v32"]["traffic_bytes_per_launch"],
-                "scan": k["scan_64x512_qk16_v32"]["traffic_bytes_per_launch"]}
+        summary = json.loads(PREFILL_TRAFFIC_SUMMARY.read_text())
+        if summary.get("sources_sha") != sources_sha(PREFILL_SOURCES):
+            return None
+        k = summary["kernels"]
+        return {"prep": k["prep"]["traffic_bytes_per_launch"],
+                "scan": k["scan"]["traffic_bytes_per_launch"]}
     except (OSError, ValueError, KeyError):
         return None
 
@@ -782,7 +820,7 @@ def prefill_roofline(prefill: dict) -> dict:
     ku = r["kernel_us"]
     achieved = flop / (ku["kernels"] * 1e-6) / 1e12
     L = sum(lens)
-    prep_in = L * (2 * H * 128 * 2 + HV * 128 * 2 + 2 * HV * 2)
+    prep_in = L * (2 * H * 128 * 2 + 2 * HV * 2)          # q, k, a, b
     prep_bytes = prep_in + r["prep_workspace_bytes"]
     prep_gbs = prep_bytes / (ku["prep"] * 1e-6) / 1e9
     tr = _prefill_traffic()
@@ -860,8 +898,7 @@ def prefill_inputs(name: str, device) -> dict:
 def pmc_prefill(device):
     """Short run for rocprofv3 counter passes over the prefill: three plain
     256 MiB copies (calibrate FETCH_SIZE / WRITE_SIZE against known bytes),
-    then three prefills each of the 1 x 16384 qk4_v8 and 64 x 512 qk16_v32
-    workloads."""
+    then three prefills of the 64 x 512 qk16_v32 workload."""
     n = 256 * 1024 * 1024 // 4
     src = torch.randn(n, device=device)
     dst = torch.empty_like(src)
@@ -869,7 +906,7 @@ def pmc_prefill(device):
         dst.copy_(src)
     torch.cuda.synchronize()
     del src, dst
-    for name in ("prefill_qk4_v8_1x16384", "prefill_qk16_v32_64x512"):
+    for name in (PREFILL_ROOFLINE_WORKLOAD,):
         t = prefill_inputs(name, device)
         for _ in range(3):
             gdn.kernel_prefill_hip(**t)
@@ -974,6 +1011,8 @@ def main():
                     help="write the decode counter summary from two --pmc-pass runs")
     ap.add_argument("--pmc-prefill", action="store_true",
                     help="short prefill run for rocprofv3 counter passes")
+    ap.add_argument("--summarize-pmc-prefill", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="write the prefill counter summary from two --pmc-prefill runs")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--prefill-only", action="store_true",
                     help="time the prefill workloads only and print them as JSON")
@@ -997,6 +1036,13 @@ def main():
         TRAFFIC_SUMMARY.write_text(json.dumps(summary, indent=1) + "\n")
         log(f"[bench] wrote {TRAFFIC_SUMMARY.relative_to(ROOT)}: "
             f"{summary['traffic_bytes_per_launch']} B per launch "
+            f"({summary['traffic_over_algorithmic']}x algorithmic)")
+        return
+    if args.summarize_pmc_prefill:
+        summary = summarize_pmc_prefill(*args.summarize_pmc_prefill)
+        PREFILL_TRAFFIC_SUMMARY.write_text(json.dumps(summary, indent=1) + "\n")
+        log(f"[bench] wrote {PREFILL_TRAFFIC_SUMMARY.relative_to(ROOT)}: "
+            f"{summary['traffic_bytes_per_prefill']} B per prefill "
             f"({summary['traffic_over_algorithmic']}x algorithmic)")
         return
     trace = None

@@ -10,8 +10,9 @@
 // at its start,
 //   A     = strict_lower(beta_i e^(gamma_i - gamma_j) k_i . k_j)
 //   T     = (I + A)^-1                                 (unit lower triangular)
-//   W     = T diag(beta e^gamma) K,   U = T diag(beta) V
-//   Delta = U - W S_0                  (the per-token delta-rule corrections)
+//   X     = V - diag(e^gamma) K S_0        (what the decayed state misses)
+//   Delta = T diag(beta) X                 (the per-token delta-rule corrections;
+//                                           = U - W S_0 of the WY form)
 //   O     = scale [diag(e^gamma) Q S_0 + (Q K^T (.) M) Delta],
 //           M_ij = e^(gamma_i - gamma_j) for j <= i
 //   S_C   = e^(gamma_C) S_0 + (diag(e^(gamma_C - gamma)) K)^T Delta
@@ -29,19 +30,27 @@
 //   1. chunk_offsets: one workgroup turns cu_seqlens into the first chunk
 //      slot of every sequence (token ranges clamped to [0, L]) by a scan,
 //      and writes each slot's sequence, first token and token count.  With
-//      one sequence it is not launched: chunk c is slot c.
-//   2. prep, grid (chunk slots, HV), three workgroups per CU: everything
-//      that does not depend on the state, for all chunks at once -- gates
-//      and gamma, K K^T and Q K^T (bf16 MFMA: the inputs are bf16), T by
-//      block recursion (fp32 MFMA), W and U (bf16 MFMA on hi/lo-split T) --
-//      into a workspace slot per (chunk, v-head), and K^T and a copy of Q
-//      into one per (chunk, q/k head), in the order the scan's MFMAs read
-//      them.
-//   3. scan, one workgroup per (sequence, v-head, 16- or 32-column slice of
-//      the state), XCD-aware order: the sequential part, Delta, O and S_C
-//      chunk after chunk (bf16 MFMA on hi/lo-split fp32 operands), the state
-//      slice kept in registers and the next chunk's operands loaded while
-//      this one runs.
+//      one sequence, or a few (their slots found in the kernels), it is not
+//      launched.
+//   2. prep, grid (chunk slots, HV), three workgroups per CU: what does not
+//      depend on the state, for all chunks at once -- gates and gamma, K K^T
+//      and Q K^T (bf16 MFMA: the inputs are bf16), T by block recursion
+//      (fp32 MFMA) -- into a 25 KiB workspace slot per (chunk, v-head): the
+//      lower blocks of T diag(beta) and of P = Q K^T (.) M, split into bf16
+//      hi + lo in the order the scan's MFMAs read them, and the row scales.
+//   3. scan, one workgroup per (sequence, v-head), XCD-aware order: the
+//      sequential part chunk after chunk with the whole 128 x 128 state in
+//      the registers of four wavefronts (32 columns each); the chunk's K, Q,
+//      V and slot are staged in LDS, loaded a chunk ahead.  Products with
+//      fp32 operands run as bf16 MFMA on hi/lo splits.  Each workgroup reads
+//      its chunks' inputs once, so the workspace is the only HBM traffic
+//      beyond the algorithmic bytes.
+//   One long sequence is cut into segments of kSegChunks chunks, since its
+//   scan alone would occupy HV workgroups for the whole run: a first scan
+//   launch runs segment 0 with its outputs and, from each later segment's
+//   start, the transition columns (an identity start, no values) and the
+//   zero-start end state; a combine kernel chains the segment starts; a
+//   second scan launch runs segments 1.. from their starts with the outputs.
 //
 // MFMA lane layouts (v_mfma_f32_16x16x4_f32, v_mfma_f32_16x16x32_bf16):
 // A[i][k] from lane i + 16 g, B[k][j] from lane j + 16 g (k = g for fp32;
@@ -75,7 +84,6 @@ typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 constexpr int kDim = 128;            // K == V == 128
 constexpr int kChunk = 64;           // tokens per chunk
 constexpr int kThreads = 256;        // 4 wavefronts
-constexpr long long kScanWideHeads = 256;  // N * HV from which the scan takes 32 columns
 // Batches whose chunk slots the kernels find themselves, without the offsets
 // kernel: at most kFewSeqs sequences and kFewPrepGroups preparation
 // workgroups (slots x v-heads).  Each workgroup then scans the batch's
@@ -112,29 +120,27 @@ constexpr float kSoftplusThreshold = 20.0f;
 constexpr float kLn2 = 0.693147180559945309f;
 
 // Workspace slot of one (chunk, v-head), offsets in floats.  The scan's MFMA
-// operands (W, P, K^T and a copy of Q) are stored in operand order: a
-// 16 x 32 block of an operand is 64 lanes x 8 bf16 contiguous (lane = row +
-// 16 g, items in the k order above), so each scan load instruction reads
-// 1 KiB contiguous.  fp32 operands are split into a bf16 high and low part
-// (x ~ hi + lo to ~2^-16 relative).  U is stored in the MFMA result order
-// the scan consumes (per 16 x 16 block, lane-major 4 floats).
+// operands T diag(beta) and P are stored in operand order: a 16 x 32 block
+// is 64 lanes x 8 bf16 contiguous (lane = row + 16 g, items in the k order
+// above), so a wave reads one with a single 1 KiB access.  Both are lower
+// triangular 64 x 64, so only the blocks (row block rb, token block kb) with
+// kb <= rb / 2 are kept, six of eight.  fp32 values are split into a bf16
+// high and low part (x ~ hi + lo to ~2^-16 relative).
 constexpr int kBlk = 512;                             // bf16 per 16 x 32 operand block
-constexpr int kSlotWh = 0;                            // W hi: blocks (row blk 0..3, k blk 0..3)
-constexpr int kSlotWl = kSlotWh + 16 * kBlk / 2;      // W lo
-constexpr int kSlotU = kSlotWl + 16 * kBlk / 2;       // U: blocks (row blk 0..3, col blk 0..7)
-constexpr int kSlotPh = kSlotU + kChunk * kDim;       // P hi: blocks (row blk 0..3, j blk 0..1),
-constexpr int kSlotPl = kSlotPh + 8 * kBlk / 2;       //   P = scale rq_i rk_j M_ij (Q K^T)_ij; lo
-constexpr int kSlotQs = kSlotPl + 8 * kBlk / 2;       // scale * rq_i e^gamma_i [64]
+constexpr int kBlkF = kBlk / 2;                       // the same in floats
+constexpr int kTriBlocks = 6;
+__host__ __device__ constexpr int tri_blk(int rb, int kb) { return (rb < 3 ? rb : 4) + kb; }
+constexpr int kSlotTh = 0;                            // T diag(beta), hi
+constexpr int kSlotTl = kSlotTh + kTriBlocks * kBlkF; //   lo
+constexpr int kSlotPh = kSlotTl + kTriBlocks * kBlkF; // P = scale rq_i rk_j M_ij (Q K^T)_ij, hi
+constexpr int kSlotPl = kSlotPh + kTriBlocks * kBlkF; //   lo
+constexpr int kSlotXg = kSlotPl + kTriBlocks * kBlkF; // rk_i e^gamma_i [64]
+constexpr int kSlotQs = kSlotXg + kChunk;             // scale rq_i e^gamma_i [64]
 constexpr int kSlotKs = kSlotQs + kChunk;             // rk_i e^(gamma_C - gamma_i) [64]
 constexpr int kSlotGl = kSlotKs + kChunk;             // e^gamma_C [1], padded to 64
 constexpr int kSlotFloats = kSlotGl + 64;
 static_assert(kSlotFloats % 64 == 0, "slots stay 256-byte aligned");
-// Slot of one (chunk, q/k head), shared by the v-heads of the group: K^T and
-// the copy of Q, written by the group's first v-head.
-constexpr int kQkSlotKt = 0;                          // K^T: blocks (key blk 0..7, token blk 0..1)
-constexpr int kQkSlotQ = kQkSlotKt + 16 * kBlk / 2;   // Q: blocks (token blk 0..3, k blk 0..3)
-constexpr int kQkSlotFloats = kQkSlotQ + 16 * kBlk / 2;
-static_assert(kQkSlotFloats % 64 == 0, "slots stay 256-byte aligned");
+static_assert(tri_blk(3, 1) == kTriBlocks - 1, "six lower blocks");
 
 // k (0..31) of item e of lane group g inside a 32-long block.
 __host__ __device__ constexpr int k_of(int g, int e) { return 16 * (e >> 2) + 4 * g + (e & 3); }
@@ -211,7 +217,6 @@ struct Params {
   const i32x4* slot_info;    // [max_slots] per chunk slot: sequence, first token, tokens
                              // (0 past the last slot) (workspace)
   float* slots;              // [max_slots, HV, kSlotFloats] (workspace)
-  float* qk_slots;           // [max_slots, H, kQkSlotFloats] (workspace)
   float scale;
   int L;
   int N;
@@ -223,6 +228,15 @@ struct Params {
   int few;                   // 2..kFewSeqs sequences: the kernels compute the chunk
                              // slots from cu_seqlens (no offsets kernel)
   long long max_slots;       // slots the workspace holds
+  // Segments of one long sequence (seg_chunks > 0): segment j is chunks
+  // [j seg_chunks, (j + 1) seg_chunks); per (segment, v-head) 128 x 128 fp32
+  // blocks in k-last order (element (k, c) at c * 128 + k).
+  int seg_chunks;            // chunks per segment, 0: no segments
+  int nseg;                  // segments
+  int seg_pass;              // scan launch 1 (transitions) or 2 (outputs)
+  float* seg_S;              // [nseg, HV] state at each segment's start (1 .. nseg-1)
+  float* seg_B;              // [nseg, HV] state at its end from a zero start
+  float* seg_M;              // [nseg, HV] its transition: end = M start + B (M[k][k'])
 };
 
 // Token range [start, end) of sequence s, clamped to [0, L] so that no
@@ -378,16 +392,12 @@ __device__ __forceinline__ void store_rows_bf16(uint16_t* dst, const u32x4 (&val
 // 2. per-chunk preparation
 // ---------------------------------------------------------------------------
 
-// 52 KiB, so that three workgroups share a CU: A (dead once T is built) and
-// V (staged from registers after that) share storage, and the 32 x 32
-// scratch of the block recursion is T's upper-right quarter, which T never
-// uses (rows 0..31, columns 32..63).
+// 52 KiB, so that three workgroups share a CU.  The 32 x 32 scratch of the
+// block recursion is T's upper-right quarter, which T never uses (rows
+// 0..31, columns 32..63).
 struct PrepLds {
   uint16_t K[kChunk * kBfStride];
-  union {
-    float A[kChunk * kF64Stride];     // strict lower part of (I + A) minus I
-    uint16_t V[kChunk * kBfStride];
-  };
+  float A[kChunk * kF64Stride];       // strict lower part of (I + A) minus I
   float T[kChunk * kF64Stride];       // (I + A)^-1
   float gamma[kChunk];
   float beta[kChunk];
@@ -453,21 +463,14 @@ void prep_kernel(Params p) {
   const int g4 = lane >> 4;
   float* slot = p.slots + (static_cast<size_t>(c) * p.HV + hv) * kSlotFloats;
   uint16_t* slot16 = reinterpret_cast<uint16_t*>(slot);
-  // the group's first v-head writes the shared Q copy and K^T
-  const bool qk_writer = hv == h * p.ratio;
-  uint16_t* qk16 =
-      reinterpret_cast<uint16_t*>(p.qk_slots + (static_cast<size_t>(c) * p.H + h) * kQkSlotFloats);
 
   // Every input load of the chunk is issued before the first is waited on.
-  u32x4 kreg[4], vreg[4];
+  u32x4 kreg[4];
   load_rows_bf16(kreg, p.k + (static_cast<size_t>(t0) * p.H + h) * kDim,
                  static_cast<size_t>(p.H) * kDim, n);
-  load_rows_bf16(vreg, p.v + (static_cast<size_t>(t0) * p.HV + hv) * kDim,
-                 static_cast<size_t>(p.HV) * kDim, n);
 
   // Q rows 16 wave + col straight into MFMA operand registers (k block m;
-  // rows past the chunk's end zero), which are also the scan's
-  // operand-ordered copy of Q; with the L2-norm, their row norms.
+  // rows past the chunk's end zero); with the L2-norm, their row norms.
   s16x8 qa[4];
   const int ra = wave * 16 + col;
   const bool row_ok = ra < n;
@@ -483,7 +486,7 @@ void prep_kernel(Params p) {
   token_gates(p, t0 + (lane < n ? lane : n - 1), hv, logg, beta);
   if (lane >= n) logg = beta = 0.0f;
 
-  store_rows_bf16(lds.K, kreg, n);       // V waits in registers until A is dead
+  store_rows_bf16(lds.K, kreg, n);
   // T's upper blocks that the block recursion multiplies, T_01 and T_23, are
   // zero; the diagonal and lower blocks are all written, the other upper
   // blocks never read.
@@ -503,8 +506,6 @@ void prep_kernel(Params p) {
         const float x = bf16_to_f32(static_cast<uint16_t>(qa[m][e]));
         sq = fmaf(x, x, sq);
       }
-      if (qk_writer)
-        *reinterpret_cast<s16x8*>(qk16 + 2 * kQkSlotQ + (wave * 4 + m) * kBlk + lane * 8) = qa[m];
     }
     sq += __shfl_xor(sq, 16, 64);
     sq += __shfl_xor(sq, 32, 64);
@@ -582,12 +583,14 @@ void prep_kernel(Params p) {
         lds.A[(ia + e) * kF64Stride + j] = j < ia + e ? x : 0.0f;
       }
     }
-    // P[i][j], i = 16 wave + col, j = 16 nj + 4 g + e
+    // P[i][j], i = 16 wave + col, j = 16 nj + 4 g + e; the token blocks
+    // jb <= wave / 2 (the others are zero)
     const int i = wave * 16 + col;
     const float gi = lds.gamma[i];
     const float sqi = p.scale * lds.rq[i];
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb) {
+      if (jb > (wave >> 1)) break;                 // uniform per wave
       s16x4 hi[2], lo[2];
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
@@ -604,7 +607,7 @@ void prep_kernel(Params p) {
         }
         split4(pv, hi[hf], lo[hf]);
       }
-      const int bo = (wave * 2 + jb) * kBlk + lane * 8;
+      const int bo = tri_blk(wave, jb) * kBlk + lane * 8;
       *reinterpret_cast<s16x8*>(slot16 + 2 * kSlotPh + bo) = cat(hi[0], hi[1]);
       *reinterpret_cast<s16x8*>(slot16 + 2 * kSlotPl + bo) = cat(lo[0], lo[1]);
     }
@@ -655,7 +658,6 @@ void prep_kernel(Params p) {
     store16(&lds.T[16 * rb * kF64Stride + 32 + 16 * cb], kF64Stride, x, 1.0f, col, g4);
   }
   block_sync_lds();
-  store_rows_bf16(lds.V, vreg, n);       // A is dead: V takes its storage
   {
     const int rb = wave >> 1, cb = wave & 1;
     const float* Trow = &lds.T[(32 + 16 * rb) * kF64Stride + 32];
@@ -667,246 +669,278 @@ void prep_kernel(Params p) {
   }
   block_sync_lds();
 
-  // W = (T diag(beta e^gamma rk)) K (computed transposed, as K^T (T diag)^T,
-  // so the result registers are in the scan's operand order) and U =
-  // (T diag(beta)) V with bf16 MFMA over 32-token blocks jb: the scaled T is
-  // split into hi + lo, K and V are exact bf16.  Wave `wave` computes column
-  // tiles 2 wave and 2 wave + 1 (one 32-wide k block of W) for all row
-  // blocks; T is lower triangular, so token block 1 only meets row blocks
-  // 2 and 3.
-  {
-    f32x4 w[4][2], u[4][2];
+  // T diag(beta) in operand order: lower block (rb, kb) holds, for lane
+  // (col, g), T[16 rb + col][32 kb + k] beta[32 kb + k] at the 8 k of its
+  // items.  Wave w writes block w, waves 0 and 1 also blocks 4 and 5.
+  // Blocks (0, 0) and (2, 1) read T_01 and T_23 (zero); none reads the
+  // recursion's scratch quarter.
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
+  for (int rep = 0; rep < 2; ++rep) {
+    const int idx = wave + 4 * rep;
+    if (idx >= kTriBlocks) break;                  // uniform per wave
+    const int rb = idx < 3 ? idx : (idx + 2) >> 1;     // tri_blk(rb, kb) == idx
+    const int kb = idx == 3 || idx == 5 ? 1 : 0;
+    const float* trow = &lds.T[(16 * rb + col) * kF64Stride + 32 * kb + 4 * g4];
+    const float* brow = &lds.beta[32 * kb + 4 * g4];
+    s16x4 hi[2], lo[2];
 #pragma unroll
-      for (int q2 = 0; q2 < 2; ++q2) {
-        w[rb][q2] = f32x4{0, 0, 0, 0};
-        u[rb][q2] = f32x4{0, 0, 0, 0};
-      }
-#pragma unroll
-    for (int jb = 0; jb < 2; ++jb) {
-      s16x8 bk[2], bv[2];
-#pragma unroll
-      for (int q2 = 0; q2 < 2; ++q2) {
-        const int cc = (2 * wave + q2) * 16 + col;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int j = 32 * jb + k_of(g4, e);
-          bk[q2][e] = static_cast<short>(lds.K[j * kBfStride + cc]);
-          bv[q2][e] = static_cast<short>(lds.V[j * kBfStride + cc]);
-        }
-      }
-      f32x4 xs[2], ys[2];
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        const int j0 = 32 * jb + 16 * hf + 4 * g4;
-        ys[hf] = *reinterpret_cast<const f32x4*>(&lds.beta[j0]);
-        const f32x4 gj = *reinterpret_cast<const f32x4*>(&lds.gamma[j0]);
-        const f32x4 rkj = *reinterpret_cast<const f32x4*>(&lds.rk[j0]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) xs[hf][e] = ys[hf][e] * __expf(gj[e]) * rkj[e];
-      }
-#pragma unroll
-      for (int rb = 2 * jb; rb < 4; ++rb) {
-        const float* trow = &lds.T[(rb * 16 + col) * kF64Stride + 32 * jb + 4 * g4];
-        s16x4 wh[2], wl[2], uh[2], ul[2];
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          const f32x4 tv = *reinterpret_cast<const f32x4*>(trow + 16 * hf);
-          split4(tv * xs[hf], wh[hf], wl[hf]);
-          split4(tv * ys[hf], uh[hf], ul[hf]);
-        }
-        const s16x8 awh = cat(wh[0], wh[1]), awl = cat(wl[0], wl[1]);
-        const s16x8 auh = cat(uh[0], uh[1]), aul = cat(ul[0], ul[1]);
-#pragma unroll
-        for (int q2 = 0; q2 < 2; ++q2) {
-          // W^T tile (rows: key index, cols: token), U tile (rows: token)
-          w[rb][q2] = mfma_bf16(bk[q2], awh, w[rb][q2]);
-          w[rb][q2] = mfma_bf16(bk[q2], awl, w[rb][q2]);
-          u[rb][q2] = mfma_bf16(auh, bv[q2], u[rb][q2]);
-          u[rb][q2] = mfma_bf16(aul, bv[q2], u[rb][q2]);
-        }
-      }
-    }
-    // Lane (col, g) of W^T tile (rb, 2 wave + q2) holds W[16 rb + col][32
-    // wave + 16 q2 + 4 g + e]: items 4 q2 + e of the scan's operand block
-    // (rb, wave).
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-      s16x4 hi[2], lo[2];
-#pragma unroll
-      for (int q2 = 0; q2 < 2; ++q2) {
-        split4(w[rb][q2], hi[q2], lo[q2]);
-        *reinterpret_cast<f32x4*>(slot + kSlotU + ((rb * 8 + 2 * wave + q2) * 64 + lane) * 4) =
-            u[rb][q2];
-      }
-      const int bo = (rb * 4 + wave) * kBlk + lane * 8;
-      *reinterpret_cast<s16x8*>(slot16 + 2 * kSlotWh + bo) = cat(hi[0], hi[1]);
-      *reinterpret_cast<s16x8*>(slot16 + 2 * kSlotWl + bo) = cat(lo[0], lo[1]);
-    }
+    for (int hf = 0; hf < 2; ++hf)
+      split4(*reinterpret_cast<const f32x4*>(trow + 16 * hf) *
+                 *reinterpret_cast<const f32x4*>(brow + 16 * hf),
+             hi[hf], lo[hf]);
+    const int bo = idx * kBlk + lane * 8;
+    *reinterpret_cast<s16x8*>(slot16 + 2 * kSlotTh + bo) = cat(hi[0], hi[1]);
+    *reinterpret_cast<s16x8*>(slot16 + 2 * kSlotTl + bo) = cat(lo[0], lo[1]);
   }
 
-  // Row scales for the scan: Q rows, decayed K rows and the chunk decay.
+  // Row scales for the scan: the decayed K rows of X, the Q rows of the
+  // output, the K rows of the state update, and the chunk decay.
   if (wave == 1) {
     const float gl = lds.gamma[kChunk - 1];        // padded rows carry gamma forward
     const float gi = lds.gamma[lane];
+    const float rki = lds.rk[lane];
+    slot[kSlotXg + lane] = rki * __expf(gi);
     slot[kSlotQs + lane] = p.scale * lds.rq[lane] * __expf(gi);
-    slot[kSlotKs + lane] = lds.rk[lane] * __expf(gl - gi);
+    slot[kSlotKs + lane] = rki * __expf(gl - gi);
     slot[kSlotGl + lane] = __expf(gl);
-  }
-
-  // K^T (A operand of the scan's state update: rows = key index, k =
-  // token), in operand order, 16 bytes per store; rows past the chunk's end
-  // are zero.  A wave reads 64 consecutive keys of one token row at a time.
-  if (!qk_writer) return;                          // uniform per workgroup
-#pragma unroll
-  for (int it = 0; it < kDim * 8 / kThreads; ++it) {
-    const int idx = threadIdx.x + it * kThreads;
-    const int kc = idx & (kDim - 1);         // key index 0..127
-    const int jg = idx >> 7;                 // token block jb = jg / 4, lane group jg % 4
-    s16x8 v8;
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      v8[e] = static_cast<short>(lds.K[(32 * (jg >> 2) + k_of(jg & 3, e)) * kBfStride + kc]);
-    *reinterpret_cast<s16x8*>(qk16 + 2 * kQkSlotKt + ((kc >> 4) * 2 + (jg >> 2)) * kBlk +
-                              ((kc & 15) + 16 * (jg & 3)) * 8) = v8;
   }
 }
 
 // ---------------------------------------------------------------------------
-// 3. sequential scan over the chunks of a sequence
+// 3. the scan: one workgroup per (sequence, v-head), the whole state
 // ---------------------------------------------------------------------------
-// Every product is a bf16 MFMA (16x16x32); fp32 operands enter split into
-// hi + lo and a product x y is hi_x hi_y + hi_x lo_y + lo_x hi_y (the lo lo
-// term is ~2^-16 relative and dropped); q and k are bf16 already.  The state
-// slice and Delta are split once per chunk by the wave that owns them and
-// kept transposed in LDS, so every B operand is one 8-byte read.
-constexpr int kStStride = kDim + 8;     // S^T rows ([col][k]), bf16
-constexpr int kDtStride = kChunk + 8;   // Delta^T and K^T rows, bf16
+// Wave w keeps state columns 16 kScanCT w .. (the wave's kScanCT 16-column
+// tiles ct) of all 128 keys in registers, in the MFMA result layout:
+// st[t][ct] holds keys 16 t + 4 g + e of column 16 kScanCT w + 16 ct + col.  Read as runs of the k order,
+// the same registers are the state's operand of a product over keys in
+// either role (B of K S, A of S^T Q^T), and every per-chunk result is the
+// next product's operand in place, so the waves never exchange data: they
+// share only the chunk's inputs, staged in LDS once per chunk -- K rows and
+// Q rows (A of K S, B of S^T Q^T), K^T and V^T (A of the state update, and
+// X), and the chunk's workspace slot.  Per chunk, with S its start state:
+//   X      = V - diag(rk e^gamma) K S
+//   Delta  = T diag(beta) X
+//   O^T    = S^T Q^T diag(scale rq e^gamma) + Delta^T P^T
+//   S     <- e^gamma_C S + K^T diag(rk e^(gamma_C - gamma)) Delta
+// as bf16 MFMA (16x16x32): K, Q are bf16; S, X, Delta, T diag(beta) and P
+// enter split into hi + lo, and a product x y is hi_x hi_y + hi_x lo_y +
+// lo_x hi_y (the lo lo term is ~2^-16 relative and dropped).
+constexpr int kRowStride = kDim + 4;    // bf16 rows of 128 keys (K, Q): 66 dwords, so the
+                                        // 16 rows of an operand read hit distinct banks
+constexpr int kColStride = kChunk + 8;  // bf16 rows of 64 tokens (K^T, V^T)
+constexpr int kScanCT = 2;               // 16-column tiles of the state per wave
+constexpr int kScanWaves = 8 / kScanCT;  // one workgroup holds all 128 columns
+constexpr int kScanThreads = 64 * kScanWaves;
+constexpr int kKvLoads = 512 / kScanThreads;   // (token pair, 8 keys) units per thread
+constexpr int kQLoads = 1024 / kScanThreads;   // 16-byte pieces of Q per thread
+constexpr int kSlotPieces = kSlotFloats / 4;
+constexpr int kSlotLoads = (kSlotPieces + kScanThreads - 1) / kScanThreads;
 
-template <int NT>   // 16-column tiles of the state slice per workgroup
 struct ScanLds {
-  uint16_t Sh[16 * NT * kStStride];      // state slice^T at the chunk start, hi
-  uint16_t Sl[16 * NT * kStStride];      //   lo
-  uint16_t Dh[16 * NT * kDtStride];      // Delta^T [col][i], hi
-  uint16_t Dl[16 * NT * kDtStride];      //   lo
-  uint16_t Eh[16 * NT * kDtStride];      // (ks (.) Delta)^T, hi
-  uint16_t El[16 * NT * kDtStride];      //   lo
+  uint16_t Kr[kChunk * kRowStride];
+  uint16_t Qr[kChunk * kRowStride];
+  uint16_t Kt[kDim * kColStride];
+  uint16_t Vt[kDim * kColStride];
+  float slot[kSlotFloats];
+};
+static_assert(sizeof(ScanLds) <= 100 * 1024, "one scan workgroup per CU");
+
+// Token index XOR of K^T / V^T row r: a multiple of 4 below 32, so the
+// 4-token runs a lane reads stay whole and inside their 32-token block,
+// while the transposing writes of 16 consecutive 8-key groups spread over
+// the LDS banks.
+__device__ __forceinline__ int tok_swz(int r) { return ((r >> 3) & 7) << 2; }
+
+// The inputs of one chunk, loaded into registers a chunk ahead: per thread
+// two (token pair, 8 keys) units of K and V, four 16-byte pieces of Q and
+// kSlotLoads of the slot.  Rows >= n read row n - 1 and the pieces past the
+// slot read its last one, so that every load is unconditional.
+struct ScanStage {
+  u32x4 k[kKvLoads][2], v[kKvLoads][2], q[kQLoads];
+  f32x4 s[kSlotLoads];
 };
 
-// Per-lane operands of one chunk, loaded ahead of use.
-template <int NT>
-struct ScanOps {
-  s16x8 wh[4], wl[4];   // W rows 16 wave + (lane % 16), k block m (keys)
-  s16x8 q[4];           // Q rows (the slot's copy), same k
-  s16x8 ph[2], pl[2];   // P rows 16 wave + (lane % 16), k block m (tokens)
-  f32x4 u[NT];          // U rows 16 wave + 4 g + e, columns of the NT tiles
-  f32x4 ks;             // row scales of the same rows
-  float qs;             // output row scale of row 16 wave + (lane % 16)
-  float gl;             // chunk decay e^gamma_C
-  s16x8 kt[2][2];       // K^T rows 32 wave + 16 t + lane % 16, k block m (tokens)
-};
+// kbase / qbase / vbase: the chunk's first row of K and Q (q/k head h) and
+// of V (v-head hv); kstep / vstep: elements from one token's row to the next.
+__device__ __forceinline__ void scan_load(ScanStage& sg, const uint16_t* kbase,
+                                          const uint16_t* qbase, const uint16_t* vbase,
+                                          unsigned kstep, unsigned vstep, int n,
+                                          const float* slot) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int s = 0; s < kKvLoads; ++s) {
+    const int u = tid + s * kScanThreads;
+    const unsigned m8 = (u & 15) * 8;
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int r = 2 * (u >> 4) + hf;
+      const unsigned rr = r < n ? r : n - 1;
+      sg.k[s][hf] = *reinterpret_cast<const u32x4*>(kbase + (rr * kstep + m8));
+      sg.v[s][hf] = *reinterpret_cast<const u32x4*>(vbase + (rr * vstep + m8));
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < kQLoads; ++s) {
+    const int u = tid + s * kScanThreads;
+    const int r = u >> 4;
+    const unsigned rr = r < n ? r : n - 1;
+    sg.q[s] = *reinterpret_cast<const u32x4*>(qbase + (rr * kstep + (u & 15) * 8));
+  }
+#pragma unroll
+  for (int s = 0; s < kSlotLoads; ++s) {
+    const unsigned u = min(tid + s * kScanThreads, kSlotPieces - 1);
+    sg.s[s] = *reinterpret_cast<const f32x4*>(slot + 4 * u);
+  }
+}
 
-__device__ __forceinline__ s16x8 ld_s16x8(const uint16_t* ptr) {
+// Stage a chunk into LDS: rows >= n zero; V zero without values (the
+// transition columns).  K^T and V^T get two tokens per 4-byte write.
+__device__ __forceinline__ void scan_store(ScanLds& L, const ScanStage& sg, int n, bool values) {
+  const int tid = threadIdx.x;
+  const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int s = 0; s < kKvLoads; ++s) {
+    const int u = tid + s * kScanThreads;
+    const int m = u & 15;
+    const int r0 = 2 * (u >> 4);
+    const u32x4 k0 = r0 < n ? sg.k[s][0] : z;
+    const u32x4 k1 = r0 + 1 < n ? sg.k[s][1] : z;
+    const u32x4 v0 = values && r0 < n ? sg.v[s][0] : z;
+    const u32x4 v1 = values && r0 + 1 < n ? sg.v[s][1] : z;
+    *reinterpret_cast<u32x2*>(&L.Kr[r0 * kRowStride + m * 8]) = u32x2{k0.x, k0.y};
+    *reinterpret_cast<u32x2*>(&L.Kr[r0 * kRowStride + m * 8 + 4]) = u32x2{k0.z, k0.w};
+    *reinterpret_cast<u32x2*>(&L.Kr[(r0 + 1) * kRowStride + m * 8]) = u32x2{k1.x, k1.y};
+    *reinterpret_cast<u32x2*>(&L.Kr[(r0 + 1) * kRowStride + m * 8 + 4]) = u32x2{k1.z, k1.w};
+    const int tc = r0 ^ tok_swz(8 * m);              // the same for rows 8 m .. 8 m + 7
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      // low halves (even e) or high halves (odd e) of the two tokens' words
+      const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+      *reinterpret_cast<uint32_t*>(&L.Kt[(8 * m + e) * kColStride + tc]) =
+          __builtin_amdgcn_perm(k1[e >> 1], k0[e >> 1], sel);
+      *reinterpret_cast<uint32_t*>(&L.Vt[(8 * m + e) * kColStride + tc]) =
+          __builtin_amdgcn_perm(v1[e >> 1], v0[e >> 1], sel);
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < kQLoads; ++s) {
+    const int u = tid + s * kScanThreads;
+    const int r = u >> 4;
+    const u32x4 qv = r < n ? sg.q[s] : z;
+    *reinterpret_cast<u32x2*>(&L.Qr[r * kRowStride + (u & 15) * 8]) = u32x2{qv.x, qv.y};
+    *reinterpret_cast<u32x2*>(&L.Qr[r * kRowStride + (u & 15) * 8 + 4]) = u32x2{qv.z, qv.w};
+  }
+#pragma unroll
+  for (int s = 0; s < kSlotLoads; ++s) {
+    const int u = min(tid + s * kScanThreads, kSlotPieces - 1);
+    *reinterpret_cast<f32x4*>(&L.slot[4 * u]) = sg.s[s];
+  }
+}
+
+__device__ __forceinline__ s16x8 split_hi_lo(const f32x4& a, const f32x4& b, s16x8& lo) {
+  s16x4 ha, la, hb, lb;
+  split4(a, ha, la);
+  split4(b, hb, lb);
+  lo = cat(la, lb);
+  return cat(ha, hb);
+}
+
+__device__ __forceinline__ s16x8 ld_op(const float* ptr) {
   return *reinterpret_cast<const s16x8*>(ptr);
 }
 
-// Loads of one chunk's operands from its workspace slot.  Every load is
-// unconditional and in straight-line code so that the compiler can count the
-// loads in flight and wait only for the ones a use needs (a load under a
-// branch makes it drain every outstanding load); all of them are 1 KiB
-// contiguous wave accesses in the slot's operand order.
-template <int NT>
-__device__ __forceinline__ void load_w_q_u(const float* slot, const float* qk, int tile0,
-                                           int wave, int lane, int g4, ScanOps<NT>& o) {
-  const uint16_t* slot16 = reinterpret_cast<const uint16_t*>(slot);
-  const uint16_t* qk16 = reinterpret_cast<const uint16_t*>(qk);
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const int bo = (wave * 4 + m) * kBlk + lane * 8;
-    o.wh[m] = ld_s16x8(slot16 + 2 * kSlotWh + bo);
-    o.wl[m] = ld_s16x8(slot16 + 2 * kSlotWl + bo);
-    o.q[m] = ld_s16x8(qk16 + 2 * kQkSlotQ + bo);
-  }
-#pragma unroll
-  for (int cq = 0; cq < NT; ++cq)
-    o.u[cq] = *reinterpret_cast<const f32x4*>(slot + kSlotU +
-                                              ((wave * 8 + tile0 + cq) * 64 + lane) * 4);
-  o.ks = *reinterpret_cast<const f32x4*>(slot + kSlotKs + wave * 16 + g4 * 4);
-}
-
-template <int NT>
-__device__ __forceinline__ void load_p_qs(const float* slot, int wave, int lane,
-                                          ScanOps<NT>& o) {
-  const uint16_t* slot16 = reinterpret_cast<const uint16_t*>(slot);
-#pragma unroll
-  for (int m = 0; m < 2; ++m) {
-    const int bo = (wave * 2 + m) * kBlk + lane * 8;
-    o.ph[m] = ld_s16x8(slot16 + 2 * kSlotPh + bo);
-    o.pl[m] = ld_s16x8(slot16 + 2 * kSlotPl + bo);
-  }
-  o.qs = slot[kSlotQs + wave * 16 + (lane & 15)];
-  o.gl = slot[kSlotGl];
-}
-
-template <int NT>
-__device__ __forceinline__ void load_kt(const float* qk, int wave, int lane, ScanOps<NT>& o) {
-  const uint16_t* qk16 = reinterpret_cast<const uint16_t*>(qk);
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-#pragma unroll
-    for (int m = 0; m < 2; ++m)
-      o.kt[t][m] = ld_s16x8(qk16 + 2 * kQkSlotKt + ((wave * 2 + t) * 2 + m) * kBlk + lane * 8);
-  }
-}
-
-// One-dimensional grid over (head group of 8, column tile, head in group):
-// workgroup b serves head 8 (b / (8 tiles)) + b % 8 and tile (b / 8) % tiles.
-// Workgroups are handed to the 8 XCDs round-robin by index, so every tile of
-// a head runs on the same XCD (b % 8 is fixed) and the tiles are dispatched
-// 8 apart -- together -- sharing that XCD's L2 copy of the chunk operands
-// they all read.  Heads past N * HV (padding to a multiple of 8) exit.  FEW
-// as for prep_kernel.
-template <int NT, bool FEW>
-__global__ __launch_bounds__(kThreads) void scan_kernel(Params p) {
-  __shared__ ScanLds<NT> lds;
-  constexpr int kTiles = 8 / NT;
+// Grid: (unit, q/k head) pairs in groups of 8 times the GVA ratio.
+// Workgroup b serves pair 8 (b / (8 ratio)) + b % 8 and its v-head
+// (b / 8) % ratio: the v-heads that read the same K and Q are dispatched 8
+// apart, all to XCD b % 8 (workgroups go to the XCDs round-robin), and share
+// its L2 copy.  A unit is a sequence, or with SEG a role of one segment of
+// sequence 0: launch 1 (seg_pass 1) runs segment 0 with its outputs (end:
+// seg_S[1]), then segments 1 .. nseg-2 from a zero start (end: seg_B) and
+// from the identity without values (end: seg_M); launch 2 runs segments
+// 1 .. nseg-1 from seg_S with their outputs (the last one's end is the new
+// state).
+template <bool FEW, bool SEG>
+__global__ __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_eu(kScanWaves / 4, kScanWaves / 4)))
+void scan_kernel(Params p) {
+  __shared__ ScanLds L;
   const long long b = blockIdx.x;
-  const long long head_id = (b / (8 * kTiles)) * 8 + (b & 7);
-  if (head_id >= static_cast<long long>(p.N) * p.HV) return;   // uniform per workgroup
-  const int s = static_cast<int>(head_id / p.HV);
-  const int hv = static_cast<int>(head_id % p.HV);
-  const int tile0 = static_cast<int>((b >> 3) % kTiles) * NT;  // first 16-column tile
-  const int v0 = tile0 * 16;
+  const int ratio = p.ratio;
+  const long long pair = (b / (8LL * ratio)) * 8 + (b & 7);
+  const int jr = static_cast<int>((b >> 3) % ratio);
+  const long long units = SEG ? (p.seg_pass == 1 ? 2LL * p.nseg - 3 : p.nseg - 1)
+                              : static_cast<long long>(p.N);
+  if (pair >= units * p.H) return;                              // uniform per workgroup
+  const int unit = static_cast<int>(pair / p.H);
+  const int h = static_cast<int>(pair % p.H);
+  const int hv = h * ratio + jr;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int col = lane & 15;
   const int g4 = lane >> 4;
-  int start, end;
-  seq_range(p, s, start, end);
+  const size_t blk = static_cast<size_t>(kDim) * kDim;
 
-  // This wave's state tiles: rows k = 32 wave + 16 t + 4 g4 + e, columns
-  // v0 + 16 cq + col (k-last storage: 4 consecutive k are one 16-byte vector).
-  const size_t head = static_cast<size_t>(s) * p.HV + hv;
-  const float* st_in = p.state + head * kDim * kDim;
-  float* st_out = p.new_state + head * kDim * kDim;
-  f32x4 st[2][NT];
+  // role: start state, values, outputs, where the end state goes
+  const float* st_in = nullptr;       // null: zeros (or the identity)
+  bool identity = false, values = true, outputs = true;
+  float* st_out;
+  int s = 0, start, end, slot0 = 0, nchunks = 0;
+  if (SEG) {
+    int j;
+    if (p.seg_pass == 1) {
+      const int mid = p.nseg - 2;                 // segments 1 .. nseg-2
+      if (unit == 0) {
+        j = 0;
+        st_in = p.state ? p.state + static_cast<size_t>(hv) * blk : nullptr;
+        st_out = p.seg_S + (static_cast<size_t>(p.HV) + hv) * blk;
+      } else if (unit <= mid) {
+        j = unit;
+        outputs = false;
+        st_out = p.seg_B + (static_cast<size_t>(j) * p.HV + hv) * blk;
+      } else {
+        j = unit - mid;
+        identity = true;
+        values = outputs = false;
+        st_out = p.seg_M + (static_cast<size_t>(j) * p.HV + hv) * blk;
+      }
+    } else {
+      j = unit + 1;
+      st_in = p.seg_S + (static_cast<size_t>(j) * p.HV + hv) * blk;
+      st_out = j == p.nseg - 1 ? p.new_state + static_cast<size_t>(hv) * blk : nullptr;
+    }
+    seq_range(p, 0, start, end);               // one sequence: chunk c is slot c
+    const int total = (end - start + kChunk - 1) / kChunk;
+    slot0 = j * p.seg_chunks;
+    nchunks = min(p.seg_chunks, total - slot0);
+    start += slot0 * kChunk;
+    end = min(end, start + nchunks * kChunk);
+  } else {
+    s = unit;
+    seq_range(p, s, start, end);
+    st_in = p.state ? p.state + (static_cast<size_t>(s) * p.HV + hv) * blk : nullptr;
+    st_out = p.new_state + (static_cast<size_t>(s) * p.HV + hv) * blk;
+  }
+
+  // state registers; k-last storage: 4 consecutive keys are one 16-byte vector
+  f32x4 st[8][kScanCT];
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+  for (int t = 0; t < 8; ++t)
 #pragma unroll
-    for (int cq = 0; cq < NT; ++cq) {
-      const int kr = wave * 32 + t * 16 + g4 * 4;
-      st[t][cq] = (p.state != nullptr && end > start)
-                      ? *reinterpret_cast<const f32x4*>(
-                            st_in + static_cast<size_t>(v0 + cq * 16 + col) * kDim + kr)
+    for (int ct = 0; ct < kScanCT; ++ct) {
+      const int c = wave * 16 * kScanCT + ct * 16 + col;
+      const int kr = t * 16 + g4 * 4;
+      st[t][ct] = st_in != nullptr && (end > start || (SEG && p.seg_pass == 2))
+                      ? *reinterpret_cast<const f32x4*>(st_in + static_cast<size_t>(c) * kDim + kr)
                       : f32x4{0, 0, 0, 0};
+      if (identity) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) st[t][ct][e] = kr + e == c ? 1.0f : 0.0f;
+      }
     }
 
-  // Chunk count from the slot offsets (never more than the range holds, and
-  // never more slots than the workspace has, whatever cu_seqlens contains).
-  int slot0, nchunks;
-  if (p.single) {
-    slot0 = 0;
+  // Chunk slots of a sequence (never more than the range holds, and never
+  // more slots than the workspace has, whatever cu_seqlens contains).
+  if (SEG) {
+  } else if (p.single) {
     nchunks = (end - start + kChunk - 1) / kChunk;
   } else if (FEW) {
     const FewSlots f = few_slots(p);
@@ -916,150 +950,262 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Params p) {
     slot0 = p.offs[s];
     nchunks = p.offs[s + 1] - slot0;
   }
-  if (nchunks <= 0) {                 // no tokens: zeros, as the reference
+  // No tokens: a sequence ends in zeros, as the reference; a segment past
+  // the end of its sequence (cu_seqlens covering fewer tokens than L) passes
+  // its start through (transition: the identity, zero-start end: zeros), and
+  // so does the sequence's end state.
+  if (nchunks <= 0) {
+    if (st_out != nullptr) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < 8; ++t)
 #pragma unroll
-      for (int cq = 0; cq < NT; ++cq)
-        *reinterpret_cast<f32x4*>(st_out + static_cast<size_t>(v0 + cq * 16 + col) * kDim +
-                                  wave * 32 + t * 16 + g4 * 4) = f32x4{0, 0, 0, 0};
+        for (int ct = 0; ct < kScanCT; ++ct)
+          *reinterpret_cast<f32x4*>(st_out + static_cast<size_t>(wave * 16 * kScanCT + ct * 16 + col) * kDim +
+                                    t * 16 + g4 * 4) = SEG ? st[t][ct] : f32x4{0, 0, 0, 0};
+    }
     return;
   }
   const float* slot_base = p.slots + (static_cast<size_t>(slot0) * p.HV + hv) * kSlotFloats;
   const size_t slot_step = static_cast<size_t>(p.HV) * kSlotFloats;
-  const float* qk_base =
-      p.qk_slots + (static_cast<size_t>(slot0) * p.H + hv / p.ratio) * kQkSlotFloats;
-  const size_t qk_step = static_cast<size_t>(p.H) * kQkSlotFloats;
 
-  ScanOps<NT> op;
-  load_kt(qk_base, wave, lane, op);
-  load_w_q_u(slot_base, qk_base, tile0, wave, lane, g4, op);
-  load_p_qs(slot_base, wave, lane, op);
+  const unsigned kstep = static_cast<unsigned>(p.H) * kDim;
+  const unsigned vstep = static_cast<unsigned>(p.HV) * kDim;
+  auto stage = [&](ScanStage& sg, int c) {     // chunk c's loads
+    const int tc = start + c * kChunk;
+    const uint16_t* kb = p.k + (static_cast<size_t>(tc) * p.H + h) * kDim;
+    const uint16_t* qb = p.q + (static_cast<size_t>(tc) * p.H + h) * kDim;
+    const uint16_t* vb = p.v + (static_cast<size_t>(tc) * p.HV + hv) * kDim;
+    scan_load(sg, kb, qb, vb, kstep, vstep, min(kChunk, end - tc), slot_base + c * slot_step);
+  };
+  ScanStage sg;
+  stage(sg, 0);
 
   for (int ci = 0; ci < nchunks; ++ci) {
     const int t0 = start + ci * kChunk;
     const int n = min(kChunk, end - t0);
-    // operands of the next chunk, or of this one again after the last
-    const int cn = ci + 1 < nchunks ? ci + 1 : ci;
-    const float* slot_next = slot_base + cn * slot_step;
-    const float* qk_next = qk_base + cn * qk_step;
-
-    // A. state slice (split) into LDS.  No barrier is needed before these
-    // writes: the previous chunk's reads of Sh / Sl (step B) precede its
-    // second barrier.
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int cq = 0; cq < NT; ++cq) {
-        s16x4 hi, lo;
-        split4(st[t][cq], hi, lo);
-        const int so = (cq * 16 + col) * kStStride + wave * 32 + t * 16 + g4 * 4;
-        *reinterpret_cast<s16x4*>(&lds.Sh[so]) = hi;
-        *reinterpret_cast<s16x4*>(&lds.Sl[so]) = lo;
-      }
+    block_sync_lds();                  // every read of the previous chunk's LDS is done
+    scan_store(L, sg, n, values);
     block_sync_lds();
+    // the next chunk's inputs (after the last: this one's again), issued
+    // here and kept here, so that they arrive while this chunk computes
+    stage(sg, ci + 1 < nchunks ? ci + 1 : ci);
+    __builtin_amdgcn_sched_barrier(0);
 
-    // B. Delta rows 16 wave .. +15 = U - W S, and (Q S)^T for the output
-    // rows (S^T Q^T: the state fragment is the A operand, Q the B operand);
-    // two accumulators per product halve the dependent MFMA chains
-    f32x4 ws0[NT], ws1[NT], qs0[NT], qs1[NT];
+    // K S (token rows) and S^T Q^T (the output's first term, transposed),
+    // one 32-key block of the state at a time
+    f32x4 x[4][kScanCT], o[4][kScanCT];
 #pragma unroll
-    for (int cq = 0; cq < NT; ++cq) {
-      ws0[cq] = ws1[cq] = qs0[cq] = qs1[cq] = f32x4{0, 0, 0, 0};
-    }
+    for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
+      for (int ct = 0; ct < kScanCT; ++ct) x[r][ct] = o[r][ct] = f32x4{0, 0, 0, 0};
 #pragma unroll
-      for (int cq = 0; cq < NT; ++cq) {
-        const int so = (cq * 16 + col) * kStStride;
-        const s16x8 sh = frag(&lds.Sh[so], m, g4);
-        const s16x8 sl = frag(&lds.Sl[so], m, g4);
-        ws0[cq] = mfma_bf16(op.wh[m], sh, ws0[cq]);
-        ws1[cq] = mfma_bf16(op.wh[m], sl, ws1[cq]);
-        ws0[cq] = mfma_bf16(op.wl[m], sh, ws0[cq]);
-        qs0[cq] = mfma_bf16(sh, op.q[m], qs0[cq]);
-        qs1[cq] = mfma_bf16(sl, op.q[m], qs1[cq]);
-      }
-    }
-    f32x4 qsum[NT];       // (Q S)^T: lane (row i, g) holds columns 4 g + e
+    for (int kb = 0; kb < 4; ++kb) {
+      s16x8 sh[kScanCT], sl[kScanCT];
 #pragma unroll
-    for (int cq = 0; cq < NT; ++cq) {
-      const f32x4 ws = ws0[cq] + ws1[cq];
-      qsum[cq] = qs0[cq] + qs1[cq];
-      f32x4 d, dk;
+      for (int ct = 0; ct < kScanCT; ++ct) sh[ct] = split_hi_lo(st[2 * kb][ct], st[2 * kb + 1][ct], sl[ct]);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        d[e] = op.u[cq][e] - ws[e];
-        dk[e] = op.ks[e] * d[e];
-      }
-      s16x4 hi, lo;
-      const int dof = (cq * 16 + col) * kDtStride + wave * 16 + g4 * 4;
-      split4(d, hi, lo);
-      *reinterpret_cast<s16x4*>(&lds.Dh[dof]) = hi;
-      *reinterpret_cast<s16x4*>(&lds.Dl[dof]) = lo;
-      split4(dk, hi, lo);
-      *reinterpret_cast<s16x4*>(&lds.Eh[dof]) = hi;
-      *reinterpret_cast<s16x4*>(&lds.El[dof]) = lo;
-    }
-    load_w_q_u(slot_next, qk_next, tile0, wave, lane, g4, op);
-    block_sync_lds();
-
-    // C. output rows, transposed: qs (.) (Q S)^T + Delta^T P^T; lane (row
-    // i, g) ends with columns 4 g .. +3 of token row 16 wave + i, stored as
-    // one 8-byte piece
-    const int orow = wave * 16 + col;
+      for (int r = 0; r < 4; ++r) {
+        const s16x8 ak = frag(&L.Kr[(r * 16 + col) * kRowStride], kb, g4);
 #pragma unroll
-    for (int cq = 0; cq < NT; ++cq) {
-      f32x4 pd0 = {0, 0, 0, 0}, pd1 = {0, 0, 0, 0};
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        const int dof = (cq * 16 + col) * kDtStride;
-        const s16x8 dh = frag(&lds.Dh[dof], m, g4);
-        const s16x8 dl = frag(&lds.Dl[dof], m, g4);
-        pd0 = mfma_bf16(dh, op.ph[m], pd0);
-        pd1 = mfma_bf16(dl, op.ph[m], pd1);
-        pd0 = mfma_bf16(dh, op.pl[m], pd0);
-      }
-      const f32x4 pd = pd0 + pd1;
-      const float qsc = op.qs;
-      const u32x2 ob = {pack_bf16x2(fmaf(qsc, qsum[cq][0], pd[0]), fmaf(qsc, qsum[cq][1], pd[1])),
-                        pack_bf16x2(fmaf(qsc, qsum[cq][2], pd[2]), fmaf(qsc, qsum[cq][3], pd[3]))};
-      if (orow < n)
-        *reinterpret_cast<u32x2*>(p.out + ((static_cast<size_t>(t0) + orow) * p.HV + hv) * kDim +
-                                  v0 + cq * 16 + g4 * 4) = ob;
-    }
-
-    // D. state rows 32 wave .. +31: S = e^gamma_C S + K^T (ks (.) Delta)
-    const float gl = op.gl;
-    s16x8 kt[2][2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int m = 0; m < 2; ++m) kt[t][m] = op.kt[t][m];
-    load_p_qs(slot_next, wave, lane, op);
-    load_kt(qk_next, wave, lane, op);
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int cq = 0; cq < NT; ++cq) {
-        f32x4 acc0 = st[t][cq] * gl;
-        f32x4 acc1 = {0, 0, 0, 0};
-#pragma unroll
-        for (int m = 0; m < 2; ++m) {
-          const int eo = (cq * 16 + col) * kDtStride;
-          acc0 = mfma_bf16(kt[t][m], frag(&lds.Eh[eo], m, g4), acc0);
-          acc1 = mfma_bf16(kt[t][m], frag(&lds.El[eo], m, g4), acc1);
+        for (int ct = 0; ct < kScanCT; ++ct) {
+          x[r][ct] = mfma_bf16(ak, sh[ct], x[r][ct]);
+          x[r][ct] = mfma_bf16(ak, sl[ct], x[r][ct]);
         }
-        st[t][cq] = acc0 + acc1;
+        if (outputs) {                                   // uniform
+          const s16x8 bq = frag(&L.Qr[(r * 16 + col) * kRowStride], kb, g4);
+#pragma unroll
+          for (int ct = 0; ct < kScanCT; ++ct) {
+            o[r][ct] = mfma_bf16(sh[ct], bq, o[r][ct]);
+            o[r][ct] = mfma_bf16(sl[ct], bq, o[r][ct]);
+          }
+        }
       }
+    }
+
+    // X = V - diag(rk e^gamma) K S: lane (col, g) holds tokens 16 r + 4 g + e
+    // of column 32 wave + 16 ct + col
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const f32x4 xg = *reinterpret_cast<const f32x4*>(&L.slot[kSlotXg + r * 16 + g4 * 4]);
+#pragma unroll
+      for (int ct = 0; ct < kScanCT; ++ct) {
+        const int c = wave * 16 * kScanCT + ct * 16 + col;
+        const u32x2 vv = *reinterpret_cast<const u32x2*>(
+            &L.Vt[c * kColStride + ((r * 16 + g4 * 4) ^ tok_swz(c))]);
+        const f32x4 vf = {__uint_as_float(vv.x << 16), __uint_as_float(vv.x & 0xffff0000u),
+                          __uint_as_float(vv.y << 16), __uint_as_float(vv.y & 0xffff0000u)};
+        x[r][ct] = vf - xg * x[r][ct];
+      }
+    }
+
+    // Delta = T diag(beta) X (T lower triangular: token blocks kb <= r / 2)
+    s16x8 xh[2][kScanCT], xl[2][kScanCT];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int ct = 0; ct < kScanCT; ++ct) xh[kb][ct] = split_hi_lo(x[2 * kb][ct], x[2 * kb + 1][ct], xl[kb][ct]);
+    f32x4 d[4][kScanCT];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+#pragma unroll
+      for (int ct = 0; ct < kScanCT; ++ct) d[r][ct] = f32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int kb = 0; kb <= (r >> 1); ++kb) {
+        const int bo = tri_blk(r, kb) * kBlkF + lane * 4;
+        const s16x8 th = ld_op(&L.slot[kSlotTh + bo]);
+        const s16x8 tl = ld_op(&L.slot[kSlotTl + bo]);
+#pragma unroll
+        for (int ct = 0; ct < kScanCT; ++ct) {
+          d[r][ct] = mfma_bf16(th, xh[kb][ct], d[r][ct]);
+          d[r][ct] = mfma_bf16(th, xl[kb][ct], d[r][ct]);
+          d[r][ct] = mfma_bf16(tl, xh[kb][ct], d[r][ct]);
+        }
+      }
+    }
+
+    // Delta as operand: A of Delta^T P^T and, scaled by ks, B of the update
+    s16x8 dh[2][kScanCT], dl[2][kScanCT], eh[2][kScanCT], el[2][kScanCT];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const f32x4 ks0 = *reinterpret_cast<const f32x4*>(&L.slot[kSlotKs + kb * 32 + g4 * 4]);
+      const f32x4 ks1 = *reinterpret_cast<const f32x4*>(&L.slot[kSlotKs + kb * 32 + 16 + g4 * 4]);
+#pragma unroll
+      for (int ct = 0; ct < kScanCT; ++ct) {
+        if (outputs) dh[kb][ct] = split_hi_lo(d[2 * kb][ct], d[2 * kb + 1][ct], dl[kb][ct]);
+        eh[kb][ct] = split_hi_lo(d[2 * kb][ct] * ks0, d[2 * kb + 1][ct] * ks1, el[kb][ct]);
+      }
+    }
+
+    // O^T = qs (.) S^T Q^T + Delta^T P^T; lane (col, g) ends with columns
+    // 32 wave + 16 ct + 4 g + e of token 16 r + col, one 8-byte store
+    if (outputs) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float qs = L.slot[kSlotQs + r * 16 + col];
+#pragma unroll
+        for (int ct = 0; ct < kScanCT; ++ct) o[r][ct] = o[r][ct] * qs;
+#pragma unroll
+        for (int kb = 0; kb <= (r >> 1); ++kb) {
+          const int bo = tri_blk(r, kb) * kBlkF + lane * 4;
+          const s16x8 ph = ld_op(&L.slot[kSlotPh + bo]);
+          const s16x8 pl = ld_op(&L.slot[kSlotPl + bo]);
+#pragma unroll
+          for (int ct = 0; ct < kScanCT; ++ct) {
+            o[r][ct] = mfma_bf16(dh[kb][ct], ph, o[r][ct]);
+            o[r][ct] = mfma_bf16(dh[kb][ct], pl, o[r][ct]);
+            o[r][ct] = mfma_bf16(dl[kb][ct], ph, o[r][ct]);
+          }
+        }
+        const int tok = r * 16 + col;
+#pragma unroll
+        for (int ct = 0; ct < kScanCT; ++ct) {
+          const u32x2 ob = {pack_bf16x2(o[r][ct][0], o[r][ct][1]),
+                            pack_bf16x2(o[r][ct][2], o[r][ct][3])};
+          if (tok < n)
+            *reinterpret_cast<u32x2*>(p.out + ((static_cast<size_t>(t0) + tok) * p.HV + hv) * kDim +
+                                      wave * 16 * kScanCT + ct * 16 + g4 * 4) = ob;
+        }
+      }
+    }
+
+    // S <- e^gamma_C S + K^T (ks (.) Delta), key tile t
+    const float gl = L.slot[kSlotGl];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int key = t * 16 + col;
+      const uint16_t* krow = &L.Kt[key * kColStride];
+      const int sw = tok_swz(key);
+      f32x4 acc[kScanCT];
+#pragma unroll
+      for (int ct = 0; ct < kScanCT; ++ct) acc[ct] = st[t][ct] * gl;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const s16x8 ak = cat(*reinterpret_cast<const s16x4*>(krow + ((kb * 32 + g4 * 4) ^ sw)),
+                             *reinterpret_cast<const s16x4*>(krow + ((kb * 32 + 16 + g4 * 4) ^ sw)));
+#pragma unroll
+        for (int ct = 0; ct < kScanCT; ++ct) {
+          acc[ct] = mfma_bf16(ak, eh[kb][ct], acc[ct]);
+          acc[ct] = mfma_bf16(ak, el[kb][ct], acc[ct]);
+        }
+      }
+#pragma unroll
+      for (int ct = 0; ct < kScanCT; ++ct) st[t][ct] = acc[ct];
+    }
   }
 
+  if (st_out != nullptr) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int ct = 0; ct < kScanCT; ++ct)
+        *reinterpret_cast<f32x4*>(st_out + static_cast<size_t>(wave * 16 * kScanCT + ct * 16 + col) * kDim +
+                                  t * 16 + g4 * 4) = st[t][ct];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 4. segments of one long sequence: chain the segment starts
+// ---------------------------------------------------------------------------
+// The first scan launch leaves, per v-head, S_1 and each middle segment's
+// transition M_j and zero-start end state B_j.  Combine: S_{j+1} = M_j S_j +
+// B_j for j = 1 .. nseg-2, segment after segment, with fp32 MFMA
+// (v_mfma_f32_16x16x4_f32).  One workgroup per (v-head, 16 state columns);
+// wavefront w computes key rows 32 w .. 32 w + 31 (two 16-row tiles), S_j
+// staged in LDS for the B operand.
+constexpr int kCombStride = kDim + 1;        // LDS column stride (no bank conflicts)
+
+__global__ __launch_bounds__(kThreads) void seg_combine_kernel(Params p) {
+  __shared__ float Sl[16 * kCombStride];     // S_j columns c0 .. c0 + 15, [col][k]
+  const int hv = blockIdx.x >> 3;
+  const int c0 = (blockIdx.x & 7) * 16;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int col = lane & 15;
+  const int g4 = lane >> 4;
+  const size_t blk = static_cast<size_t>(kDim) * kDim;
+  // S_1 in the MFMA result layout: tile t, lane col + 16 g4, register e is
+  // key 32 wave + 16 t + 4 g4 + e of column c0 + col
+  f32x4 S[2];
+  const float* s1 = p.seg_S + (static_cast<size_t>(p.HV) + hv) * blk;
 #pragma unroll
   for (int t = 0; t < 2; ++t)
+    S[t] = *reinterpret_cast<const f32x4*>(s1 + static_cast<size_t>(c0 + col) * kDim +
+                                           wave * 32 + t * 16 + g4 * 4);
+  for (int j = 1; j + 1 < p.nseg; ++j) {
 #pragma unroll
-    for (int cq = 0; cq < NT; ++cq)
-      *reinterpret_cast<f32x4*>(st_out + static_cast<size_t>(v0 + cq * 16 + col) * kDim +
-                                wave * 32 + t * 16 + g4 * 4) = st[t][cq];
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) Sl[col * kCombStride + wave * 32 + t * 16 + g4 * 4 + e] = S[t][e];
+    __syncthreads();
+    const float* M = p.seg_M + (static_cast<size_t>(j) * p.HV + hv) * blk;
+    const float* Bj = p.seg_B + (static_cast<size_t>(j) * p.HV + hv) * blk;
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      acc[t][0] = *reinterpret_cast<const f32x4*>(Bj + static_cast<size_t>(c0 + col) * kDim +
+                                                  wave * 32 + t * 16 + g4 * 4);
+      acc[t][1] = f32x4{0, 0, 0, 0};
+    }
+    // (M S)[k][c] = sum_k2 M[k][k2] S[k2][c]; A[i][kk] = M[row i][4 s + kk] from
+    // lane i + 16 kk, B[kk][c] = S[4 s + kk][c] from lane c + 16 kk
+    for (int st = 0; st < kDim / 4; ++st) {
+      const int k2 = 4 * st + g4;
+      const float bv = Sl[col * kCombStride + k2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const float av = M[static_cast<size_t>(k2) * kDim + wave * 32 + t * 16 + col];
+        acc[t][st & 1] = mfma_f32(av, bv, acc[t][st & 1]);
+      }
+    }
+    __syncthreads();                          // every read of Sl before the next writes
+    float* dst = p.seg_S + (static_cast<size_t>(j + 1) * p.HV + hv) * blk;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      S[t] = acc[t][0] + acc[t][1];
+      *reinterpret_cast<f32x4*>(dst + static_cast<size_t>(c0 + col) * kDim + wave * 32 +
+                                t * 16 + g4 * 4) = S[t];
+    }
+  }
 }
 
 bool aligned(const void* ptr, uintptr_t a) {
@@ -1069,8 +1215,8 @@ bool aligned(const void* ptr, uintptr_t a) {
 size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
 // Workspace: chunk offsets [N + 1] int32, slot table [max_slots] x 16 bytes,
-// the v-head slots [max_slots, HV, kSlotFloats] fp32, then the q/k-head
-// slots [max_slots, H, kQkSlotFloats]; each part 256-byte aligned.
+// the v-head slots [max_slots, HV, kSlotFloats] fp32, then with segments
+// their S, B and M blocks; each part 256-byte aligned.
 size_t offsets_bytes(long long N) { return align256(static_cast<size_t>(N + 1) * sizeof(int32_t)); }
 
 size_t slot_info_bytes(long long L, long long N) {
@@ -1078,12 +1224,37 @@ size_t slot_info_bytes(long long L, long long N) {
 }
 
 size_t slots_bytes(long long L, long long N, long long HV) {
-  return static_cast<size_t>(max_slots(L, N)) * HV * kSlotFloats * sizeof(float);
+  return align256(static_cast<size_t>(max_slots(L, N)) * HV * kSlotFloats * sizeof(float));
+}
+
+// Segments of one long sequence.  Its plain scan is a chain of chunk steps on
+// HV workgroups; with few v-heads that leaves most of the GPU idle (16384
+// tokens at 8 v-heads: 256 steps on 8 CUs), so the sequence is cut into
+// segments of kSegChunks chunks scanned at once: the two scan launches run
+// (2 nseg - 3) HV and (nseg - 1) HV workgroups of kSegChunks steps each, the
+// combine nseg - 2 small steps.
+constexpr int kSegChunks = 16;         // chunks per segment
+constexpr int kSegMinChunks = 48;      // shorter sequences are scanned whole
+constexpr long long kSegMaxHV = 32;    // more v-heads fill the GPU without segments
+
+bool use_segments(long long L, long long N, long long HV) {
+  return N == 1 && HV <= kSegMaxHV && (L + kChunk - 1) / kChunk >= kSegMinChunks;
+}
+
+long long num_segments(long long L) {
+  return ((L + kChunk - 1) / kChunk + kSegChunks - 1) / kSegChunks;
+}
+
+// Per segment and v-head one 128 x 128 fp32 block (S, B and M each).
+size_t seg_blocks_bytes(long long L, long long HV) {
+  return align256(static_cast<size_t>(num_segments(L)) * HV * kDim * kDim * sizeof(float));
 }
 
 size_t workspace_bytes(long long L, long long N, long long H, long long HV) {
-  return offsets_bytes(N) + slot_info_bytes(L, N) + slots_bytes(L, N, HV) +
-         static_cast<size_t>(max_slots(L, N)) * H * kQkSlotFloats * sizeof(float);
+  (void)H;
+  size_t bytes = offsets_bytes(N) + slot_info_bytes(L, N) + slots_bytes(L, N, HV);
+  if (use_segments(L, N, HV)) bytes += 3 * seg_blocks_bytes(L, HV);
+  return bytes;
 }
 
 }  // namespace gdn_pf
@@ -1204,7 +1375,7 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
   }
   const long long slots = max_slots(total_seq_len, num_seqs);
   if (slots > 0x7fffffffLL || num_seqs > 0x7fffffff - 1) return hipErrorInvalidValue;
-  if ((static_cast<long long>(num_seqs) * HV + 7) / 8 * 64 > 0x7fffffffLL)   // scan grid
+  if ((static_cast<long long>(num_seqs) * H + 7) / 8 * 8 * (HV / H) > 0x7fffffffLL)  // scan grid
     return hipErrorInvalidValue;
   if (fixed_scratch) {
     const hipError_t e = current_scratch(&workspace);
@@ -1230,8 +1401,19 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
   p.slot_info = slot_info;
   p.slots = reinterpret_cast<float*>(ws + offsets_bytes(num_seqs) +
                                      slot_info_bytes(total_seq_len, num_seqs));
-  p.qk_slots = reinterpret_cast<float*>(reinterpret_cast<char*>(p.slots) +
-                                        slots_bytes(total_seq_len, num_seqs, HV));
+  p.seg_chunks = 0;
+  p.nseg = 0;
+  p.seg_pass = 0;
+  p.seg_S = p.seg_B = p.seg_M = nullptr;
+  if (use_segments(total_seq_len, num_seqs, HV)) {
+    char* sg = reinterpret_cast<char*>(p.slots) + slots_bytes(total_seq_len, num_seqs, HV);
+    const size_t blocks = seg_blocks_bytes(total_seq_len, HV);
+    p.seg_chunks = kSegChunks;
+    p.nseg = static_cast<int>(num_segments(total_seq_len));
+    p.seg_S = reinterpret_cast<float*>(sg);
+    p.seg_B = reinterpret_cast<float*>(sg + blocks);
+    p.seg_M = reinterpret_cast<float*>(sg + 2 * blocks);
+  }
   p.scale = scale;
   p.L = total_seq_len;
   p.N = num_seqs;
@@ -1277,18 +1459,30 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
   }
   e = mark(2);
   if (e != hipSuccess) return e;
-  // Two 16-column tiles per workgroup once there are enough heads to fill
-  // the GPU with them (fewer redundant operand loads); one tile otherwise.
-  const long long heads = static_cast<long long>(num_seqs) * HV;
-  const long long groups = (heads + 7) / 8;
-  if (heads >= kScanWideHeads) {
-    auto* scan = p.few ? scan_kernel<2, true> : scan_kernel<2, false>;
-    hipLaunchKernelGGL(scan, dim3(static_cast<unsigned>(groups * 8 * 4)), dim3(kThreads), 0,
+  // One workgroup per (sequence or segment role, v-head), in groups of 8
+  // (unit, q/k head) pairs times the GVA ratio.
+  auto scan_grid = [&](long long units) {
+    return dim3(static_cast<unsigned>((units * H + 7) / 8 * 8 * p.ratio));
+  };
+  if (p.nseg > 1) {
+    // segments (one sequence): transitions and segment 0, the starts, the rest
+    p.seg_pass = 1;
+    hipLaunchKernelGGL((scan_kernel<false, true>), scan_grid(2LL * p.nseg - 3), dim3(kScanThreads),
+                       0, stream, p);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (p.nseg > 2) {
+      hipLaunchKernelGGL(seg_combine_kernel, dim3(static_cast<unsigned>(HV) * 8), dim3(kThreads),
+                         0, stream, p);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    }
+    p.seg_pass = 2;
+    hipLaunchKernelGGL((scan_kernel<false, true>), scan_grid(p.nseg - 1LL), dim3(kScanThreads), 0,
                        stream, p);
   } else {
-    auto* scan = p.few ? scan_kernel<1, true> : scan_kernel<1, false>;
-    hipLaunchKernelGGL(scan, dim3(static_cast<unsigned>(groups * 8 * 8)), dim3(kThreads), 0,
-                       stream, p);
+    auto* scan = p.few ? scan_kernel<true, false> : scan_kernel<false, false>;
+    hipLaunchKernelGGL(scan, scan_grid(num_seqs), dim3(kScanThreads), 0, stream, p);
   }
   e = hipGetLastError();
   if (e == hipSuccess) e = mark(3);
@@ -1342,6 +1536,8 @@ int gdn_prefill_token_path_max_tokens(void) { return kSmallTokens; }
 int gdn_prefill_dispatches(int total_seq_len, int num_seqs, int HV) {
   if (num_seqs <= 0 || total_seq_len < 0 || HV <= 0) return 0;
   if (total_seq_len <= kSmallTokens && num_seqs <= 65535) return 1;
+  if (use_segments(total_seq_len, num_seqs, HV))
+    return num_segments(total_seq_len) > 2 ? 4 : 3;
   return num_seqs == 1 || few_seqs(total_seq_len, num_seqs, HV) ? 2 : 3;
 }
 

@@ -44,11 +44,13 @@ extern "C" {
 
 /*
  * Bytes of device workspace gdn_prefill needs for L total tokens, N
- * sequences, H q/k heads and HV v-heads: per-chunk intermediates (about
- * 81 KiB per chunk per v-head and 32 KiB per chunk per q/k head, for
- * min(ceil(L / 64) + N, L) chunks, the most a well-formed batch has), a
- * 16-byte table entry per chunk and 4 bytes per sequence.  0 for invalid
- * sizes.
+ * sequences, H q/k heads and HV v-heads: per-chunk intermediates (25 KiB
+ * per chunk per v-head, for min(ceil(L / 64) + N, L) chunks, the most a
+ * well-formed batch has, rounded up to 256 bytes), a 16-byte table entry per
+ * chunk and 4 bytes per sequence, each part rounded up to 256 bytes; for one
+ * sequence of at least 48 chunks at HV <= 32 (scanned in segments of 16
+ * chunks), also 3 x 64 KiB per segment per v-head.
+ * 0 for invalid sizes.
  * The reference's FLA path allocates its intermediates per call inside
  * chunk_gated_delta_rule (solution/triton/fla_prefill_code.py:1726-1776);
  * here the caller provides them.
@@ -68,7 +70,10 @@ size_t gdn_prefill_workspace_bytes(int total_seq_len, int num_seqs, int H, int H
  * q, k, v, output, state and new_state must be 16-byte aligned.
  * Launches one kernel when total_seq_len <= gdn_prefill_token_path_max_tokens()
  * (and num_seqs <= 65535), else the chunkwise kernels: the chunk-offsets
- * scan (only when gdn_prefill_dispatches returns 3), preparation, scan.
+ * scan (only when gdn_prefill_dispatches returns 3), preparation, scan (for
+ * one long sequence with few v-heads: segments of it scanned at once in two
+ * launches with the combination of their starts between them, see
+ * gdn_prefill_dispatches).
  */
 int gdn_prefill(const void* q, const void* k, const void* v, const float* state,
                 const float* A_log, const void* a, const float* dt_bias, const void* b,
@@ -81,7 +86,8 @@ int gdn_prefill(const void* q, const void* k, const void* v, const float* state,
  * Measurement hook, no counterpart in the reference: gdn_prefill with
  * events[0..3] (hipEvent_t, all non-null) recorded on hip_stream before the
  * offsets, preparation and scan launches and after the scan, so that
- * hipEventElapsedTime gives each kernel's time.  Without an offsets launch
+ * hipEventElapsedTime gives each kernel's time (the segmented scan's two or
+ * three launches lie between events 2 and 3).  Without an offsets launch
  * (one sequence, or few: see gdn_prefill_dispatches) events 0 and 1 are
  * recorded back to back; on the
  * token-by-token path events 0..2 are, and its one launch lies between
@@ -130,7 +136,10 @@ int gdn_prefill_token_path_max_tokens(void);
 
 /*
  * Kernel launches gdn_prefill makes for these sizes: 0 for no sequences, 1
- * on the token-by-token path, 2 (preparation, scan) for one sequence or for
+ * on the token-by-token path, 4 (preparation, first segment scan, combine,
+ * second segment scan) for one sequence of at least 48 chunks at HV <= 32
+ * (3, without the combine, for two segments), 2
+ * (preparation, scan) for another single sequence or for
  * at most 64 with at most 2048 preparation workgroups (min(ceil(L / 64) + N,
  * L) x HV; the kernels then find the chunk slots from cu_seqlens
  * themselves), 3 (the chunk-offsets scan first) otherwise.  No counterpart in the

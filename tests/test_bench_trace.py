@@ -135,3 +135,35 @@ def test_traffic_only_from_a_summary_of_the_timed_kernel(tmp_path, monkeypatch):
     path.write_text(json.dumps({"kernel": kernel, "sources_sha": "0" * 16,
                                 "traffic_bytes_per_launch": 123}))
     assert bench._traffic(kernel)[0] is None
+
+
+def test_prefill_counter_summary_and_its_sources_check(tmp_path, monkeypatch):
+    """The prefill summary scales prep and scan by the calibration copies,
+    skips the first prefill, and the roofline reads it only while the
+    prefill sources are the ones it was measured on."""
+    import json
+
+    copy = "__amd_rocclr_copyBuffer"
+    prep = "void gdn_pf::prep_kernel<false>(gdn_pf::Params)"
+    scan = "void gdn_pf::scan_kernel<false, false>(gdn_pf::Params)"
+    off = "gdn_pf::chunk_offsets_kernel(gdn_pf::Params, int*, int __vector(4)*)"
+    mib = 1024 * 1024
+    calls = [(off, 1.0), (prep, 5.0), (scan, 7.0)] + [(off, 1.0), (prep, 100.0), (scan, 300.0)] * 2
+    _pmc_csv(tmp_path / "f.csv", "FETCH_SIZE", [(copy, 128.0 * 1024)] * 3 + calls)
+    _pmc_csv(tmp_path / "w.csv", "WRITE_SIZE", [(copy, 256.0 * 1024)] * 3 + calls)
+    monkeypatch.setattr(bench, "ROOT", tmp_path)
+    for rel in bench.PREFILL_SOURCES:
+        (tmp_path / rel).parent.mkdir(parents=True, exist_ok=True)
+        (tmp_path / rel).write_text(rel)
+    res = bench.summarize_pmc_prefill(tmp_path / "f.csv", tmp_path / "w.csv")
+    assert res["kernels"]["prep"]["fetch_bytes_per_launch"] == 100 * 1024 * 2   # fetch reads half
+    assert res["kernels"]["scan"]["write_bytes_per_launch"] == 300 * 1024
+    assert res["traffic_bytes_per_prefill"] == (100 * 2 + 100 + 300 * 2 + 300) * 1024
+    lens, H, HV = bench.PREFILL_CONFIGS[bench.PREFILL_ROOFLINE_WORKLOAD]
+    assert res["algorithmic_bytes_per_prefill"] == bench.prefill_bytes(lens, H, HV)
+    path = tmp_path / "prefill_traffic.json"
+    monkeypatch.setattr(bench, "PREFILL_TRAFFIC_SUMMARY", path)
+    path.write_text(json.dumps(res))
+    assert bench._prefill_traffic() == {"prep": 300 * 1024, "scan": 900 * 1024}
+    (tmp_path / bench.PREFILL_SOURCES[0]).write_text("changed")
+    assert bench._prefill_traffic() is None

@@ -120,6 +120,65 @@ def test_bench_size_prefills_match_the_fp64_oracle(lens, H, HV, a_log_range, hip
     _announce(f"  max |out - fp64| {do:.3e}, max |state - fp64| {ds:.3e}")
 
 
+@pytest.mark.parametrize("lens,H,HV,l2,with_state", [
+    ([3072], 4, 8, False, True),      # 48 chunks: 3 segments of 16, the fewest segmented
+    ([5000], 4, 16, False, True),     # 79 chunks: a partial last chunk and last segment
+    ([4100], 1, 1, False, True),      # 65 chunks: a one-chunk last segment, one head
+    ([3500], 2, 4, True, False),      # L2-norm, no initial state (segment 0 from zeros)
+    ([3100], 2, 6, False, True),      # GVA ratio 3
+])
+def test_segmented_long_sequence(lens, H, HV, l2, with_state, hip_device):
+    """One sequence of >= 48 chunks at <= 16 v-heads runs in segments of 16
+    chunks scanned at once (each from a zero start, with its 128 x 128
+    transition), combined, and the outputs of later segments corrected for
+    their true start: against the float64 chunked oracle at the prefill
+    bars."""
+    L = sum(lens)
+    assert gdn.prefill.prefill_dispatches(L, 1, HV) == 4
+    _announce(f"segmented prefill L={L} H={H} HV={HV} l2={l2} state={with_state}")
+    t = make_prefill_inputs(lens, H, HV, seed=400 + L + HV, with_state=with_state,
+                            unit_qk=not l2)
+    out, st = gdn.prefill_run(**_dev(t, hip_device), use_qk_l2norm=l2)
+    torch.cuda.synchronize()
+    do, ds = _check(t, out, st, l2=l2, loop=False)
+    _announce(f"  max |out - fp64| {do:.3e}, max |state - fp64| {ds:.3e}")
+
+
+def test_segmented_in_place_and_timed(hip_device):
+    """Segmented path: in place equals out of place bitwise, and the timed
+    entry gives the same bits with its events around the three scan-side
+    launches."""
+    import ctypes
+    _announce("segmented prefill in place / timed")
+    t = _dev(make_prefill_inputs([3200], 4, 8, seed=410), hip_device)
+    ref_o, ref_s = gdn.prefill_run(**t)
+    state = t["state"].clone()
+    out = torch.empty_like(ref_o)
+    gdn.kernel_prefill_hip(**{**t, "state": state}, output=out, new_state=state)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref_o) and torch.equal(state, ref_s)
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    evs = []
+    for _ in range(4):
+        e = ctypes.c_void_p()
+        assert hip.hipEventCreate(ctypes.byref(e)) == 0
+        evs.append(e)
+    try:
+        out2, st2 = torch.empty_like(ref_o), torch.empty_like(ref_s)
+        gdn.kernel_prefill_hip_timed(**t, output=out2, new_state=st2, events=evs)
+        torch.cuda.synchronize()
+        assert torch.equal(out2, ref_o) and torch.equal(st2, ref_s)
+        ms = []
+        for i in range(3):
+            x = ctypes.c_float()
+            assert hip.hipEventElapsedTime(ctypes.byref(x), evs[i], evs[i + 1]) == 0
+            ms.append(x.value)
+        assert ms[1] > 0.0 and ms[2] > 0.0, ms
+    finally:
+        for e in evs:
+            hip.hipEventDestroy(e)
+
+
 def test_l2norm_and_no_state(hip_device):
     _announce("prefill l2norm, state=None, raw-scale q/k")
     t = make_prefill_inputs([40, 90], 4, 8, seed=12, with_state=False, unit_qk=False)

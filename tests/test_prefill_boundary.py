@@ -40,15 +40,28 @@ def test_header_and_library_agree():
 
 def test_workspace_size_formula():
     lib = _lib.get_prefill_lib()
-    vslot = (2 * 64 * 128 + 64 * 64 + 3 * 64) * 4        # per v-head: W hi/lo, U, P hi/lo, scales
-    qkslot = 2 * 128 * 64 * 2                             # per q/k head: K^T, Q copy (bf16)
+    # per v-head: T diag(beta) and P (six 16 x 32 operand blocks each, bf16
+    # hi and lo), then four rows of 64 scales
+    vslot = (4 * 6 * 16 * 32 * 2 + 4 * 64 * 4)
+    a256 = lambda x: (x + 255) // 256 * 256  # noqa: E731
     for L, N, H, HV in ((6, 1, 4, 8), (16384, 1, 4, 8), (1000, 37, 16, 32), (0, 3, 4, 8),
-                        (100, 2, 2, 2), (40, 65600, 1, 1), (3, 10, 4, 8)):
+                        (100, 2, 2, 2), (40, 65600, 1, 1), (3, 10, 4, 8), (3000, 1, 4, 8),
+                        (3072, 1, 4, 8), (5000, 1, 16, 16), (8192, 1, 16, 32),
+                        (8192, 1, 16, 64), (2048, 1, 4, 8)):
         chunks = min((L + 63) // 64 + N, L)          # the most a well-formed batch has
-        offs = ((N + 1) * 4 + 255) // 256 * 256
-        table = (chunks * 16 + 255) // 256 * 256                         # per-chunk slot table
-        assert lib.gdn_prefill_workspace_bytes(L, N, H, HV) == (
-            offs + table + chunks * HV * vslot + chunks * H * qkslot)
+        offs = a256((N + 1) * 4)
+        table = a256(chunks * 16)                                        # per-chunk slot table
+        want = offs + table + a256(chunks * HV * vslot)
+        # one sequence of >= 48 chunks at <= 32 v-heads: segments of 16 chunks
+        seg = N == 1 and HV <= 32 and (L + 63) // 64 >= 48
+        nseg = ((L + 63) // 64 + 15) // 16
+        if seg:
+            want += 3 * a256(nseg * HV * 128 * 128 * 4)
+        assert lib.gdn_prefill_workspace_bytes(L, N, H, HV) == want, (L, N, H, HV)
+        assert lib.gdn_prefill_dispatches(L, N, HV) == (
+            0 if N == 0 else 1 if L <= 48 and N <= 65535 else
+            (4 if nseg > 2 else 3) if seg else
+            2 if N == 1 or (N <= 64 and chunks * HV <= 2048) else 3), (L, N, HV)
     assert lib.gdn_prefill_workspace_bytes(-1, 1, 4, 8) == 0
     assert lib.gdn_prefill_workspace_bytes(1, 1, 4, 0) == 0
     assert lib.gdn_prefill_workspace_bytes(1, 1, 3, 8) == 0              # HV % H != 0

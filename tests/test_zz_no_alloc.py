@@ -83,12 +83,12 @@ def test_noalloc_rejects_sizes_beyond_its_workspace(hip_device):
     hipErrorOutOfMemory before launching anything (outputs untouched) and the
     Python entry raises ValueError naming the limit."""
     _announce("noalloc rejects oversize")
-    lens, H, HV = [4096] * 2, 16, 32
+    lens, H, HV = [4096] * 3, 16, 32
     assert gdn.prefill.workspace_bytes(sum(lens), len(lens), H, HV) > \
         gdn.prefill.NOALLOC_SCRATCH_BYTES
     t = _dev(make_prefill_inputs(lens, H, HV, seed=320), hip_device)
     out = torch.zeros_like(t["v"])
-    st = torch.zeros(2, HV, 128, 128, device=hip_device)
+    st = torch.zeros(len(lens), HV, 128, 128, device=hip_device)
     assert _noalloc_c_abi(t, out, st) == 2
     torch.cuda.synchronize()
     assert torch.count_nonzero(out) == 0 and torch.count_nonzero(st) == 0
