@@ -40,17 +40,18 @@
 //      hi + lo in the order the scan's MFMAs read them, and the row scales.
 //   3. scan, one workgroup per (sequence, v-head), XCD-aware order: the
 //      sequential part chunk after chunk with the whole 128 x 128 state in
-//      the registers of four wavefronts (32 columns each); the chunk's K, Q,
-//      V and slot are staged in LDS, loaded a chunk ahead.  Products with
-//      fp32 operands run as bf16 MFMA on hi/lo splits.  Each workgroup reads
-//      its chunks' inputs once, so the workspace is the only HBM traffic
-//      beyond the algorithmic bytes.
-//   One long sequence is cut into segments of kSegChunks chunks, since its
-//   scan alone would occupy HV workgroups for the whole run: a first scan
-//   launch runs segment 0 with its outputs and, from each later segment's
-//   start, the transition columns (an identity start, no values) and the
-//   zero-start end state; a combine kernel chains the segment starts; a
-//   second scan launch runs segments 1.. from their starts with the outputs.
+//      the registers of four wavefronts (32 columns each); the chunk's K,
+//      Q rows and slot reach LDS by DMA a chunk ahead, into the other of two
+//      buffers.  Products with fp32 operands run as bf16 MFMA on hi/lo
+//      splits.  Each workgroup reads its chunks' inputs once, so the
+//      workspace is the only HBM traffic beyond the algorithmic bytes.
+//   One long sequence at few v-heads is cut into segments, since its scan
+//   alone would occupy HV workgroups for the whole run: a first scan launch
+//   runs, without outputs, segment 0 from the sequence's state and, from
+//   each later segment's start, the transition columns (an identity start,
+//   no values) and the zero-start end state; a combine kernel chains the
+//   segment starts; a second scan launch runs every segment from its start
+//   with the outputs.
 //
 // MFMA lane layouts (v_mfma_f32_16x16x4_f32, v_mfma_f32_16x16x32_bf16):
 // A[i][k] from lane i + 16 g, B[k][j] from lane j + 16 g (k = g for fp32;
@@ -233,7 +234,6 @@ struct Params {
   // blocks in k-last order (element (k, c) at c * 128 + k).
   int seg_chunks;            // chunks per segment, 0: no segments
   int nseg;                  // segments
-  int seg_pass;              // scan launch 1 (transitions) or 2 (outputs)
   float* seg_S;              // [nseg, HV] state at each segment's start (1 .. nseg-1)
   float* seg_B;              // [nseg, HV] state at its end from a zero start
   float* seg_M;              // [nseg, HV] its transition: end = M start + B (M[k][k'])
@@ -709,131 +709,111 @@ void prep_kernel(Params p) {
 // ---------------------------------------------------------------------------
 // 3. the scan: one workgroup per (sequence, v-head), the whole state
 // ---------------------------------------------------------------------------
-// Wave w keeps state columns 16 kScanCT w .. (the wave's kScanCT 16-column
-// tiles ct) of all 128 keys in registers, in the MFMA result layout:
-// st[t][ct] holds keys 16 t + 4 g + e of column 16 kScanCT w + 16 ct + col.  Read as runs of the k order,
+// Wave w keeps state columns 32 w .. 32 w + 31 (two 16-column tiles ct) of
+// all 128 keys in registers, in the MFMA result layout: st[t][ct] holds keys
+// 16 t + 4 g + e of column 32 w + 16 ct + col.  Read as runs of the k order,
 // the same registers are the state's operand of a product over keys in
 // either role (B of K S, A of S^T Q^T), and every per-chunk result is the
-// next product's operand in place, so the waves never exchange data: they
-// share only the chunk's inputs, staged in LDS once per chunk -- K rows and
-// Q rows (A of K S, B of S^T Q^T), K^T and V^T (A of the state update, and
-// X), and the chunk's workspace slot.  Per chunk, with S its start state:
+// next product's operand in place, so the waves never exchange data.  Per
+// chunk, with S its start state:
 //   X      = V - diag(rk e^gamma) K S
 //   Delta  = T diag(beta) X
 //   O^T    = S^T Q^T diag(scale rq e^gamma) + Delta^T P^T
 //   S     <- e^gamma_C S + K^T diag(rk e^(gamma_C - gamma)) Delta
-// as bf16 MFMA (16x16x32): K, Q are bf16; S, X, Delta, T diag(beta) and P
-// enter split into hi + lo, and a product x y is hi_x hi_y + hi_x lo_y +
+// as bf16 MFMA (16x16x32): K, Q, V are bf16; S, X, Delta, T diag(beta) and
+// P enter split into hi + lo, and a product x y is hi_x hi_y + hi_x lo_y +
 // lo_x hi_y (the lo lo term is ~2^-16 relative and dropped).
-constexpr int kRowStride = kDim + 4;    // bf16 rows of 128 keys (K, Q): 66 dwords, so the
-                                        // 16 rows of an operand read hit distinct banks
-constexpr int kColStride = kChunk + 8;  // bf16 rows of 64 tokens (K^T, V^T)
-constexpr int kScanCT = 2;               // 16-column tiles of the state per wave
-constexpr int kScanWaves = 8 / kScanCT;  // one workgroup holds all 128 columns
+//
+// The waves share the chunk's K rows, Q rows and workspace slot, which the
+// LDS DMA (global_load_lds_dwordx4: each lane's 16 bytes land at the wave's
+// LDS base + 16 lane, no registers) brings into one of two LDS buffers while
+// the chunk before runs on the other, so a chunk needs one barrier.  The
+// operands with tokens as the contracted index come from products with a
+// selector (a 32 x 16 block of the identity), which moves a 16 x 32 row
+// block's columns into the result layout exactly: V^T tiles (each wave's own
+// 32 columns of V, loaded into registers a chunk ahead) and K^T tiles (from
+// the K rows in LDS).
+constexpr int kScanWaves = 4;
 constexpr int kScanThreads = 64 * kScanWaves;
-constexpr int kKvLoads = 512 / kScanThreads;   // (token pair, 8 keys) units per thread
-constexpr int kQLoads = 1024 / kScanThreads;   // 16-byte pieces of Q per thread
-constexpr int kSlotPieces = kSlotFloats / 4;
-constexpr int kSlotLoads = (kSlotPieces + kScanThreads - 1) / kScanThreads;
+constexpr int kRowPieces = kDim / 8 + 1;          // 16-byte pieces per K / Q row, one of padding
+constexpr int kRowStride = kRowPieces * 8;        // bf16 (68 dwords)
+constexpr int kRowDma = kChunk * kRowPieces / 64; // DMA instructions per K / Q chunk (17)
+constexpr int kSlotDma = kSlotFloats / 4 / 64;    // DMA instructions per slot (25)
+static_assert(kChunk * kRowPieces % 64 == 0 && kSlotFloats % 256 == 0, "whole DMA instructions");
+// Without outputs a chunk needs neither Q nor P: its LDS slot holds T
+// diag(beta) (hi, lo) and then the row scales.
+constexpr int kSlotTFloats = 2 * kTriBlocks * kBlkF;
+constexpr int kSlotGates = kSlotFloats - kSlotXg;     // the four rows of scales
+static_assert(kSlotTFloats == kSlotPh && kSlotXg == 2 * kSlotTFloats, "slot layout");
 
-struct ScanLds {
+template <bool OUT> struct ScanBuf;
+template <> struct ScanBuf<true> {
   uint16_t Kr[kChunk * kRowStride];
   uint16_t Qr[kChunk * kRowStride];
-  uint16_t Kt[kDim * kColStride];
-  uint16_t Vt[kDim * kColStride];
   float slot[kSlotFloats];
 };
-static_assert(sizeof(ScanLds) <= 100 * 1024, "one scan workgroup per CU");
-
-// Token index XOR of K^T / V^T row r: a multiple of 4 below 32, so the
-// 4-token runs a lane reads stay whole and inside their 32-token block,
-// while the transposing writes of 16 consecutive 8-key groups spread over
-// the LDS banks.
-__device__ __forceinline__ int tok_swz(int r) { return ((r >> 3) & 7) << 2; }
-
-// The inputs of one chunk, loaded into registers a chunk ahead: per thread
-// two (token pair, 8 keys) units of K and V, four 16-byte pieces of Q and
-// kSlotLoads of the slot.  Rows >= n read row n - 1 and the pieces past the
-// slot read its last one, so that every load is unconditional.
-struct ScanStage {
-  u32x4 k[kKvLoads][2], v[kKvLoads][2], q[kQLoads];
-  f32x4 s[kSlotLoads];
+template <> struct ScanBuf<false> {
+  uint16_t Kr[kChunk * kRowStride];
+  float slot[kSlotTFloats + kSlotGates];
 };
+static_assert(2 * sizeof(ScanBuf<true>) <= 160 * 1024, "one scan workgroup per CU");
+// LDS offset of the row scales (Xg, then Qs, Ks, Gl as in the slot)
+template <bool OUT> __device__ constexpr int lds_gates() { return OUT ? kSlotXg : kSlotTFloats; }
 
-// kbase / qbase / vbase: the chunk's first row of K and Q (q/k head h) and
-// of V (v-head hv); kstep / vstep: elements from one token's row to the next.
-__device__ __forceinline__ void scan_load(ScanStage& sg, const uint16_t* kbase,
-                                          const uint16_t* qbase, const uint16_t* vbase,
-                                          unsigned kstep, unsigned vstep, int n,
-                                          const float* slot) {
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int s = 0; s < kKvLoads; ++s) {
-    const int u = tid + s * kScanThreads;
-    const unsigned m8 = (u & 15) * 8;
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      const int r = 2 * (u >> 4) + hf;
-      const unsigned rr = r < n ? r : n - 1;
-      sg.k[s][hf] = *reinterpret_cast<const u32x4*>(kbase + (rr * kstep + m8));
-      sg.v[s][hf] = *reinterpret_cast<const u32x4*>(vbase + (rr * vstep + m8));
+typedef __attribute__((address_space(1))) void global_void;
+typedef __attribute__((address_space(3))) void lds_void;
+
+// One wave's DMA instruction: lane l's 16 bytes from src_l to dst + 16 l
+// (dst the same for the whole wave).
+__device__ __forceinline__ void dma16(const void* src_l, void* dst) {
+  __builtin_amdgcn_global_load_lds((global_void*)src_l, (lds_void*)dst, 16, 0, 0);
+}
+
+// Wait for this wave's outstanding vector memory operations (its DMA among
+// them): s_waitcnt vmcnt(0), the other counters left alone.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// DMA of a chunk's K rows, Q rows (OUT; rows >= n repeat row n - 1; each
+// row's padding piece repeats its last piece) and slot (without outputs: T
+// diag(beta) and the row scales) into one LDS buffer; wave w issues
+// instructions w, w + 4, ....
+template <bool OUT>
+__device__ __forceinline__ void scan_dma(ScanBuf<OUT>& B, const uint16_t* kbase,
+                                         const uint16_t* qbase, unsigned step, int n,
+                                         const float* slot, int wave, int lane) {
+  for (int i = wave; i < kRowDma; i += kScanWaves) {        // uniform per wave
+    const int pc = i * 64 + lane;
+    const int r = pc / kRowPieces, c = pc % kRowPieces;
+    const unsigned off = static_cast<unsigned>(r < n ? r : n - 1) * step + (c < 16 ? c : 15) * 8;
+    dma16(kbase + off, &B.Kr[i * 512]);
+    if constexpr (OUT) dma16(qbase + off, &B.Qr[i * 512]);
+  }
+  if constexpr (OUT) {
+    for (int i = wave; i < kSlotDma; i += kScanWaves)
+      dma16(slot + (i * 64 + lane) * 4, &B.slot[i * 256]);
+  } else {
+    constexpr int kT = kSlotTFloats / 256, kG = kSlotGates / 256;
+    for (int i = wave; i < kT + kG; i += kScanWaves) {
+      const int from = i < kT ? i * 256 : kSlotXg + (i - kT) * 256;
+      dma16(slot + from + lane * 4, &B.slot[i * 256]);
     }
-  }
-#pragma unroll
-  for (int s = 0; s < kQLoads; ++s) {
-    const int u = tid + s * kScanThreads;
-    const int r = u >> 4;
-    const unsigned rr = r < n ? r : n - 1;
-    sg.q[s] = *reinterpret_cast<const u32x4*>(qbase + (rr * kstep + (u & 15) * 8));
-  }
-#pragma unroll
-  for (int s = 0; s < kSlotLoads; ++s) {
-    const unsigned u = min(tid + s * kScanThreads, kSlotPieces - 1);
-    sg.s[s] = *reinterpret_cast<const f32x4*>(slot + 4 * u);
   }
 }
 
-// Stage a chunk into LDS: rows >= n zero; V zero without values (the
-// transition columns).  K^T and V^T get two tokens per 4-byte write.
-__device__ __forceinline__ void scan_store(ScanLds& L, const ScanStage& sg, int n, bool values) {
-  const int tid = threadIdx.x;
-  const u32x4 z = {0u, 0u, 0u, 0u};
+// This wave's 32 columns of V for token tile r as a 16 x 32 A operand
+// (lane (col, g): token 16 r + col, rows >= n repeating row n - 1).
+struct VFrags {
+  u32x2 lo[4], hi[4];
+};
+__device__ __forceinline__ void load_v(VFrags& f, const uint16_t* vbase, unsigned step, int n,
+                                       int wave, int col, int g4) {
 #pragma unroll
-  for (int s = 0; s < kKvLoads; ++s) {
-    const int u = tid + s * kScanThreads;
-    const int m = u & 15;
-    const int r0 = 2 * (u >> 4);
-    const u32x4 k0 = r0 < n ? sg.k[s][0] : z;
-    const u32x4 k1 = r0 + 1 < n ? sg.k[s][1] : z;
-    const u32x4 v0 = values && r0 < n ? sg.v[s][0] : z;
-    const u32x4 v1 = values && r0 + 1 < n ? sg.v[s][1] : z;
-    *reinterpret_cast<u32x2*>(&L.Kr[r0 * kRowStride + m * 8]) = u32x2{k0.x, k0.y};
-    *reinterpret_cast<u32x2*>(&L.Kr[r0 * kRowStride + m * 8 + 4]) = u32x2{k0.z, k0.w};
-    *reinterpret_cast<u32x2*>(&L.Kr[(r0 + 1) * kRowStride + m * 8]) = u32x2{k1.x, k1.y};
-    *reinterpret_cast<u32x2*>(&L.Kr[(r0 + 1) * kRowStride + m * 8 + 4]) = u32x2{k1.z, k1.w};
-    const int tc = r0 ^ tok_swz(8 * m);              // the same for rows 8 m .. 8 m + 7
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      // low halves (even e) or high halves (odd e) of the two tokens' words
-      const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-      *reinterpret_cast<uint32_t*>(&L.Kt[(8 * m + e) * kColStride + tc]) =
-          __builtin_amdgcn_perm(k1[e >> 1], k0[e >> 1], sel);
-      *reinterpret_cast<uint32_t*>(&L.Vt[(8 * m + e) * kColStride + tc]) =
-          __builtin_amdgcn_perm(v1[e >> 1], v0[e >> 1], sel);
-    }
-  }
-#pragma unroll
-  for (int s = 0; s < kQLoads; ++s) {
-    const int u = tid + s * kScanThreads;
-    const int r = u >> 4;
-    const u32x4 qv = r < n ? sg.q[s] : z;
-    *reinterpret_cast<u32x2*>(&L.Qr[r * kRowStride + (u & 15) * 8]) = u32x2{qv.x, qv.y};
-    *reinterpret_cast<u32x2*>(&L.Qr[r * kRowStride + (u & 15) * 8 + 4]) = u32x2{qv.z, qv.w};
-  }
-#pragma unroll
-  for (int s = 0; s < kSlotLoads; ++s) {
-    const int u = min(tid + s * kScanThreads, kSlotPieces - 1);
-    *reinterpret_cast<f32x4*>(&L.slot[4 * u]) = sg.s[s];
+  for (int r = 0; r < 4; ++r) {
+    const int row = r * 16 + col;
+    const uint16_t* p = vbase + static_cast<unsigned>(row < n ? row : n - 1) * step + wave * 32 +
+                        g4 * 4;
+    f.lo[r] = *reinterpret_cast<const u32x2*>(p);
+    f.hi[r] = *reinterpret_cast<const u32x2*>(p + 16);
   }
 }
 
@@ -849,26 +829,289 @@ __device__ __forceinline__ s16x8 ld_op(const float* ptr) {
   return *reinterpret_cast<const s16x8*>(ptr);
 }
 
+// bf16 values held in fp32 back to bf16 (exact), 4 at a time.
+__device__ __forceinline__ s16x4 to_bf16x4(const f32x4& x) {
+  const u32x2 w = {pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])};
+  return __builtin_bit_cast(s16x4, w);
+}
+
+// The per-workgroup constants of a scan.
+struct ScanCtx {
+  const uint16_t* k;
+  const uint16_t* q;
+  const uint16_t* v;
+  uint16_t* out;
+  const float* slot_base;      // the first chunk's slot
+  size_t slot_step;            // floats from one chunk's slot to the next
+  unsigned kstep, vstep;       // elements from one token's K / Q row (V row) to the next
+  int start, end, nchunks;     // token range and chunks
+  int H, HV, h, hv;
+  bool values;
+};
+
+// Chunk c's DMA into buf and its V into registers.
+template <bool OUT>
+__device__ __forceinline__ void scan_issue(ScanBuf<OUT>* buf, const ScanCtx& cx, int c, VFrags& vf) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int tc = cx.start + c * kChunk;
+  const int nc = min(kChunk, cx.end - tc);
+  scan_dma(*buf, cx.k + (static_cast<size_t>(tc) * cx.H + cx.h) * kDim,
+           cx.q + (static_cast<size_t>(tc) * cx.H + cx.h) * kDim, cx.kstep, nc,
+           cx.slot_base + c * cx.slot_step, wave, lane);
+  load_v(vf, cx.v + (static_cast<size_t>(tc) * cx.HV + cx.hv) * kDim, cx.vstep, nc, wave,
+         lane & 15, lane >> 4);
+}
+
+// Chunk ci from buffer B, with the next chunk's DMA into Bn.  B and Bn are
+// restrict: the compiler then knows that the DMA in flight into Bn never
+// writes what this chunk reads from B, and waits for it only at the end.
+// OUT: the outputs too (else only the state).
+template <bool OUT>
+__device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
+                                           ScanBuf<OUT>* __restrict__ Bn,
+                                           const ScanCtx& cx, f32x4 (&st)[8][2], VFrags& vnext,
+                                           const s16x8 (&sel)[2], int ci) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int col = lane & 15;
+  const int g4 = lane >> 4;
+  const int t0 = cx.start + ci * kChunk;
+  const int n = min(kChunk, cx.end - t0);
+  const VFrags vf = vnext;
+  // the next chunk's inputs into the other buffer (after the last chunk:
+  // this one's again, unused), in flight while this chunk computes
+  // the chunk's row scales, read before the DMA below is issued
+  constexpr int kG = lds_gates<OUT>();
+  f32x4 xg[4], ks[4];
+  float qs[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    xg[r] = *reinterpret_cast<const f32x4*>(&B->slot[kG + r * 16 + g4 * 4]);
+    ks[r] = *reinterpret_cast<const f32x4*>(&B->slot[kG + 128 + r * 16 + g4 * 4]);
+    qs[r] = OUT ? B->slot[kG + 64 + r * 16 + col] : 0.0f;
+  }
+  const float gl = B->slot[kG + 192];
+  scan_issue(Bn, cx, ci + 1 < cx.nchunks ? ci + 1 : ci, vnext);
+
+  // K S (token rows) and S^T Q^T (the output's first term, transposed),
+  // one 32-key block of the state at a time
+  f32x4 x[4][2], o[4][2];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) x[r][ct] = o[r][ct] = f32x4{0, 0, 0, 0};
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    s16x8 sh[2], sl[2];
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) sh[ct] = split_hi_lo(st[2 * kb][ct], st[2 * kb + 1][ct], sl[ct]);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const s16x8 ak = frag(&B->Kr[(r * 16 + col) * kRowStride], kb, g4);
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        x[r][ct] = mfma_bf16(ak, sh[ct], x[r][ct]);
+        x[r][ct] = mfma_bf16(ak, sl[ct], x[r][ct]);
+      }
+      if constexpr (OUT) {
+        const s16x8 bq = frag(&B->Qr[(r * 16 + col) * kRowStride], kb, g4);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+          o[r][ct] = mfma_bf16(sh[ct], bq, o[r][ct]);
+          o[r][ct] = mfma_bf16(sl[ct], bq, o[r][ct]);
+        }
+      }
+    }
+  }
+
+  // X = V - diag(rk e^gamma) K S: lane (col, g) holds tokens 16 r + 4 g + e
+  // of column 32 wave + 16 ct + col; V^T tiles from the selector products
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const s16x8 av = cx.values ? __builtin_bit_cast(s16x8, u32x4{vf.lo[r].x, vf.lo[r].y,
+                                                            vf.hi[r].x, vf.hi[r].y})
+                            : s16x8{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      const f32x4 v = mfma_bf16(av, sel[ct], f32x4{0, 0, 0, 0});
+      x[r][ct] = v - xg[r] * x[r][ct];
+    }
+  }
+
+  // Delta = T diag(beta) X (T lower triangular: token blocks kb <= r / 2)
+  s16x8 xh[2][2], xl[2][2];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) xh[kb][ct] = split_hi_lo(x[2 * kb][ct], x[2 * kb + 1][ct], xl[kb][ct]);
+  f32x4 d[4][2];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) d[r][ct] = f32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int kb = 0; kb <= (r >> 1); ++kb) {
+      const int bo = tri_blk(r, kb) * kBlkF + lane * 4;
+      const s16x8 th = ld_op(&B->slot[kSlotTh + bo]);
+      const s16x8 tl = ld_op(&B->slot[kSlotTl + bo]);
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        d[r][ct] = mfma_bf16(th, xh[kb][ct], d[r][ct]);
+        d[r][ct] = mfma_bf16(th, xl[kb][ct], d[r][ct]);
+        d[r][ct] = mfma_bf16(tl, xh[kb][ct], d[r][ct]);
+      }
+    }
+  }
+
+  // Delta as operand: A of Delta^T P^T and, scaled by ks, B of the update
+  s16x8 dh[2][2], dl[2][2], eh[2][2], el[2][2];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    const f32x4 ks0 = ks[2 * kb], ks1 = ks[2 * kb + 1];
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      if constexpr (OUT) dh[kb][ct] = split_hi_lo(d[2 * kb][ct], d[2 * kb + 1][ct], dl[kb][ct]);
+      eh[kb][ct] = split_hi_lo(d[2 * kb][ct] * ks0, d[2 * kb + 1][ct] * ks1, el[kb][ct]);
+    }
+  }
+
+  // O^T = qs (.) S^T Q^T + Delta^T P^T; lane (col, g) ends with columns
+  // 32 wave + 16 ct + 4 g + e of token 16 r + col, one 8-byte store
+  if constexpr (OUT) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) o[r][ct] = o[r][ct] * qs[r];
+#pragma unroll
+      for (int kb = 0; kb <= (r >> 1); ++kb) {
+        const int bo = tri_blk(r, kb) * kBlkF + lane * 4;
+        const s16x8 ph = ld_op(&B->slot[kSlotPh + bo]);
+        const s16x8 pl = ld_op(&B->slot[kSlotPl + bo]);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+          o[r][ct] = mfma_bf16(dh[kb][ct], ph, o[r][ct]);
+          o[r][ct] = mfma_bf16(dh[kb][ct], pl, o[r][ct]);
+          o[r][ct] = mfma_bf16(dl[kb][ct], ph, o[r][ct]);
+        }
+      }
+      const int tok = r * 16 + col;
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        const u32x2 ob = {pack_bf16x2(o[r][ct][0], o[r][ct][1]),
+                          pack_bf16x2(o[r][ct][2], o[r][ct][3])};
+        if (tok < n)
+          *reinterpret_cast<u32x2*>(cx.out + ((static_cast<size_t>(t0) + tok) * cx.HV + cx.hv) * kDim +
+                                    wave * 32 + ct * 16 + g4 * 4) = ob;
+      }
+    }
+  }
+
+  // S <- e^gamma_C S + K^T (ks (.) Delta).  Keys 32 m .. 32 m + 31 (tiles
+  // t = 2 m + hf): the selector products of the K row blocks (r, m) give
+  // lane (col, g) tokens 16 r + 4 g + e of key 16 t + col, the K^T operand
+  // items of token block r / 2.
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    s16x4 kt[4][2];                                  // [token tile r][hf]
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const s16x8 ak = frag(&B->Kr[(r * 16 + col) * kRowStride], m, g4);
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+        kt[r][hf] = to_bf16x4(mfma_bf16(ak, sel[hf], f32x4{0, 0, 0, 0}));
+    }
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int t = 2 * m + hf;
+      f32x4 acc[2];
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) acc[ct] = st[t][ct] * gl;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const s16x8 ak = cat(kt[2 * kb][hf], kt[2 * kb + 1][hf]);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+          acc[ct] = mfma_bf16(ak, eh[kb][ct], acc[ct]);
+          acc[ct] = mfma_bf16(ak, el[kb][ct], acc[ct]);
+        }
+      }
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) st[t][ct] = acc[ct];
+    }
+  }
+
+  wait_vmem();                       // the next chunk's DMA has landed
+  block_sync_lds();                  // for every wave; this buffer's reads are done
+}
+
+// The end state of a scan: k-last fp32 (element (k, c) at c * 128 + k), or,
+// for a transition M (identity start), as the A operand blocks of the
+// combine's product M S: for row tile t and column block kb, 64 lanes x 8
+// bf16, hi then lo (block ((t * 4 + kb) * 2 + hl) * 512).  Wave w holds
+// columns 32 w .. 32 w + 31, block kb = w: the selector products of its
+// state read as an operand with the columns as rows give lane (col, g) the
+// 4 columns 32 w + 16 ct + 4 g + e of row 16 t + col, the block's items.
+__device__ __forceinline__ void store_end(float* st_out, bool transition,
+                                          const f32x4 (&st)[8][2], const s16x8 (&sel)[2]) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int col = lane & 15;
+  const int g4 = lane >> 4;
+  if (!transition) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct)
+        *reinterpret_cast<f32x4*>(st_out + static_cast<size_t>(wave * 32 + ct * 16 + col) * kDim +
+                                  t * 16 + g4 * 4) = st[t][ct];
+    return;
+  }
+  uint16_t* ma = reinterpret_cast<uint16_t*>(st_out);
+#pragma unroll
+  for (int kb2 = 0; kb2 < 4; ++kb2) {                 // rows 32 kb2 .. 32 kb2 + 31
+    s16x8 ah[2], al[2];
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) ah[ct] = split_hi_lo(st[2 * kb2][ct], st[2 * kb2 + 1][ct], al[ct]);
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int t = 2 * kb2 + hf;
+      s16x4 h[2], l[2];
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        h[ct] = to_bf16x4(mfma_bf16(ah[ct], sel[hf], f32x4{0, 0, 0, 0}));
+        l[ct] = to_bf16x4(mfma_bf16(al[ct], sel[hf], f32x4{0, 0, 0, 0}));
+      }
+      const int blk0 = (t * 4 + wave) * 2;
+      *reinterpret_cast<s16x8*>(ma + blk0 * kBlk + lane * 8) = cat(h[0], h[1]);
+      *reinterpret_cast<s16x8*>(ma + (blk0 + 1) * kBlk + lane * 8) = cat(l[0], l[1]);
+    }
+  }
+}
+
 // Grid: (unit, q/k head) pairs in groups of 8 times the GVA ratio.
 // Workgroup b serves pair 8 (b / (8 ratio)) + b % 8 and its v-head
 // (b / 8) % ratio: the v-heads that read the same K and Q are dispatched 8
 // apart, all to XCD b % 8 (workgroups go to the XCDs round-robin), and share
 // its L2 copy.  A unit is a sequence, or with SEG a role of one segment of
-// sequence 0: launch 1 (seg_pass 1) runs segment 0 with its outputs (end:
-// seg_S[1]), then segments 1 .. nseg-2 from a zero start (end: seg_B) and
-// from the identity without values (end: seg_M); launch 2 runs segments
-// 1 .. nseg-1 from seg_S with their outputs (the last one's end is the new
-// state).
-template <bool FEW, bool SEG>
-__global__ __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_eu(kScanWaves / 4, kScanWaves / 4)))
+// sequence 0.  The first segment launch (OUT false, no outputs) runs
+// segment 0 from the sequence's state (end: seg_S[1]) and segments
+// 1 .. nseg-2 from a zero start (end: seg_B) and from the identity without
+// values (end: seg_M, as the combine's operand); the second (OUT) runs every
+// segment from its start (segment 0: the sequence's state, then seg_S) with
+// the outputs, the last one's end being the new state.
+template <bool FEW, bool SEG, bool OUT>
+__global__ __launch_bounds__(kScanThreads)
+__attribute__((amdgpu_waves_per_eu(1, 1)))
 void scan_kernel(Params p) {
-  __shared__ ScanLds L;
+  static_assert(OUT || SEG, "only segments run without outputs");
+  // two separate LDS objects, so that the compiler sees that the DMA into
+  // one never writes what the chunk reads from the other
+  __shared__ ScanBuf<OUT> L0, L1;
   const long long b = blockIdx.x;
   const int ratio = p.ratio;
   const long long pair = (b / (8LL * ratio)) * 8 + (b & 7);
   const int jr = static_cast<int>((b >> 3) % ratio);
-  const long long units = SEG ? (p.seg_pass == 1 ? 2LL * p.nseg - 3 : p.nseg - 1)
-                              : static_cast<long long>(p.N);
+  const long long units = SEG ? (OUT ? p.nseg : 2LL * p.nseg - 3) : static_cast<long long>(p.N);
   if (pair >= units * p.H) return;                              // uniform per workgroup
   const int unit = static_cast<int>(pair / p.H);
   const int h = static_cast<int>(pair % p.H);
@@ -879,14 +1122,14 @@ void scan_kernel(Params p) {
   const int g4 = lane >> 4;
   const size_t blk = static_cast<size_t>(kDim) * kDim;
 
-  // role: start state, values, outputs, where the end state goes
+  // role: start state, values, where the end state goes
   const float* st_in = nullptr;       // null: zeros (or the identity)
-  bool identity = false, values = true, outputs = true;
+  bool identity = false, values = true, pass_through = false;
   float* st_out;
   int s = 0, start, end, slot0 = 0, nchunks = 0;
   if (SEG) {
     int j;
-    if (p.seg_pass == 1) {
+    if (!OUT) {
       const int mid = p.nseg - 2;                 // segments 1 .. nseg-2
       if (unit == 0) {
         j = 0;
@@ -894,18 +1137,19 @@ void scan_kernel(Params p) {
         st_out = p.seg_S + (static_cast<size_t>(p.HV) + hv) * blk;
       } else if (unit <= mid) {
         j = unit;
-        outputs = false;
         st_out = p.seg_B + (static_cast<size_t>(j) * p.HV + hv) * blk;
       } else {
         j = unit - mid;
         identity = true;
-        values = outputs = false;
+        values = false;
         st_out = p.seg_M + (static_cast<size_t>(j) * p.HV + hv) * blk;
       }
     } else {
-      j = unit + 1;
-      st_in = p.seg_S + (static_cast<size_t>(j) * p.HV + hv) * blk;
+      j = unit;
+      st_in = j == 0 ? (p.state ? p.state + static_cast<size_t>(hv) * blk : nullptr)
+                     : p.seg_S + (static_cast<size_t>(j) * p.HV + hv) * blk;
       st_out = j == p.nseg - 1 ? p.new_state + static_cast<size_t>(hv) * blk : nullptr;
+      pass_through = j > 0;
     }
     seq_range(p, 0, start, end);               // one sequence: chunk c is slot c
     const int total = (end - start + kChunk - 1) / kChunk;
@@ -921,14 +1165,14 @@ void scan_kernel(Params p) {
   }
 
   // state registers; k-last storage: 4 consecutive keys are one 16-byte vector
-  f32x4 st[8][kScanCT];
+  f32x4 st[8][2];
 #pragma unroll
   for (int t = 0; t < 8; ++t)
 #pragma unroll
-    for (int ct = 0; ct < kScanCT; ++ct) {
-      const int c = wave * 16 * kScanCT + ct * 16 + col;
+    for (int ct = 0; ct < 2; ++ct) {
+      const int c = wave * 32 + ct * 16 + col;
       const int kr = t * 16 + g4 * 4;
-      st[t][ct] = st_in != nullptr && (end > start || (SEG && p.seg_pass == 2))
+      st[t][ct] = st_in != nullptr && (end > start || pass_through)
                       ? *reinterpret_cast<const f32x4*>(st_in + static_cast<size_t>(c) * kDim + kr)
                       : f32x4{0, 0, 0, 0};
       if (identity) {
@@ -936,6 +1180,13 @@ void scan_kernel(Params p) {
         for (int e = 0; e < 4; ++e) st[t][ct][e] = kr + e == c ? 1.0f : 0.0f;
       }
     }
+  // selector operands: Sel_ct[k][j] = (k == 16 ct + j) over a 32-long k block
+  s16x8 sel[2];
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      sel[ct][e] = (e == 4 * ct + (col & 3) && g4 == (col >> 2)) ? 0x3f80 : 0;
 
   // Chunk slots of a sequence (never more than the range holds, and never
   // more slots than the workspace has, whatever cu_seqlens contains).
@@ -956,206 +1207,58 @@ void scan_kernel(Params p) {
   // so does the sequence's end state.
   if (nchunks <= 0) {
     if (st_out != nullptr) {
+      if (!SEG) {
 #pragma unroll
-      for (int t = 0; t < 8; ++t)
+        for (int t = 0; t < 8; ++t)
 #pragma unroll
-        for (int ct = 0; ct < kScanCT; ++ct)
-          *reinterpret_cast<f32x4*>(st_out + static_cast<size_t>(wave * 16 * kScanCT + ct * 16 + col) * kDim +
-                                    t * 16 + g4 * 4) = SEG ? st[t][ct] : f32x4{0, 0, 0, 0};
+          for (int ct = 0; ct < 2; ++ct) st[t][ct] = f32x4{0, 0, 0, 0};
+      }
+      store_end(st_out, identity, st, sel);
     }
     return;
   }
-  const float* slot_base = p.slots + (static_cast<size_t>(slot0) * p.HV + hv) * kSlotFloats;
-  const size_t slot_step = static_cast<size_t>(p.HV) * kSlotFloats;
+  ScanCtx cx;
+  cx.k = p.k;
+  cx.q = p.q;
+  cx.v = p.v;
+  cx.out = p.out;
+  cx.slot_base = p.slots + (static_cast<size_t>(slot0) * p.HV + hv) * kSlotFloats;
+  cx.slot_step = static_cast<size_t>(p.HV) * kSlotFloats;
+  cx.kstep = static_cast<unsigned>(p.H) * kDim;
+  cx.vstep = static_cast<unsigned>(p.HV) * kDim;
+  cx.start = start;
+  cx.end = end;
+  cx.nchunks = nchunks;
+  cx.H = p.H;
+  cx.HV = p.HV;
+  cx.h = h;
+  cx.hv = hv;
+  cx.values = values;
 
-  const unsigned kstep = static_cast<unsigned>(p.H) * kDim;
-  const unsigned vstep = static_cast<unsigned>(p.HV) * kDim;
-  auto stage = [&](ScanStage& sg, int c) {     // chunk c's loads
-    const int tc = start + c * kChunk;
-    const uint16_t* kb = p.k + (static_cast<size_t>(tc) * p.H + h) * kDim;
-    const uint16_t* qb = p.q + (static_cast<size_t>(tc) * p.H + h) * kDim;
-    const uint16_t* vb = p.v + (static_cast<size_t>(tc) * p.HV + hv) * kDim;
-    scan_load(sg, kb, qb, vb, kstep, vstep, min(kChunk, end - tc), slot_base + c * slot_step);
-  };
-  ScanStage sg;
-  stage(sg, 0);
-
-  for (int ci = 0; ci < nchunks; ++ci) {
-    const int t0 = start + ci * kChunk;
-    const int n = min(kChunk, end - t0);
-    block_sync_lds();                  // every read of the previous chunk's LDS is done
-    scan_store(L, sg, n, values);
-    block_sync_lds();
-    // the next chunk's inputs (after the last: this one's again), issued
-    // here and kept here, so that they arrive while this chunk computes
-    stage(sg, ci + 1 < nchunks ? ci + 1 : ci);
-    __builtin_amdgcn_sched_barrier(0);
-
-    // K S (token rows) and S^T Q^T (the output's first term, transposed),
-    // one 32-key block of the state at a time
-    f32x4 x[4][kScanCT], o[4][kScanCT];
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int ct = 0; ct < kScanCT; ++ct) x[r][ct] = o[r][ct] = f32x4{0, 0, 0, 0};
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      s16x8 sh[kScanCT], sl[kScanCT];
-#pragma unroll
-      for (int ct = 0; ct < kScanCT; ++ct) sh[ct] = split_hi_lo(st[2 * kb][ct], st[2 * kb + 1][ct], sl[ct]);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const s16x8 ak = frag(&L.Kr[(r * 16 + col) * kRowStride], kb, g4);
-#pragma unroll
-        for (int ct = 0; ct < kScanCT; ++ct) {
-          x[r][ct] = mfma_bf16(ak, sh[ct], x[r][ct]);
-          x[r][ct] = mfma_bf16(ak, sl[ct], x[r][ct]);
-        }
-        if (outputs) {                                   // uniform
-          const s16x8 bq = frag(&L.Qr[(r * 16 + col) * kRowStride], kb, g4);
-#pragma unroll
-          for (int ct = 0; ct < kScanCT; ++ct) {
-            o[r][ct] = mfma_bf16(sh[ct], bq, o[r][ct]);
-            o[r][ct] = mfma_bf16(sl[ct], bq, o[r][ct]);
-          }
-        }
-      }
-    }
-
-    // X = V - diag(rk e^gamma) K S: lane (col, g) holds tokens 16 r + 4 g + e
-    // of column 32 wave + 16 ct + col
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const f32x4 xg = *reinterpret_cast<const f32x4*>(&L.slot[kSlotXg + r * 16 + g4 * 4]);
-#pragma unroll
-      for (int ct = 0; ct < kScanCT; ++ct) {
-        const int c = wave * 16 * kScanCT + ct * 16 + col;
-        const u32x2 vv = *reinterpret_cast<const u32x2*>(
-            &L.Vt[c * kColStride + ((r * 16 + g4 * 4) ^ tok_swz(c))]);
-        const f32x4 vf = {__uint_as_float(vv.x << 16), __uint_as_float(vv.x & 0xffff0000u),
-                          __uint_as_float(vv.y << 16), __uint_as_float(vv.y & 0xffff0000u)};
-        x[r][ct] = vf - xg * x[r][ct];
-      }
-    }
-
-    // Delta = T diag(beta) X (T lower triangular: token blocks kb <= r / 2)
-    s16x8 xh[2][kScanCT], xl[2][kScanCT];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int ct = 0; ct < kScanCT; ++ct) xh[kb][ct] = split_hi_lo(x[2 * kb][ct], x[2 * kb + 1][ct], xl[kb][ct]);
-    f32x4 d[4][kScanCT];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-#pragma unroll
-      for (int ct = 0; ct < kScanCT; ++ct) d[r][ct] = f32x4{0, 0, 0, 0};
-#pragma unroll
-      for (int kb = 0; kb <= (r >> 1); ++kb) {
-        const int bo = tri_blk(r, kb) * kBlkF + lane * 4;
-        const s16x8 th = ld_op(&L.slot[kSlotTh + bo]);
-        const s16x8 tl = ld_op(&L.slot[kSlotTl + bo]);
-#pragma unroll
-        for (int ct = 0; ct < kScanCT; ++ct) {
-          d[r][ct] = mfma_bf16(th, xh[kb][ct], d[r][ct]);
-          d[r][ct] = mfma_bf16(th, xl[kb][ct], d[r][ct]);
-          d[r][ct] = mfma_bf16(tl, xh[kb][ct], d[r][ct]);
-        }
-      }
-    }
-
-    // Delta as operand: A of Delta^T P^T and, scaled by ks, B of the update
-    s16x8 dh[2][kScanCT], dl[2][kScanCT], eh[2][kScanCT], el[2][kScanCT];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const f32x4 ks0 = *reinterpret_cast<const f32x4*>(&L.slot[kSlotKs + kb * 32 + g4 * 4]);
-      const f32x4 ks1 = *reinterpret_cast<const f32x4*>(&L.slot[kSlotKs + kb * 32 + 16 + g4 * 4]);
-#pragma unroll
-      for (int ct = 0; ct < kScanCT; ++ct) {
-        if (outputs) dh[kb][ct] = split_hi_lo(d[2 * kb][ct], d[2 * kb + 1][ct], dl[kb][ct]);
-        eh[kb][ct] = split_hi_lo(d[2 * kb][ct] * ks0, d[2 * kb + 1][ct] * ks1, el[kb][ct]);
-      }
-    }
-
-    // O^T = qs (.) S^T Q^T + Delta^T P^T; lane (col, g) ends with columns
-    // 32 wave + 16 ct + 4 g + e of token 16 r + col, one 8-byte store
-    if (outputs) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float qs = L.slot[kSlotQs + r * 16 + col];
-#pragma unroll
-        for (int ct = 0; ct < kScanCT; ++ct) o[r][ct] = o[r][ct] * qs;
-#pragma unroll
-        for (int kb = 0; kb <= (r >> 1); ++kb) {
-          const int bo = tri_blk(r, kb) * kBlkF + lane * 4;
-          const s16x8 ph = ld_op(&L.slot[kSlotPh + bo]);
-          const s16x8 pl = ld_op(&L.slot[kSlotPl + bo]);
-#pragma unroll
-          for (int ct = 0; ct < kScanCT; ++ct) {
-            o[r][ct] = mfma_bf16(dh[kb][ct], ph, o[r][ct]);
-            o[r][ct] = mfma_bf16(dh[kb][ct], pl, o[r][ct]);
-            o[r][ct] = mfma_bf16(dl[kb][ct], ph, o[r][ct]);
-          }
-        }
-        const int tok = r * 16 + col;
-#pragma unroll
-        for (int ct = 0; ct < kScanCT; ++ct) {
-          const u32x2 ob = {pack_bf16x2(o[r][ct][0], o[r][ct][1]),
-                            pack_bf16x2(o[r][ct][2], o[r][ct][3])};
-          if (tok < n)
-            *reinterpret_cast<u32x2*>(p.out + ((static_cast<size_t>(t0) + tok) * p.HV + hv) * kDim +
-                                      wave * 16 * kScanCT + ct * 16 + g4 * 4) = ob;
-        }
-      }
-    }
-
-    // S <- e^gamma_C S + K^T (ks (.) Delta), key tile t
-    const float gl = L.slot[kSlotGl];
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const int key = t * 16 + col;
-      const uint16_t* krow = &L.Kt[key * kColStride];
-      const int sw = tok_swz(key);
-      f32x4 acc[kScanCT];
-#pragma unroll
-      for (int ct = 0; ct < kScanCT; ++ct) acc[ct] = st[t][ct] * gl;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const s16x8 ak = cat(*reinterpret_cast<const s16x4*>(krow + ((kb * 32 + g4 * 4) ^ sw)),
-                             *reinterpret_cast<const s16x4*>(krow + ((kb * 32 + 16 + g4 * 4) ^ sw)));
-#pragma unroll
-        for (int ct = 0; ct < kScanCT; ++ct) {
-          acc[ct] = mfma_bf16(ak, eh[kb][ct], acc[ct]);
-          acc[ct] = mfma_bf16(ak, el[kb][ct], acc[ct]);
-        }
-      }
-#pragma unroll
-      for (int ct = 0; ct < kScanCT; ++ct) st[t][ct] = acc[ct];
-    }
+  VFrags vnext;
+  scan_issue<OUT>(&L0, cx, 0, vnext);
+  wait_vmem();
+  block_sync_lds();
+  for (int ci = 0; ci < nchunks; ci += 2) {
+    scan_chunk<OUT>(&L0, &L1, cx, st, vnext, sel, ci);
+    if (ci + 1 < nchunks) scan_chunk<OUT>(&L1, &L0, cx, st, vnext, sel, ci + 1);   // uniform
   }
-
-  if (st_out != nullptr) {
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-#pragma unroll
-      for (int ct = 0; ct < kScanCT; ++ct)
-        *reinterpret_cast<f32x4*>(st_out + static_cast<size_t>(wave * 16 * kScanCT + ct * 16 + col) * kDim +
-                                  t * 16 + g4 * 4) = st[t][ct];
-  }
+  if (st_out != nullptr) store_end(st_out, identity, st, sel);
 }
 
 // ---------------------------------------------------------------------------
 // 4. segments of one long sequence: chain the segment starts
 // ---------------------------------------------------------------------------
-// The first scan launch leaves, per v-head, S_1 and each middle segment's
-// transition M_j and zero-start end state B_j.  Combine: S_{j+1} = M_j S_j +
-// B_j for j = 1 .. nseg-2, segment after segment, with fp32 MFMA
-// (v_mfma_f32_16x16x4_f32).  One workgroup per (v-head, 16 state columns);
-// wavefront w computes key rows 32 w .. 32 w + 31 (two 16-row tiles), S_j
-// staged in LDS for the B operand.
-constexpr int kCombStride = kDim + 1;        // LDS column stride (no bank conflicts)
-
+// The first segment launch leaves, per v-head, S_1 and for each middle
+// segment j its transition M_j (as the A operand blocks of M S, bf16 hi/lo)
+// and zero-start end B_j.  Combine: S_{j+1} = M_j S_j + B_j for j = 1 ..
+// nseg-2, segment after segment, as bf16 MFMA with S_j split into hi + lo.
+// One workgroup per (v-head, 16 state columns); wave w computes rows 32 w ..
+// 32 w + 31 (row tiles 2 w, 2 w + 1) and hands its rows of S_j to the other
+// waves as the B operand's k block w through LDS (two buffers: one barrier a
+// step); the next step's M blocks and B tiles load while this one runs.
 __global__ __launch_bounds__(kThreads) void seg_combine_kernel(Params p) {
-  __shared__ float Sl[16 * kCombStride];     // S_j columns c0 .. c0 + 15, [col][k]
+  __shared__ s16x8 Sop[2][4][2][64];          // [buffer][k block][hi, lo][lane]
   const int hv = blockIdx.x >> 3;
   const int c0 = (blockIdx.x & 7) * 16;
   const int lane = threadIdx.x & 63;
@@ -1163,47 +1266,63 @@ __global__ __launch_bounds__(kThreads) void seg_combine_kernel(Params p) {
   const int col = lane & 15;
   const int g4 = lane >> 4;
   const size_t blk = static_cast<size_t>(kDim) * kDim;
-  // S_1 in the MFMA result layout: tile t, lane col + 16 g4, register e is
-  // key 32 wave + 16 t + 4 g4 + e of column c0 + col
+  if (p.nseg < 3) return;                     // nothing to chain
+  const size_t tile = static_cast<size_t>(c0 + col) * kDim + wave * 32 + g4 * 4;
+  // S_1, this wave's row tiles 2 w + tt in the MFMA result layout
   f32x4 S[2];
   const float* s1 = p.seg_S + (static_cast<size_t>(p.HV) + hv) * blk;
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
-    S[t] = *reinterpret_cast<const f32x4*>(s1 + static_cast<size_t>(c0 + col) * kDim +
-                                           wave * 32 + t * 16 + g4 * 4);
-  for (int j = 1; j + 1 < p.nseg; ++j) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) Sl[col * kCombStride + wave * 32 + t * 16 + g4 * 4 + e] = S[t][e];
-    __syncthreads();
-    const float* M = p.seg_M + (static_cast<size_t>(j) * p.HV + hv) * blk;
+  for (int tt = 0; tt < 2; ++tt) S[tt] = *reinterpret_cast<const f32x4*>(s1 + tile + tt * 16);
+  auto load_step = [&](int j, s16x8 (&ma)[2][4][2], f32x4 (&bt)[2]) {
+    const uint16_t* M =
+        reinterpret_cast<const uint16_t*>(p.seg_M + (static_cast<size_t>(j) * p.HV + hv) * blk);
     const float* Bj = p.seg_B + (static_cast<size_t>(j) * p.HV + hv) * blk;
-    f32x4 acc[2][2];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      acc[t][0] = *reinterpret_cast<const f32x4*>(Bj + static_cast<size_t>(c0 + col) * kDim +
-                                                  wave * 32 + t * 16 + g4 * 4);
-      acc[t][1] = f32x4{0, 0, 0, 0};
+    for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int hl = 0; hl < 2; ++hl)
+          ma[tt][kb][hl] = *reinterpret_cast<const s16x8*>(
+              M + ((((wave * 2 + tt) * 4 + kb) * 2 + hl) * kBlk + lane * 8));
+      bt[tt] = *reinterpret_cast<const f32x4*>(Bj + tile + tt * 16);
     }
-    // (M S)[k][c] = sum_k2 M[k][k2] S[k2][c]; A[i][kk] = M[row i][4 s + kk] from
-    // lane i + 16 kk, B[kk][c] = S[4 s + kk][c] from lane c + 16 kk
-    for (int st = 0; st < kDim / 4; ++st) {
-      const int k2 = 4 * st + g4;
-      const float bv = Sl[col * kCombStride + k2];
+  };
+  s16x8 ma[2][4][2];
+  f32x4 bt[2];
+  load_step(1, ma, bt);
+  for (int j = 1; j + 1 < p.nseg; ++j) {
+    const int buf = j & 1;
+    s16x8 lo;
+    const s16x8 hi = split_hi_lo(S[0], S[1], lo);
+    Sop[buf][wave][0][lane] = hi;
+    Sop[buf][wave][1][lane] = lo;
+    s16x8 man[2][4][2];                       // the next step's (after the last: this one's)
+    f32x4 btn[2];
+    load_step(j + 2 < p.nseg ? j + 1 : j, man, btn);
+    block_sync_lds();
+    f32x4 acc[2] = {bt[0], bt[1]};
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const float av = M[static_cast<size_t>(k2) * kDim + wave * 32 + t * 16 + col];
-        acc[t][st & 1] = mfma_f32(av, bv, acc[t][st & 1]);
+    for (int kb = 0; kb < 4; ++kb) {
+      const s16x8 sh = Sop[buf][kb][0][lane];
+      const s16x8 sl = Sop[buf][kb][1][lane];
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        acc[tt] = mfma_bf16(ma[tt][kb][0], sh, acc[tt]);
+        acc[tt] = mfma_bf16(ma[tt][kb][0], sl, acc[tt]);
+        acc[tt] = mfma_bf16(ma[tt][kb][1], sh, acc[tt]);
       }
     }
-    __syncthreads();                          // every read of Sl before the next writes
     float* dst = p.seg_S + (static_cast<size_t>(j + 1) * p.HV + hv) * blk;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      S[t] = acc[t][0] + acc[t][1];
-      *reinterpret_cast<f32x4*>(dst + static_cast<size_t>(c0 + col) * kDim + wave * 32 +
-                                t * 16 + g4 * 4) = S[t];
+    for (int tt = 0; tt < 2; ++tt) {
+      S[tt] = acc[tt];
+      *reinterpret_cast<f32x4*>(dst + tile + tt * 16) = S[tt];
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int hl = 0; hl < 2; ++hl) ma[tt][kb][hl] = man[tt][kb][hl];
+      bt[tt] = btn[tt];
     }
   }
 }
@@ -1230,24 +1349,46 @@ size_t slots_bytes(long long L, long long N, long long HV) {
 // Segments of one long sequence.  Its plain scan is a chain of chunk steps on
 // HV workgroups; with few v-heads that leaves most of the GPU idle (16384
 // tokens at 8 v-heads: 256 steps on 8 CUs), so the sequence is cut into
-// segments of kSegChunks chunks scanned at once: the two scan launches run
-// (2 nseg - 3) HV and (nseg - 1) HV workgroups of kSegChunks steps each, the
-// combine nseg - 2 small steps.
-constexpr int kSegChunks = 16;         // chunks per segment
+// nseg segments of len chunks scanned at once: the first launch runs
+// (2 nseg - 3) HV workgroups and the second nseg HV, one per CU, each of len
+// chunk steps, and the combine nseg - 2 small steps.  The length is the one
+// that minimises the estimated critical path, (rounds of the first launch +
+// rounds of the second) x len chunk steps + (nseg - 2) combine steps, with a
+// round of kCUs workgroups and a chunk step costing kStepPerCombine combine
+// steps (measured: ~5.4 us against ~1 us).
 constexpr int kSegMinChunks = 48;      // shorter sequences are scanned whole
 constexpr long long kSegMaxHV = 32;    // more v-heads fill the GPU without segments
+constexpr long long kSegMinLen = 4;
+constexpr long long kCUs = 256;
+constexpr long long kStepPerCombine = 5;
 
 bool use_segments(long long L, long long N, long long HV) {
   return N == 1 && HV <= kSegMaxHV && (L + kChunk - 1) / kChunk >= kSegMinChunks;
 }
 
-long long num_segments(long long L) {
-  return ((L + kChunk - 1) / kChunk + kSegChunks - 1) / kSegChunks;
+long long seg_chunks(long long L, long long HV) {
+  const long long chunks = (L + kChunk - 1) / kChunk;
+  long long best_len = chunks, best = -1;
+  for (long long len = kSegMinLen; 3 * len <= chunks; ++len) {
+    const long long n = (chunks + len - 1) / len;
+    const long long rounds = ((2 * n - 3) * HV + kCUs - 1) / kCUs + (n * HV + kCUs - 1) / kCUs;
+    const long long cost = rounds * len * kStepPerCombine + (n - 2);
+    if (best < 0 || cost < best) {
+      best = cost;
+      best_len = len;
+    }
+  }
+  return best_len;
+}
+
+long long num_segments(long long L, long long HV) {
+  const long long len = seg_chunks(L, HV);
+  return ((L + kChunk - 1) / kChunk + len - 1) / len;
 }
 
 // Per segment and v-head one 128 x 128 fp32 block (S, B and M each).
 size_t seg_blocks_bytes(long long L, long long HV) {
-  return align256(static_cast<size_t>(num_segments(L)) * HV * kDim * kDim * sizeof(float));
+  return align256(static_cast<size_t>(num_segments(L, HV)) * HV * kDim * kDim * sizeof(float));
 }
 
 size_t workspace_bytes(long long L, long long N, long long H, long long HV) {
@@ -1403,13 +1544,12 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
                                      slot_info_bytes(total_seq_len, num_seqs));
   p.seg_chunks = 0;
   p.nseg = 0;
-  p.seg_pass = 0;
   p.seg_S = p.seg_B = p.seg_M = nullptr;
   if (use_segments(total_seq_len, num_seqs, HV)) {
     char* sg = reinterpret_cast<char*>(p.slots) + slots_bytes(total_seq_len, num_seqs, HV);
     const size_t blocks = seg_blocks_bytes(total_seq_len, HV);
-    p.seg_chunks = kSegChunks;
-    p.nseg = static_cast<int>(num_segments(total_seq_len));
+    p.seg_chunks = static_cast<int>(seg_chunks(total_seq_len, HV));
+    p.nseg = static_cast<int>(num_segments(total_seq_len, HV));
     p.seg_S = reinterpret_cast<float*>(sg);
     p.seg_B = reinterpret_cast<float*>(sg + blocks);
     p.seg_M = reinterpret_cast<float*>(sg + 2 * blocks);
@@ -1465,10 +1605,10 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
     return dim3(static_cast<unsigned>((units * H + 7) / 8 * 8 * p.ratio));
   };
   if (p.nseg > 1) {
-    // segments (one sequence): transitions and segment 0, the starts, the rest
-    p.seg_pass = 1;
-    hipLaunchKernelGGL((scan_kernel<false, true>), scan_grid(2LL * p.nseg - 3), dim3(kScanThreads),
-                       0, stream, p);
+    // segments (one sequence): transitions and zero-start ends, the starts,
+    // then every segment with its outputs
+    hipLaunchKernelGGL((scan_kernel<false, true, false>), scan_grid(2LL * p.nseg - 3),
+                       dim3(kScanThreads), 0, stream, p);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (p.nseg > 2) {
@@ -1477,11 +1617,10 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
       e = hipGetLastError();
       if (e != hipSuccess) return e;
     }
-    p.seg_pass = 2;
-    hipLaunchKernelGGL((scan_kernel<false, true>), scan_grid(p.nseg - 1LL), dim3(kScanThreads), 0,
+    hipLaunchKernelGGL((scan_kernel<false, true, true>), scan_grid(p.nseg), dim3(kScanThreads), 0,
                        stream, p);
   } else {
-    auto* scan = p.few ? scan_kernel<true, false> : scan_kernel<false, false>;
+    auto* scan = p.few ? scan_kernel<true, false, true> : scan_kernel<false, false, true>;
     hipLaunchKernelGGL(scan, scan_grid(num_seqs), dim3(kScanThreads), 0, stream, p);
   }
   e = hipGetLastError();
@@ -1537,7 +1676,7 @@ int gdn_prefill_dispatches(int total_seq_len, int num_seqs, int HV) {
   if (num_seqs <= 0 || total_seq_len < 0 || HV <= 0) return 0;
   if (total_seq_len <= kSmallTokens && num_seqs <= 65535) return 1;
   if (use_segments(total_seq_len, num_seqs, HV))
-    return num_segments(total_seq_len) > 2 ? 4 : 3;
+    return num_segments(total_seq_len, HV) > 2 ? 4 : 3;
   return num_seqs == 1 || few_seqs(total_seq_len, num_seqs, HV) ? 2 : 3;
 }
 

@@ -52,9 +52,17 @@ def test_workspace_size_formula():
         offs = a256((N + 1) * 4)
         table = a256(chunks * 16)                                        # per-chunk slot table
         want = offs + table + a256(chunks * HV * vslot)
-        # one sequence of >= 48 chunks at <= 32 v-heads: segments of 16 chunks
-        seg = N == 1 and HV <= 32 and (L + 63) // 64 >= 48
-        nseg = ((L + 63) // 64 + 15) // 16
+        # one sequence of >= 48 chunks at <= 32 v-heads: segments of the length
+        # that minimises (rounds of 256 workgroups) x length x 5 + combine steps
+        nch = (L + 63) // 64
+        seg = N == 1 and HV <= 32 and nch >= 48
+
+        def cost(n_len):
+            n = -(-nch // n_len)
+            rounds = -(-(2 * n - 3) * HV // 256) + -(-n * HV // 256)
+            return rounds * n_len * 5 + (n - 2)
+        seg_len = min(range(4, nch // 3 + 1), key=cost) if seg else max(nch, 1)
+        nseg = -(-nch // seg_len)
         if seg:
             want += 3 * a256(nseg * HV * 128 * 128 * 4)
         assert lib.gdn_prefill_workspace_bytes(L, N, H, HV) == want, (L, N, H, HV)
