@@ -709,13 +709,12 @@ void prep_kernel(Params p) {
 // ---------------------------------------------------------------------------
 // 3. the scan: one workgroup per (sequence, v-head), the whole state
 // ---------------------------------------------------------------------------
-// Wave w keeps state columns 32 w .. 32 w + 31 (two 16-column tiles ct) of
-// all 128 keys in registers, in the MFMA result layout: st[t][ct] holds keys
-// 16 t + 4 g + e of column 32 w + 16 ct + col.  Read as runs of the k order,
-// the same registers are the state's operand of a product over keys in
-// either role (B of K S, A of S^T Q^T), and every per-chunk result is the
-// next product's operand in place, so the waves never exchange data.  Per
-// chunk, with S its start state:
+// Eight waves, two per SIMD: wave w keeps state columns 16 w .. 16 w + 15 of
+// all 128 keys in registers, in the MFMA result layout: st[t] holds keys
+// 16 t + 4 g + e of column 16 w + col.  Read as runs of the k order, the
+// same registers are the state's operand of a product over keys in either
+// role (B of K S, A of S^T Q^T), and every per-chunk result is the next
+// product's operand in place.  Per chunk, with S its start state:
 //   X      = V - diag(rk e^gamma) K S
 //   Delta  = T diag(beta) X
 //   O^T    = S^T Q^T diag(scale rq e^gamma) + Delta^T P^T
@@ -727,13 +726,14 @@ void prep_kernel(Params p) {
 // The waves share the chunk's K rows, Q rows and workspace slot, which the
 // LDS DMA (global_load_lds_dwordx4: each lane's 16 bytes land at the wave's
 // LDS base + 16 lane, no registers) brings into one of two LDS buffers while
-// the chunk before runs on the other, so a chunk needs one barrier.  The
-// operands with tokens as the contracted index come from products with a
-// selector (a 32 x 16 block of the identity), which moves a 16 x 32 row
-// block's columns into the result layout exactly: V^T tiles (each wave's own
-// 32 columns of V, loaded into registers a chunk ahead) and K^T tiles (from
-// the K rows in LDS).
-constexpr int kScanWaves = 4;
+// the chunk before runs on the other.  The operands with tokens as the
+// contracted index come from products with a selector (a 32 x 16 block of
+// the identity), which moves a 16 x 32 row block's columns into the result
+// layout exactly: V^T tiles (each wave's own 16 columns of V, loaded into
+// registers a chunk ahead) and K^T tiles (wave w makes key tile w from the K
+// rows in LDS and shares it through LDS: a second barrier per chunk, before
+// the state update).
+constexpr int kScanWaves = 8;
 constexpr int kScanThreads = 64 * kScanWaves;
 constexpr int kRowPieces = kDim / 8 + 1;          // 16-byte pieces per K / Q row, one of padding
 constexpr int kRowStride = kRowPieces * 8;        // bf16 (68 dwords)
@@ -745,6 +745,8 @@ static_assert(kChunk * kRowPieces % 64 == 0 && kSlotFloats % 256 == 0, "whole DM
 constexpr int kSlotTFloats = 2 * kTriBlocks * kBlkF;
 constexpr int kSlotGates = kSlotFloats - kSlotXg;     // the four rows of scales
 static_assert(kSlotTFloats == kSlotPh && kSlotXg == 2 * kSlotTFloats, "slot layout");
+// K^T operand blocks of a chunk: (key tile t, token block kb), 64 lanes x 8 bf16
+constexpr int kKtElems = 8 * 2 * 64 * 8;
 
 template <bool OUT> struct ScanBuf;
 template <> struct ScanBuf<true> {
@@ -756,7 +758,7 @@ template <> struct ScanBuf<false> {
   uint16_t Kr[kChunk * kRowStride];
   float slot[kSlotTFloats + kSlotGates];
 };
-static_assert(2 * sizeof(ScanBuf<true>) <= 160 * 1024, "one scan workgroup per CU");
+static_assert(2 * sizeof(ScanBuf<true>) + kKtElems * 2 <= 160 * 1024, "one scan workgroup per CU");
 // LDS offset of the row scales (Xg, then Qs, Ks, Gl as in the slot)
 template <bool OUT> __device__ constexpr int lds_gates() { return OUT ? kSlotXg : kSlotTFloats; }
 
@@ -773,10 +775,21 @@ __device__ __forceinline__ void dma16(const void* src_l, void* dst) {
 // them): s_waitcnt vmcnt(0), the other counters left alone.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// Workgroup barrier after this wave's LDS reads and writes (s_waitcnt
+// lgkmcnt(0)) but not its DMA: a fence on LDS would wait for the DMA in
+// flight too (it writes LDS), which only the next chunk reads.  The empty
+// asm statements keep the compiler from moving memory accesses across.
+__device__ __forceinline__ void barrier_lds_no_dma() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // DMA of a chunk's K rows, Q rows (OUT; rows >= n repeat row n - 1; each
 // row's padding piece repeats its last piece) and slot (without outputs: T
 // diag(beta) and the row scales) into one LDS buffer; wave w issues
-// instructions w, w + 4, ....
+// instructions w, w + 8, ....
 template <bool OUT>
 __device__ __forceinline__ void scan_dma(ScanBuf<OUT>& B, const uint16_t* kbase,
                                          const uint16_t* qbase, unsigned step, int n,
@@ -800,20 +813,15 @@ __device__ __forceinline__ void scan_dma(ScanBuf<OUT>& B, const uint16_t* kbase,
   }
 }
 
-// This wave's 32 columns of V for token tile r as a 16 x 32 A operand
-// (lane (col, g): token 16 r + col, rows >= n repeating row n - 1).
-struct VFrags {
-  u32x2 lo[4], hi[4];
-};
-__device__ __forceinline__ void load_v(VFrags& f, const uint16_t* vbase, unsigned step, int n,
+// This wave's 16 columns of V for token tile r (lane (col, g): token
+// 16 r + col, columns 16 w + 4 g .. + 3; rows >= n repeat row n - 1).
+__device__ __forceinline__ void load_v(u32x2 (&f)[4], const uint16_t* vbase, unsigned step, int n,
                                        int wave, int col, int g4) {
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int row = r * 16 + col;
-    const uint16_t* p = vbase + static_cast<unsigned>(row < n ? row : n - 1) * step + wave * 32 +
-                        g4 * 4;
-    f.lo[r] = *reinterpret_cast<const u32x2*>(p);
-    f.hi[r] = *reinterpret_cast<const u32x2*>(p + 16);
+    f[r] = *reinterpret_cast<const u32x2*>(vbase + static_cast<unsigned>(row < n ? row : n - 1) *
+                                                       step + wave * 16 + g4 * 4);
   }
 }
 
@@ -825,7 +833,7 @@ __device__ __forceinline__ s16x8 split_hi_lo(const f32x4& a, const f32x4& b, s16
   return cat(ha, hb);
 }
 
-__device__ __forceinline__ s16x8 ld_op(const float* ptr) {
+__device__ __forceinline__ s16x8 ld_op(const void* ptr) {
   return *reinterpret_cast<const s16x8*>(ptr);
 }
 
@@ -851,7 +859,8 @@ struct ScanCtx {
 
 // Chunk c's DMA into buf and its V into registers.
 template <bool OUT>
-__device__ __forceinline__ void scan_issue(ScanBuf<OUT>* buf, const ScanCtx& cx, int c, VFrags& vf) {
+__device__ __forceinline__ void scan_issue(ScanBuf<OUT>* buf, const ScanCtx& cx, int c,
+                                           u32x2 (&vf)[4]) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int tc = cx.start + c * kChunk;
   const int nc = min(kChunk, cx.end - tc);
@@ -862,197 +871,159 @@ __device__ __forceinline__ void scan_issue(ScanBuf<OUT>* buf, const ScanCtx& cx,
          lane & 15, lane >> 4);
 }
 
-// Chunk ci from buffer B, with the next chunk's DMA into Bn.  B and Bn are
-// restrict: the compiler then knows that the DMA in flight into Bn never
-// writes what this chunk reads from B, and waits for it only at the end.
-// OUT: the outputs too (else only the state).
+// Chunk ci from buffer B, with the next chunk's DMA into Bn; Kt: the K^T
+// operand blocks.  B, Bn and Kt are restrict: the compiler then knows that
+// the DMA in flight into Bn never writes what this chunk reads, and waits
+// for it only at the end.  OUT: the outputs too (else only the state).
 template <bool OUT>
 __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
                                            ScanBuf<OUT>* __restrict__ Bn,
-                                           const ScanCtx& cx, f32x4 (&st)[8][2], VFrags& vnext,
-                                           const s16x8 (&sel)[2], int ci) {
+                                           uint16_t* __restrict__ Kt, const ScanCtx& cx,
+                                           f32x4 (&st)[8], u32x2 (&vnext)[4], const s16x8& sel,
+                                           int ci) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int col = lane & 15;
   const int g4 = lane >> 4;
   const int t0 = cx.start + ci * kChunk;
   const int n = min(kChunk, cx.end - t0);
-  const VFrags vf = vnext;
-  // the next chunk's inputs into the other buffer (after the last chunk:
-  // this one's again, unused), in flight while this chunk computes
-  // the chunk's row scales, read before the DMA below is issued
+  const u32x2 vf[4] = {vnext[0], vnext[1], vnext[2], vnext[3]};
+  // the chunk's row scales, and key tile `wave` of K^T (the selector
+  // products of the K row blocks (r, wave / 2) give lane (col, g) tokens
+  // 16 r + 4 g + e of key 16 wave + col), read before the DMA below is issued
   constexpr int kG = lds_gates<OUT>();
   f32x4 xg[4], ks[4];
   float qs[4];
+  s16x4 kt[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     xg[r] = *reinterpret_cast<const f32x4*>(&B->slot[kG + r * 16 + g4 * 4]);
     ks[r] = *reinterpret_cast<const f32x4*>(&B->slot[kG + 128 + r * 16 + g4 * 4]);
     qs[r] = OUT ? B->slot[kG + 64 + r * 16 + col] : 0.0f;
+    kt[r] = to_bf16x4(mfma_bf16(frag(&B->Kr[(r * 16 + col) * kRowStride], wave >> 1, g4), sel,
+                                f32x4{0, 0, 0, 0}));
   }
   const float gl = B->slot[kG + 192];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+    *reinterpret_cast<s16x8*>(Kt + ((wave * 2 + kb) * 64 + lane) * 8) =
+        cat(kt[2 * kb], kt[2 * kb + 1]);
+  // the next chunk's inputs into the other buffer (after the last chunk:
+  // this one's again, unused), in flight while this chunk computes
   scan_issue(Bn, cx, ci + 1 < cx.nchunks ? ci + 1 : ci, vnext);
 
   // K S (token rows) and S^T Q^T (the output's first term, transposed),
   // one 32-key block of the state at a time
-  f32x4 x[4][2], o[4][2];
+  f32x4 x[4], o[4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) x[r][ct] = o[r][ct] = f32x4{0, 0, 0, 0};
+  for (int r = 0; r < 4; ++r) x[r] = o[r] = f32x4{0, 0, 0, 0};
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
-    s16x8 sh[2], sl[2];
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) sh[ct] = split_hi_lo(st[2 * kb][ct], st[2 * kb + 1][ct], sl[ct]);
+    s16x8 sl;
+    const s16x8 sh = split_hi_lo(st[2 * kb], st[2 * kb + 1], sl);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const s16x8 ak = frag(&B->Kr[(r * 16 + col) * kRowStride], kb, g4);
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        x[r][ct] = mfma_bf16(ak, sh[ct], x[r][ct]);
-        x[r][ct] = mfma_bf16(ak, sl[ct], x[r][ct]);
-      }
+      x[r] = mfma_bf16(ak, sh, x[r]);
+      x[r] = mfma_bf16(ak, sl, x[r]);
       if constexpr (OUT) {
         const s16x8 bq = frag(&B->Qr[(r * 16 + col) * kRowStride], kb, g4);
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-          o[r][ct] = mfma_bf16(sh[ct], bq, o[r][ct]);
-          o[r][ct] = mfma_bf16(sl[ct], bq, o[r][ct]);
-        }
+        o[r] = mfma_bf16(sh, bq, o[r]);
+        o[r] = mfma_bf16(sl, bq, o[r]);
       }
     }
   }
 
   // X = V - diag(rk e^gamma) K S: lane (col, g) holds tokens 16 r + 4 g + e
-  // of column 32 wave + 16 ct + col; V^T tiles from the selector products
+  // of column 16 wave + col; V^T tiles from the selector products (the
+  // wave's 16 columns sit in the half `wave % 2` of a 32-column block)
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const s16x8 av = cx.values ? __builtin_bit_cast(s16x8, u32x4{vf.lo[r].x, vf.lo[r].y,
-                                                            vf.hi[r].x, vf.hi[r].y})
-                            : s16x8{0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-      const f32x4 v = mfma_bf16(av, sel[ct], f32x4{0, 0, 0, 0});
-      x[r][ct] = v - xg[r] * x[r][ct];
-    }
+    const u32x2 vv = cx.values ? vf[r] : u32x2{0u, 0u};
+    const u32x4 w4 = (wave & 1) ? u32x4{0u, 0u, vv.x, vv.y} : u32x4{vv.x, vv.y, 0u, 0u};
+    const f32x4 v = mfma_bf16(__builtin_bit_cast(s16x8, w4), sel, f32x4{0, 0, 0, 0});
+    x[r] = v - xg[r] * x[r];
   }
 
   // Delta = T diag(beta) X (T lower triangular: token blocks kb <= r / 2)
-  s16x8 xh[2][2], xl[2][2];
+  s16x8 xh[2], xl[2];
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) xh[kb][ct] = split_hi_lo(x[2 * kb][ct], x[2 * kb + 1][ct], xl[kb][ct]);
-  f32x4 d[4][2];
+  for (int kb = 0; kb < 2; ++kb) xh[kb] = split_hi_lo(x[2 * kb], x[2 * kb + 1], xl[kb]);
+  f32x4 d[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) d[r][ct] = f32x4{0, 0, 0, 0};
+    d[r] = f32x4{0, 0, 0, 0};
 #pragma unroll
     for (int kb = 0; kb <= (r >> 1); ++kb) {
       const int bo = tri_blk(r, kb) * kBlkF + lane * 4;
       const s16x8 th = ld_op(&B->slot[kSlotTh + bo]);
       const s16x8 tl = ld_op(&B->slot[kSlotTl + bo]);
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        d[r][ct] = mfma_bf16(th, xh[kb][ct], d[r][ct]);
-        d[r][ct] = mfma_bf16(th, xl[kb][ct], d[r][ct]);
-        d[r][ct] = mfma_bf16(tl, xh[kb][ct], d[r][ct]);
-      }
+      d[r] = mfma_bf16(th, xh[kb], d[r]);
+      d[r] = mfma_bf16(th, xl[kb], d[r]);
+      d[r] = mfma_bf16(tl, xh[kb], d[r]);
     }
   }
 
   // Delta as operand: A of Delta^T P^T and, scaled by ks, B of the update
-  s16x8 dh[2][2], dl[2][2], eh[2][2], el[2][2];
+  s16x8 dh[2], dl[2], eh[2], el[2];
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
-    const f32x4 ks0 = ks[2 * kb], ks1 = ks[2 * kb + 1];
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-      if constexpr (OUT) dh[kb][ct] = split_hi_lo(d[2 * kb][ct], d[2 * kb + 1][ct], dl[kb][ct]);
-      eh[kb][ct] = split_hi_lo(d[2 * kb][ct] * ks0, d[2 * kb + 1][ct] * ks1, el[kb][ct]);
-    }
+    if constexpr (OUT) dh[kb] = split_hi_lo(d[2 * kb], d[2 * kb + 1], dl[kb]);
+    eh[kb] = split_hi_lo(d[2 * kb] * ks[2 * kb], d[2 * kb + 1] * ks[2 * kb + 1], el[kb]);
   }
 
   // O^T = qs (.) S^T Q^T + Delta^T P^T; lane (col, g) ends with columns
-  // 32 wave + 16 ct + 4 g + e of token 16 r + col, one 8-byte store
+  // 16 wave + 4 g + e of token 16 r + col, one 8-byte store
   if constexpr (OUT) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) o[r][ct] = o[r][ct] * qs[r];
+      o[r] = o[r] * qs[r];
 #pragma unroll
       for (int kb = 0; kb <= (r >> 1); ++kb) {
         const int bo = tri_blk(r, kb) * kBlkF + lane * 4;
         const s16x8 ph = ld_op(&B->slot[kSlotPh + bo]);
         const s16x8 pl = ld_op(&B->slot[kSlotPl + bo]);
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-          o[r][ct] = mfma_bf16(dh[kb][ct], ph, o[r][ct]);
-          o[r][ct] = mfma_bf16(dh[kb][ct], pl, o[r][ct]);
-          o[r][ct] = mfma_bf16(dl[kb][ct], ph, o[r][ct]);
-        }
+        o[r] = mfma_bf16(dh[kb], ph, o[r]);
+        o[r] = mfma_bf16(dh[kb], pl, o[r]);
+        o[r] = mfma_bf16(dl[kb], ph, o[r]);
       }
       const int tok = r * 16 + col;
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        const u32x2 ob = {pack_bf16x2(o[r][ct][0], o[r][ct][1]),
-                          pack_bf16x2(o[r][ct][2], o[r][ct][3])};
-        if (tok < n)
-          *reinterpret_cast<u32x2*>(cx.out + ((static_cast<size_t>(t0) + tok) * cx.HV + cx.hv) * kDim +
-                                    wave * 32 + ct * 16 + g4 * 4) = ob;
-      }
+      const u32x2 ob = {pack_bf16x2(o[r][0], o[r][1]), pack_bf16x2(o[r][2], o[r][3])};
+      if (tok < n)
+        *reinterpret_cast<u32x2*>(cx.out + ((static_cast<size_t>(t0) + tok) * cx.HV + cx.hv) *
+                                               kDim + wave * 16 + g4 * 4) = ob;
     }
   }
 
-  // S <- e^gamma_C S + K^T (ks (.) Delta).  Keys 32 m .. 32 m + 31 (tiles
-  // t = 2 m + hf): the selector products of the K row blocks (r, m) give
-  // lane (col, g) tokens 16 r + 4 g + e of key 16 t + col, the K^T operand
-  // items of token block r / 2.
+  // S <- e^gamma_C S + K^T (ks (.) Delta), key tile t; every wave's K^T
+  // tile is in LDS past this barrier
+  barrier_lds_no_dma();
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    s16x4 kt[4][2];                                  // [token tile r][hf]
+  for (int t = 0; t < 8; ++t) {
+    f32x4 acc = st[t] * gl;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const s16x8 ak = frag(&B->Kr[(r * 16 + col) * kRowStride], m, g4);
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf)
-        kt[r][hf] = to_bf16x4(mfma_bf16(ak, sel[hf], f32x4{0, 0, 0, 0}));
+    for (int kb = 0; kb < 2; ++kb) {
+      const s16x8 ak = ld_op(Kt + ((t * 2 + kb) * 64 + lane) * 8);
+      acc = mfma_bf16(ak, eh[kb], acc);
+      acc = mfma_bf16(ak, el[kb], acc);
     }
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      const int t = 2 * m + hf;
-      f32x4 acc[2];
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) acc[ct] = st[t][ct] * gl;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const s16x8 ak = cat(kt[2 * kb][hf], kt[2 * kb + 1][hf]);
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-          acc[ct] = mfma_bf16(ak, eh[kb][ct], acc[ct]);
-          acc[ct] = mfma_bf16(ak, el[kb][ct], acc[ct]);
-        }
-      }
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) st[t][ct] = acc[ct];
-    }
+    st[t] = acc;
   }
 
   wait_vmem();                       // the next chunk's DMA has landed
-  block_sync_lds();                  // for every wave; this buffer's reads are done
+  block_sync_lds();                  // for every wave; this chunk's LDS reads are done
 }
 
 // The end state of a scan: k-last fp32 (element (k, c) at c * 128 + k), or,
 // for a transition M (identity start), as the A operand blocks of the
 // combine's product M S: for row tile t and column block kb, 64 lanes x 8
 // bf16, hi then lo (block ((t * 4 + kb) * 2 + hl) * 512).  Wave w holds
-// columns 32 w .. 32 w + 31, block kb = w: the selector products of its
-// state read as an operand with the columns as rows give lane (col, g) the
-// 4 columns 32 w + 16 ct + 4 g + e of row 16 t + col, the block's items.
-__device__ __forceinline__ void store_end(float* st_out, bool transition,
-                                          const f32x4 (&st)[8][2], const s16x8 (&sel)[2]) {
+// columns 16 w .. 16 w + 15, half w % 2 of block kb = w / 2: the selector
+// products of its state read as an operand with the columns as rows give
+// lane (col, g) the columns 16 w + 4 g + e of row 16 t + col, items
+// 4 (w % 2) .. + 3 of the block's lane.
+__device__ __forceinline__ void store_end(float* st_out, bool transition, const f32x4 (&st)[8],
+                                          const s16x8 (&sels)[2]) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int col = lane & 15;
@@ -1060,30 +1031,24 @@ __device__ __forceinline__ void store_end(float* st_out, bool transition,
   if (!transition) {
 #pragma unroll
     for (int t = 0; t < 8; ++t)
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
-        *reinterpret_cast<f32x4*>(st_out + static_cast<size_t>(wave * 32 + ct * 16 + col) * kDim +
-                                  t * 16 + g4 * 4) = st[t][ct];
+      *reinterpret_cast<f32x4*>(st_out + static_cast<size_t>(wave * 16 + col) * kDim + t * 16 +
+                                g4 * 4) = st[t];
     return;
   }
   uint16_t* ma = reinterpret_cast<uint16_t*>(st_out);
 #pragma unroll
   for (int kb2 = 0; kb2 < 4; ++kb2) {                 // rows 32 kb2 .. 32 kb2 + 31
-    s16x8 ah[2], al[2];
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) ah[ct] = split_hi_lo(st[2 * kb2][ct], st[2 * kb2 + 1][ct], al[ct]);
+    s16x8 al;
+    const s16x8 ah = split_hi_lo(st[2 * kb2], st[2 * kb2 + 1], al);
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
       const int t = 2 * kb2 + hf;
-      s16x4 h[2], l[2];
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        h[ct] = to_bf16x4(mfma_bf16(ah[ct], sel[hf], f32x4{0, 0, 0, 0}));
-        l[ct] = to_bf16x4(mfma_bf16(al[ct], sel[hf], f32x4{0, 0, 0, 0}));
-      }
-      const int blk0 = (t * 4 + wave) * 2;
-      *reinterpret_cast<s16x8*>(ma + blk0 * kBlk + lane * 8) = cat(h[0], h[1]);
-      *reinterpret_cast<s16x8*>(ma + (blk0 + 1) * kBlk + lane * 8) = cat(l[0], l[1]);
+      const int blk0 = (t * 4 + (wave >> 1)) * 2;
+      const int item = lane * 8 + (wave & 1) * 4;
+      *reinterpret_cast<s16x4*>(ma + blk0 * kBlk + item) =
+          to_bf16x4(mfma_bf16(ah, sels[hf], f32x4{0, 0, 0, 0}));
+      *reinterpret_cast<s16x4*>(ma + (blk0 + 1) * kBlk + item) =
+          to_bf16x4(mfma_bf16(al, sels[hf], f32x4{0, 0, 0, 0}));
     }
   }
 }
@@ -1100,13 +1065,13 @@ __device__ __forceinline__ void store_end(float* st_out, bool transition,
 // segment from its start (segment 0: the sequence's state, then seg_S) with
 // the outputs, the last one's end being the new state.
 template <bool FEW, bool SEG, bool OUT>
-__global__ __launch_bounds__(kScanThreads)
-__attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void scan_kernel(Params p) {
   static_assert(OUT || SEG, "only segments run without outputs");
-  // two separate LDS objects, so that the compiler sees that the DMA into
-  // one never writes what the chunk reads from the other
+  // separate LDS objects, so that the compiler sees that the DMA into one
+  // buffer never writes what the chunk reads from the other
   __shared__ ScanBuf<OUT> L0, L1;
+  __shared__ __attribute__((aligned(16))) uint16_t Kt[kKtElems];
   const long long b = blockIdx.x;
   const int ratio = p.ratio;
   const long long pair = (b / (8LL * ratio)) * 8 + (b & 7);
@@ -1165,28 +1130,26 @@ void scan_kernel(Params p) {
   }
 
   // state registers; k-last storage: 4 consecutive keys are one 16-byte vector
-  f32x4 st[8][2];
+  f32x4 st[8];
+  const int c = wave * 16 + col;
 #pragma unroll
-  for (int t = 0; t < 8; ++t)
+  for (int t = 0; t < 8; ++t) {
+    const int kr = t * 16 + g4 * 4;
+    st[t] = st_in != nullptr && (end > start || pass_through)
+                ? *reinterpret_cast<const f32x4*>(st_in + static_cast<size_t>(c) * kDim + kr)
+                : f32x4{0, 0, 0, 0};
+    if (identity) {
 #pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-      const int c = wave * 32 + ct * 16 + col;
-      const int kr = t * 16 + g4 * 4;
-      st[t][ct] = st_in != nullptr && (end > start || pass_through)
-                      ? *reinterpret_cast<const f32x4*>(st_in + static_cast<size_t>(c) * kDim + kr)
-                      : f32x4{0, 0, 0, 0};
-      if (identity) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) st[t][ct][e] = kr + e == c ? 1.0f : 0.0f;
-      }
+      for (int e = 0; e < 4; ++e) st[t][e] = kr + e == c ? 1.0f : 0.0f;
     }
-  // selector operands: Sel_ct[k][j] = (k == 16 ct + j) over a 32-long k block
-  s16x8 sel[2];
+  }
+  // selector operands: Sel_h[k][j] = (k == 16 h + j) over a 32-long k block
+  s16x8 sels[2];
 #pragma unroll
-  for (int ct = 0; ct < 2; ++ct)
+  for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
     for (int e = 0; e < 8; ++e)
-      sel[ct][e] = (e == 4 * ct + (col & 3) && g4 == (col >> 2)) ? 0x3f80 : 0;
+      sels[hf][e] = (e == 4 * hf + (col & 3) && g4 == (col >> 2)) ? 0x3f80 : 0;
 
   // Chunk slots of a sequence (never more than the range holds, and never
   // more slots than the workspace has, whatever cu_seqlens contains).
@@ -1209,11 +1172,9 @@ void scan_kernel(Params p) {
     if (st_out != nullptr) {
       if (!SEG) {
 #pragma unroll
-        for (int t = 0; t < 8; ++t)
-#pragma unroll
-          for (int ct = 0; ct < 2; ++ct) st[t][ct] = f32x4{0, 0, 0, 0};
+        for (int t = 0; t < 8; ++t) st[t] = f32x4{0, 0, 0, 0};
       }
-      store_end(st_out, identity, st, sel);
+      store_end(st_out, identity, st, sels);
     }
     return;
   }
@@ -1235,15 +1196,16 @@ void scan_kernel(Params p) {
   cx.hv = hv;
   cx.values = values;
 
-  VFrags vnext;
+  const s16x8 sel = sels[wave & 1];       // this wave's half of a 32-key / 32-column block
+  u32x2 vnext[4];
   scan_issue<OUT>(&L0, cx, 0, vnext);
   wait_vmem();
   block_sync_lds();
   for (int ci = 0; ci < nchunks; ci += 2) {
-    scan_chunk<OUT>(&L0, &L1, cx, st, vnext, sel, ci);
-    if (ci + 1 < nchunks) scan_chunk<OUT>(&L1, &L0, cx, st, vnext, sel, ci + 1);   // uniform
+    scan_chunk<OUT>(&L0, &L1, Kt, cx, st, vnext, sel, ci);
+    if (ci + 1 < nchunks) scan_chunk<OUT>(&L1, &L0, Kt, cx, st, vnext, sel, ci + 1);  // uniform
   }
-  if (st_out != nullptr) store_end(st_out, identity, st, sel);
+  if (st_out != nullptr) store_end(st_out, identity, st, sels);
 }
 
 // ---------------------------------------------------------------------------
