@@ -431,7 +431,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3)))
 void prep_kernel(Params p) {
   __shared__ PrepLds lds;
   const int c = blockIdx.x;
-  const int hv = blockIdx.y;
+  const int h = blockIdx.y;
   int t0, n;                                       // n: 1..64, 0 past the last slot
   if (p.single) {
     int start, end;
@@ -456,13 +456,10 @@ void prep_kernel(Params p) {
     n = info.z;
   }
   if (n <= 0) return;                              // uniform per workgroup
-  const int h = hv / p.ratio;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int col = lane & 15;
   const int g4 = lane >> 4;
-  float* slot = p.slots + (static_cast<size_t>(c) * p.HV + hv) * kSlotFloats;
-  uint16_t* slot16 = reinterpret_cast<uint16_t*>(slot);
 
   // Every input load of the chunk is issued before the first is waited on.
   u32x4 kreg[4];
@@ -480,12 +477,6 @@ void prep_kernel(Params p) {
 #pragma unroll
     for (int m = 0; m < 4; ++m) qa[m] = frag(qrow, m, g4);
   }
-  // Gates of token t0 + lane (every wave computes them, wave 0 keeps them);
-  // padded rows: no decay, no update.
-  float logg, beta;
-  token_gates(p, t0 + (lane < n ? lane : n - 1), hv, logg, beta);
-  if (lane >= n) logg = beta = 0.0f;
-
   store_rows_bf16(lds.K, kreg, n);
   // T's upper blocks that the block recursion multiplies, T_01 and T_23, are
   // zero; the diagonal and lower blocks are all written, the other upper
@@ -511,16 +502,6 @@ void prep_kernel(Params p) {
     sq += __shfl_xor(sq, 32, 64);
     if (g4 == 0) lds.rq[ra] = p.l2norm ? __builtin_amdgcn_rsqf(sq + kL2Eps) : 1.0f;
   }
-  if (wave == 0) {
-    float g = logg;                                // inclusive scan over the chunk
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const float y = __shfl_up(g, d, 64);
-      if (lane >= d) g += y;
-    }
-    lds.gamma[lane] = g;
-    lds.beta[lane] = beta;
-  }
   block_sync_lds();
 
   // K row scales of the L2-norm (1 when off): 4 threads per row.
@@ -545,8 +526,8 @@ void prep_kernel(Params p) {
   // the 128-long rows.  The transposed product leaves each lane holding 4
   // consecutive j of one row i of P, two of which make the scan's operand
   // items, so P goes out as one 16-byte store per lane and k block.
+  f32x4 kk[4], pt[4];
   {
-    f32x4 kk[4], pt[4];
 #pragma unroll
     for (int nj = 0; nj < 4; ++nj) {
       kk[nj] = f32x4{0, 0, 0, 0};
@@ -563,146 +544,174 @@ void prep_kernel(Params p) {
         pt[nj] = mfma_bf16(bk, qa[m], pt[nj]);
       }
     }
-    // Row and column factors, read once.  The decays are computed for every
-    // element with the exponent clamped to <= 0 (it is <= 0 wherever the
-    // element is kept: gamma does not increase) and the masks are selects.
-    // A[i][j], i = 16 wave + 4 g + e, j = 16 nj + col (K K^T is symmetric)
-    const int ia = wave * 16 + g4 * 4;
-    const f32x4 gi4 = *reinterpret_cast<const f32x4*>(&lds.gamma[ia]);
-    const f32x4 bri4 = *reinterpret_cast<const f32x4*>(&lds.beta[ia]) *
-                       *reinterpret_cast<const f32x4*>(&lds.rk[ia]);
+  }
+
+  // Each v-head of the group: its gates, A and P from the shared products,
+  // T, and its slot.  The LDS the previous v-head used (gamma, beta, A, T)
+  // is rewritten only after the barrier that ends its use.
+  for (int j = 0; j < p.ratio; ++j) {
+    const int hv = h * p.ratio + j;
+    float* slot = p.slots + (static_cast<size_t>(c) * p.HV + hv) * kSlotFloats;
+    uint16_t* slot16 = reinterpret_cast<uint16_t*>(slot);
+    // gates of token t0 + lane (padded rows: no decay, no update), and the
+    // inclusive scan of the log-decay over the chunk
+    if (wave == 0) {
+      float logg, beta;
+      token_gates(p, t0 + (lane < n ? lane : n - 1), hv, logg, beta);
+      if (lane >= n) logg = beta = 0.0f;
+      float g = logg;
 #pragma unroll
-    for (int nj = 0; nj < 4; ++nj) {
-      const int j = nj * 16 + col;
-      const float gj = lds.gamma[j];
-      const float rkj = lds.rk[j];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float dec = __expf(fminf(gi4[e] - gj, 0.0f));
-        const float x = bri4[e] * rkj * dec * kk[nj][e];
-        lds.A[(ia + e) * kF64Stride + j] = j < ia + e ? x : 0.0f;
+      for (int d = 1; d < 64; d <<= 1) {
+        const float y = __shfl_up(g, d, 64);
+        if (lane >= d) g += y;
       }
+      lds.gamma[lane] = g;
+      lds.beta[lane] = beta;
     }
-    // P[i][j], i = 16 wave + col, j = 16 nj + 4 g + e; the token blocks
-    // jb <= wave / 2 (the others are zero)
-    const int i = wave * 16 + col;
-    const float gi = lds.gamma[i];
-    const float sqi = p.scale * lds.rq[i];
+    block_sync_lds();
+    {
+      // Row and column factors, read once.  The decays are computed for every
+      // element with the exponent clamped to <= 0 (it is <= 0 wherever the
+      // element is kept: gamma does not increase) and the masks are selects.
+      // A[i][j], i = 16 wave + 4 g + e, j = 16 nj + col (K K^T is symmetric)
+      const int ia = wave * 16 + g4 * 4;
+      const f32x4 gi4 = *reinterpret_cast<const f32x4*>(&lds.gamma[ia]);
+      const f32x4 bri4 = *reinterpret_cast<const f32x4*>(&lds.beta[ia]) *
+                         *reinterpret_cast<const f32x4*>(&lds.rk[ia]);
 #pragma unroll
-    for (int jb = 0; jb < 2; ++jb) {
-      if (jb > (wave >> 1)) break;                 // uniform per wave
-      s16x4 hi[2], lo[2];
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        const int nj = 2 * jb + hf;
-        const int j0 = nj * 16 + g4 * 4;
-        const f32x4 gj4 = *reinterpret_cast<const f32x4*>(&lds.gamma[j0]);
-        const f32x4 rkj4 = *reinterpret_cast<const f32x4*>(&lds.rk[j0]);
-        f32x4 pv;
+      for (int nj = 0; nj < 4; ++nj) {
+        const int j = nj * 16 + col;
+        const float gj = lds.gamma[j];
+        const float rkj = lds.rk[j];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float dec = __expf(fminf(gi - gj4[e], 0.0f));
-          const float x = sqi * rkj4[e] * dec * pt[nj][e];
-          pv[e] = j0 + e <= i ? x : 0.0f;
+          const float dec = __expf(fminf(gi4[e] - gj, 0.0f));
+          const float x = bri4[e] * rkj * dec * kk[nj][e];
+          lds.A[(ia + e) * kF64Stride + j] = j < ia + e ? x : 0.0f;
         }
-        split4(pv, hi[hf], lo[hf]);
       }
-      const int bo = tri_blk(wave, jb) * kBlk + lane * 8;
-      *reinterpret_cast<s16x8*>(slot16 + 2 * kSlotPh + bo) = cat(hi[0], hi[1]);
-      *reinterpret_cast<s16x8*>(slot16 + 2 * kSlotPl + bo) = cat(lo[0], lo[1]);
-    }
-  }
-  block_sync_lds();
-
-  // T = (I + A)^-1 by block recursion on 16 x 16 blocks (A is strictly lower
-  // triangular, so T is unit lower triangular; the upper blocks stay zero):
-  // 1. each wave inverts one diagonal block by forward substitution (one
-  //    column per lane, two partial sums per dot product);
-  if (lane < 16) {
-    const int b0 = wave * 16;
-    float t[16];
+      // P[i][j], i = 16 wave + col, j = 16 nj + 4 g + e; the token blocks
+      // jb <= wave / 2 (the others are zero)
+      const int i = wave * 16 + col;
+      const float gi = lds.gamma[i];
+      const float sqi = p.scale * lds.rq[i];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float s0 = (r == lane) ? 1.0f : 0.0f, s1 = 0.0f;
+      for (int jb = 0; jb < 2; ++jb) {
+        if (jb > (wave >> 1)) break;                 // uniform per wave
+        s16x4 hi[2], lo[2];
 #pragma unroll
-      for (int j = 0; j < r; ++j) {
-        const float aij = lds.A[(b0 + r) * kF64Stride + b0 + j];
-        if (j & 1) s1 = fmaf(-aij, t[j], s1); else s0 = fmaf(-aij, t[j], s0);
+        for (int hf = 0; hf < 2; ++hf) {
+          const int nj = 2 * jb + hf;
+          const int j0 = nj * 16 + g4 * 4;
+          const f32x4 gj4 = *reinterpret_cast<const f32x4*>(&lds.gamma[j0]);
+          const f32x4 rkj4 = *reinterpret_cast<const f32x4*>(&lds.rk[j0]);
+          f32x4 pv;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float dec = __expf(fminf(gi - gj4[e], 0.0f));
+            const float x = sqi * rkj4[e] * dec * pt[nj][e];
+            pv[e] = j0 + e <= i ? x : 0.0f;
+          }
+          split4(pv, hi[hf], lo[hf]);
+        }
+        const int bo = tri_blk(wave, jb) * kBlk + lane * 8;
+        *reinterpret_cast<s16x8*>(slot16 + 2 * kSlotPh + bo) = cat(hi[0], hi[1]);
+        *reinterpret_cast<s16x8*>(slot16 + 2 * kSlotPl + bo) = cat(lo[0], lo[1]);
       }
-      t[r] = s0 + s1;
-      lds.T[(b0 + r) * kF64Stride + b0 + lane] = t[r];
     }
-  }
-  block_sync_lds();
-  // 2. the 32 x 32 diagonal halves: T_10 = -T_11 A_10 T_00 (wave 0) and
-  //    T_32 = -T_33 A_32 T_22 (wave 1), through LDS within the wave;
-  if (wave < 2) {
-    const int b = wave * 32;
-    float* Xw = &lds.T[32] + wave * 16 * kF64Stride;
-    const f32x4 x = mm16_f32(&lds.A[(b + 16) * kF64Stride + b], kF64Stride,
-                             &lds.T[b * kF64Stride + b], kF64Stride, col, g4);
-    store16(Xw, kF64Stride, x, 1.0f, col, g4);
-    const f32x4 y = mm16_f32(&lds.T[(b + 16) * kF64Stride + b + 16], kF64Stride, Xw,
-                             kF64Stride, col, g4);
-    store16(&lds.T[(b + 16) * kF64Stride + b], kF64Stride, y, -1.0f, col, g4);
-  }
-  block_sync_lds();
-  // 3. the lower-left 32 x 32 quarter: T_BA = -T_B (A_BA T_A), one 16 x 16
-  //    tile per wave.
-  {
-    const int rb = wave >> 1, cb = wave & 1;
-    const float* Arow = &lds.A[(32 + 16 * rb) * kF64Stride];
-    const f32x4 x = mm16_f32(Arow, kF64Stride, &lds.T[16 * cb], kF64Stride, col, g4) +
-                    mm16_f32(Arow + 16, kF64Stride, &lds.T[16 * kF64Stride + 16 * cb],
-                             kF64Stride, col, g4);
-    store16(&lds.T[16 * rb * kF64Stride + 32 + 16 * cb], kF64Stride, x, 1.0f, col, g4);
-  }
-  block_sync_lds();
-  {
-    const int rb = wave >> 1, cb = wave & 1;
-    const float* Trow = &lds.T[(32 + 16 * rb) * kF64Stride + 32];
-    const float* X = &lds.T[32];
-    const f32x4 y = mm16_f32(Trow, kF64Stride, &X[16 * cb], kF64Stride, col, g4) +
-                    mm16_f32(Trow + 16, kF64Stride, &X[16 * kF64Stride + 16 * cb], kF64Stride,
-                             col, g4);
-    store16(&lds.T[(32 + 16 * rb) * kF64Stride + 16 * cb], kF64Stride, y, -1.0f, col, g4);
-  }
-  block_sync_lds();
+    block_sync_lds();
 
-  // T diag(beta) in operand order: lower block (rb, kb) holds, for lane
-  // (col, g), T[16 rb + col][32 kb + k] beta[32 kb + k] at the 8 k of its
-  // items.  Wave w writes block w, waves 0 and 1 also blocks 4 and 5.
-  // Blocks (0, 0) and (2, 1) read T_01 and T_23 (zero); none reads the
-  // recursion's scratch quarter.
+    // T = (I + A)^-1 by block recursion on 16 x 16 blocks (A is strictly lower
+    // triangular, so T is unit lower triangular; the upper blocks stay zero):
+    // 1. each wave inverts one diagonal block by forward substitution (one
+    //    column per lane, two partial sums per dot product);
+    if (lane < 16) {
+      const int b0 = wave * 16;
+      float t[16];
 #pragma unroll
-  for (int rep = 0; rep < 2; ++rep) {
-    const int idx = wave + 4 * rep;
-    if (idx >= kTriBlocks) break;                  // uniform per wave
-    const int rb = idx < 3 ? idx : (idx + 2) >> 1;     // tri_blk(rb, kb) == idx
-    const int kb = idx == 3 || idx == 5 ? 1 : 0;
-    const float* trow = &lds.T[(16 * rb + col) * kF64Stride + 32 * kb + 4 * g4];
-    const float* brow = &lds.beta[32 * kb + 4 * g4];
-    s16x4 hi[2], lo[2];
+      for (int r = 0; r < 16; ++r) {
+        float s0 = (r == lane) ? 1.0f : 0.0f, s1 = 0.0f;
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf)
-      split4(*reinterpret_cast<const f32x4*>(trow + 16 * hf) *
-                 *reinterpret_cast<const f32x4*>(brow + 16 * hf),
-             hi[hf], lo[hf]);
-    const int bo = idx * kBlk + lane * 8;
-    *reinterpret_cast<s16x8*>(slot16 + 2 * kSlotTh + bo) = cat(hi[0], hi[1]);
-    *reinterpret_cast<s16x8*>(slot16 + 2 * kSlotTl + bo) = cat(lo[0], lo[1]);
-  }
+        for (int j = 0; j < r; ++j) {
+          const float aij = lds.A[(b0 + r) * kF64Stride + b0 + j];
+          if (j & 1) s1 = fmaf(-aij, t[j], s1); else s0 = fmaf(-aij, t[j], s0);
+        }
+        t[r] = s0 + s1;
+        lds.T[(b0 + r) * kF64Stride + b0 + lane] = t[r];
+      }
+    }
+    block_sync_lds();
+    // 2. the 32 x 32 diagonal halves: T_10 = -T_11 A_10 T_00 (wave 0) and
+    //    T_32 = -T_33 A_32 T_22 (wave 1), through LDS within the wave;
+    if (wave < 2) {
+      const int b = wave * 32;
+      float* Xw = &lds.T[32] + wave * 16 * kF64Stride;
+      const f32x4 x = mm16_f32(&lds.A[(b + 16) * kF64Stride + b], kF64Stride,
+                               &lds.T[b * kF64Stride + b], kF64Stride, col, g4);
+      store16(Xw, kF64Stride, x, 1.0f, col, g4);
+      const f32x4 y = mm16_f32(&lds.T[(b + 16) * kF64Stride + b + 16], kF64Stride, Xw,
+                               kF64Stride, col, g4);
+      store16(&lds.T[(b + 16) * kF64Stride + b], kF64Stride, y, -1.0f, col, g4);
+    }
+    block_sync_lds();
+    // 3. the lower-left 32 x 32 quarter: T_BA = -T_B (A_BA T_A), one 16 x 16
+    //    tile per wave.
+    {
+      const int rb = wave >> 1, cb = wave & 1;
+      const float* Arow = &lds.A[(32 + 16 * rb) * kF64Stride];
+      const f32x4 x = mm16_f32(Arow, kF64Stride, &lds.T[16 * cb], kF64Stride, col, g4) +
+                      mm16_f32(Arow + 16, kF64Stride, &lds.T[16 * kF64Stride + 16 * cb],
+                               kF64Stride, col, g4);
+      store16(&lds.T[16 * rb * kF64Stride + 32 + 16 * cb], kF64Stride, x, 1.0f, col, g4);
+    }
+    block_sync_lds();
+    {
+      const int rb = wave >> 1, cb = wave & 1;
+      const float* Trow = &lds.T[(32 + 16 * rb) * kF64Stride + 32];
+      const float* X = &lds.T[32];
+      const f32x4 y = mm16_f32(Trow, kF64Stride, &X[16 * cb], kF64Stride, col, g4) +
+                      mm16_f32(Trow + 16, kF64Stride, &X[16 * kF64Stride + 16 * cb], kF64Stride,
+                               col, g4);
+      store16(&lds.T[(32 + 16 * rb) * kF64Stride + 16 * cb], kF64Stride, y, -1.0f, col, g4);
+    }
+    block_sync_lds();
 
-  // Row scales for the scan: the decayed K rows of X, the Q rows of the
-  // output, the K rows of the state update, and the chunk decay.
-  if (wave == 1) {
-    const float gl = lds.gamma[kChunk - 1];        // padded rows carry gamma forward
-    const float gi = lds.gamma[lane];
-    const float rki = lds.rk[lane];
-    slot[kSlotXg + lane] = rki * __expf(gi);
-    slot[kSlotQs + lane] = p.scale * lds.rq[lane] * __expf(gi);
-    slot[kSlotKs + lane] = rki * __expf(gl - gi);
-    slot[kSlotGl + lane] = __expf(gl);
+    // T diag(beta) in operand order: lower block (rb, kb) holds, for lane
+    // (col, g), T[16 rb + col][32 kb + k] beta[32 kb + k] at the 8 k of its
+    // items.  Wave w writes block w, waves 0 and 1 also blocks 4 and 5.
+    // Blocks (0, 0) and (2, 1) read T_01 and T_23 (zero); none reads the
+    // recursion's scratch quarter.
+#pragma unroll
+    for (int rep = 0; rep < 2; ++rep) {
+      const int idx = wave + 4 * rep;
+      if (idx >= kTriBlocks) break;                  // uniform per wave
+      const int rb = idx < 3 ? idx : (idx + 2) >> 1;     // tri_blk(rb, kb) == idx
+      const int kb = idx == 3 || idx == 5 ? 1 : 0;
+      const float* trow = &lds.T[(16 * rb + col) * kF64Stride + 32 * kb + 4 * g4];
+      const float* brow = &lds.beta[32 * kb + 4 * g4];
+      s16x4 hi[2], lo[2];
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+        split4(*reinterpret_cast<const f32x4*>(trow + 16 * hf) *
+                   *reinterpret_cast<const f32x4*>(brow + 16 * hf),
+               hi[hf], lo[hf]);
+      const int bo = idx * kBlk + lane * 8;
+      *reinterpret_cast<s16x8*>(slot16 + 2 * kSlotTh + bo) = cat(hi[0], hi[1]);
+      *reinterpret_cast<s16x8*>(slot16 + 2 * kSlotTl + bo) = cat(lo[0], lo[1]);
+    }
+
+    // Row scales for the scan: the decayed K rows of X, the Q rows of the
+    // output, the K rows of the state update, and the chunk decay.
+    if (wave == 1) {
+      const float gl = lds.gamma[kChunk - 1];        // padded rows carry gamma forward
+      const float gi = lds.gamma[lane];
+      const float rki = lds.rk[lane];
+      slot[kSlotXg + lane] = rki * __expf(gi);
+      slot[kSlotQs + lane] = p.scale * lds.rq[lane] * __expf(gi);
+      slot[kSlotKs + lane] = rki * __expf(gl - gi);
+      slot[kSlotGl + lane] = __expf(gl);
+    }
+    block_sync_lds();                        // this v-head's LDS reads are done
   }
 }
 
@@ -1554,7 +1563,7 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
   if (e != hipSuccess) return e;
   if (slots > 0) {
     auto* prep = p.few ? prep_kernel<true> : prep_kernel<false>;
-    hipLaunchKernelGGL(prep, dim3(static_cast<unsigned>(slots), HV), dim3(kThreads), 0,
+    hipLaunchKernelGGL(prep, dim3(static_cast<unsigned>(slots), H), dim3(kThreads), 0,
                        stream, p);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
