@@ -745,10 +745,10 @@ def prefill_bytes(lens, H, HV) -> int:
 
 def prefill_workspace_bytes(lens, H, HV) -> int:
     """Bytes the preparation kernel writes: a slot per (chunk, v-head), the
-    six lower 16 x 32 operand blocks of T diag(beta) and of P as bf16 hi/lo,
-    and four rows of 64 fp32 scales."""
+    six lower 16 x 32 operand blocks of T diag(beta) as bf16 hi/lo and eight
+    rows of 64 fp32 scales (six used)."""
     chunks = sum((n + 63) // 64 for n in lens)
-    vslot = 4 * 6 * 16 * 32 * 2 + 4 * 64 * 4
+    vslot = 2 * 6 * 16 * 32 * 2 + 8 * 64 * 4
     return chunks * HV * vslot
 
 
@@ -820,7 +820,7 @@ def prefill_roofline(prefill: dict) -> dict:
     ku = r["kernel_us"]
     achieved = flop / (ku["kernels"] * 1e-6) / 1e12
     L = sum(lens)
-    prep_in = L * (2 * H * 128 * 2 + 2 * HV * 2)          # q, k, a, b
+    prep_in = L * (H * 128 * 2 + 2 * HV * 2)              # k, a, b
     prep_bytes = prep_in + r["prep_workspace_bytes"]
     prep_gbs = prep_bytes / (ku["prep"] * 1e-6) / 1e9
     tr = _prefill_traffic()

@@ -32,12 +32,13 @@
 //      and writes each slot's sequence, first token and token count.  With
 //      one sequence, or a few (their slots found in the kernels), it is not
 //      launched.
-//   2. prep, grid (chunk slots, HV), three workgroups per CU: what does not
-//      depend on the state, for all chunks at once -- gates and gamma, K K^T
-//      and Q K^T (bf16 MFMA: the inputs are bf16), T by block recursion
-//      (fp32 MFMA) -- into a 25 KiB workspace slot per (chunk, v-head): the
-//      lower blocks of T diag(beta) and of P = Q K^T (.) M, split into bf16
-//      hi + lo in the order the scan's MFMAs read them, and the row scales.
+//   2. prep, grid (chunk slots, H), three workgroups per CU: what does not
+//      depend on the state, for all chunks at once -- K K^T (bf16 MFMA: the
+//      inputs are bf16, once per q/k head), then per v-head the gates and
+//      gamma and T by block recursion (fp32 MFMA) -- into a 14 KiB workspace
+//      slot per (chunk, v-head): the lower blocks of T diag(beta), split
+//      into bf16 hi + lo in the order the scan's MFMAs read them, and the
+//      row scales.
 //   3. scan, one workgroup per (sequence, v-head), XCD-aware order: the
 //      sequential part chunk after chunk with the whole 128 x 128 state in
 //      the registers of four wavefronts (32 columns each); the chunk's K,
@@ -121,26 +122,26 @@ constexpr float kSoftplusThreshold = 20.0f;
 constexpr float kLn2 = 0.693147180559945309f;
 
 // Workspace slot of one (chunk, v-head), offsets in floats.  The scan's MFMA
-// operands T diag(beta) and P are stored in operand order: a 16 x 32 block
-// is 64 lanes x 8 bf16 contiguous (lane = row + 16 g, items in the k order
-// above), so a wave reads one with a single 1 KiB access.  Both are lower
-// triangular 64 x 64, so only the blocks (row block rb, token block kb) with
-// kb <= rb / 2 are kept, six of eight.  fp32 values are split into a bf16
-// high and low part (x ~ hi + lo to ~2^-16 relative).
+// operand T diag(beta) is stored in operand order: a 16 x 32 block is 64
+// lanes x 8 bf16 contiguous (lane = row + 16 g, items in the k order above),
+// so a wave reads one with a single 1 KiB access.  It is lower triangular
+// 64 x 64, so only the blocks (row block rb, token block kb) with kb <= rb / 2
+// are kept, six of eight, split into a bf16 high and low part (x ~ hi + lo
+// to ~2^-16 relative).  Then rows of 64 per-token scales.
 constexpr int kBlk = 512;                             // bf16 per 16 x 32 operand block
 constexpr int kBlkF = kBlk / 2;                       // the same in floats
 constexpr int kTriBlocks = 6;
 __host__ __device__ constexpr int tri_blk(int rb, int kb) { return (rb < 3 ? rb : 4) + kb; }
 constexpr int kSlotTh = 0;                            // T diag(beta), hi
 constexpr int kSlotTl = kSlotTh + kTriBlocks * kBlkF; //   lo
-constexpr int kSlotPh = kSlotTl + kTriBlocks * kBlkF; // P = scale rq_i rk_j M_ij (Q K^T)_ij, hi
-constexpr int kSlotPl = kSlotPh + kTriBlocks * kBlkF; //   lo
-constexpr int kSlotXg = kSlotPl + kTriBlocks * kBlkF; // rk_i e^gamma_i [64]
-constexpr int kSlotQs = kSlotXg + kChunk;             // scale rq_i e^gamma_i [64]
-constexpr int kSlotKs = kSlotQs + kChunk;             // rk_i e^(gamma_C - gamma_i) [64]
-constexpr int kSlotGl = kSlotKs + kChunk;             // e^gamma_C [1], padded to 64
-constexpr int kSlotFloats = kSlotGl + 64;
-static_assert(kSlotFloats % 64 == 0, "slots stay 256-byte aligned");
+constexpr int kSlotXg = kSlotTl + kTriBlocks * kBlkF; // rk_i e^gamma_i [64]
+constexpr int kSlotEg = kSlotXg + kChunk;             // e^gamma_i [64]
+constexpr int kSlotKs = kSlotEg + kChunk;             // rk_i e^(gamma_C - gamma_i) [64]
+constexpr int kSlotGl = kSlotKs + kChunk;             // e^gamma_C [64 copies]
+constexpr int kSlotGa = kSlotGl + kChunk;             // gamma_i [64]
+constexpr int kSlotRk = kSlotGa + kChunk;             // rk_i [64]
+constexpr int kSlotFloats = kSlotRk + 3 * kChunk;     // padded to whole 1 KiB DMA pieces
+static_assert(kSlotFloats % 256 == 0, "slots stay 1 KiB aligned");
 static_assert(tri_blk(3, 1) == kTriBlocks - 1, "six lower blocks");
 
 // k (0..31) of item e of lane group g inside a 32-long block.
@@ -401,7 +402,6 @@ struct PrepLds {
   float T[kChunk * kF64Stride];       // (I + A)^-1
   float gamma[kChunk];
   float beta[kChunk];
-  float rq[kChunk];
   float rk[kChunk];
 };
 static_assert(sizeof(PrepLds) <= 160 * 1024 / 3, "three preparation workgroups per CU");
@@ -466,17 +466,6 @@ void prep_kernel(Params p) {
   load_rows_bf16(kreg, p.k + (static_cast<size_t>(t0) * p.H + h) * kDim,
                  static_cast<size_t>(p.H) * kDim, n);
 
-  // Q rows 16 wave + col straight into MFMA operand registers (k block m;
-  // rows past the chunk's end zero); with the L2-norm, their row norms.
-  s16x8 qa[4];
-  const int ra = wave * 16 + col;
-  const bool row_ok = ra < n;
-  {
-    const uint16_t* qrow =
-        p.q + ((static_cast<size_t>(t0) + (row_ok ? ra : n - 1)) * p.H + h) * kDim;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) qa[m] = frag(qrow, m, g4);
-  }
   store_rows_bf16(lds.K, kreg, n);
   // T's upper blocks that the block recursion multiplies, T_01 and T_23, are
   // zero; the diagonal and lower blocks are all written, the other upper
@@ -486,21 +475,6 @@ void prep_kernel(Params p) {
     const int idx = threadIdx.x + it * kThreads;
     const int o = 32 * (idx >> 8);
     lds.T[(o + ((idx >> 4) & 15)) * kF64Stride + o + 16 + (idx & 15)] = 0.0f;
-  }
-  {
-    float sq = 0.0f;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      qa[m] = row_ok ? qa[m] : s16x8{0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float x = bf16_to_f32(static_cast<uint16_t>(qa[m][e]));
-        sq = fmaf(x, x, sq);
-      }
-    }
-    sq += __shfl_xor(sq, 16, 64);
-    sq += __shfl_xor(sq, 32, 64);
-    if (g4 == 0) lds.rq[ra] = p.l2norm ? __builtin_amdgcn_rsqf(sq + kL2Eps) : 1.0f;
   }
   block_sync_lds();
 
@@ -521,18 +495,12 @@ void prep_kernel(Params p) {
   }
   block_sync_lds();
 
-  // K K^T for row block `wave` (rows 16 wave .. +15) and (Q K^T)^T = K Q^T
-  // for column block `wave`, all 4 blocks of the other index; bf16 MFMA over
-  // the 128-long rows.  The transposed product leaves each lane holding 4
-  // consecutive j of one row i of P, two of which make the scan's operand
-  // items, so P goes out as one 16-byte store per lane and k block.
-  f32x4 kk[4], pt[4];
+  // K K^T for row block `wave` (rows 16 wave .. +15), all 4 column blocks;
+  // bf16 MFMA over the 128-long rows
+  f32x4 kk[4];
   {
 #pragma unroll
-    for (int nj = 0; nj < 4; ++nj) {
-      kk[nj] = f32x4{0, 0, 0, 0};
-      pt[nj] = f32x4{0, 0, 0, 0};
-    }
+    for (int nj = 0; nj < 4; ++nj) kk[nj] = f32x4{0, 0, 0, 0};
     const int ra = wave * 16 + col;
 #pragma unroll
     for (int m = 0; m < kDim / 32; ++m) {
@@ -541,13 +509,12 @@ void prep_kernel(Params p) {
       for (int nj = 0; nj < 4; ++nj) {
         const s16x8 bk = frag(&lds.K[(nj * 16 + col) * kBfStride], m, g4);
         kk[nj] = mfma_bf16(ak, bk, kk[nj]);
-        pt[nj] = mfma_bf16(bk, qa[m], pt[nj]);
       }
     }
   }
 
-  // Each v-head of the group: its gates, A and P from the shared products,
-  // T, and its slot.  The LDS the previous v-head used (gamma, beta, A, T)
+  // Each v-head of the group: its gates, A from the shared product, T, and
+  // its slot.  The LDS the previous v-head used (gamma, beta, A, T)
   // is rewritten only after the barrier that ends its use.
   for (int j = 0; j < p.ratio; ++j) {
     const int hv = h * p.ratio + j;
@@ -589,34 +556,6 @@ void prep_kernel(Params p) {
           const float x = bri4[e] * rkj * dec * kk[nj][e];
           lds.A[(ia + e) * kF64Stride + j] = j < ia + e ? x : 0.0f;
         }
-      }
-      // P[i][j], i = 16 wave + col, j = 16 nj + 4 g + e; the token blocks
-      // jb <= wave / 2 (the others are zero)
-      const int i = wave * 16 + col;
-      const float gi = lds.gamma[i];
-      const float sqi = p.scale * lds.rq[i];
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb) {
-        if (jb > (wave >> 1)) break;                 // uniform per wave
-        s16x4 hi[2], lo[2];
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          const int nj = 2 * jb + hf;
-          const int j0 = nj * 16 + g4 * 4;
-          const f32x4 gj4 = *reinterpret_cast<const f32x4*>(&lds.gamma[j0]);
-          const f32x4 rkj4 = *reinterpret_cast<const f32x4*>(&lds.rk[j0]);
-          f32x4 pv;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float dec = __expf(fminf(gi - gj4[e], 0.0f));
-            const float x = sqi * rkj4[e] * dec * pt[nj][e];
-            pv[e] = j0 + e <= i ? x : 0.0f;
-          }
-          split4(pv, hi[hf], lo[hf]);
-        }
-        const int bo = tri_blk(wave, jb) * kBlk + lane * 8;
-        *reinterpret_cast<s16x8*>(slot16 + 2 * kSlotPh + bo) = cat(hi[0], hi[1]);
-        *reinterpret_cast<s16x8*>(slot16 + 2 * kSlotPl + bo) = cat(lo[0], lo[1]);
       }
     }
     block_sync_lds();
@@ -700,16 +639,20 @@ void prep_kernel(Params p) {
       *reinterpret_cast<s16x8*>(slot16 + 2 * kSlotTl + bo) = cat(lo[0], lo[1]);
     }
 
-    // Row scales for the scan: the decayed K rows of X, the Q rows of the
-    // output, the K rows of the state update, and the chunk decay.
+    // Row scales for the scan: the decayed K rows of X, the decay of the
+    // output's rows, the K rows of the state update, the chunk decay, and
+    // gamma and the K row scales for its P.
     if (wave == 1) {
       const float gl = lds.gamma[kChunk - 1];        // padded rows carry gamma forward
       const float gi = lds.gamma[lane];
       const float rki = lds.rk[lane];
-      slot[kSlotXg + lane] = rki * __expf(gi);
-      slot[kSlotQs + lane] = p.scale * lds.rq[lane] * __expf(gi);
+      const float egi = __expf(gi);
+      slot[kSlotXg + lane] = rki * egi;
+      slot[kSlotEg + lane] = egi;
       slot[kSlotKs + lane] = rki * __expf(gl - gi);
       slot[kSlotGl + lane] = __expf(gl);
+      slot[kSlotGa + lane] = gi;
+      slot[kSlotRk + lane] = rki;
     }
     block_sync_lds();                        // this v-head's LDS reads are done
   }
@@ -747,15 +690,12 @@ constexpr int kScanThreads = 64 * kScanWaves;
 constexpr int kRowPieces = kDim / 8 + 1;          // 16-byte pieces per K / Q row, one of padding
 constexpr int kRowStride = kRowPieces * 8;        // bf16 (68 dwords)
 constexpr int kRowDma = kChunk * kRowPieces / 64; // DMA instructions per K / Q chunk (17)
-constexpr int kSlotDma = kSlotFloats / 4 / 64;    // DMA instructions per slot (25)
+constexpr int kSlotDma = kSlotFloats / 4 / 64;    // DMA instructions per slot (14)
 static_assert(kChunk * kRowPieces % 64 == 0 && kSlotFloats % 256 == 0, "whole DMA instructions");
-// Without outputs a chunk needs neither Q nor P: its LDS slot holds T
-// diag(beta) (hi, lo) and then the row scales.
-constexpr int kSlotTFloats = 2 * kTriBlocks * kBlkF;
-constexpr int kSlotGates = kSlotFloats - kSlotXg;     // the four rows of scales
-static_assert(kSlotTFloats == kSlotPh && kSlotXg == 2 * kSlotTFloats, "slot layout");
 // K^T operand blocks of a chunk: (key tile t, token block kb), 64 lanes x 8 bf16
 constexpr int kKtElems = 8 * 2 * 64 * 8;
+// P' operand blocks (the six lower (row block, token block) ones), hi then lo
+constexpr int kPElems = 2 * kTriBlocks * kBlk;
 
 template <bool OUT> struct ScanBuf;
 template <> struct ScanBuf<true> {
@@ -763,13 +703,12 @@ template <> struct ScanBuf<true> {
   uint16_t Qr[kChunk * kRowStride];
   float slot[kSlotFloats];
 };
-template <> struct ScanBuf<false> {
+template <> struct ScanBuf<false> {       // without outputs a chunk needs no Q
   uint16_t Kr[kChunk * kRowStride];
-  float slot[kSlotTFloats + kSlotGates];
+  float slot[kSlotFloats];
 };
-static_assert(2 * sizeof(ScanBuf<true>) + kKtElems * 2 <= 160 * 1024, "one scan workgroup per CU");
-// LDS offset of the row scales (Xg, then Qs, Ks, Gl as in the slot)
-template <bool OUT> __device__ constexpr int lds_gates() { return OUT ? kSlotXg : kSlotTFloats; }
+static_assert(2 * sizeof(ScanBuf<true>) + 2 * (kKtElems + kPElems) <= 160 * 1024,
+              "one scan workgroup per CU");
 
 typedef __attribute__((address_space(1))) void global_void;
 typedef __attribute__((address_space(3))) void lds_void;
@@ -796,9 +735,8 @@ __device__ __forceinline__ void barrier_lds_no_dma() {
 }
 
 // DMA of a chunk's K rows, Q rows (OUT; rows >= n repeat row n - 1; each
-// row's padding piece repeats its last piece) and slot (without outputs: T
-// diag(beta) and the row scales) into one LDS buffer; wave w issues
-// instructions w, w + 8, ....
+// row's padding piece repeats its last piece) and slot into one LDS buffer;
+// wave w issues instructions w, w + 8, ....
 template <bool OUT>
 __device__ __forceinline__ void scan_dma(ScanBuf<OUT>& B, const uint16_t* kbase,
                                          const uint16_t* qbase, unsigned step, int n,
@@ -810,16 +748,8 @@ __device__ __forceinline__ void scan_dma(ScanBuf<OUT>& B, const uint16_t* kbase,
     dma16(kbase + off, &B.Kr[i * 512]);
     if constexpr (OUT) dma16(qbase + off, &B.Qr[i * 512]);
   }
-  if constexpr (OUT) {
-    for (int i = wave; i < kSlotDma; i += kScanWaves)
-      dma16(slot + (i * 64 + lane) * 4, &B.slot[i * 256]);
-  } else {
-    constexpr int kT = kSlotTFloats / 256, kG = kSlotGates / 256;
-    for (int i = wave; i < kT + kG; i += kScanWaves) {
-      const int from = i < kT ? i * 256 : kSlotXg + (i - kT) * 256;
-      dma16(slot + from + lane * 4, &B.slot[i * 256]);
-    }
-  }
+  for (int i = wave; i < kSlotDma; i += kScanWaves)
+    dma16(slot + (i * 64 + lane) * 4, &B.slot[i * 256]);
 }
 
 // This wave's 16 columns of V for token tile r (lane (col, g): token
@@ -863,7 +793,8 @@ struct ScanCtx {
   unsigned kstep, vstep;       // elements from one token's K / Q row (V row) to the next
   int start, end, nchunks;     // token range and chunks
   int H, HV, h, hv;
-  bool values;
+  float scale;
+  bool values, l2norm;
 };
 
 // Chunk c's DMA into buf and its V into registers.
@@ -880,16 +811,32 @@ __device__ __forceinline__ void scan_issue(ScanBuf<OUT>* buf, const ScanCtx& cx,
          lane & 15, lane >> 4);
 }
 
+// P' tiles (row tile r, token tile jt) of a chunk, 10 nonzero and the two
+// zero ones inside the stored blocks (0, 1) and (2, 3); wave w makes tiles w
+// and w + 8.
+__device__ constexpr int kPTiles = 12;
+__device__ constexpr int8_t kPTileR[kPTiles] = {0, 1, 1, 2, 2, 2, 3, 3, 3, 3, 0, 2};
+__device__ constexpr int8_t kPTileJ[kPTiles] = {0, 0, 1, 0, 1, 2, 0, 1, 2, 3, 1, 3};
+
 // Chunk ci from buffer B, with the next chunk's DMA into Bn; Kt: the K^T
-// operand blocks.  B, Bn and Kt are restrict: the compiler then knows that
-// the DMA in flight into Bn never writes what this chunk reads, and waits
-// for it only at the end.  OUT: the outputs too (else only the state).
+// operand blocks; Pb: the P' operand blocks (OUT).  B, Bn, Kt and Pb are
+// restrict: the compiler then knows that the DMA in flight into Bn never
+// writes what this chunk reads, and waits for it only at the end.  OUT: the
+// outputs too (else only the state).
+//
+// The output's intra-chunk term uses P = diag(rq) P' with
+//   P'_ij = scale rk_j e^(gamma_i - gamma_j) (Q K^T)_ij,  j <= i,
+// made here from the chunk's K and Q rows: (K Q^T) tiles on bf16 MFMA leave
+// each lane 4 consecutive j of one row i, the operand items of P' as the B
+// operand of Delta^T P'^T.  The Q row norms rq (L2-norm) come from the
+// squares of the Q items the S^T Q^T product reads, and scale the output
+// row: O = diag(rq) (diag(scale e^gamma) Q S + P' Delta).
 template <bool OUT>
 __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
                                            ScanBuf<OUT>* __restrict__ Bn,
-                                           uint16_t* __restrict__ Kt, const ScanCtx& cx,
-                                           f32x4 (&st)[8], u32x2 (&vnext)[4], const s16x8& sel,
-                                           int ci) {
+                                           uint16_t* __restrict__ Kt, uint16_t* __restrict__ Pb,
+                                           const ScanCtx& cx, f32x4 (&st)[8],
+                                           u32x2 (&vnext)[4], const s16x8& sel, int ci) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int col = lane & 15;
@@ -900,23 +847,54 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
   // the chunk's row scales, and key tile `wave` of K^T (the selector
   // products of the K row blocks (r, wave / 2) give lane (col, g) tokens
   // 16 r + 4 g + e of key 16 wave + col), read before the DMA below is issued
-  constexpr int kG = lds_gates<OUT>();
   f32x4 xg[4], ks[4];
   float qs[4];
   s16x4 kt[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    xg[r] = *reinterpret_cast<const f32x4*>(&B->slot[kG + r * 16 + g4 * 4]);
-    ks[r] = *reinterpret_cast<const f32x4*>(&B->slot[kG + 128 + r * 16 + g4 * 4]);
-    qs[r] = OUT ? B->slot[kG + 64 + r * 16 + col] : 0.0f;
+    xg[r] = *reinterpret_cast<const f32x4*>(&B->slot[kSlotXg + r * 16 + g4 * 4]);
+    ks[r] = *reinterpret_cast<const f32x4*>(&B->slot[kSlotKs + r * 16 + g4 * 4]);
+    qs[r] = OUT ? cx.scale * B->slot[kSlotEg + r * 16 + col] : 0.0f;
     kt[r] = to_bf16x4(mfma_bf16(frag(&B->Kr[(r * 16 + col) * kRowStride], wave >> 1, g4), sel,
                                 f32x4{0, 0, 0, 0}));
   }
-  const float gl = B->slot[kG + 192];
+  const float gl = B->slot[kSlotGl];
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
     *reinterpret_cast<s16x8*>(Kt + ((wave * 2 + kb) * 64 + lane) * 8) =
         cat(kt[2 * kb], kt[2 * kb + 1]);
+  if constexpr (OUT) {
+    // P' tiles (r, jt): lane (col, g) holds row i = 16 r + col, tokens
+    // j = 16 jt + 4 g + e; items 4 (jt % 2) .. + 3 of block (r, jt / 2)
+#pragma unroll
+    for (int rep = 0; rep < 2; ++rep) {
+      const int idx = wave + kScanWaves * rep;
+      if (idx >= kPTiles) break;                       // uniform per wave
+      const int r = kPTileR[idx], jt = kPTileJ[idx];
+      f32x4 pv = {0, 0, 0, 0};
+      if (jt <= r) {                                   // uniform per wave
+        f32x4 acc = {0, 0, 0, 0};
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+          acc = mfma_bf16(frag(&B->Kr[(jt * 16 + col) * kRowStride], kb, g4),
+                          frag(&B->Qr[(r * 16 + col) * kRowStride], kb, g4), acc);
+        const int i = r * 16 + col, j0 = jt * 16 + g4 * 4;
+        const float gi = B->slot[kSlotGa + i];
+        const f32x4 gj = *reinterpret_cast<const f32x4*>(&B->slot[kSlotGa + j0]);
+        const f32x4 rkj = *reinterpret_cast<const f32x4*>(&B->slot[kSlotRk + j0]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x = cx.scale * rkj[e] * __expf(fminf(gi - gj[e], 0.0f)) * acc[e];
+          pv[e] = j0 + e <= i ? x : 0.0f;
+        }
+      }
+      s16x4 hi, lo;
+      split4(pv, hi, lo);
+      const int at = tri_blk(r, jt >> 1) * kBlk + lane * 8 + (jt & 1) * 4;
+      *reinterpret_cast<s16x4*>(Pb + at) = hi;
+      *reinterpret_cast<s16x4*>(Pb + kTriBlocks * kBlk + at) = lo;
+    }
+  }
   // the next chunk's inputs into the other buffer (after the last chunk:
   // this one's again, unused), in flight while this chunk computes
   scan_issue(Bn, cx, ci + 1 < cx.nchunks ? ci + 1 : ci, vnext);
@@ -924,8 +902,12 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
   // K S (token rows) and S^T Q^T (the output's first term, transposed),
   // one 32-key block of the state at a time
   f32x4 x[4], o[4];
+  float qq[4];                                     // sums of squares of Q row 16 r + col
 #pragma unroll
-  for (int r = 0; r < 4; ++r) x[r] = o[r] = f32x4{0, 0, 0, 0};
+  for (int r = 0; r < 4; ++r) {
+    x[r] = o[r] = f32x4{0, 0, 0, 0};
+    qq[r] = 0.0f;
+  }
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
     s16x8 sl;
@@ -939,6 +921,13 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
         const s16x8 bq = frag(&B->Qr[(r * 16 + col) * kRowStride], kb, g4);
         o[r] = mfma_bf16(sh, bq, o[r]);
         o[r] = mfma_bf16(sl, bq, o[r]);
+        if (cx.l2norm) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float y = bf16_to_f32(static_cast<uint16_t>(bq[e]));
+            qq[r] = fmaf(y, y, qq[r]);
+          }
+        }
       }
     }
   }
@@ -981,20 +970,29 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
     eh[kb] = split_hi_lo(d[2 * kb] * ks[2 * kb], d[2 * kb + 1] * ks[2 * kb + 1], el[kb]);
   }
 
-  // O^T = qs (.) S^T Q^T + Delta^T P^T; lane (col, g) ends with columns
-  // 16 wave + 4 g + e of token 16 r + col, one 8-byte store
+  // every wave's K^T tile and P' tiles are in LDS past this barrier
+  barrier_lds_no_dma();
+
+  // O^T = rq (.) (qs (.) S^T Q^T + Delta^T P'^T); lane (col, g) ends with
+  // columns 16 wave + 4 g + e of token 16 r + col, one 8-byte store
   if constexpr (OUT) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       o[r] = o[r] * qs[r];
 #pragma unroll
       for (int kb = 0; kb <= (r >> 1); ++kb) {
-        const int bo = tri_blk(r, kb) * kBlkF + lane * 4;
-        const s16x8 ph = ld_op(&B->slot[kSlotPh + bo]);
-        const s16x8 pl = ld_op(&B->slot[kSlotPl + bo]);
+        const int bo = tri_blk(r, kb) * kBlk + lane * 8;
+        const s16x8 ph = ld_op(Pb + bo);
+        const s16x8 pl = ld_op(Pb + kTriBlocks * kBlk + bo);
         o[r] = mfma_bf16(dh[kb], ph, o[r]);
         o[r] = mfma_bf16(dh[kb], pl, o[r]);
         o[r] = mfma_bf16(dl[kb], ph, o[r]);
+      }
+      if (cx.l2norm) {
+        float q2 = qq[r];
+        q2 += __shfl_xor(q2, 16, 64);
+        q2 += __shfl_xor(q2, 32, 64);
+        o[r] = o[r] * __builtin_amdgcn_rsqf(q2 + kL2Eps);
       }
       const int tok = r * 16 + col;
       const u32x2 ob = {pack_bf16x2(o[r][0], o[r][1]), pack_bf16x2(o[r][2], o[r][3])};
@@ -1004,9 +1002,7 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
     }
   }
 
-  // S <- e^gamma_C S + K^T (ks (.) Delta), key tile t; every wave's K^T
-  // tile is in LDS past this barrier
-  barrier_lds_no_dma();
+  // S <- e^gamma_C S + K^T (ks (.) Delta), key tile t
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
     f32x4 acc = st[t] * gl;
@@ -1081,6 +1077,7 @@ void scan_kernel(Params p) {
   // buffer never writes what the chunk reads from the other
   __shared__ ScanBuf<OUT> L0, L1;
   __shared__ __attribute__((aligned(16))) uint16_t Kt[kKtElems];
+  __shared__ __attribute__((aligned(16))) uint16_t Pb[OUT ? kPElems : 8];
   const long long b = blockIdx.x;
   const int ratio = p.ratio;
   const long long pair = (b / (8LL * ratio)) * 8 + (b & 7);
@@ -1204,6 +1201,8 @@ void scan_kernel(Params p) {
   cx.h = h;
   cx.hv = hv;
   cx.values = values;
+  cx.scale = p.scale;
+  cx.l2norm = p.l2norm != 0;
 
   const s16x8 sel = sels[wave & 1];       // this wave's half of a 32-key / 32-column block
   u32x2 vnext[4];
@@ -1211,8 +1210,8 @@ void scan_kernel(Params p) {
   wait_vmem();
   block_sync_lds();
   for (int ci = 0; ci < nchunks; ci += 2) {
-    scan_chunk<OUT>(&L0, &L1, Kt, cx, st, vnext, sel, ci);
-    if (ci + 1 < nchunks) scan_chunk<OUT>(&L1, &L0, Kt, cx, st, vnext, sel, ci + 1);  // uniform
+    scan_chunk<OUT>(&L0, &L1, Kt, Pb, cx, st, vnext, sel, ci);
+    if (ci + 1 < nchunks) scan_chunk<OUT>(&L1, &L0, Kt, Pb, cx, st, vnext, sel, ci + 1);  // uniform
   }
   if (st_out != nullptr) store_end(st_out, identity, st, sels);
 }

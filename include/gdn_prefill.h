@@ -44,7 +44,7 @@ extern "C" {
 
 /*
  * Bytes of device workspace gdn_prefill needs for L total tokens, N
- * sequences, H q/k heads and HV v-heads: per-chunk intermediates (25 KiB
+ * sequences, H q/k heads and HV v-heads: per-chunk intermediates (14 KiB
  * per chunk per v-head, for min(ceil(L / 64) + N, L) chunks, the most a
  * well-formed batch has, rounded up to 256 bytes), a 16-byte table entry per
  * chunk and 4 bytes per sequence, each part rounded up to 256 bytes; for one

@@ -40,9 +40,9 @@ def test_header_and_library_agree():
 
 def test_workspace_size_formula():
     lib = _lib.get_prefill_lib()
-    # per v-head: T diag(beta) and P (six 16 x 32 operand blocks each, bf16
-    # hi and lo), then four rows of 64 scales
-    vslot = (4 * 6 * 16 * 32 * 2 + 4 * 64 * 4)
+    # per v-head: T diag(beta) (six 16 x 32 operand blocks, bf16 hi and lo),
+    # then eight rows of 64 scales
+    vslot = (2 * 6 * 16 * 32 * 2 + 8 * 64 * 4)
     a256 = lambda x: (x + 255) // 256 * 256  # noqa: E731
     for L, N, H, HV in ((6, 1, 4, 8), (16384, 1, 4, 8), (1000, 37, 16, 32), (0, 3, 4, 8),
                         (100, 2, 2, 2), (40, 65600, 1, 1), (3, 10, 4, 8), (3000, 1, 4, 8),

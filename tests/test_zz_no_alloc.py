@@ -83,7 +83,7 @@ def test_noalloc_rejects_sizes_beyond_its_workspace(hip_device):
     hipErrorOutOfMemory before launching anything (outputs untouched) and the
     Python entry raises ValueError naming the limit."""
     _announce("noalloc rejects oversize")
-    lens, H, HV = [4096] * 3, 16, 32
+    lens, H, HV = [4096] * 5, 16, 32
     assert gdn.prefill.workspace_bytes(sum(lens), len(lens), H, HV) > \
         gdn.prefill.NOALLOC_SCRATCH_BYTES
     t = _dev(make_prefill_inputs(lens, H, HV, seed=320), hip_device)
