@@ -1223,77 +1223,82 @@ void scan_kernel(Params p) {
 // segment j its transition M_j (as the A operand blocks of M S, bf16 hi/lo)
 // and zero-start end B_j.  Combine: S_{j+1} = M_j S_j + B_j for j = 1 ..
 // nseg-2, segment after segment, as bf16 MFMA with S_j split into hi + lo.
-// One workgroup per (v-head, 16 state columns); wave w computes rows 32 w ..
-// 32 w + 31 (row tiles 2 w, 2 w + 1) and hands its rows of S_j to the other
-// waves as the B operand's k block w through LDS (two buffers: one barrier a
-// step); the next step's M blocks and B tiles load while this one runs.
-__global__ __launch_bounds__(kThreads) void seg_combine_kernel(Params p) {
+// One workgroup per (v-head, 16 state columns); wave w computes row tile w
+// (rows 16 w .. 16 w + 15) and hands its rows of S_j to the other waves as
+// half of the B operand's k block w / 2 through LDS (two buffers: one
+// barrier a step).  A step is short (12 MFMAs a wave), so each wave's M
+// blocks and B tile are loaded three steps ahead, into three register sets
+// used in turn.  Every workgroup reads all of M_j: the eight of a v-head
+// are numbered hv + 8k (HV rounded up to 8 between them), so all of them run
+// on XCD hv % 8 (workgroups go to the XCDs round-robin) and read M_j from
+// its L2 after the first.
+constexpr int kCombWaves = 8;
+
+struct CombStage {
+  s16x8 ma[4][2];                             // [k block][hi, lo] of row tile w
+  f32x4 bt;                                   // B_j rows of row tile w
+};
+
+__global__ __launch_bounds__(64 * kCombWaves) void seg_combine_kernel(Params p) {
   __shared__ s16x8 Sop[2][4][2][64];          // [buffer][k block][hi, lo][lane]
-  const int hv = blockIdx.x >> 3;
-  const int c0 = (blockIdx.x & 7) * 16;
+  const int hv_pad = (p.HV + 7) & ~7;
+  const int hv = static_cast<int>(blockIdx.x) % hv_pad;
+  const int c0 = static_cast<int>(blockIdx.x) / hv_pad * 16;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int col = lane & 15;
   const int g4 = lane >> 4;
   const size_t blk = static_cast<size_t>(kDim) * kDim;
-  if (p.nseg < 3) return;                     // nothing to chain
-  const size_t tile = static_cast<size_t>(c0 + col) * kDim + wave * 32 + g4 * 4;
-  // S_1, this wave's row tiles 2 w + tt in the MFMA result layout
-  f32x4 S[2];
-  const float* s1 = p.seg_S + (static_cast<size_t>(p.HV) + hv) * blk;
-#pragma unroll
-  for (int tt = 0; tt < 2; ++tt) S[tt] = *reinterpret_cast<const f32x4*>(s1 + tile + tt * 16);
-  auto load_step = [&](int j, s16x8 (&ma)[2][4][2], f32x4 (&bt)[2]) {
+  if (p.nseg < 3 || hv >= p.HV) return;       // nothing to chain; padding
+  const int last = p.nseg - 2;                // steps j = 1 .. last
+  const size_t tile = static_cast<size_t>(c0 + col) * kDim + wave * 16 + g4 * 4;
+  // S_1, this wave's row tile in the MFMA result layout
+  f32x4 S = *reinterpret_cast<const f32x4*>(p.seg_S + (static_cast<size_t>(p.HV) + hv) * blk +
+                                            tile);
+  auto load = [&](int j, CombStage& cs) {     // past the last step: the last one's again
+    j = j < last ? j : last;
     const uint16_t* M =
         reinterpret_cast<const uint16_t*>(p.seg_M + (static_cast<size_t>(j) * p.HV + hv) * blk);
-    const float* Bj = p.seg_B + (static_cast<size_t>(j) * p.HV + hv) * blk;
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
+    for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int hl = 0; hl < 2; ++hl)
-          ma[tt][kb][hl] = *reinterpret_cast<const s16x8*>(
-              M + ((((wave * 2 + tt) * 4 + kb) * 2 + hl) * kBlk + lane * 8));
-      bt[tt] = *reinterpret_cast<const f32x4*>(Bj + tile + tt * 16);
-    }
+      for (int hl = 0; hl < 2; ++hl)
+        cs.ma[kb][hl] =
+            *reinterpret_cast<const s16x8*>(M + (((wave * 4 + kb) * 2 + hl) * kBlk + lane * 8));
+    cs.bt = *reinterpret_cast<const f32x4*>(p.seg_B + (static_cast<size_t>(j) * p.HV + hv) * blk +
+                                            tile);
   };
-  s16x8 ma[2][4][2];
-  f32x4 bt[2];
-  load_step(1, ma, bt);
-  for (int j = 1; j + 1 < p.nseg; ++j) {
+  auto step = [&](int j, CombStage& cs) {
     const int buf = j & 1;
-    s16x8 lo;
-    const s16x8 hi = split_hi_lo(S[0], S[1], lo);
-    Sop[buf][wave][0][lane] = hi;
-    Sop[buf][wave][1][lane] = lo;
-    s16x8 man[2][4][2];                       // the next step's (after the last: this one's)
-    f32x4 btn[2];
-    load_step(j + 2 < p.nseg ? j + 1 : j, man, btn);
+    s16x4 hi, lo;
+    split4(S, hi, lo);
+    const int item = (wave & 1) * 4;
+    uint16_t* sh16 = reinterpret_cast<uint16_t*>(&Sop[buf][wave >> 1][0][lane]);
+    uint16_t* sl16 = reinterpret_cast<uint16_t*>(&Sop[buf][wave >> 1][1][lane]);
+    *reinterpret_cast<s16x4*>(sh16 + item) = hi;
+    *reinterpret_cast<s16x4*>(sl16 + item) = lo;
     block_sync_lds();
-    f32x4 acc[2] = {bt[0], bt[1]};
+    f32x4 acc = cs.bt;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      const s16x8 sh = Sop[buf][kb][0][lane];
-      const s16x8 sl = Sop[buf][kb][1][lane];
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        acc[tt] = mfma_bf16(ma[tt][kb][0], sh, acc[tt]);
-        acc[tt] = mfma_bf16(ma[tt][kb][0], sl, acc[tt]);
-        acc[tt] = mfma_bf16(ma[tt][kb][1], sh, acc[tt]);
-      }
+      const s16x8 bh = Sop[buf][kb][0][lane];
+      const s16x8 bl = Sop[buf][kb][1][lane];
+      acc = mfma_bf16(cs.ma[kb][0], bh, acc);
+      acc = mfma_bf16(cs.ma[kb][0], bl, acc);
+      acc = mfma_bf16(cs.ma[kb][1], bh, acc);
     }
-    float* dst = p.seg_S + (static_cast<size_t>(j + 1) * p.HV + hv) * blk;
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      S[tt] = acc[tt];
-      *reinterpret_cast<f32x4*>(dst + tile + tt * 16) = S[tt];
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int hl = 0; hl < 2; ++hl) ma[tt][kb][hl] = man[tt][kb][hl];
-      bt[tt] = btn[tt];
-    }
+    S = acc;
+    *reinterpret_cast<f32x4*>(p.seg_S + (static_cast<size_t>(j + 1) * p.HV + hv) * blk + tile) = S;
+    load(j + 3, cs);                          // this set's next use: three steps on
+  };
+  CombStage s0, s1, s2;
+  load(1, s0);
+  load(2, s1);
+  load(3, s2);
+  for (int j = 1; j <= last; j += 3) {        // uniform
+    step(j, s0);
+    if (j + 1 <= last) step(j + 1, s1);
+    if (j + 2 <= last) step(j + 2, s2);
   }
 }
 
@@ -1582,8 +1587,8 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (p.nseg > 2) {
-      hipLaunchKernelGGL(seg_combine_kernel, dim3(static_cast<unsigned>(HV) * 8), dim3(kThreads),
-                         0, stream, p);
+      hipLaunchKernelGGL(seg_combine_kernel, dim3(static_cast<unsigned>((HV + 7) & ~7) * 8),
+                         dim3(64 * kCombWaves), 0, stream, p);
       e = hipGetLastError();
       if (e != hipSuccess) return e;
     }
