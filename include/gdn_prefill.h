@@ -48,8 +48,10 @@ extern "C" {
  * per chunk per v-head, for min(ceil(L / 64) + N, L) chunks, the most a
  * well-formed batch has, rounded up to 256 bytes), a 16-byte table entry per
  * chunk and 4 bytes per sequence, each part rounded up to 256 bytes; for one
- * sequence of C >= 48 chunks at HV <= 32 (scanned in segments of
- * max(4, ceil(C HV / 128)) chunks), also 3 x 64 KiB per segment per v-head.
+ * sequence of C >= 48 chunks at HV <= 32 (scanned in segments of at least
+ * 4 chunks, the length that minimises the estimated critical path of the
+ * two segment scans and the combine), also 3 x 64 KiB per segment per
+ * v-head.
  * 0 for invalid sizes.
  * The reference's FLA path allocates its intermediates per call inside
  * chunk_gated_delta_rule (solution/triton/fla_prefill_code.py:1726-1776);
