@@ -926,7 +926,7 @@ def prefill_bench(device, iters: int = 20):
     for name, (lens, H, HV) in PREFILL_CONFIGS.items():
         L, N = sum(lens), len(lens)
         t = prefill_inputs(name, device)
-        for _ in range(3):
+        for _ in range(PREFILL_WARMUP_CALLS):
             gdn.kernel_prefill_hip(**t)
         stream = torch.cuda.current_stream()
         ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
@@ -960,6 +960,46 @@ def prefill_bench(device, iters: int = 20):
         del t
     stamps.close()
     return out
+
+
+PREFILL_WARMUP_CALLS = 3
+
+
+def summarize_prefill_trace(trace_csv: str, iters: int = 20) -> str:
+    """Per prefill workload of a ``--prefill-only`` run under ``rocprofv3
+    --kernel-trace``: the median kernel-trace duration of each kernel and of
+    the whole call (first start to last end) over the timed calls, as a
+    markdown table.  The run's calls are, per workload in order, the warmup
+    calls, ``iters`` event-timed calls and ``iters`` calls of the timed entry,
+    each of ``gdn_prefill_dispatches`` kernels."""
+    with open(trace_csv, newline="") as f:
+        rows = [r for r in csv.DictReader(f) if "gdn" in r["Kernel_Name"]]
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    lib = _lib.load_prefill()
+    lines = ["| workload | kernels per call | kernel: median us | call, first start to "
+             "last end: median us |", "|---|---|---|---|"]
+    i = 0
+    for name, (lens, H, HV) in PREFILL_CONFIGS.items():
+        nd = lib.gdn_prefill_dispatches(sum(lens), len(lens), HV)
+        calls = []
+        for _ in range(PREFILL_WARMUP_CALLS + 2 * iters):
+            calls.append(rows[i:i + nd])
+            i += nd
+        per: dict[str, list[float]] = {}
+        span = []
+        for call in calls[PREFILL_WARMUP_CALLS:]:
+            for r in call:
+                k = r["Kernel_Name"].replace("void ", "").split("(")[0]
+                per.setdefault(k, []).append(
+                    (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+            span.append((int(call[-1]["End_Timestamp"]) - int(call[0]["Start_Timestamp"])) / 1e3)
+        kern = "; ".join(f"`{k}` {statistics.median(v):.2f}" + (f" (x{len(v) // (2 * iters)})"
+                         if len(v) > 2 * iters else "") for k, v in per.items())
+        lines.append(f"| {name} ({len(lens)} x {lens[0]}, H={H} HV={HV}) | {nd} | {kern} | "
+                     f"{statistics.median(span):.2f} |")
+    if i != len(rows):
+        raise ValueError(f"{trace_csv}: {len(rows)} prefill kernels, expected {i}")
+    return "\n".join(lines)
 
 
 def pmc_pass(device, shape: str = "b256_qk16_v32_l2"):
@@ -1013,6 +1053,8 @@ def main():
                     help="short prefill run for rocprofv3 counter passes")
     ap.add_argument("--summarize-pmc-prefill", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="write the prefill counter summary from two --pmc-prefill runs")
+    ap.add_argument("--summarize-prefill-trace", metavar="TRACE_CSV",
+                    help="print per-workload kernel medians of a traced --prefill-only run")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--prefill-only", action="store_true",
                     help="time the prefill workloads only and print them as JSON")
@@ -1044,6 +1086,9 @@ def main():
         log(f"[bench] wrote {PREFILL_TRAFFIC_SUMMARY.relative_to(ROOT)}: "
             f"{summary['traffic_bytes_per_prefill']} B per prefill "
             f"({summary['traffic_over_algorithmic']}x algorithmic)")
+        return
+    if args.summarize_prefill_trace:
+        print(summarize_prefill_trace(args.summarize_prefill_trace))
         return
     trace = None
     if not (args.trace_child or args.no_kernel_trace or args.no_per_config or args.pmc_pass
