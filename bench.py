@@ -225,7 +225,7 @@ def per_config_shapes():
 
 # Kernel-name substrings in the trace: the decode kernel and the floor
 # kernels of libgdn_calib.so.
-TRACE_DECODE = "gdn_decode_k128"
+TRACE_DECODE = "gdn_decode_"      # gdn_decode_k128 and gdn_decode_block
 TRACE_RMW = "gdn_calib::rmw"
 TRACE_EMPTY = "gdn_calib::empty"
 TRACE_WARMUP = 5
@@ -439,11 +439,14 @@ def decode_kernel_name(ns: int, waves: int, l2: bool, policy: int, bf16: bool = 
     """Name prefix of the decode kernel instantiation a launch shape runs,
     as rocprofv3 reports it."""
     b = lambda x: "true" if x else "false"  # noqa: E731
+    if ns in (16, 32, 64):    # the block kernel (T = 2..4): 16-row tiles per wave
+        return f"gdn::gdn_decode_block<{ns // 16}, {waves}, {b(l2)}, {b(bf16)}>"
     return (f"gdn::gdn_decode_k128<{ns}, {waves}, {b(l2)}, {policy}, {b(bf16)}, {b(multi)}, "
             f"false>")
 
 
 DECODE_SOURCES = ("flashinfer_competition_codebase_amd/csrc/gdn_decode_kernel.h",
+                  "flashinfer_competition_codebase_amd/csrc/gdn_decode_block.h",
                   "flashinfer_competition_codebase_amd/csrc/gdn_decode.hip",
                   "flashinfer_competition_codebase_amd/build.py")
 PREFILL_SOURCES = ("flashinfer_competition_codebase_amd/csrc/gdn_prefill.hip",

@@ -56,7 +56,7 @@ SIGNATURES = {
     "gdn_decode_abi_version": (_I, []),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _S = ctypes.c_size_t
 PREFILL_SIGNATURES = {

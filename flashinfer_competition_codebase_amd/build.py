@@ -34,11 +34,12 @@ PREFILL_PATH = PKG_DIR / "libgdn_prefill.so"
 # library -> source
 LIBRARIES = {LIB_PATH: CSRC, PREFILL_PATH: PREFILL_SRC, CALIB_PATH: CALIB_SRC}
 OFFLOAD_ARCH = "gfx950"
-# Per-library extra flags.  The prefill's MFMA results go to VGPRs (the
-# VALU work that follows every product then reads them without a
-# v_accvgpr_read copy; in the scan loop those copies were a quarter of the
-# VALU instructions).
-EXTRA_FLAGS = {PREFILL_PATH: ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# Per-library extra flags.  MFMA results go to VGPRs (the VALU work that
+# follows every product then reads them without a v_accvgpr_read copy; in
+# the prefill's scan loop those copies were a quarter of the VALU
+# instructions, in the block decode kernel a quarter of its instructions).
+EXTRA_FLAGS = {PREFILL_PATH: ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+               LIB_PATH: ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 KERNARG_PRELOAD_ARGS = int(os.environ.get("GDN_KERNARG_PRELOAD_ARGS", "8"))
 
 

@@ -11,7 +11,9 @@
 // as fp32 (the reference's) or bf16 (fp32 arithmetic either way).
 //
 // The kernel's device code is in gdn_decode_kernel.h (shared with the
-// prefill library, which runs its variable-length mode for small prefills);
+// prefill library, which runs its variable-length mode for small prefills)
+// and, for T = 2..4 tokens at the head counts where it is faster, in
+// gdn_decode_block.h (the tokens applied as one block on the matrix cores);
 // this file is the host side: validation, launch-shape tables, template
 // dispatch and the C ABI.
 //
@@ -45,6 +47,7 @@
 #include <new>
 
 #include "gdn_decode.h"
+#include "gdn_decode_block.h"
 #include "gdn_decode_kernel.h"
 
 namespace gdn {
@@ -69,6 +72,13 @@ struct Variant {
   bool bf16;
   bool multi;
 };
+
+// Launch shapes: rows_per_lane_group 1, 2, 4 or 8 runs the token-by-token
+// kernel (a wave holds 4 lane groups of that many rows); 16, 32 or 64 runs
+// the block kernel for T = 2..4 (a wave holds that many rows, as 16-row MFMA
+// tiles).
+bool is_block_shape(int ns) { return ns == 16 || ns == 32 || ns == 64; }
+int rows_per_wave(int ns) { return is_block_shape(ns) ? ns : kLaneGroups * ns; }
 
 template <int NS, int W, int POL, bool BF16, bool MULTI>
 hipError_t launch_one(bool l2, const Params& p, unsigned nb, const Launch& l) {
@@ -133,15 +143,60 @@ hipError_t by_ns(int ns, int w, int pol, bool l2, const Params& p, unsigned nb,
   }
 }
 
+// Block kernel (gdn_decode_block.h): R tiles of 16 rows per wave.
+template <int R, int W, bool BF16>
+hipError_t launch_block(bool l2, const Params& p, unsigned nb, const Launch& l) {
+  constexpr unsigned kT = kDim / (16 * R * W);
+  const dim3 grid(static_cast<unsigned>(p.ratio) * kT, static_cast<unsigned>(p.H), nb);
+  const dim3 block(64 * W);
+  auto* kern = l2 ? gdn_decode_block<R, W, true, BF16> : gdn_decode_block<R, W, false, BF16>;
+  const unsigned h_ratio = static_cast<unsigned>(p.H) | (static_cast<unsigned>(p.ratio) << 16);
+  if (l.start || l.stop) {
+    hipExtLaunchKernelGGL(kern, grid, block, 0, l.stream, l.start, l.stop, 0, p.state, p.q,
+                          p.k, p.v, p.a, p.b, h_ratio, p.T, p.A_log, p.dt_bias, p.out,
+                          p.new_state, p.scale);
+  } else {
+    hipLaunchKernelGGL(kern, grid, block, 0, l.stream, p.state, p.q, p.k, p.v, p.a, p.b,
+                       h_ratio, p.T, p.A_log, p.dt_bias, p.out, p.new_state, p.scale);
+  }
+  return hipGetLastError();
+}
+
+template <bool BF16>
+hipError_t dispatch_block(int rows, int w, bool l2, const Params& p, unsigned nb,
+                          const Launch& l) {
+  switch (rows * 16 + w) {
+    case 16 * 16 + 1: return launch_block<1, 1, BF16>(l2, p, nb, l);
+    case 16 * 16 + 2: return launch_block<1, 2, BF16>(l2, p, nb, l);
+    case 16 * 16 + 4: return launch_block<1, 4, BF16>(l2, p, nb, l);
+    case 16 * 16 + 8: return launch_block<1, 8, BF16>(l2, p, nb, l);
+    case 32 * 16 + 1: return launch_block<2, 1, BF16>(l2, p, nb, l);
+    case 32 * 16 + 2: return launch_block<2, 2, BF16>(l2, p, nb, l);
+    case 32 * 16 + 4: return launch_block<2, 4, BF16>(l2, p, nb, l);
+    case 64 * 16 + 1: return launch_block<4, 1, BF16>(l2, p, nb, l);
+    case 64 * 16 + 2: return launch_block<4, 2, BF16>(l2, p, nb, l);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 hipError_t dispatch(const Variant& v, int ns, int w, int pol, const Params& p, unsigned nb,
                     const Launch& l) {
+  if (is_block_shape(ns)) {
+    return v.bf16 ? dispatch_block<true>(ns, w, v.l2, p, nb, l)
+                  : dispatch_block<false>(ns, w, v.l2, p, nb, l);
+  }
   if (!v.bf16 && !v.multi) return by_ns<false, false>(ns, w, pol, v.l2, p, nb, l);
   if (!v.bf16 && v.multi) return by_ns<false, true>(ns, w, pol, v.l2, p, nb, l);
   if (v.bf16 && !v.multi) return by_ns<true, false>(ns, w, pol, v.l2, p, nb, l);
   return by_ns<true, true>(ns, w, pol, v.l2, p, nb, l);
 }
 
-bool shape_supported(const Variant& v, int ns, int w, int pol) {
+bool shape_supported(const Variant& v, int T, int ns, int w, int pol) {
+  if (is_block_shape(ns)) {
+    // block kernel: T = 2..4, nontemporal state stream, <= 128 rows a block
+    return T >= 2 && T <= kBlockMaxTokens && pol == kPolicyNtBoth &&
+           (w == 1 || w == 2 || w == 4 || w == 8) && ns * w <= kDim;
+  }
   const bool pow2 = (ns == 1 || ns == 2 || ns == 4 || ns == 8) &&
                     (w == 1 || w == 2 || w == 4 || w == 8);
   if (!pow2 || ns * w > 32) return false;
@@ -197,8 +252,38 @@ void pick_row(const ShapeRow (&table)[N], long long heads, int* ns, int* waves) 
   }
 }
 
+// Head counts at which the block kernel (rows_per_lane_group 16/32/64)
+// runs T = 2..4 tokens, from rocprofv3 kernel-trace sweeps of every block
+// shape against the token-by-token table at qk16_v32 B = 8..512 (steady
+// regime).  bf16 state at T = 4: 0.72-0.91x the token loop's time from 512
+// heads on (B=256: 108.0 against 119.1 us); T = 3: 0.87-0.97x at 512-4096
+// heads, not faster above; T = 2: 0.92-0.96x at 1024-2048 heads only.  An
+// fp32 state's dots take 32 fp32 MFMAs per tile: faster only at 256-512
+// heads (0.85-0.93x), 8-13% slower from 1024 heads on.
+struct BlockRow {
+  int T;
+  bool bf16;
+  long long min_heads;
+  long long max_heads;   // -1: no limit
+  int rows;
+  int waves;
+};
+constexpr BlockRow kBlockRows[] = {
+    {4, true, 257, 4096, 64, 1}, {4, true, 4097, -1, 32, 4}, {3, true, 257, 4096, 64, 1},
+    {2, true, 513, 2048, 64, 1}, {4, false, 129, 256, 32, 1}, {4, false, 257, 512, 64, 1},
+    {3, false, 129, 256, 32, 1},
+};
+
 void choose_shape(long long heads, bool bf16, int T, int* ns, int* waves, int* policy) {
   *policy = kPolicyNtBoth;
+  for (const BlockRow& r : kBlockRows) {
+    if (r.T == T && r.bf16 == bf16 && heads >= r.min_heads &&
+        (r.max_heads < 0 || heads <= r.max_heads)) {
+      *ns = r.rows;
+      *waves = r.waves;
+      return;
+    }
+  }
   if (bf16 && T >= 3) {
     pick_row(kShapeBf16T3Plus, heads, ns, waves);
   } else if (bf16) {
@@ -246,7 +331,7 @@ hipError_t validate(const StepArgs& s) {
   if (s.K != kDim || s.V != kDim) return hipErrorInvalidValue;
   if (s.state_bf16 != 0 && s.state_bf16 != 1) return hipErrorInvalidValue;
   const Variant var = variant_of(s);
-  if (!shape_supported(var, s.ns, s.waves, s.policy)) return hipErrorInvalidValue;
+  if (!shape_supported(var, s.T, s.ns, s.waves, s.policy)) return hipErrorInvalidValue;
   if (s.B == 0) return hipSuccess;
   if (!s.q || !s.k || !s.v || !s.A_log || !s.a || !s.dt_bias || !s.b || !s.output ||
       !s.new_state)
@@ -264,7 +349,7 @@ hipError_t validate(const StepArgs& s) {
     if (s0 < d0 + state_bytes && d0 < s0 + state_bytes)
       return hipErrorInvalidValue;  // partial overlap: only exact aliasing
   }
-  const long long tiles = kDim / (kLaneGroups * s.ns * s.waves);
+  const long long tiles = kDim / (rows_per_wave(s.ns) * s.waves);
   const long long max_blocks = (1LL << 31) / (64LL * s.waves);
   if (max_blocks / (tiles * s.HV) < 1) return hipErrorInvalidValue;
   return hipSuccess;
@@ -277,7 +362,7 @@ hipError_t launch(const StepArgs& s, hipStream_t stream, hipEvent_t start_event,
   if (s.B == 0) return hipSuccess;
   const Variant var = variant_of(s);
   const size_t elem = s.state_bf16 ? 2 : 4;
-  const long long tiles = kDim / (kLaneGroups * s.ns * s.waves);
+  const long long tiles = kDim / (rows_per_wave(s.ns) * s.waves);
   const long long max_blocks = (1LL << 31) / (64LL * s.waves);
   long long batches_per_launch = max_blocks / (tiles * s.HV);
   if (batches_per_launch > 65535) batches_per_launch = 65535;  // grid z limit
@@ -388,7 +473,7 @@ int gdn_decode_launch_shape(int B, int T, int HV, int state_bf16,
   *rows_per_lane_group = ns;
   *waves_per_block = waves;
   *cache_policy = policy;
-  *num_blocks = static_cast<long long>(B) * HV * (kDim / (kLaneGroups * ns * waves));
+  *num_blocks = static_cast<long long>(B) * HV * (kDim / (rows_per_wave(ns) * waves));
   return hipSuccess;
 }
 
@@ -534,6 +619,6 @@ const char* gdn_decode_error_string(int code) {
   return hipGetErrorString(static_cast<hipError_t>(code));
 }
 
-int gdn_decode_abi_version(void) { return 5; }
+int gdn_decode_abi_version(void) { return 6; }
 
 }  // extern "C"

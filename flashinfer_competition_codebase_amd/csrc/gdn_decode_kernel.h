@@ -55,8 +55,13 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) {
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float x) {
   return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(x)));
 }
+// Two floats to a packed bf16 pair (round to nearest even), lo in the low
+// half: one v_cvt_pk_bf16_f32 (two separate conversions would also need a
+// v_or to merge the halves).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
 }
 
 template <int CTRL>
@@ -699,11 +704,15 @@ __device__ __forceinline__ void decode_body(
     GateBits gb = load_gate_bits(p, tok0, 0, T, hv, lane);
     __builtin_amdgcn_sched_barrier(0);
 
+    // The state loads are unconditional: with no state they read new_state
+    // (same size, a valid address) and the values are replaced by zeros
+    // after the per-head math.  Loads inside a branch would make every later
+    // wait for the small inputs assume the branch skipped them, i.e. wait
+    // for the whole state before the per-head math.
+    const void* src = has_state ? p.state : static_cast<const void*>(p.new_state);
     RowRaw<BF16> raw[NS];
-    if (has_state) {
 #pragma unroll
-      for (int n = 0; n < NS; ++n) raw[n] = load_row<BF16, POLICY>(p.state, row_base + n, j);
-    }
+    for (int n = 0; n < NS; ++n) raw[n] = load_row<BF16, POLICY>(src, row_base + n, j);
     // Variable-length (small prefill: one wave of few rows per head, latency
     // bound): the inputs of the next kDepth = 3 tokens are in flight while a
     // token is applied, so each load has two tokens' time to arrive; token
@@ -730,16 +739,13 @@ __device__ __forceinline__ void decode_body(
     head_of<NS, L2NORM>(in0.q, in0.k, in0.v, lane_value(gl, 0), lane_value(bl, 0), p.scale, h);
     __builtin_amdgcn_sched_barrier(0);
 
+    if (!has_state) {                         // uniform: start from zeros
+#pragma unroll
+      for (int n = 0; n < NS; ++n) raw[n] = RowRaw<BF16>{};
+    }
     float s[NS][8];
 #pragma unroll
-    for (int n = 0; n < NS; ++n) {
-      if (has_state) {
-        unpack_row<BF16>(raw[n], s[n]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) s[n][i] = 0.0f;
-      }
-    }
+    for (int n = 0; n < NS; ++n) unpack_row<BF16>(raw[n], s[n]);
 
     // Per-head quantities of token tt >= 1 (uniform) from its inputs.
     auto head_at = [&](const TokenQkv<NS>& in, int tt) {

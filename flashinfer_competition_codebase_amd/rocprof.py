@@ -11,7 +11,10 @@ those files into the short summaries kept with the results:
   dispatches);
 * ``trace_average``: the average duration of a kernel's dispatches
   ``[skip, skip + count)`` in a kernel trace (the timed region of a run), and
-  the average over all of its dispatches.
+  the average over all of its dispatches;
+* ``trace_groups``: every decode/calibration kernel's dispatches grouped by
+  instantiation and grid, with the median duration overall, right after a
+  cache-evicting read, and otherwise (the per-shape table of a bench run).
 
 Command line (prints JSON):
 
@@ -19,6 +22,7 @@ Command line (prints JSON):
         --kernel NAME_PREFIX --copy-bytes N [--skip 2] [--copies 3]
     python -m flashinfer_competition_codebase_amd.rocprof trace TRACE_CSV \
         --kernel NAME_PREFIX --skip W --count K
+    python -m flashinfer_competition_codebase_amd.rocprof groups TRACE_CSV
 
 The reference profiles with NVIDIA's tools (scripts/profile_ncu.py,
 scripts/profile_proton.py); this is the rocprofv3 side of the same job.
@@ -117,6 +121,51 @@ def trace_average(trace_csv: str, kernel: str, skip: int, count: int) -> dict:
             "avg_us_all_dispatches": round(statistics.fmean(every), 3)}
 
 
+def trace_groups(trace_csv: str, prefixes=("gdn::", "gdn_calib::"),
+                 after: str = "reduce_kernel") -> list[dict]:
+    """Dispatches of the kernels whose names start with one of ``prefixes``,
+    grouped by instantiation and grid (in order of first appearance): count
+    and median duration (µs) over all of them, over those that start right
+    after a dispatch whose name contains ``after`` (a cache-evicting read),
+    and over the others.  Grid as ``X x Y x Z / workgroup`` in work-items."""
+    rows = sorted(_rows(trace_csv), key=lambda r: int(r["Start_Timestamp"]))
+    groups: dict[tuple, dict] = {}
+    prev = ""
+    for r in rows:
+        name = _kernel_name(r)
+        if name.startswith(prefixes):
+            key = (name.split("(")[0],
+                   f"{r['Grid_Size_X']}x{r['Grid_Size_Y']}x{r['Grid_Size_Z']} / "
+                   f"{r['Workgroup_Size_X']}")
+            g = groups.setdefault(key, {"kernel": key[0], "grid": key[1], "all": [],
+                                        "after": [], "other": []})
+            d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+            g["all"].append(d)
+            g["after" if after in prev else "other"].append(d)
+        prev = name
+    out = []
+    for g in groups.values():
+        med = {k: (round(statistics.median(g[k]), 2) if g[k] else None)
+               for k in ("all", "after", "other")}
+        out.append({"kernel": g["kernel"], "grid": g["grid"], "dispatches": len(g["all"]),
+                    "median_us": med["all"], "median_us_after_read": med["after"],
+                    "median_us_otherwise": med["other"]})
+    return out
+
+
+def groups_table(groups: list[dict]) -> str:
+    """``trace_groups`` as a Markdown table."""
+    lines = ["| kernel | grid / block | dispatches | median all (us) | "
+             "median after a cache-evicting read (us) | median otherwise (us) |",
+             "|---|---|---|---|---|---|"]
+    fmt = lambda x: "-" if x is None else f"{x:.2f}"  # noqa: E731
+    for g in groups:
+        lines.append(f"| `{g['kernel']}` | {g['grid']} | {g['dispatches']} | "
+                     f"{fmt(g['median_us'])} | {fmt(g['median_us_after_read'])} | "
+                     f"{fmt(g['median_us_otherwise'])} |")
+    return "\n".join(lines)
+
+
 def main(argv=None) -> None:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -132,7 +181,12 @@ def main(argv=None) -> None:
     t.add_argument("--kernel", required=True)
     t.add_argument("--skip", type=int, required=True)
     t.add_argument("--count", type=int, required=True)
+    g = sub.add_parser("groups")
+    g.add_argument("trace_csv")
     a = ap.parse_args(argv)
+    if a.cmd == "groups":
+        sys.stdout.write(groups_table(trace_groups(a.trace_csv)) + "\n")
+        return
     if a.cmd == "pmc":
         res = pmc_traffic(a.fetch_csv, a.write_csv, a.kernel, a.copy_bytes, a.copies, a.skip)
     else:

@@ -89,7 +89,14 @@ int gdn_decode_steps(const void* q, const void* k, const void* v,
  * their product is at most 32.  cache_policy selects how the state stream
  * is accessed: 0 ordinary loads and stores, 1 nontemporal loads and stores,
  * 2 nontemporal stores only, 3 nontemporal loads only.  With T > 1, a
- * bf16 state or a NULL state, cache_policy is 0 or 1.  start_event / stop_event (hipEvent_t, may be
+ * bf16 state or a NULL state, cache_policy is 0 or 1.
+ * rows_per_lane_group 16, 32 or 64 (T = 2..4 only, cache_policy 1) selects
+ * the block kernel instead: the T tokens' dot products are taken against the
+ * starting state on the matrix cores and the state is updated once; each
+ * wavefront owns rows_per_lane_group consecutive state rows as 16-row MFMA
+ * tiles, rows_per_lane_group * waves_per_block <= 128, and a head is split
+ * over 128 / (rows_per_lane_group * waves_per_block) workgroups.
+ * start_event / stop_event (hipEvent_t, may be
  * NULL) are stamped with the kernel's own start and end timestamps
  * (hipExtLaunchKernelGGL), so hipEventElapsedTime gives the kernel duration
  * without event-marker overhead.  Used for launch-shape sweeps and timing.
@@ -196,8 +203,8 @@ void gdn_decode_graph_destroy(gdn_decode_graph* graph);
  */
 const char* gdn_decode_error_string(int code);
 
-/* ABI version of this header: 5 (4 had no gdn_decode_step_stamped; 3 had no
- * plans or graphs and no NULL state). */
+/* ABI version of this header: 6 (5 had no block kernel shapes; 4 had no
+ * gdn_decode_step_stamped; 3 had no plans or graphs and no NULL state). */
 int gdn_decode_abi_version(void);
 
 #ifdef __cplusplus

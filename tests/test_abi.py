@@ -73,10 +73,15 @@ def test_launch_shape_query():
 def test_launch_shape_table_stays_in_the_supported_space(T, bf16):
     """Every head count gets a shape the kernel is built for: at most 32
     rows per lane group x waves, power-of-two tiles per head, and a cache
-    policy every variant has (0 or 1)."""
+    policy every variant has (0 or 1); or, for T = 2..4, the block kernel
+    (16, 32 or 64 rows per wave, at most 128 rows per block, policy 1)."""
     for heads in (1, 7, 8, 9, 16, 32, 33, 64, 100, 128, 256, 257, 384, 512, 1000, 8192,
                   1 << 20):
         ns, w, pol, blocks = _lib.launch_shape(heads, 1, T=T, state_bf16=bf16)
+        if ns in (16, 32, 64):
+            assert 2 <= T <= 4 and w in (1, 2, 4, 8) and ns * w <= 128 and pol == 1
+            assert blocks == heads * 128 // (ns * w)
+            continue
         assert ns in (1, 2, 4, 8) and w in (1, 2, 4, 8) and ns * w <= 32
         assert pol in (0, 1)
         assert blocks == heads * 128 // (4 * ns * w)
@@ -122,6 +127,15 @@ def test_validation_rejects_bad_sizes_without_launching():
     assert sh(1, 0, 2, 4, 3, state=None) == 1   # a null state runs the multi-token loop
     assert sh(0, 0, 2, 4, 1) == 1     # T < 1
     assert sh(1, 2, 2, 4, 1) == 1     # state_bf16 is 0 or 1
+    # the block kernel: 16, 32 or 64 rows per wave, T = 2..4, cache policy 1
+    assert sh(4, 1, 64, 2, 1) == 0
+    assert sh(2, 0, 16, 8, 1) == 0
+    assert sh(3, 1, 32, 4, 1, state=None) == 0
+    assert sh(1, 1, 32, 2, 1) == 1    # one token: the token-by-token kernel
+    assert sh(5, 1, 32, 2, 1) == 1    # more than four tokens
+    assert sh(4, 1, 32, 2, 0) == 1    # ordinary stores are not built
+    assert sh(4, 0, 64, 4, 1) == 1    # 256 rows per block: more than one head
+    assert sh(4, 0, 48, 1, 1) == 1    # not a multiple of the 16-row tile
     steps = lib.gdn_decode_steps
     assert steps(*nulls, f, None, None, 1, 0, 16, 32, 128, 128, 0, 1, None) == 1
     assert steps(*nulls, f, None, None, 0, 4, 16, 32, 128, 128, 1, 1, None) == 0

@@ -167,3 +167,33 @@ def test_prefill_counter_summary_and_its_sources_check(tmp_path, monkeypatch):
     assert bench._prefill_traffic() == {"prep": 300 * 1024, "scan": 900 * 1024}
     (tmp_path / bench.PREFILL_SOURCES[0]).write_text("changed")
     assert bench._prefill_traffic() is None
+
+
+def test_trace_groups_splits_after_read(tmp_path):
+    """rocprof.trace_groups: per instantiation and grid, in first-seen order,
+    medians over all dispatches, those right after a reduce_kernel (a
+    cache-evicting read), and the others."""
+    from flashinfer_competition_codebase_amd import rocprof
+
+    cols = ("Kernel_Name", "Start_Timestamp", "End_Timestamp", "Grid_Size_X", "Grid_Size_Y",
+            "Grid_Size_Z", "Workgroup_Size_X")
+    rows = [("void gdn::gdn_decode_k128<2, 4>(int)", 0, 2000, 256, 16, 1, 256),
+            ("reduce_kernel", 3000, 4000, 64, 1, 1, 64),
+            ("void gdn::gdn_decode_k128<2, 4>(int)", 5000, 9000, 256, 16, 1, 256),
+            ("void gdn::gdn_decode_block<4, 2, true, true>(int)", 10000, 13000, 128, 16, 1, 128),
+            ("void gdn::gdn_decode_k128<2, 4>(int)", 14000, 17000, 256, 16, 1, 256),
+            ("void gdn::gdn_decode_k128<2, 4>(int)", 18000, 19000, 256, 16, 2, 256)]
+    path = tmp_path / "trace.csv"
+    path.write_text(",".join(cols) + "\n" + "".join(",".join(f'"{x}"' for x in r) + "\n"
+                                                    for r in rows))
+    g = rocprof.trace_groups(str(path))
+    assert [x["kernel"] for x in g] == ["gdn::gdn_decode_k128<2, 4>",
+                                        "gdn::gdn_decode_block<4, 2, true, true>",
+                                        "gdn::gdn_decode_k128<2, 4>"]
+    assert g[0]["grid"] == "256x16x1 / 256" and g[0]["dispatches"] == 3
+    assert g[0]["median_us"] == 3.0                      # 2, 4, 3 us
+    assert g[0]["median_us_after_read"] == 4.0
+    assert g[0]["median_us_otherwise"] == 2.5
+    assert g[2]["grid"] == "256x16x2 / 256" and g[2]["median_us_after_read"] is None
+    assert "| `gdn::gdn_decode_block<4, 2, true, true>` | 128x16x1 / 128 | 1 |" in \
+        rocprof.groups_table(g)
