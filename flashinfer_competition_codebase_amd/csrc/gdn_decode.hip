@@ -253,15 +253,17 @@ void pick_row(const ShapeRow (&table)[N], long long heads, int* ns, int* waves) 
 }
 
 // Head counts at which the block kernel (rows_per_lane_group 16/32/64)
-// runs T = 2..4 tokens, from rocprofv3 kernel-trace sweeps of every block
-// shape against the token-by-token table at qk16_v32 B = 8..512 (steady
-// regime).  bf16 state at T = 4: 0.72-0.91x the token loop's time from 512
-// heads on (B=256: 108.0 against 119.1 us); T = 3: 0.87-0.97x at 512-4096
-// heads, not faster above; T = 2: 0.92-0.96x at 1024-2048 heads only.  An
-// fp32 state's dots take 32 fp32 MFMAs per tile: faster only at 256-512
-// heads (0.85-0.93x), 8-13% slower from 1024 heads on.
+// runs T = 2..4 tokens, and its shape, from rocprofv3 kernel-trace sweeps at
+// qk16_v32 B = 1..512 (steady regime) that launch every block shape and the
+// token loop's shapes in turn, round after round, so that all of them run
+// in the same GPU state.  bf16 state: the block kernel is faster from B = 1
+// at T = 4 (4.18 against 4.52 us), from B = 2 at T = 3 and from B = 4 at
+// T = 2, by 10-25% from B = 8 on (B=256: T = 4 96.2 against 134.6 us, T = 2
+// 92.1 against 106.9 us); (32, 2) is within 2% of the best shape from 1024
+// heads on.  fp32 state (three bf16 products per dot): 2-15% faster at T = 4
+// and 256 or 513-4096 heads only.
 struct BlockRow {
-  int T;
+  int T;                 // 0: any of 2..4
   bool bf16;
   long long min_heads;
   long long max_heads;   // -1: no limit
@@ -269,15 +271,19 @@ struct BlockRow {
   int waves;
 };
 constexpr BlockRow kBlockRows[] = {
-    {4, true, 257, 4096, 64, 1}, {4, true, 4097, -1, 32, 4}, {3, true, 257, 4096, 64, 1},
-    {2, true, 513, 2048, 64, 1}, {4, false, 129, 256, 32, 1}, {4, false, 257, 512, 64, 1},
-    {3, false, 129, 256, 32, 1},
+    // bf16 state
+    {4, true, 1, 128, 32, 1},     {3, true, 33, 128, 32, 1},   {2, true, 65, 128, 32, 1},
+    {0, true, 129, 256, 32, 4},   {0, true, 257, 512, 32, 2},  {0, true, 513, 1024, 64, 1},
+    {0, true, 1025, -1, 32, 2},
+    // fp32 state
+    {4, false, 256, 256, 16, 8},  {4, false, 513, 4096, 64, 1},
 };
 
 void choose_shape(long long heads, bool bf16, int T, int* ns, int* waves, int* policy) {
   *policy = kPolicyNtBoth;
   for (const BlockRow& r : kBlockRows) {
-    if (r.T == T && r.bf16 == bf16 && heads >= r.min_heads &&
+    const bool t_ok = r.T == 0 ? (T >= 2 && T <= kBlockMaxTokens) : r.T == T;
+    if (t_ok && r.bf16 == bf16 && heads >= r.min_heads &&
         (r.max_heads < 0 || heads <= r.max_heads)) {
       *ns = r.rows;
       *waves = r.waves;

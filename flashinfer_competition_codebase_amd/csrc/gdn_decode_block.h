@@ -29,11 +29,12 @@
 //     tile, at k = 32 s + 8 g + e for s, e = 0..7 (four 8-element runs,
 //     16 contiguous bytes of a bf16 row, 32 of an fp32 row, per run);
 //   * k.S and q.S: the state is the B operand (B[k][n] = S0[n][k]) of
-//     v_mfma_f32_16x16x32_bf16 for a bf16 state -- the loaded bits as they
-//     are -- and of v_mfma_f32_16x16x4_f32 for an fp32 state (exact either
-//     way); row m of the A operand is token m % 4's k (or q), so every lane
-//     group receives all four tokens' dots with its row (D[m][n] in lane
-//     n + 16 (m / 4), register m % 4);
+//     v_mfma_f32_16x16x32_bf16: for a bf16 state the loaded bits as they
+//     are, for an fp32 state three bf16 parts of it (hi + mid + lo, three
+//     products); row m of the A operand is token m % 4's k (m & 4 clear) or
+//     q (m & 4 set), so lane n + 16 g receives the dots of row n with the
+//     k's (g even) or the q's (g odd), D[m][n] being in lane n + 16 (m / 4),
+//     register m % 4, and a v_permlane16_swap gives every lane both;
 //   * the update is v_mfma_f32_16x16x4_f32 per 16 x 16 tile of (k, row):
 //     D[m][n] = C[m][n] + sum_t A[m][t] B[t][n], with C = Gamma S0 at the
 //     lane's own elements, B[t][n] = D(t,T-1) x_t of row n from lane n + 16 t,
@@ -91,6 +92,24 @@ __device__ __forceinline__ float bf16_item(u32x4 w, int e) {
   return e & 1 ? bf16_hi(word) : bf16_lo(word);
 }
 
+// Eight fp32 values (a, then b) as three packed bf16 runs with a + b ~ hi +
+// mid + lo: each part is the round-to-nearest bf16 of what the parts before
+// it leave, so the sum misses x by at most ~2^-27 |x|.
+__device__ __forceinline__ void split3(const f32x4& a, const f32x4& b, u32x4& hi, u32x4& mid,
+                                       u32x4& lo) {
+  float x[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+#pragma unroll
+  for (int w = 0; w < 4; ++w) hi[w] = pack_bf16x2(x[2 * w], x[2 * w + 1]);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] -= bf16_item(hi, e);
+#pragma unroll
+  for (int w = 0; w < 4; ++w) mid[w] = pack_bf16x2(x[2 * w], x[2 * w + 1]);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] -= bf16_item(mid, e);
+#pragma unroll
+  for (int w = 0; w < 4; ++w) lo[w] = pack_bf16x2(x[2 * w], x[2 * w + 1]);
+}
+
 // Selector operand h (B of v_mfma_f32_16x16x32_bf16) of lane (n, g): item e
 // is 1.0 where k index 8 g + e of the 32-long block is the tile's n-th,
 // 8 (n / 4) + 4 h + n % 4.
@@ -114,11 +133,12 @@ __device__ __forceinline__ u32x4 selector(int n, int g, int h) {
 // measured 1.34x the state's bytes in HBM writes (rocprofv3 WRITE_SIZE,
 // B=256 T=4 bf16: 119.7 us) against 1.00x and 104.5 us through 16 padded
 // LDS rows and whole-row stores; ordinary (write-back) stores from the
-// registers also write 1.00x but took 117.5 us.  The R = 4 bf16 kernels are
-// held to 168 VGPRs (3 waves per SIMD).
+// registers also write 1.00x but took 117.5 us.  The R = 4 bf16 and R = 2
+// fp32 kernels are held to 168 VGPRs (3 waves per SIMD).
 template <int R, int WAVES, bool L2NORM, bool BF16>
 __global__ __launch_bounds__(64 * WAVES)
-__attribute__((amdgpu_waves_per_eu(R == 4 && BF16 ? 3 : 1, 8))) void gdn_decode_block(
+__attribute__((amdgpu_waves_per_eu((R == 4 && BF16) || (R == 2 && !BF16) ? 3 : 1, 8)))
+void gdn_decode_block(
     const void* state, const uint16_t* q, const uint16_t* k, const uint16_t* v,
     const uint16_t* a, const uint16_t* b, unsigned h_ratio, int T, const float* A_log_p,
     const float* dt_bias_p, uint16_t* out, void* new_state, float scale) {
@@ -144,9 +164,12 @@ __attribute__((amdgpu_waves_per_eu(R == 4 && BF16 ? 3 : 1, 8))) void gdn_decode_
   const int row0 = tile * kRowsPerBlock + wave * kRowsPerWave;
   const size_t tok0 = static_cast<size_t>(bi) * T;
   const bool has_state = state != nullptr;
-  // staging rows of the new state: 16 rows, padded by 16 bytes so that the
-  // 16 rows' writes of one instruction spread over the banks
+  // LDS rows of one 16-row tile (the loaded state on its way into the MFMA
+  // layout, then the new state on its way out), padded by 16 bytes so that
+  // the 16 rows' accesses of one instruction spread over the banks
   constexpr int kRowBytes = kDim * (BF16 ? 2 : 4);
+  constexpr int kPieces = kRowBytes / 16;           // 16-byte pieces a row
+  constexpr int kLoads = 16 * kPieces / 64;         // 16-byte loads a lane per tile
   constexpr int kStageRow = kRowBytes + 16;
   constexpr int kStageBytes = 16 * kStageRow;
   __shared__ __attribute__((aligned(16))) char stage_mem[WAVES * kStageBytes];
@@ -191,29 +214,24 @@ __attribute__((amdgpu_waves_per_eu(R == 4 && BF16 ? 3 : 1, 8))) void gdn_decode_
   // size, a valid address) and discards it below.  Loads that a branch may
   // skip would make the compiler's wait for the small inputs count as if
   // they had been skipped -- i.e. wait for the whole state first.
-  const size_t row_base = static_cast<size_t>(head) * kDim + row0 + n;
-  const void* src = has_state ? state : static_cast<const void*>(new_state);
-  u32x4 sb[R][4];       // bf16 state: the runs as loaded
-  f32x4 sf[R][4][2];    // fp32 state: the runs as loaded
-  if constexpr (BF16) {
-    const uint16_t* st = static_cast<const uint16_t*>(src);
+  // Whole rows: load i of tile r gives lane l 16 bytes, piece (64 i + l) % P
+  // of row (64 i + l) / P (P pieces a row), so an instruction reads 1 KiB of
+  // 4 (bf16) or 2 (fp32) whole rows; the tile is moved into the MFMA layout
+  // through its LDS rows.  (Loaded directly in the MFMA layout, 64 bytes of
+  // each of 16 rows an instruction, an in-place read-modify-write of 256 MiB
+  // ran at half the bandwidth.)
+  const size_t row_base = static_cast<size_t>(head) * kDim + row0;   // the wave's first row
+  const char* src = static_cast<const char*>(has_state ? state
+                                                       : static_cast<const void*>(new_state));
+  u32x4 raw[R][kLoads];
 #pragma unroll
-    for (int r = 0; r < R; ++r)
+  for (int r = 0; r < R; ++r)
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-        sb[r][s] = load_stream<u32x4, kPolicyNtBoth>(st + (row_base + 16 * r) * kDim + 32 * s +
-                                                     8 * g);
-  } else {
-    const float* st = static_cast<const float*>(src);
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-          sf[r][s][h] = load_stream<f32x4, kPolicyNtBoth>(st + (row_base + 16 * r) * kDim +
-                                                          32 * s + 8 * g + 4 * h);
-  }
+    for (int i = 0; i < kLoads; ++i) {
+      const int pc = i * 64 + lane;
+      raw[r][i] = load_stream<u32x4, kPolicyNtBoth>(
+          src + (row_base + 16 * r + pc / kPieces) * kRowBytes + (pc % kPieces) * 16);
+    }
   __builtin_amdgcn_sched_barrier(0);
   const float A_log = A_log_p[hv];
   const float dt_bias = dt_bias_p[hv];
@@ -318,43 +336,57 @@ __attribute__((amdgpu_waves_per_eu(R == 4 && BF16 ? 3 : 1, 8))) void gdn_decode_
       ku[2 * s + 1] = pick_by_group(mfma_bf16x32(vk[s], sel1, f32x4{0.0f, 0.0f, 0.0f, 0.0f}), g);
     }
   }
-  // fp32 state: the k/q operand as fp32 items for the fp32 products
-  float vnf[4][8];
-  if constexpr (!BF16) {
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) vnf[s][e] = bf16_item(vn[s], e);
-  }
   __builtin_amdgcn_sched_barrier(0);
   if (!has_state) {                    // uniform: start from zeros
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        if constexpr (BF16) {
-          sb[r][s] = u32x4{0u, 0u, 0u, 0u};
-        } else {
-          sf[r][s][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-          sf[r][s][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        }
-      }
+      for (int i = 0; i < kLoads; ++i) raw[r][i] = u32x4{0u, 0u, 0u, 0u};
   }
 
   // ---- per tile of 16 rows: dots, recurrence, output, update --------------
 #pragma unroll
   for (int r = 0; r < R; ++r) {
+    // the tile into the MFMA layout: lane (n, g) gets row n at k = 32 s + 8 g
+    // .. + 7 (bf16: one piece, 4 s + g; fp32: two, 8 s + 2 g + h)
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int pc = i * 64 + lane;
+      *reinterpret_cast<u32x4*>(stage + (pc / kPieces) * kStageRow + (pc % kPieces) * 16) =
+          raw[r][i];
+    }
+    __builtin_amdgcn_wave_barrier();
+    u32x4 sb[4];          // bf16 state: the row's runs
+    f32x4 sf[4][2];       // fp32 state
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      if constexpr (BF16) {
+        sb[s] = *reinterpret_cast<const u32x4*>(stage + n * kStageRow + 64 * s + 16 * g);
+      } else {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          sf[s][h] = *reinterpret_cast<const f32x4*>(stage + n * kStageRow + 128 * s + 32 * g +
+                                                     16 * h);
+      }
+    }
     // k_t . S0 in the even lane groups, q_t . S0 in the odd ones; one swap of
     // odd and even groups (v_permlane16_swap) gives every lane both.
     f32x4 pn = {0.0f, 0.0f, 0.0f, 0.0f};
     if constexpr (BF16) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) pn = mfma_bf16x32(vn[s], sb[r][s], pn);
+      for (int s = 0; s < 4; ++s) pn = mfma_bf16x32(vn[s], sb[s], pn);
     } else {
+      // fp32 state: each run split into three bf16 parts, x = hi + mid + lo
+      // to ~2^-27 relative, the B operands of three bf16 products (exact
+      // products, fp32 sums; the small parts first)
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) pn = mfma_f32x4(vnf[s][e], sf[r][s][e >> 2][e & 3], pn);
+      for (int s = 0; s < 4; ++s) {
+        u32x4 hi, mid, lo;
+        split3(sf[s][0], sf[s][1], hi, mid, lo);
+        pn = mfma_bf16x32(vn[s], lo, pn);
+        pn = mfma_bf16x32(vn[s], mid, pn);
+        pn = mfma_bf16x32(vn[s], hi, pn);
+      }
     }
     f32x4 pk, pq;
 #pragma unroll
@@ -388,8 +420,8 @@ __attribute__((amdgpu_waves_per_eu(R == 4 && BF16 ? 3 : 1, 8))) void gdn_decode_
         f32x4 c0, c1;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          c0[i] = gam_fin * bf16_item(sb[r][s], i);
-          c1[i] = gam_fin * bf16_item(sb[r][s], 4 + i);
+          c0[i] = gam_fin * bf16_item(sb[s], i);
+          c1[i] = gam_fin * bf16_item(sb[s], 4 + i);
         }
         const f32x4 d0 = mfma_f32x4(ku[2 * s], w, c0);
         const f32x4 d1 = mfma_f32x4(ku[2 * s + 1], w, c1);
@@ -402,7 +434,7 @@ __attribute__((amdgpu_waves_per_eu(R == 4 && BF16 ? 3 : 1, 8))) void gdn_decode_
       for (int s = 0; s < 4; ++s)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const f32x4 d = mfma_f32x4(ku[2 * s + h], w, gam_fin * sf[r][s][h]);
+          const f32x4 d = mfma_f32x4(ku[2 * s + h], w, gam_fin * sf[s][h]);
           *reinterpret_cast<f32x4*>(stage + n * kStageRow + 128 * s + 32 * g + 16 * h) = d;
         }
     }
