@@ -32,7 +32,7 @@
 //      and writes each slot's sequence, first token and token count.  With
 //      one sequence, or a few (their slots found in the kernels), it is not
 //      launched.
-//   2. prep, grid (chunk slots, H), three workgroups per CU: what does not
+//   2. prep, grid (chunk slots, H), four workgroups per CU: what does not
 //      depend on the state, for all chunks at once -- K K^T (bf16 MFMA: the
 //      inputs are bf16, once per q/k head), then per v-head the gates and
 //      gamma and T by block recursion (fp32 MFMA) -- into a 14 KiB workspace
@@ -393,18 +393,22 @@ __device__ __forceinline__ void store_rows_bf16(uint16_t* dst, const u32x4 (&val
 // 2. per-chunk preparation
 // ---------------------------------------------------------------------------
 
-// 52 KiB, so that three workgroups share a CU.  The 32 x 32 scratch of the
-// block recursion is T's upper-right quarter, which T never uses (rows
-// 0..31, columns 32..63).
+// 35 KiB, so that four workgroups share a CU: A takes the place of the K
+// rows, which no wave reads once K K^T is in registers (every wave passes a
+// barrier between its last K read and the first write of A).  The 32 x 32
+// scratch of the block recursion is T's upper-right quarter, which T never
+// uses (rows 0..31, columns 32..63).
 struct PrepLds {
-  uint16_t K[kChunk * kBfStride];
-  float A[kChunk * kF64Stride];       // strict lower part of (I + A) minus I
+  union {
+    uint16_t K[kChunk * kBfStride];   // the chunk's K rows, until K K^T
+    float A[kChunk * kF64Stride];     // then: strict lower part of (I + A) minus I
+  };
   float T[kChunk * kF64Stride];       // (I + A)^-1
   float gamma[kChunk];
   float beta[kChunk];
   float rk[kChunk];
 };
-static_assert(sizeof(PrepLds) <= 160 * 1024 / 3, "three preparation workgroups per CU");
+static_assert(sizeof(PrepLds) <= 160 * 1024 / 4, "four preparation workgroups per CU");
 
 // 16 x 16 x 16 fp32 block product A[0:16, 0:16] B[0:16, 0:16] from LDS rows
 // of stride lda / ldb, as an MFMA result (lane (col, g) holds rows 4 g + e).
@@ -427,7 +431,7 @@ __device__ __forceinline__ void store16(float* D, int ldd, const f32x4& v, float
 // sequences, no offsets kernel); a template flag, so that the kernels of the
 // other modes are compiled without that code.
 template <bool FEW>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3)))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4)))
 void prep_kernel(Params p) {
   __shared__ PrepLds lds;
   const int c = blockIdx.x;
