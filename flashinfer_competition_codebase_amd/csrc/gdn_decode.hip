@@ -256,15 +256,17 @@ void pick_row(const ShapeRow (&table)[N], long long heads, int* ns, int* waves) 
 // runs T = 2..4 tokens, and its shape, from rocprofv3 kernel-trace sweeps at
 // qk16_v32 B = 1..512 (steady regime) that launch every block shape and the
 // token loop's shapes in turn, round after round, so that all of them run
-// in the same GPU state.  bf16 state: the block kernel is faster from B = 1
-// at T = 4 (4.18 against 4.52 us), from B = 2 at T = 3 and from B = 4 at
-// T = 2, by 10-25% from B = 8 on (B=256: T = 4 96.2 against 134.6 us, T = 2
-// 92.1 against 106.9 us); (32, 2) is within 2% of the best shape from 1024
-// heads on.  fp32 state (three bf16 products per dot): 2-15% faster at T = 4
-// and 256 or 513-4096 heads only.
+// in the same GPU state, checked at large batches by back-to-back launches
+// (which is how a model's layers run).  bf16 state: the block kernel is
+// faster from B = 1 at T = 4 (4.18 against 4.52 us), from B = 2 at T = 3
+// and from B = 4 at T = 2 (B=256 back to back: T = 4 89.5 against 116.0 us,
+// T = 3 88.1 against 98.0 us, T = 2 86.2 against 87.5 us); (32, 2) is within
+// 2% of the best shape from 1024 heads on.  fp32 state (three bf16 products
+// per dot): never faster back to back (B=64 and 128, T = 4: 2-4% slower,
+// though faster in the interleaved sweep), so it keeps the token loop.
 struct BlockRow {
   int T;                 // 0: any of 2..4
-  bool bf16;
+  bool bf16;             // the state's dtype (only bf16 rows so far)
   long long min_heads;
   long long max_heads;   // -1: no limit
   int rows;
@@ -275,8 +277,6 @@ constexpr BlockRow kBlockRows[] = {
     {4, true, 1, 128, 32, 1},     {3, true, 33, 128, 32, 1},   {2, true, 65, 128, 32, 1},
     {0, true, 129, 256, 32, 4},   {0, true, 257, 512, 32, 2},  {0, true, 513, 1024, 64, 1},
     {0, true, 1025, -1, 32, 2},
-    // fp32 state
-    {4, false, 256, 256, 16, 8},  {4, false, 513, 4096, 64, 1},
 };
 
 void choose_shape(long long heads, bool bf16, int T, int* ns, int* waves, int* policy) {
