@@ -261,12 +261,16 @@ void pick_row(const ShapeRow (&table)[N], long long heads, int* ns, int* waves) 
 // faster from B = 1 at T = 4 (4.18 against 4.52 us), from B = 2 at T = 3
 // and from B = 4 at T = 2 (B=256 back to back: T = 4 89.5 against 116.0 us,
 // T = 3 88.1 against 98.0 us, T = 2 86.2 against 87.5 us); (32, 2) is within
-// 2% of the best shape from 1024 heads on.  fp32 state (three bf16 products
-// per dot): never faster back to back (B=64 and 128, T = 4: 2-4% slower,
-// though faster in the interleaved sweep), so it keeps the token loop.
+// 2% of the best shape from 1024 heads on.  fp32 state (the dots on
+// v_mfma_f32_16x16x4_f32): faster at T = 4 from B = 4 to B = 64 (kernel
+// trace: B=4 6.42 against 6.82 us, B=8 8.36 against 9.48, B=32 25.9
+// against 26.8, B=64 49.3 against 52.4; back to back at B=64 47.1 against
+// 48.7) and at T = 3 around B = 32 (24.9 against 26.2 us); the same time
+// as the token loop from B = 128 on (B=256 T=4: 176.8 against 176.6 us)
+// and slower at T = 2, where the token loop stays.
 struct BlockRow {
   int T;                 // 0: any of 2..4
-  bool bf16;             // the state's dtype (only bf16 rows so far)
+  bool bf16;             // the state's dtype
   long long min_heads;
   long long max_heads;   // -1: no limit
   int rows;
@@ -277,6 +281,9 @@ constexpr BlockRow kBlockRows[] = {
     {4, true, 1, 128, 32, 1},     {3, true, 33, 128, 32, 1},   {2, true, 65, 128, 32, 1},
     {0, true, 129, 256, 32, 4},   {0, true, 257, 512, 32, 2},  {0, true, 513, 1024, 64, 1},
     {0, true, 1025, -1, 32, 2},
+    // fp32 state
+    {4, false, 65, 128, 32, 1},   {4, false, 129, 256, 16, 2}, {4, false, 257, 2048, 32, 1},
+    {3, false, 513, 1024, 32, 2},
 };
 
 void choose_shape(long long heads, bool bf16, int T, int* ns, int* waves, int* policy) {

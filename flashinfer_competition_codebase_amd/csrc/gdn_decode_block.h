@@ -28,13 +28,14 @@
 //   * a wave holds R tiles of 16 state rows; lane (n, g) holds row n of each
 //     tile, at k = 32 s + 8 g + e for s, e = 0..7 (four 8-element runs,
 //     16 contiguous bytes of a bf16 row, 32 of an fp32 row, per run);
-//   * k.S and q.S: the state is the B operand (B[k][n] = S0[n][k]) of
-//     v_mfma_f32_16x16x32_bf16: for a bf16 state the loaded bits as they
-//     are, for an fp32 state three bf16 parts of it (hi + mid + lo, three
-//     products); row m of the A operand is token m % 4's k (m & 4 clear) or
-//     q (m & 4 set), so lane n + 16 g receives the dots of row n with the
-//     k's (g even) or the q's (g odd), D[m][n] being in lane n + 16 (m / 4),
-//     register m % 4, and a v_permlane16_swap gives every lane both;
+//   * k.S and q.S: the state is the B operand (B[k][n] = S0[n][k]): for a
+//     bf16 state the loaded bits as they are, of v_mfma_f32_16x16x32_bf16;
+//     for an fp32 state each register as it is, of v_mfma_f32_16x16x4_f32
+//     (32 products a tile, k = 32 s + 8 g + 4 h + i); row m of the A operand
+//     is token m % 4's k (m & 4 clear) or q (m & 4 set), so lane n + 16 g
+//     receives the dots of row n with the k's (g even) or the q's (g odd),
+//     D[m][n] being in lane n + 16 (m / 4), register m % 4 (both products),
+//     and a v_permlane16_swap gives every lane both;
 //   * the update is v_mfma_f32_16x16x4_f32 per 16 x 16 tile of (k, row):
 //     D[m][n] = C[m][n] + sum_t A[m][t] B[t][n], with C = Gamma S0 at the
 //     lane's own elements, B[t][n] = D(t,T-1) x_t of row n from lane n + 16 t,
@@ -92,24 +93,6 @@ __device__ __forceinline__ float bf16_item(u32x4 w, int e) {
   return e & 1 ? bf16_hi(word) : bf16_lo(word);
 }
 
-// Eight fp32 values (a, then b) as three packed bf16 runs with a + b ~ hi +
-// mid + lo: each part is the round-to-nearest bf16 of what the parts before
-// it leave, so the sum misses x by at most ~2^-27 |x|.
-__device__ __forceinline__ void split3(const f32x4& a, const f32x4& b, u32x4& hi, u32x4& mid,
-                                       u32x4& lo) {
-  float x[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-#pragma unroll
-  for (int w = 0; w < 4; ++w) hi[w] = pack_bf16x2(x[2 * w], x[2 * w + 1]);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) x[e] -= bf16_item(hi, e);
-#pragma unroll
-  for (int w = 0; w < 4; ++w) mid[w] = pack_bf16x2(x[2 * w], x[2 * w + 1]);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) x[e] -= bf16_item(mid, e);
-#pragma unroll
-  for (int w = 0; w < 4; ++w) lo[w] = pack_bf16x2(x[2 * w], x[2 * w + 1]);
-}
-
 // Selector operand h (B of v_mfma_f32_16x16x32_bf16) of lane (n, g): item e
 // is 1.0 where k index 8 g + e of the 32-long block is the tile's n-th,
 // 8 (n / 4) + 4 h + n % 4.
@@ -133,11 +116,12 @@ __device__ __forceinline__ u32x4 selector(int n, int g, int h) {
 // measured 1.34x the state's bytes in HBM writes (rocprofv3 WRITE_SIZE,
 // B=256 T=4 bf16: 119.7 us) against 1.00x and 104.5 us through 16 padded
 // LDS rows and whole-row stores; ordinary (write-back) stores from the
-// registers also write 1.00x but took 117.5 us.  The R = 4 bf16 and R = 2
-// fp32 kernels are held to 168 VGPRs (3 waves per SIMD).
+// registers also write 1.00x but took 117.5 us.  The R = 4 bf16 kernel is
+// held to 168 VGPRs (3 waves per SIMD); held there too, the R = 2 fp32 one
+// spills (B=64 T=4: 56 us against 49 us at 188 VGPRs, 2 waves per SIMD).
 template <int R, int WAVES, bool L2NORM, bool BF16>
 __global__ __launch_bounds__(64 * WAVES)
-__attribute__((amdgpu_waves_per_eu((R == 4 && BF16) || (R == 2 && !BF16) ? 3 : 1, 8)))
+__attribute__((amdgpu_waves_per_eu((R == 4 && BF16) ? 3 : 1, 8)))
 void gdn_decode_block(
     const void* state, const uint16_t* q, const uint16_t* k, const uint16_t* v,
     const uint16_t* a, const uint16_t* b, unsigned h_ratio, int T, const float* A_log_p,
@@ -376,17 +360,22 @@ void gdn_decode_block(
 #pragma unroll
       for (int s = 0; s < 4; ++s) pn = mfma_bf16x32(vn[s], sb[s], pn);
     } else {
-      // fp32 state: each run split into three bf16 parts, x = hi + mid + lo
-      // to ~2^-27 relative, the B operands of three bf16 products (exact
-      // products, fp32 sums; the small parts first)
+      // fp32 state: v_mfma_f32_16x16x4_f32 with the contraction index k =
+      // 32 s + 8 g + 4 h + i in lane group g, so the state registers are
+      // the B operands as loaded and A is the k/q item at the same k (bf16
+      // widened, exact); two accumulators halve the chain of dependent
+      // products.
+      f32x4 pn1 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        u32x4 hi, mid, lo;
-        split3(sf[s][0], sf[s][1], hi, mid, lo);
-        pn = mfma_bf16x32(vn[s], lo, pn);
-        pn = mfma_bf16x32(vn[s], mid, pn);
-        pn = mfma_bf16x32(vn[s], hi, pn);
-      }
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if (h == 0) pn = mfma_f32x4(bf16_item(vn[s], i), sf[s][0][i], pn);
+            else pn1 = mfma_f32x4(bf16_item(vn[s], 4 + i), sf[s][1][i], pn1);
+          }
+      pn += pn1;
     }
     f32x4 pk, pq;
 #pragma unroll

@@ -196,7 +196,8 @@ def test_block_rejects_other_token_counts(hip_device):
 
 
 @pytest.mark.parametrize("B,T,bf16", [(1, 4, True), (4, 2, True), (16, 4, True), (32, 3, True),
-                                      (32, 2, True)])
+                                      (32, 2, True), (4, 4, False), (8, 4, False), (32, 3, False),
+                                      (64, 4, False)])
 def test_library_runs_block_kernel(B, T, bf16, hip_device):
     """Shapes at which the library's launch table picks the block kernel, through
     the value-returning entry point, against the oracle."""
