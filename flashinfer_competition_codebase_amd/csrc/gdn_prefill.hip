@@ -179,6 +179,16 @@ __device__ __forceinline__ void split4(const f32x4& x, s16x4& hi, s16x4& lo) {
 // exchange data through LDS alone, so global loads issued ahead of a barrier
 // (the next chunk's operands) stay in flight across it instead of being
 // drained as __syncthreads' all-memory fence would.
+// The wavefront's index in its workgroup, as a value the compiler knows is
+// the same in every lane (a scalar register): branches on it are scalar
+// branches and LDS bases derived from it need no per-lane waterfall.  Used by
+// the scan (64 x 512 qk16_v32: scan 485.9 -> 457.8 us with the L2-norm as a
+// template flag); the preparation kernel keeps threadIdx.x >> 6, with which
+// it measured faster (118.8 against 138.9 us).
+__device__ __forceinline__ int wave_index() {
+  return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+}
+
 __device__ __forceinline__ void block_sync_lds() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
@@ -798,14 +808,14 @@ struct ScanCtx {
   int start, end, nchunks;     // token range and chunks
   int H, HV, h, hv;
   float scale;
-  bool values, l2norm;
+  bool values;
 };
 
 // Chunk c's DMA into buf and its V into registers.
 template <bool OUT>
 __device__ __forceinline__ void scan_issue(ScanBuf<OUT>* buf, const ScanCtx& cx, int c,
                                            u32x2 (&vf)[4]) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = wave_index(), lane = threadIdx.x & 63;
   const int tc = cx.start + c * kChunk;
   const int nc = min(kChunk, cx.end - tc);
   scan_dma(*buf, cx.k + (static_cast<size_t>(tc) * cx.H + cx.h) * kDim,
@@ -823,26 +833,29 @@ __device__ constexpr int8_t kPTileR[kPTiles] = {0, 1, 1, 2, 2, 2, 3, 3, 3, 3, 0,
 __device__ constexpr int8_t kPTileJ[kPTiles] = {0, 0, 1, 0, 1, 2, 0, 1, 2, 3, 1, 3};
 
 // Chunk ci from buffer B, with the next chunk's DMA into Bn; Kt: the K^T
-// operand blocks; Pb: the P' operand blocks (OUT).  B, Bn, Kt and Pb are
-// restrict: the compiler then knows that the DMA in flight into Bn never
-// writes what this chunk reads, and waits for it only at the end.  OUT: the
-// outputs too (else only the state).
+// operand blocks; Pb: the P' operand blocks (OUT); Qn: the Q row scales
+// (L2).  B, Bn, Kt, Pb and Qn are restrict: the compiler then knows that the
+// DMA in flight into Bn never writes what this chunk reads, and waits for it
+// only at the end.  OUT: the outputs too (else only the state).  L2: the
+// L2-norm (a template flag: as a run-time branch inside the product loop it
+// split the loop into blocks the scheduler could not interleave).
 //
 // The output's intra-chunk term uses P = diag(rq) P' with
 //   P'_ij = scale rk_j e^(gamma_i - gamma_j) (Q K^T)_ij,  j <= i,
 // made here from the chunk's K and Q rows: (K Q^T) tiles on bf16 MFMA leave
 // each lane 4 consecutive j of one row i, the operand items of P' as the B
-// operand of Delta^T P'^T.  The Q row norms rq (L2-norm) come from the
-// squares of the Q items the S^T Q^T product reads, and scale the output
-// row: O = diag(rq) (diag(scale e^gamma) Q S + P' Delta).
-template <bool OUT>
+// operand of Delta^T P'^T.  The Q row scales rq = 1 / |q_i| (L2-norm; each
+// wave computes eight rows' from the Q rows in LDS and shares them through
+// Qn) scale the output row: O = diag(rq) (diag(scale e^gamma) Q S + P' Delta).
+template <bool OUT, bool L2>
 __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
                                            ScanBuf<OUT>* __restrict__ Bn,
                                            uint16_t* __restrict__ Kt, uint16_t* __restrict__ Pb,
-                                           const ScanCtx& cx, f32x4 (&st)[8],
+                                           float* __restrict__ Qn, const ScanCtx& cx,
+                                           f32x4 (&st)[8],
                                            u32x2 (&vnext)[4], const s16x8& sel, int ci) {
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = wave_index();
   const int col = lane & 15;
   const int g4 = lane >> 4;
   const int t0 = cx.start + ci * kChunk;
@@ -903,15 +916,34 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
   // this one's again, unused), in flight while this chunk computes
   scan_issue(Bn, cx, ci + 1 < cx.nchunks ? ci + 1 : ci, vnext);
 
+  // L2-norm: 1 / |q_i| of Q rows 8 wave .. 8 wave + 7 into Qn (lane: row
+  // 8 wave + lane / 8, items 16 (lane % 8) .. + 15); read after the barrier
+  // below.  (The previous chunk's reads of Qn ended before its last barrier.)
+  if constexpr (L2) {
+    const int row = 8 * wave + (lane >> 3);
+    const uint16_t* qr = &B->Qr[row * kRowStride + (lane & 7) * 16];
+    const u32x4 w[2] = {*reinterpret_cast<const u32x4*>(qr),
+                        *reinterpret_cast<const u32x4*>(qr + 8)};
+    float q2 = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float lo = __uint_as_float(w[h][i] << 16);
+        const float hi = __uint_as_float(w[h][i] & 0xffff0000u);
+        q2 = fmaf(hi, hi, fmaf(lo, lo, q2));
+      }
+    q2 += __shfl_xor(q2, 1, 64);
+    q2 += __shfl_xor(q2, 2, 64);
+    q2 += __shfl_xor(q2, 4, 64);
+    if ((lane & 7) == 0) Qn[row] = __builtin_amdgcn_rsqf(q2 + kL2Eps);
+  }
+
   // K S (token rows) and S^T Q^T (the output's first term, transposed),
   // one 32-key block of the state at a time
   f32x4 x[4], o[4];
-  float qq[4];                                     // sums of squares of Q row 16 r + col
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    x[r] = o[r] = f32x4{0, 0, 0, 0};
-    qq[r] = 0.0f;
-  }
+  for (int r = 0; r < 4; ++r) x[r] = o[r] = f32x4{0, 0, 0, 0};
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
     s16x8 sl;
@@ -925,13 +957,6 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
         const s16x8 bq = frag(&B->Qr[(r * 16 + col) * kRowStride], kb, g4);
         o[r] = mfma_bf16(sh, bq, o[r]);
         o[r] = mfma_bf16(sl, bq, o[r]);
-        if (cx.l2norm) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float y = bf16_to_f32(static_cast<uint16_t>(bq[e]));
-            qq[r] = fmaf(y, y, qq[r]);
-          }
-        }
       }
     }
   }
@@ -992,12 +1017,7 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
         o[r] = mfma_bf16(dh[kb], pl, o[r]);
         o[r] = mfma_bf16(dl[kb], ph, o[r]);
       }
-      if (cx.l2norm) {
-        float q2 = qq[r];
-        q2 += __shfl_xor(q2, 16, 64);
-        q2 += __shfl_xor(q2, 32, 64);
-        o[r] = o[r] * __builtin_amdgcn_rsqf(q2 + kL2Eps);
-      }
+      if constexpr (L2) o[r] = o[r] * Qn[r * 16 + col];
       const int tok = r * 16 + col;
       const u32x2 ob = {pack_bf16x2(o[r][0], o[r][1]), pack_bf16x2(o[r][2], o[r][3])};
       if (tok < n)
@@ -1034,7 +1054,7 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
 __device__ __forceinline__ void store_end(float* st_out, bool transition, const f32x4 (&st)[8],
                                           const s16x8 (&sels)[2]) {
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = wave_index();
   const int col = lane & 15;
   const int g4 = lane >> 4;
   if (!transition) {
@@ -1073,15 +1093,17 @@ __device__ __forceinline__ void store_end(float* st_out, bool transition, const 
 // values (end: seg_M, as the combine's operand); the second (OUT) runs every
 // segment from its start (segment 0: the sequence's state, then seg_S) with
 // the outputs, the last one's end being the new state.
-template <bool FEW, bool SEG, bool OUT>
+template <bool FEW, bool SEG, bool OUT, bool L2>
 __global__ __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void scan_kernel(Params p) {
   static_assert(OUT || SEG, "only segments run without outputs");
+  static_assert(OUT || !L2, "the L2-norm scales outputs only");
   // separate LDS objects, so that the compiler sees that the DMA into one
   // buffer never writes what the chunk reads from the other
   __shared__ ScanBuf<OUT> L0, L1;
   __shared__ __attribute__((aligned(16))) uint16_t Kt[kKtElems];
   __shared__ __attribute__((aligned(16))) uint16_t Pb[OUT ? kPElems : 8];
+  __shared__ float Qn[L2 ? kChunk : 1];    // 1 / |q_i| of the chunk's Q rows (L2-norm)
   const long long b = blockIdx.x;
   const int ratio = p.ratio;
   const long long pair = (b / (8LL * ratio)) * 8 + (b & 7);
@@ -1092,7 +1114,7 @@ void scan_kernel(Params p) {
   const int h = static_cast<int>(pair % p.H);
   const int hv = h * ratio + jr;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = wave_index();
   const int col = lane & 15;
   const int g4 = lane >> 4;
   const size_t blk = static_cast<size_t>(kDim) * kDim;
@@ -1206,7 +1228,6 @@ void scan_kernel(Params p) {
   cx.hv = hv;
   cx.values = values;
   cx.scale = p.scale;
-  cx.l2norm = p.l2norm != 0;
 
   const s16x8 sel = sels[wave & 1];       // this wave's half of a 32-key / 32-column block
   u32x2 vnext[4];
@@ -1214,8 +1235,8 @@ void scan_kernel(Params p) {
   wait_vmem();
   block_sync_lds();
   for (int ci = 0; ci < nchunks; ci += 2) {
-    scan_chunk<OUT>(&L0, &L1, Kt, Pb, cx, st, vnext, sel, ci);
-    if (ci + 1 < nchunks) scan_chunk<OUT>(&L1, &L0, Kt, Pb, cx, st, vnext, sel, ci + 1);  // uniform
+    scan_chunk<OUT, L2>(&L0, &L1, Kt, Pb, Qn, cx, st, vnext, sel, ci);
+    if (ci + 1 < nchunks) scan_chunk<OUT, L2>(&L1, &L0, Kt, Pb, Qn, cx, st, vnext, sel, ci + 1);  // uniform
   }
   if (st_out != nullptr) store_end(st_out, identity, st, sels);
 }
@@ -1586,7 +1607,7 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
   if (p.nseg > 1) {
     // segments (one sequence): transitions and zero-start ends, the starts,
     // then every segment with its outputs
-    hipLaunchKernelGGL((scan_kernel<false, true, false>), scan_grid(2LL * p.nseg - 3),
+    hipLaunchKernelGGL((scan_kernel<false, true, false, false>), scan_grid(2LL * p.nseg - 3),
                        dim3(kScanThreads), 0, stream, p);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -1596,10 +1617,14 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
       e = hipGetLastError();
       if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL((scan_kernel<false, true, true>), scan_grid(p.nseg), dim3(kScanThreads), 0,
-                       stream, p);
+    auto* scan = p.l2norm ? scan_kernel<false, true, true, true>
+                          : scan_kernel<false, true, true, false>;
+    hipLaunchKernelGGL(scan, scan_grid(p.nseg), dim3(kScanThreads), 0, stream, p);
   } else {
-    auto* scan = p.few ? scan_kernel<true, false, true> : scan_kernel<false, false, true>;
+    auto* scan = p.few ? (p.l2norm ? scan_kernel<true, false, true, true>
+                                   : scan_kernel<true, false, true, false>)
+                       : (p.l2norm ? scan_kernel<false, false, true, true>
+                                   : scan_kernel<false, false, true, false>);
     hipLaunchKernelGGL(scan, scan_grid(num_seqs), dim3(kScanThreads), 0, stream, p);
   }
   e = hipGetLastError();
