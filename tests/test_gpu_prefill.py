@@ -92,14 +92,16 @@ def test_long_sequence_and_many_sequences(hip_device):
     _check(t, out, st, loop=False)
 
 
-@pytest.mark.parametrize("lens,H,HV,a_log_range", [
-    ([16384], 4, 8, None),            # the benchmark's prefill workloads, full size
-    ([1024] * 16, 4, 8, None),
-    ([8192], 16, 32, None),
-    ([512] * 64, 16, 32, None),
-    ([16384], 4, 8, (1e-3, 1e-2)),    # slow decay (g ~ 0.993-0.9993): a long memory
+@pytest.mark.parametrize("lens,H,HV,a_log_range,l2", [
+    ([16384], 4, 8, None, False),     # the benchmark's prefill workloads, full size
+    ([1024] * 16, 4, 8, None, False),
+    ([8192], 16, 32, None, False),
+    ([512] * 64, 16, 32, None, False),
+    ([16384], 4, 8, (1e-3, 1e-2), False),  # slow decay (g ~ 0.993-0.9993): a long memory
+    ([512] * 64, 16, 32, None, True),  # with the q/k L2-norm (raw-scale q/k)
+    ([1024] * 16, 4, 8, None, True),
 ])
-def test_bench_size_prefills_match_the_fp64_oracle(lens, H, HV, a_log_range, hip_device):
+def test_bench_size_prefills_match_the_fp64_oracle(lens, H, HV, a_log_range, l2, hip_device):
     """The benchmark's prefill workloads at their full sizes against the
     float64 chunked oracle, at the bars of every other prefill test: fp32
     rounding carried through 128-256 chained chunk steps stays inside them.
@@ -108,15 +110,15 @@ def test_bench_size_prefills_match_the_fp64_oracle(lens, H, HV, a_log_range, hip
     draws A_log = log U[1e-3, 1e-2], so the state carries ~1000 tokens of
     history through 256 chunk steps and every step's rounding with it."""
     _announce(f"prefill bench size lens={lens[0]}x{len(lens)} H={H} HV={HV} "
-              f"A_log range={a_log_range}")
-    t = make_prefill_inputs(lens, H, HV, seed=200 + len(lens) + H)
+              f"A_log range={a_log_range} l2={l2}")
+    t = make_prefill_inputs(lens, H, HV, seed=200 + len(lens) + H, unit_qk=not l2)
     if a_log_range is not None:
         lo, hi = a_log_range
         g = torch.Generator().manual_seed(201)
         t["A_log"] = torch.log(torch.rand(HV, generator=g) * (hi - lo) + lo)
-    out, st = gdn.prefill_run(**_dev(t, hip_device))
+    out, st = gdn.prefill_run(**_dev(t, hip_device), use_qk_l2norm=l2)
     torch.cuda.synchronize()
-    do, ds = _check(t, out, st, loop=False)
+    do, ds = _check(t, out, st, l2=l2, loop=False)
     _announce(f"  max |out - fp64| {do:.3e}, max |state - fp64| {ds:.3e}")
 
 
@@ -182,6 +184,19 @@ def test_segmented_in_place_and_timed(hip_device):
 def test_l2norm_and_no_state(hip_device):
     _announce("prefill l2norm, state=None, raw-scale q/k")
     t = make_prefill_inputs([40, 90], 4, 8, seed=12, with_state=False, unit_qk=False)
+    out, st = gdn.prefill_run(**_dev(t, hip_device), use_qk_l2norm=True)
+    torch.cuda.synchronize()
+    _check(t, out, st, l2=True)
+
+
+@pytest.mark.parametrize("with_state", [True, False])
+def test_l2norm_past_the_in_kernel_chunk_slots(with_state, hip_device):
+    """65 sequences (the chunk-offsets scan and the plain scan kernel) with
+    the L2-norm, whose Q row scales each wave computes for eight rows and
+    shares through LDS."""
+    _announce(f"prefill l2norm, 65 sequences, state={with_state}")
+    t = make_prefill_inputs([70, 129] + [1] * 63, 4, 8, seed=13, with_state=with_state,
+                            unit_qk=False)
     out, st = gdn.prefill_run(**_dev(t, hip_device), use_qk_l2norm=True)
     torch.cuda.synchronize()
     _check(t, out, st, l2=True)
