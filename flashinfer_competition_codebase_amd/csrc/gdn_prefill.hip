@@ -509,8 +509,9 @@ void prep_kernel(Params p) {
   }
   block_sync_lds();
 
-  // K K^T for row block `wave` (rows 16 wave .. +15), all 4 column blocks;
-  // bf16 MFMA over the 128-long rows
+  // K K^T for row block `wave` (rows 16 wave .. +15), column blocks 0 ..
+  // wave (A is strictly lower triangular: the blocks right of the diagonal
+  // are neither computed nor written); bf16 MFMA over the 128-long rows
   f32x4 kk[4];
   {
 #pragma unroll
@@ -521,6 +522,7 @@ void prep_kernel(Params p) {
       const s16x8 ak = frag(&lds.K[ra * kBfStride], m, g4);
 #pragma unroll
       for (int nj = 0; nj < 4; ++nj) {
+        if (nj > wave) break;                      // uniform per wave
         const s16x8 bk = frag(&lds.K[(nj * 16 + col) * kBfStride], m, g4);
         kk[nj] = mfma_bf16(ak, bk, kk[nj]);
       }
@@ -561,6 +563,7 @@ void prep_kernel(Params p) {
                          *reinterpret_cast<const f32x4*>(&lds.rk[ia]);
 #pragma unroll
       for (int nj = 0; nj < 4; ++nj) {
+        if (nj > wave) break;                      // uniform: never read
         const int j = nj * 16 + col;
         const float gj = lds.gamma[j];
         const float rkj = lds.rk[j];
