@@ -240,8 +240,9 @@ struct Params {
   int few;                   // 2..kFewSeqs sequences: the kernels compute the chunk
                              // slots from cu_seqlens (no offsets kernel)
   long long max_slots;       // slots the workspace holds
-  // Segments of one long sequence (seg_chunks > 0): segment j is chunks
-  // [j seg_chunks, (j + 1) seg_chunks); per (segment, v-head) 128 x 128 fp32
+  // Segments (seg_chunks > 0): segment j of a sequence is its chunks
+  // [j seg_chunks, (j + 1) seg_chunks), and the segments of all sequences are
+  // numbered in sequence order (at most nseg); per (segment, v-head) 128 x 128 fp32
   // blocks in k-last order (element (k, c) at c * 128 + k).
   int seg_chunks;            // chunks per segment, 0: no segments
   int nseg;                  // segments
@@ -289,6 +290,55 @@ __device__ __forceinline__ FewSlots few_slots(const Params& p) {
   const long long incl = x, excl = static_cast<long long>(x) - cnt;
   f.incl = incl < p.max_slots ? incl : p.max_slots;
   f.excl = excl < p.max_slots ? excl : p.max_slots;
+  return f;
+}
+
+// Segments of a batch of at most 64 sequences, in one wave (lane s: sequence
+// s): its token range, its segment count (seg_chunks chunks a segment; one
+// for an empty sequence), the segments of the sequences before it, and its
+// units of a segment launch (OUT: one a segment; else 2 nseg - 3: segment 0
+// from the sequence's state, the middle ones from a zero start and from the
+// identity; none for a sequence of one segment).
+struct SegSeqs {
+  int start, end;
+  int nseg, seg_excl;
+  int u_excl, u_incl;
+};
+
+// Units of the first segment launch for nseg segments in all: one sequence
+// has 2 nseg - 3, several at most 2 nseg.
+__host__ __device__ inline long long seg_units1(long long nseg, long long N) {
+  return N == 1 ? 2 * nseg - 3 : 2 * nseg;
+}
+
+template <bool OUT>
+__device__ __forceinline__ SegSeqs seg_seqs(const Params& p) {
+  const int lane = threadIdx.x & 63;
+  SegSeqs f{0, 0, 0, 0, 0, 0};
+  int units = 0;
+  if (lane < p.N) {
+    seq_range(p, lane, f.start, f.end);
+    const int nch = (f.end - f.start + kChunk - 1) / kChunk;
+    f.nseg = nch > p.seg_chunks ? (nch + p.seg_chunks - 1) / p.seg_chunks : 1;
+    units = OUT ? f.nseg : (f.nseg >= 2 ? 2 * f.nseg - 3 : 0);
+  }
+  if (p.N == 1) {                                  // uniform: nothing to scan
+    f.u_incl = units;
+    return f;
+  }
+  int xs = f.nseg, xu = units;                     // inclusive scans over the wave
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int ys = __shfl_up(xs, d, 64);
+    const int yu = __shfl_up(xu, d, 64);
+    if (lane >= d) {
+      xs += ys;
+      xu += yu;
+    }
+  }
+  f.seg_excl = xs - f.nseg;
+  f.u_excl = xu - units;
+  f.u_incl = xu;
   return f;
 }
 
@@ -1111,7 +1161,10 @@ void scan_kernel(Params p) {
   const int ratio = p.ratio;
   const long long pair = (b / (8LL * ratio)) * 8 + (b & 7);
   const int jr = static_cast<int>((b >> 3) % ratio);
-  const long long units = SEG ? (OUT ? p.nseg : 2LL * p.nseg - 3) : static_cast<long long>(p.N);
+  // units the grid covers: with SEG the launch's bound, each workgroup
+  // finding its sequence's segment below (those past the batch's exit)
+  const long long units = SEG ? (OUT ? p.nseg : seg_units1(p.nseg, p.N))
+                              : static_cast<long long>(p.N);
   if (pair >= units * p.H) return;                              // uniform per workgroup
   const int unit = static_cast<int>(pair / p.H);
   const int h = static_cast<int>(pair % p.H);
@@ -1127,41 +1180,69 @@ void scan_kernel(Params p) {
   bool identity = false, values = true, pass_through = false;
   float* st_out;
   int s = 0, start, end, slot0 = 0, nchunks = 0;
+  // the sequence's chunk slots (never more than its range holds, and never
+  // more slots than the workspace has, whatever cu_seqlens contains)
+  auto seq_slots = [&](int sq, int& base, int& count) {
+    if (p.single) {
+      base = 0;
+      count = (end - start + kChunk - 1) / kChunk;
+    } else if (FEW) {
+      const FewSlots f = few_slots(p);
+      base = static_cast<int>(__shfl(f.excl, sq, 64));
+      count = static_cast<int>(__shfl(f.incl, sq, 64)) - base;
+    } else {
+      base = p.offs[sq];
+      count = p.offs[sq + 1] - base;
+    }
+  };
   if (SEG) {
+    const SegSeqs f = seg_seqs<OUT>(p);
+    const unsigned long long own = __ballot(lane < p.N && f.u_excl <= unit && unit < f.u_incl);
+    if (own == 0) return;                         // past the batch's units (uniform)
+    s = __builtin_ctzll(own);                     // uniform: lane reads, no shuffles
+    const int nseg = __builtin_amdgcn_readlane(f.nseg, s);
+    const int g0 = __builtin_amdgcn_readlane(f.seg_excl, s);   // the sequence's first segment
+    if (g0 + nseg > p.nseg) return;               // past the workspace's (a malformed batch)
+    const int u = unit - __builtin_amdgcn_readlane(f.u_excl, s);
+    start = __builtin_amdgcn_readlane(f.start, s);
+    end = __builtin_amdgcn_readlane(f.end, s);
+    const size_t sh = static_cast<size_t>(s) * p.HV + hv;        // the sequence's state
+    auto seg_blk = [&](float* base, int g) { return base + (static_cast<size_t>(g) * p.HV + hv) * blk; };
     int j;
     if (!OUT) {
-      const int mid = p.nseg - 2;                 // segments 1 .. nseg-2
-      if (unit == 0) {
+      const int mid = nseg - 2;                   // segments 1 .. nseg-2
+      if (u == 0) {
         j = 0;
-        st_in = p.state ? p.state + static_cast<size_t>(hv) * blk : nullptr;
-        st_out = p.seg_S + (static_cast<size_t>(p.HV) + hv) * blk;
-      } else if (unit <= mid) {
-        j = unit;
-        st_out = p.seg_B + (static_cast<size_t>(j) * p.HV + hv) * blk;
+        st_in = p.state ? p.state + sh * blk : nullptr;
+        st_out = seg_blk(p.seg_S, g0 + 1);
+      } else if (u <= mid) {
+        j = u;
+        st_out = seg_blk(p.seg_B, g0 + j);
       } else {
-        j = unit - mid;
+        j = u - mid;
         identity = true;
         values = false;
-        st_out = p.seg_M + (static_cast<size_t>(j) * p.HV + hv) * blk;
+        st_out = seg_blk(p.seg_M, g0 + j);
       }
     } else {
-      j = unit;
-      st_in = j == 0 ? (p.state ? p.state + static_cast<size_t>(hv) * blk : nullptr)
-                     : p.seg_S + (static_cast<size_t>(j) * p.HV + hv) * blk;
-      st_out = j == p.nseg - 1 ? p.new_state + static_cast<size_t>(hv) * blk : nullptr;
+      j = u;
+      st_in = j == 0 ? (p.state ? p.state + sh * blk : nullptr) : seg_blk(p.seg_S, g0 + j);
+      st_out = j == nseg - 1 ? p.new_state + sh * blk : nullptr;
       pass_through = j > 0;
     }
-    seq_range(p, 0, start, end);               // one sequence: chunk c is slot c
-    const int total = (end - start + kChunk - 1) / kChunk;
-    slot0 = j * p.seg_chunks;
-    nchunks = min(p.seg_chunks, total - slot0);
-    start += slot0 * kChunk;
-    end = min(end, start + nchunks * kChunk);
+    int base, count;
+    seq_slots(s, base, count);
+    const int first = j * p.seg_chunks;
+    slot0 = base + first;
+    nchunks = min(p.seg_chunks, count - first);
+    start = min(end, start + first * kChunk);
+    if (nchunks > 0) end = min(end, start + nchunks * kChunk);
   } else {
     s = unit;
     seq_range(p, s, start, end);
     st_in = p.state ? p.state + (static_cast<size_t>(s) * p.HV + hv) * blk : nullptr;
     st_out = p.new_state + (static_cast<size_t>(s) * p.HV + hv) * blk;
+    seq_slots(s, slot0, nchunks);
   }
 
   // state registers; k-last storage: 4 consecutive keys are one 16-byte vector
@@ -1186,23 +1267,10 @@ void scan_kernel(Params p) {
     for (int e = 0; e < 8; ++e)
       sels[hf][e] = (e == 4 * hf + (col & 3) && g4 == (col >> 2)) ? 0x3f80 : 0;
 
-  // Chunk slots of a sequence (never more than the range holds, and never
-  // more slots than the workspace has, whatever cu_seqlens contains).
-  if (SEG) {
-  } else if (p.single) {
-    nchunks = (end - start + kChunk - 1) / kChunk;
-  } else if (FEW) {
-    const FewSlots f = few_slots(p);
-    slot0 = static_cast<int>(__shfl(f.excl, s, 64));
-    nchunks = static_cast<int>(__shfl(f.incl, s, 64)) - slot0;
-  } else {
-    slot0 = p.offs[s];
-    nchunks = p.offs[s + 1] - slot0;
-  }
-  // No tokens: a sequence ends in zeros, as the reference; a segment past
-  // the end of its sequence (cu_seqlens covering fewer tokens than L) passes
-  // its start through (transition: the identity, zero-start end: zeros), and
-  // so does the sequence's end state.
+  // No tokens: a sequence ends in zeros, as the reference; a segment with no
+  // chunk slots (a malformed batch whose slots ran past the workspace's)
+  // passes its start through (transition: the identity, zero-start end:
+  // zeros), and so does the sequence's end state.
   if (nchunks <= 0) {
     if (st_out != nullptr) {
       if (!SEG) {
@@ -1245,21 +1313,21 @@ void scan_kernel(Params p) {
 }
 
 // ---------------------------------------------------------------------------
-// 4. segments of one long sequence: chain the segment starts
+// 4. segments: chain each sequence's segment starts
 // ---------------------------------------------------------------------------
-// The first segment launch leaves, per v-head, S_1 and for each middle
-// segment j its transition M_j (as the A operand blocks of M S, bf16 hi/lo)
-// and zero-start end B_j.  Combine: S_{j+1} = M_j S_j + B_j for j = 1 ..
-// nseg-2, segment after segment, as bf16 MFMA with S_j split into hi + lo.
-// One workgroup per (v-head, 16 state columns); wave w computes row tile w
-// (rows 16 w .. 16 w + 15) and hands its rows of S_j to the other waves as
-// half of the B operand's k block w / 2 through LDS (two buffers: one
-// barrier a step).  A step is short (12 MFMAs a wave), so each wave's M
+// The first segment launch leaves, per (sequence, v-head), S_1 and for each
+// middle segment j its transition M_j (as the A operand blocks of M S, bf16
+// hi/lo) and zero-start end B_j.  Combine: S_{j+1} = M_j S_j + B_j for j = 1
+// .. nseg-2, segment after segment, as bf16 MFMA with S_j split into hi + lo.
+// One workgroup per (sequence, v-head, 16 state columns); wave w computes row
+// tile w (rows 16 w .. 16 w + 15) and hands its rows of S_j to the other
+// waves as half of the B operand's k block w / 2 through LDS (two buffers:
+// one barrier a step).  A step is short (12 MFMAs a wave), so each wave's M
 // blocks and B tile are loaded three steps ahead, into three register sets
-// used in turn.  Every workgroup reads all of M_j: the eight of a v-head
-// are numbered hv + 8k (HV rounded up to 8 between them), so all of them run
-// on XCD hv % 8 (workgroups go to the XCDs round-robin) and read M_j from
-// its L2 after the first.
+// used in turn.  Every workgroup reads all of M_j: the eight of a (sequence,
+// v-head) are numbered hv + 8k within the sequence's (HV rounded up to 8
+// between them), so all of them run on XCD hv % 8 (workgroups go to the XCDs
+// round-robin) and read M_j from its L2 after the first.
 constexpr int kCombWaves = 8;
 
 struct CombStage {
@@ -1270,31 +1338,43 @@ struct CombStage {
 __global__ __launch_bounds__(64 * kCombWaves) void seg_combine_kernel(Params p) {
   __shared__ s16x8 Sop[2][4][2][64];          // [buffer][k block][hi, lo][lane]
   const int hv_pad = (p.HV + 7) & ~7;
+  const int per_seq = hv_pad * 8;
+  const int sq = static_cast<int>(blockIdx.x) / per_seq;
   const int hv = static_cast<int>(blockIdx.x) % hv_pad;
-  const int c0 = static_cast<int>(blockIdx.x) / hv_pad * 16;
+  const int c0 = static_cast<int>(blockIdx.x) % per_seq / hv_pad * 16;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int col = lane & 15;
   const int g4 = lane >> 4;
   const size_t blk = static_cast<size_t>(kDim) * kDim;
-  if (p.nseg < 3 || hv >= p.HV) return;       // nothing to chain; padding
-  const int last = p.nseg - 2;                // steps j = 1 .. last
+  if (sq >= p.N || hv >= p.HV) return;        // padding (uniform)
+  // the sequence's segments: one sequence has the workspace's (its chain
+  // starts without reading cu_seqlens; steps past a shorter sequence's last
+  // segment chain values nothing reads); several count theirs
+  int nseg = p.nseg, g0 = 0;
+  if (p.N > 1) {
+    const SegSeqs f = seg_seqs<true>(p);
+    nseg = __builtin_amdgcn_readlane(f.nseg, sq);
+    g0 = __builtin_amdgcn_readlane(f.seg_excl, sq);
+  }
+  if (nseg < 3 || g0 + nseg > p.nseg) return; // nothing to chain; past the workspace's
+  const int last = nseg - 2;                  // steps j = 1 .. last
   const size_t tile = static_cast<size_t>(c0 + col) * kDim + wave * 16 + g4 * 4;
+  auto seg_blk = [&](const float* base, int j) {
+    return base + (static_cast<size_t>(g0 + j) * p.HV + hv) * blk;
+  };
   // S_1, this wave's row tile in the MFMA result layout
-  f32x4 S = *reinterpret_cast<const f32x4*>(p.seg_S + (static_cast<size_t>(p.HV) + hv) * blk +
-                                            tile);
+  f32x4 S = *reinterpret_cast<const f32x4*>(seg_blk(p.seg_S, 1) + tile);
   auto load = [&](int j, CombStage& cs) {     // past the last step: the last one's again
     j = j < last ? j : last;
-    const uint16_t* M =
-        reinterpret_cast<const uint16_t*>(p.seg_M + (static_cast<size_t>(j) * p.HV + hv) * blk);
+    const uint16_t* M = reinterpret_cast<const uint16_t*>(seg_blk(p.seg_M, j));
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
       for (int hl = 0; hl < 2; ++hl)
         cs.ma[kb][hl] =
             *reinterpret_cast<const s16x8*>(M + (((wave * 4 + kb) * 2 + hl) * kBlk + lane * 8));
-    cs.bt = *reinterpret_cast<const f32x4*>(p.seg_B + (static_cast<size_t>(j) * p.HV + hv) * blk +
-                                            tile);
+    cs.bt = *reinterpret_cast<const f32x4*>(seg_blk(p.seg_B, j) + tile);
   };
   auto step = [&](int j, CombStage& cs) {
     const int buf = j & 1;
@@ -1316,7 +1396,7 @@ __global__ __launch_bounds__(64 * kCombWaves) void seg_combine_kernel(Params p) 
       acc = mfma_bf16(cs.ma[kb][1], bh, acc);
     }
     S = acc;
-    *reinterpret_cast<f32x4*>(p.seg_S + (static_cast<size_t>(j + 1) * p.HV + hv) * blk + tile) = S;
+    *reinterpret_cast<f32x4*>(const_cast<float*>(seg_blk(p.seg_S, j + 1)) + tile) = S;
     load(j + 3, cs);                          // this set's next use: three steps on
   };
   CombStage s0, s1, s2;
@@ -1349,55 +1429,77 @@ size_t slots_bytes(long long L, long long N, long long HV) {
   return align256(static_cast<size_t>(max_slots(L, N)) * HV * kSlotFloats * sizeof(float));
 }
 
-// Segments of one long sequence.  Its plain scan is a chain of chunk steps on
-// HV workgroups; with few v-heads that leaves most of the GPU idle (16384
-// tokens at 8 v-heads: 256 steps on 8 CUs), so the sequence is cut into
-// nseg segments of len chunks scanned at once: the first launch runs
-// (2 nseg - 3) HV workgroups and the second nseg HV, one per CU, each of len
-// chunk steps, and the combine nseg - 2 small steps.  The length is the one
+// Segments.  A sequence's plain scan is a chain of chunk steps on HV
+// workgroups; with few sequences and v-heads that leaves most of the GPU idle
+// (16384 tokens at 8 v-heads: 256 steps on 8 CUs), so each sequence is cut
+// into segments of len chunks scanned at once: the first launch runs 2 nseg
+// - 3 units of a sequence of nseg segments (HV workgroups each), the second
+// nseg, one workgroup per CU, each of len chunk steps, and the combine nseg -
+// 2 small steps.  The host knows only the total tokens and the sequence
+// count, so it plans for sequences of the mean length: the length is the one
 // that minimises the estimated critical path, (rounds of the first launch +
-// rounds of the second) x len chunk steps + (nseg - 2) combine steps, with a
-// round of kCUs workgroups and a chunk step costing kStepPerCombine combine
-// steps (measured: ~5.4 us against ~1 us).
-constexpr int kSegMinChunks = 48;      // shorter sequences are scanned whole
-constexpr long long kSegMaxHV = 32;    // more v-heads fill the GPU without segments
-constexpr long long kSegMinLen = 4;
+// rounds of the second) x len chunk steps + (nseg - 2) combine steps + the
+// two more launches, with a round of kCUs workgroups and a chunk step
+// costing kStepPerCombine combine steps (measured: ~5.4 us against ~1 us);
+// the batch is cut when that beats its plain scan, (rounds of N HV
+// workgroups) x chunks x kStepPerCombine: from 6 chunks a sequence at N HV
+// = 8 (one 2048-token sequence at qk4_v8: 195 -> ~66 us).  The kernels count
+// each sequence's segments from cu_seqlens (so sequences shorter or longer
+// than the mean get as many as they need), in one wave: at most kFewSeqs
+// sequences.
+constexpr long long kSegMaxHeads = 256;  // N HV workgroups that fill the GPU unsegmented
+constexpr long long kSegMinLen = 2;
 constexpr long long kCUs = 256;
 constexpr long long kStepPerCombine = 5;
+constexpr long long kSegLaunches = 8;    // the segment path's two more launches
 
-bool use_segments(long long L, long long N, long long HV) {
-  return N == 1 && HV <= kSegMaxHV && (L + kChunk - 1) / kChunk >= kSegMinChunks;
-}
+struct SegPlan {
+  long long len;    // chunks a segment (the mean sequence if not cut)
+  long long cost;   // estimated critical path, combine steps; -1: cannot be cut
+};
 
-long long seg_chunks(long long L, long long HV) {
-  const long long chunks = (L + kChunk - 1) / kChunk;
-  long long best_len = chunks, best = -1;
+SegPlan seg_plan(long long L, long long N, long long HV) {
+  const long long chunks = ((L + kChunk - 1) / kChunk + N - 1) / N;   // a sequence, mean
+  SegPlan best{chunks, -1};
   for (long long len = kSegMinLen; 3 * len <= chunks; ++len) {
     const long long n = (chunks + len - 1) / len;
-    const long long rounds = ((2 * n - 3) * HV + kCUs - 1) / kCUs + (n * HV + kCUs - 1) / kCUs;
-    const long long cost = rounds * len * kStepPerCombine + (n - 2);
-    if (best < 0 || cost < best) {
-      best = cost;
-      best_len = len;
-    }
+    const long long rounds =
+        (N * (2 * n - 3) * HV + kCUs - 1) / kCUs + (N * n * HV + kCUs - 1) / kCUs;
+    const long long cost = rounds * len * kStepPerCombine + (n - 2) + kSegLaunches;
+    if (best.cost < 0 || cost < best.cost) best = SegPlan{len, cost};
   }
-  return best_len;
+  return best;
 }
 
-long long num_segments(long long L, long long HV) {
-  const long long len = seg_chunks(L, HV);
-  return ((L + kChunk - 1) / kChunk + len - 1) / len;
+bool use_segments(long long L, long long N, long long HV) {
+  if (N < 1 || N > kFewSeqs || N * HV > kSegMaxHeads) return false;
+  const SegPlan plan = seg_plan(L, N, HV);
+  const long long chunks = ((L + kChunk - 1) / kChunk + N - 1) / N;
+  const long long whole = (N * HV + kCUs - 1) / kCUs * chunks * kStepPerCombine;
+  return plan.cost >= 0 && plan.cost < whole;
+}
+
+long long seg_chunks(long long L, long long N, long long HV) { return seg_plan(L, N, HV).len; }
+
+// Segments the workspace holds: one sequence's exactly; for several, the most
+// a well-formed batch can have, sum(ceil(chunks_i / len)) <= (chunks + N
+// (len - 1)) / len with chunks <= max_slots.  The kernels skip the segments of
+// a (malformed) batch past this count.
+long long num_segments(long long L, long long N, long long HV) {
+  const long long len = seg_chunks(L, N, HV);
+  if (N == 1) return ((L + kChunk - 1) / kChunk + len - 1) / len;
+  return (max_slots(L, N) + N * (len - 1)) / len;
 }
 
 // Per segment and v-head one 128 x 128 fp32 block (S, B and M each).
-size_t seg_blocks_bytes(long long L, long long HV) {
-  return align256(static_cast<size_t>(num_segments(L, HV)) * HV * kDim * kDim * sizeof(float));
+size_t seg_blocks_bytes(long long L, long long N, long long HV) {
+  return align256(static_cast<size_t>(num_segments(L, N, HV)) * HV * kDim * kDim * sizeof(float));
 }
 
 size_t workspace_bytes(long long L, long long N, long long H, long long HV) {
   (void)H;
   size_t bytes = offsets_bytes(N) + slot_info_bytes(L, N) + slots_bytes(L, N, HV);
-  if (use_segments(L, N, HV)) bytes += 3 * seg_blocks_bytes(L, HV);
+  if (use_segments(L, N, HV)) bytes += 3 * seg_blocks_bytes(L, N, HV);
   return bytes;
 }
 
@@ -1550,9 +1652,9 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
   p.seg_S = p.seg_B = p.seg_M = nullptr;
   if (use_segments(total_seq_len, num_seqs, HV)) {
     char* sg = reinterpret_cast<char*>(p.slots) + slots_bytes(total_seq_len, num_seqs, HV);
-    const size_t blocks = seg_blocks_bytes(total_seq_len, HV);
-    p.seg_chunks = static_cast<int>(seg_chunks(total_seq_len, HV));
-    p.nseg = static_cast<int>(num_segments(total_seq_len, HV));
+    const size_t blocks = seg_blocks_bytes(total_seq_len, num_seqs, HV);
+    p.seg_chunks = static_cast<int>(seg_chunks(total_seq_len, num_seqs, HV));
+    p.nseg = static_cast<int>(num_segments(total_seq_len, num_seqs, HV));
     p.seg_S = reinterpret_cast<float*>(sg);
     p.seg_B = reinterpret_cast<float*>(sg + blocks);
     p.seg_M = reinterpret_cast<float*>(sg + 2 * blocks);
@@ -1607,21 +1709,25 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
   auto scan_grid = [&](long long units) {
     return dim3(static_cast<unsigned>((units * H + 7) / 8 * 8 * p.ratio));
   };
-  if (p.nseg > 1) {
-    // segments (one sequence): transitions and zero-start ends, the starts,
-    // then every segment with its outputs
-    hipLaunchKernelGGL((scan_kernel<false, true, false, false>), scan_grid(2LL * p.nseg - 3),
-                       dim3(kScanThreads), 0, stream, p);
+  if (p.seg_chunks > 0) {
+    // segments: transitions and zero-start ends, the starts, then every
+    // segment with its outputs (grids: the workspace's segments bound the
+    // batch's units; workgroups past them exit)
+    auto* scan1 = p.few ? scan_kernel<true, true, false, false>
+                        : scan_kernel<false, true, false, false>;
+    hipLaunchKernelGGL(scan1, scan_grid(seg_units1(p.nseg, num_seqs)), dim3(kScanThreads), 0,
+                       stream, p);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    if (p.nseg > 2) {
-      hipLaunchKernelGGL(seg_combine_kernel, dim3(static_cast<unsigned>((HV + 7) & ~7) * 8),
-                         dim3(64 * kCombWaves), 0, stream, p);
-      e = hipGetLastError();
-      if (e != hipSuccess) return e;
-    }
-    auto* scan = p.l2norm ? scan_kernel<false, true, true, true>
-                          : scan_kernel<false, true, true, false>;
+    hipLaunchKernelGGL(seg_combine_kernel,
+                       dim3(static_cast<unsigned>(num_seqs * ((HV + 7) & ~7) * 8)),
+                       dim3(64 * kCombWaves), 0, stream, p);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    auto* scan = p.few ? (p.l2norm ? scan_kernel<true, true, true, true>
+                                   : scan_kernel<true, true, true, false>)
+                       : (p.l2norm ? scan_kernel<false, true, true, true>
+                                   : scan_kernel<false, true, true, false>);
     hipLaunchKernelGGL(scan, scan_grid(p.nseg), dim3(kScanThreads), 0, stream, p);
   } else {
     auto* scan = p.few ? (p.l2norm ? scan_kernel<true, false, true, true>
@@ -1682,9 +1788,9 @@ int gdn_prefill_token_path_max_tokens(void) { return kSmallTokens; }
 int gdn_prefill_dispatches(int total_seq_len, int num_seqs, int HV) {
   if (num_seqs <= 0 || total_seq_len < 0 || HV <= 0) return 0;
   if (total_seq_len <= kSmallTokens && num_seqs <= 65535) return 1;
-  if (use_segments(total_seq_len, num_seqs, HV))
-    return num_segments(total_seq_len, HV) > 2 ? 4 : 3;
-  return num_seqs == 1 || few_seqs(total_seq_len, num_seqs, HV) ? 2 : 3;
+  const int offsets = num_seqs == 1 || few_seqs(total_seq_len, num_seqs, HV) ? 0 : 1;
+  if (use_segments(total_seq_len, num_seqs, HV)) return offsets + 4;
+  return offsets + 2;
 }
 
 int gdn_prefill_abi_version(void) { return 6; }

@@ -47,11 +47,13 @@ extern "C" {
  * sequences, H q/k heads and HV v-heads: per-chunk intermediates (14 KiB
  * per chunk per v-head, for min(ceil(L / 64) + N, L) chunks, the most a
  * well-formed batch has, rounded up to 256 bytes), a 16-byte table entry per
- * chunk and 4 bytes per sequence, each part rounded up to 256 bytes; for one
- * sequence of C >= 48 chunks at HV <= 32 (scanned in segments of at least
- * 4 chunks, the length that minimises the estimated critical path of the
- * two segment scans and the combine), also 3 x 64 KiB per segment per
- * v-head.
+ * chunk and 4 bytes per sequence, each part rounded up to 256 bytes; for a
+ * batch scanned in segments (at most 64 sequences, N x HV <= 256, sequences
+ * of the mean length long enough that segments of 2 or more chunks, the
+ * length minimising the estimated critical path of the two segment scans
+ * and the combine, beat the plain scan), also 3 x 64 KiB per segment per
+ * v-head: one sequence's ceil(ceil(L / 64) / len) segments, several
+ * sequences' (min(ceil(L / 64) + N, L) + N (len - 1)) / len.
  * 0 for invalid sizes.
  * The reference's FLA path allocates its intermediates per call inside
  * chunk_gated_delta_rule (solution/triton/fla_prefill_code.py:1726-1776);
@@ -72,10 +74,10 @@ size_t gdn_prefill_workspace_bytes(int total_seq_len, int num_seqs, int H, int H
  * q, k, v, output, state and new_state must be 16-byte aligned.
  * Launches one kernel when total_seq_len <= gdn_prefill_token_path_max_tokens()
  * (and num_seqs <= 65535), else the chunkwise kernels: the chunk-offsets
- * scan (only when gdn_prefill_dispatches returns 3), preparation, scan (for
- * one long sequence with few v-heads: segments of it scanned at once in two
- * launches with the combination of their starts between them, see
- * gdn_prefill_dispatches).
+ * scan (only when gdn_prefill_dispatches returns 3 or 5), preparation, scan
+ * (for a few sequences whose scans would leave most CUs idle: their
+ * segments scanned at once in two launches with the combination of their
+ * starts between them, see gdn_prefill_dispatches).
  */
 int gdn_prefill(const void* q, const void* k, const void* v, const float* state,
                 const float* A_log, const void* a, const float* dt_bias, const void* b,
@@ -139,8 +141,8 @@ int gdn_prefill_token_path_max_tokens(void);
 /*
  * Kernel launches gdn_prefill makes for these sizes: 0 for no sequences, 1
  * on the token-by-token path, 4 (preparation, first segment scan, combine,
- * second segment scan) for one sequence of at least 48 chunks at HV <= 32
- * (3, without the combine, for two segments), 2
+ * second segment scan) for a batch scanned in segments (5 with the
+ * chunk-offsets scan first, as below), 2
  * (preparation, scan) for another single sequence or for
  * at most 64 with at most 2048 preparation workgroups (min(ceil(L / 64) + N,
  * L) x HV; the kernels then find the chunk slots from cu_seqlens

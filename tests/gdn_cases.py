@@ -85,3 +85,29 @@ def assert_state_close(st, ref, *, what="new_state"):
     rel = (diff.norm() / ref.norm().clamp_min(1e-30)).item()
     assert rel <= 1e-3, f"{what}: relative Frobenius error {rel:.3e} > 1e-3"
     return rel
+
+
+def prefill_segment_plan(L: int, N: int, HV: int):
+    """The prefill library's segment plan, restated for the workspace-size and
+    dispatch-count checks: (segmented, chunks a segment, segments the
+    workspace holds).  Sequences of the mean length are cut into segments of
+    the length (2 chunks or more, 3 segments or more) minimising (rounds of
+    256 workgroups) x length x 5 + combine steps + 8, when that is below the
+    plain scan's (rounds of N HV workgroups) x chunks x 5; at most 64
+    sequences and N HV <= 256."""
+    if N < 1 or N > 64 or N * HV > 256:
+        return False, 0, 0
+    nch = ((L + 63) // 64 + N - 1) // N
+
+    def cost(n_len):
+        n = -(-nch // n_len)
+        rounds = -(-N * (2 * n - 3) * HV // 256) + -(-N * n * HV // 256)
+        return rounds * n_len * 5 + (n - 2) + 8
+    lens = range(2, nch // 3 + 1)
+    if len(lens) == 0 or min(map(cost, lens)) >= -(-N * HV // 256) * nch * 5:
+        return False, 0, 0
+    seg_len = min(lens, key=cost)
+    if N == 1:
+        return True, seg_len, -(-((L + 63) // 64) // seg_len)
+    max_slots = min((L + 63) // 64 + N, L)
+    return True, seg_len, (max_slots + N * (seg_len - 1)) // seg_len

@@ -123,22 +123,49 @@ def test_bench_size_prefills_match_the_fp64_oracle(lens, H, HV, a_log_range, l2,
 
 
 @pytest.mark.parametrize("lens,H,HV,l2,with_state", [
-    ([3072], 4, 8, False, True),      # 48 chunks: 3 segments of 16, the fewest segmented
+    ([3072], 4, 8, False, True),      # 48 chunks
     ([5000], 4, 16, False, True),     # 79 chunks: a partial last chunk and last segment
     ([4100], 1, 1, False, True),      # 65 chunks: a one-chunk last segment, one head
     ([3500], 2, 4, True, False),      # L2-norm, no initial state (segment 0 from zeros)
     ([3100], 2, 6, False, True),      # GVA ratio 3
+    ([384], 4, 8, False, True),       # 6 chunks: 3 segments of 2, the fewest segmented
+    ([1000], 4, 8, True, True),       # 16 chunks, the last one partial, L2-norm
+    ([2048], 4, 8, False, False),     # 32 chunks, no initial state
+    ([1100], 16, 32, False, True),    # 18 chunks at 32 v-heads
 ])
 def test_segmented_long_sequence(lens, H, HV, l2, with_state, hip_device):
-    """One sequence of >= 48 chunks at <= 16 v-heads runs in segments of 16
-    chunks scanned at once (each from a zero start, with its 128 x 128
-    transition), combined, and the outputs of later segments corrected for
-    their true start: against the float64 chunked oracle at the prefill
-    bars."""
+    """One sequence at <= 32 v-heads whose plain scan would leave most CUs
+    idle runs in segments of a few chunks scanned at once (each from a zero
+    start, with its 128 x 128 transition), combined, and the segments'
+    outputs recomputed from their true starts: against the float64 chunked
+    oracle at the prefill bars."""
     L = sum(lens)
     assert gdn.prefill.prefill_dispatches(L, 1, HV) == 4
     _announce(f"segmented prefill L={L} H={H} HV={HV} l2={l2} state={with_state}")
     t = make_prefill_inputs(lens, H, HV, seed=400 + L + HV, with_state=with_state,
+                            unit_qk=not l2)
+    out, st = gdn.prefill_run(**_dev(t, hip_device), use_qk_l2norm=l2)
+    torch.cuda.synchronize()
+    do, ds = _check(t, out, st, l2=l2, loop=False)
+    _announce(f"  max |out - fp64| {do:.3e}, max |state - fp64| {ds:.3e}")
+
+
+@pytest.mark.parametrize("lens,H,HV,l2,with_state", [
+    ([1000, 2000, 600], 4, 8, False, True),            # slots found in the kernels
+    ([5000, 4100, 6000, 3900, 5200, 4800, 5500, 4903], 4, 8, False, True),  # offsets kernel
+    ([1500, 0, 700, 3000], 4, 8, True, False),         # an empty sequence, L2-norm, no state
+    ([3000, 2000], 16, 32, False, True),               # 64 v-heads of work
+    ([900, 20, 1300], 2, 2, False, True),              # a one-segment sequence among them
+])
+def test_segmented_sequences(lens, H, HV, l2, with_state, hip_device):
+    """A few sequences whose plain scans would leave most CUs idle: each is
+    cut into as many segments as its length needs (the plan is made for the
+    mean length; the kernels count each sequence's own), against the float64
+    chunked oracle at the prefill bars."""
+    L, N = sum(lens), len(lens)
+    assert gdn.prefill.prefill_dispatches(L, N, HV) >= 4
+    _announce(f"segmented prefill lens={lens} H={H} HV={HV} l2={l2} state={with_state}")
+    t = make_prefill_inputs(lens, H, HV, seed=450 + L + HV, with_state=with_state,
                             unit_qk=not l2)
     out, st = gdn.prefill_run(**_dev(t, hip_device), use_qk_l2norm=l2)
     torch.cuda.synchronize()

@@ -161,14 +161,16 @@ def test_prefill_mix():
     assert max(max(w.lens) for w in ws) == 16384   # longest single sequence
     assert [w.dispatches for w in ws[:3]] == [1, 1, 2]   # 6 and 1 tokens: the token path
     from flashinfer_competition_codebase_amd.prefill import token_path_max_tokens
+    from tests.gdn_cases import prefill_segment_plan
     small = token_path_max_tokens()
     def expected(w):
         slots = min((w.L + 63) // 64 + w.N, w.L)
         if w.L <= small:
             return 1                                  # the token path
-        if w.N == 1 and w.HV <= 32 and (w.L + 63) // 64 >= 48:
-            return 4                                  # one long sequence: segments
-        return 2 if w.N == 1 or (w.N <= 64 and slots * w.HV <= 2048) else 3
+        offsets = 0 if w.N == 1 or (w.N <= 64 and slots * w.HV <= 2048) else 1
+        if prefill_segment_plan(w.L, w.N, w.HV)[0]:
+            return offsets + 4                        # segments
+        return offsets + 2
 
     assert all(w.dispatches == expected(w) for w in ws)
     assert harness.prefill_workloads() == ws         # seeded: the same mix every time
@@ -282,9 +284,11 @@ def test_prefill_dispatch_count_follows_the_token_path_threshold():
     assert prefill_dispatches(m + 1, 1, 8) == 2 and prefill_dispatches(m + 1, 2, 8) == 2
     assert prefill_dispatches(m + 1, 64, 8) == 2          # slots found in the kernels
     assert prefill_dispatches(m + 1, 65, 8) == 3          # the chunk-offsets scan first
-    assert prefill_dispatches(8192, 8, 8) == 2            # (128 + 8) x 8 = 1088 workgroups
-    assert prefill_dispatches(8192, 16, 32) == 3          # (128 + 16) x 32 = 4608
-    assert prefill_dispatches(16384, 1, 64) == 2          # one sequence: never offsets
+    assert prefill_dispatches(640, 8, 8) == 2             # 10 chunks + 8: slots in the kernels
+    assert prefill_dispatches(8192, 8, 8) == 4            # 8 x 16 chunks at 8 v-heads: segments
+    assert prefill_dispatches(8192, 16, 32) == 3          # (128 + 16) x 32 = 4608, 512 heads
+    assert prefill_dispatches(16384, 1, 128) == 2         # one sequence: never offsets
     assert prefill_dispatches(16384, 1, 32) == 4          # ... cut into segments
+    assert prefill_dispatches(39503, 8, 8) == 5           # offsets, then segments
     assert prefill_dispatches(m, 70_000, 8) == 3         # past the grid's z limit
     assert prefill_dispatches(100, 0, 8) == 0

@@ -12,6 +12,7 @@ import pytest
 import torch
 
 import flashinfer_competition_codebase_amd as gdn
+from tests.gdn_cases import prefill_segment_plan
 from flashinfer_competition_codebase_amd import _lib
 from flashinfer_competition_codebase_amd.prefill import check_prefill_inputs
 from oracle.gdn_prefill_oracle import make_prefill_inputs
@@ -47,29 +48,24 @@ def test_workspace_size_formula():
     for L, N, H, HV in ((6, 1, 4, 8), (16384, 1, 4, 8), (1000, 37, 16, 32), (0, 3, 4, 8),
                         (100, 2, 2, 2), (40, 65600, 1, 1), (3, 10, 4, 8), (3000, 1, 4, 8),
                         (3072, 1, 4, 8), (5000, 1, 16, 16), (8192, 1, 16, 32),
-                        (8192, 1, 16, 64), (2048, 1, 4, 8)):
+                        (8192, 1, 16, 64), (2048, 1, 4, 8), (384, 1, 4, 8), (320, 1, 4, 8),
+                        (1024, 1, 16, 32), (4096, 1, 16, 32), (700, 1, 2, 2),
+                        (39503, 8, 4, 8), (3600, 3, 4, 8), (5000, 2, 16, 32), (8192, 8, 16, 32),
+                        (20000, 64, 1, 2), (3000, 65, 1, 1)):
         chunks = min((L + 63) // 64 + N, L)          # the most a well-formed batch has
         offs = a256((N + 1) * 4)
         table = a256(chunks * 16)                                        # per-chunk slot table
         want = offs + table + a256(chunks * HV * vslot)
-        # one sequence of >= 48 chunks at <= 32 v-heads: segments of the length
-        # that minimises (rounds of 256 workgroups) x length x 5 + combine steps
-        nch = (L + 63) // 64
-        seg = N == 1 and HV <= 32 and nch >= 48
-
-        def cost(n_len):
-            n = -(-nch // n_len)
-            rounds = -(-(2 * n - 3) * HV // 256) + -(-n * HV // 256)
-            return rounds * n_len * 5 + (n - 2)
-        seg_len = min(range(4, nch // 3 + 1), key=cost) if seg else max(nch, 1)
-        nseg = -(-nch // seg_len)
+        # segments (at most 64 sequences, N HV <= 256): S, B and M blocks for
+        # the segments the workspace holds
+        seg, _, nseg = prefill_segment_plan(L, N, HV)
         if seg:
             want += 3 * a256(nseg * HV * 128 * 128 * 4)
         assert lib.gdn_prefill_workspace_bytes(L, N, H, HV) == want, (L, N, H, HV)
+        offsets = 0 if N == 1 or (N <= 64 and chunks * HV <= 2048) else 1
         assert lib.gdn_prefill_dispatches(L, N, HV) == (
             0 if N == 0 else 1 if L <= 48 and N <= 65535 else
-            (4 if nseg > 2 else 3) if seg else
-            2 if N == 1 or (N <= 64 and chunks * HV <= 2048) else 3), (L, N, HV)
+            offsets + (4 if seg else 2)), (L, N, HV)
     assert lib.gdn_prefill_workspace_bytes(-1, 1, 4, 8) == 0
     assert lib.gdn_prefill_workspace_bytes(1, 1, 4, 0) == 0
     assert lib.gdn_prefill_workspace_bytes(1, 1, 3, 8) == 0              # HV % H != 0
