@@ -425,13 +425,22 @@ def host_threads() -> dict:
 
 
 def _cpu_model() -> str:
+    """The host CPU's model name with its family, model and stepping numbers
+    (a virtualised host may report a generic name such as "AMD EPYC")."""
+    fields = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            key, _, val = line.partition(":")
+            key = key.strip()
+            if key in ("model name", "cpu family", "model", "stepping") and key not in fields:
+                fields[key] = val.strip()
+            if not line.strip() and fields:
+                break                                   # the first processor's entry
     except OSError:
         pass
-    return "unknown"
+    name = fields.get("model name", "unknown")
+    ids = ", ".join(f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping") if k in fields)
+    return f"{name} ({ids})" if ids else name
 
 
 def decode_kernel_name(ns: int, waves: int, l2: bool, policy: int, bf16: bool = False,
