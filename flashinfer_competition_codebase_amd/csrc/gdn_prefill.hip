@@ -339,6 +339,15 @@ __device__ __forceinline__ SegSeqs seg_seqs(const Params& p) {
   f.seg_excl = xs - f.nseg;
   f.u_excl = xu - units;
   f.u_incl = xu;
+  // A malformed batch (overlapping ranges) may need more segments than the
+  // workspace holds: then every sequence is one segment (a plain scan in the
+  // second launch), so each one's state is still written.
+  if (__builtin_amdgcn_readlane(xs, 63) > p.nseg) {
+    f.nseg = lane < p.N ? 1 : 0;
+    f.seg_excl = lane;
+    f.u_excl = OUT ? lane : 0;
+    f.u_incl = OUT && lane < p.N ? lane + 1 : f.u_excl;
+  }
   return f;
 }
 
@@ -1234,7 +1243,9 @@ void scan_kernel(Params p) {
     seq_slots(s, base, count);
     const int first = j * p.seg_chunks;
     slot0 = base + first;
-    nchunks = min(p.seg_chunks, count - first);
+    // the last segment takes the rest (at most seg_chunks, but the whole
+    // sequence when a malformed batch runs every sequence as one segment)
+    nchunks = j == nseg - 1 ? count - first : min(p.seg_chunks, count - first);
     start = min(end, start + first * kChunk);
     if (nchunks > 0) end = min(end, start + nchunks * kChunk);
   } else {

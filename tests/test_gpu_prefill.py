@@ -361,6 +361,32 @@ def test_malformed_cu_seqlens_stay_in_bounds(cu, L, hip_device):
     assert torch.equal(st[:1], st1)
 
 
+def test_malformed_cu_seqlens_on_the_segment_path(hip_device):
+    """Overlapping ranges on the segmented path (5 sequences at 8 v-heads):
+    the ranges need more segments than the workspace holds for 3000 tokens,
+    so every sequence is scanned as one segment; the call completes, every
+    state is finite, and the first sequence (a well-formed range) ends in the
+    float64 oracle's state of it alone (its output rows are shared with the
+    overlapping third range, which writes them too)."""
+    cu, L = [0, 1500, 200, 2600, 5000, 3000], 3000
+    N = len(cu) - 1
+    assert gdn.prefill.prefill_dispatches(L, N, 8) >= 4
+    _announce(f"malformed cu_seqlens on the segment path N={N} L={L}")
+    t = make_prefill_inputs([L] + [0] * (N - 1), 4, 8, seed=92)
+    t["cu_seqlens"] = torch.tensor(cu, dtype=torch.int32)
+    out, st = gdn.prefill_run(**_dev(t, hip_device))
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out.float()).all()) and bool(torch.isfinite(st).all())
+    n0 = cu[1]
+    alone = {**t, "q": t["q"][:n0], "k": t["k"][:n0], "v": t["v"][:n0], "a": t["a"][:n0],
+             "b": t["b"][:n0], "state": t["state"][:1],
+             "cu_seqlens": torch.tensor([0, n0], dtype=torch.int32)}
+    _, s64 = prefill_chunked_fp64(**alone)
+    sd = st[:1].cpu().double().numpy()
+    ds = np.abs(sd - s64)
+    assert np.all(ds <= 1e-3 * np.abs(s64) + 1e-5), f"state vs fp64: max {ds.max():.3e}"
+
+
 def test_timed_entry_matches_and_times_each_kernel(hip_device):
     """gdn_prefill_timed: the same results as gdn_prefill, and its four events
     bracket the three launches (each interval non-negative, the scan's
