@@ -19,7 +19,7 @@
 // Every exponent is <= 0.  With the q/k L2-norm on, the row norms enter as
 // per-row scale factors of the same products.
 //
-// Prefills of at most kSmallTokens (48) tokens in all (so every sequence is
+// Prefills of at most kSmallTokens (56) tokens in all (so every sequence is
 // that short) skip the chunkwise machinery: one launch of the decode kernel's
 // variable-length mode (gdn_decode_kernel.h) applies the recurrence token by
 // token with the state in registers, one workgroup per (sequence, v-head,
@@ -109,14 +109,13 @@ bool few_seqs(long long L, long long N, long long HV) {
   return N > 1 && N <= kFewSeqs && max_slots(L, N) * HV <= kFewPrepGroups;
 }
 // Total tokens up to which the token-by-token kernel runs the prefill (so no
-// sequence is longer).  Measured (kernel trace, one sequence): the token loop
-// costs ~3.5 us plus ~0.25 us a token, the chunkwise kernels ~15-17 us up to
-// 128 tokens at qk4_v8 (16-23 us at qk16_v32); they cross at 45-48 tokens
-// (48: 15.1 against 15.4 us at qk4_v8, 17.1 against 16.5 us at qk16_v32).
-// Several short sequences favour the token path far more (4 x 12 tokens: 6.8
-// against 24.5 us), but past the switch the longest sequence is not known on
-// the host.
-constexpr int kSmallTokens = 48;
+// sequence is longer).  Measured (one sequence, calls timed from the first to
+// the last event of the timed entry): the token path is 1-3.5 us faster up to
+// 56 tokens at qk4_v8 and qk16_v32, the chunkwise kernels faster from 64.
+// Several short sequences favour the token path far more (4 x 20 tokens: 21.2
+// against 33.5 us at qk4_v8), but past the switch the longest sequence is not
+// known on the host.
+constexpr int kSmallTokens = 56;
 constexpr float kL2Eps = 1e-6f;
 constexpr float kSoftplusThreshold = 20.0f;
 constexpr float kLn2 = 0.693147180559945309f;

@@ -51,7 +51,7 @@ Command line (arguments as scripts/shared.py:93-142):
 
 In the trace tier a prefill call is its chunk-offsets (several sequences),
 preparation and scan dispatches -- or its one dispatch of the token-by-token
-kernel for a prefill of at most 48 tokens -- timed from the first one's
+kernel for a prefill of at most 56 tokens -- timed from the first one's
 start to the last one's end.
 """
 

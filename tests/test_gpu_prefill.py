@@ -338,14 +338,16 @@ def test_many_empty_sequences_past_the_token_paths_grid(hip_device):
 
 @pytest.mark.parametrize("cu,L", [
     ([0, 30, 5, 40, 100], 40),         # decreasing and past L; 40 tokens: the token path
-    ([0, 50, 10, 60, 200, 30], 60),    # the same at 60 tokens: chunkwise, slots in the kernels
-    ([0, 50] + [10, 60, 200, 30] * 20, 60),   # 81 sequences: the chunk-offsets scan
+    ([0, 58, 10, 60, 200, 30], 60),    # the same at 60 tokens: chunkwise, slots in the kernels
+    ([0, 58] + [10, 60, 200, 30] * 20, 60),   # 81 sequences: the chunk-offsets scan
 ])
 def test_malformed_cu_seqlens_stay_in_bounds(cu, L, hip_device):
     """cu_seqlens that decrease or pass L: every kernel clamps each range to
     [0, L] (and to start <= end), so the call completes with finite results;
     the first sequence, a well-formed range, gets the state that a call with
-    it alone gives (bitwise: the same arithmetic on every path)."""
+    it alone gives (bitwise: the same arithmetic on every path; past 40 tokens
+    the first sequence is longer than the token-path switch, so that alone it
+    runs chunkwise too)."""
     N = len(cu) - 1
     _announce(f"malformed cu_seqlens N={N} L={L}")
     t = make_prefill_inputs([L] + [0] * (N - 1), 4, 8, seed=91)
@@ -490,10 +492,11 @@ def test_split_sequences_compose_at_full_size(lens, H, HV, cut, hip_device):
     assert rel <= 1e-4, rel
 
 
-# --- prefills of at most 48 tokens: the decode kernel's variable-length mode ----
+# --- prefills of at most 56 tokens: the decode kernel's variable-length mode ----
 
 @pytest.mark.parametrize("seqlens,H,HV,l2,with_state", [
-    ([48], 4, 8, False, True),            # the largest token-by-token prefill
+    ([56], 4, 8, False, True),            # the largest token-by-token prefill
+    ([48], 4, 8, False, True),
     ([16], 4, 8, False, True),
     ([47, 1], 16, 32, True, True),        # 47 tokens: not a multiple of the 3-token loop body
     ([12] * 4, 4, 8, False, True),

@@ -3,7 +3,7 @@ the oracle, across the options the named tests take one at a time: batch,
 tokens per sequence, q/k heads and GVA ratio, fp32 / bf16 / no initial
 state, the q/k L2-norm, the entry form (DPS in place, DPS out of place,
 value-returning), the scale's forms and, for the prefill, ragged sequence
-lengths with empty sequences on either side of the 48-token path switch.
+lengths with empty sequences on either side of the 56-token path switch.
 
 Bars are those of the named tests (tests/gdn_cases.py, test_gpu_tokens.py,
 test_gpu_prefill.py): outputs within 1e-2 atol/rtol of the oracle's bf16
@@ -146,15 +146,15 @@ def _prefill_cases(n=24, seed=77001):
     cases = []
     for i in range(n):
         N = rng.randint(1, 12)
-        small = rng.random() < 0.3                    # total <= 48: the token path
+        small = rng.random() < 0.3                    # total <= 56: the token path
         if small:
             lens = [rng.randint(0, 12) for _ in range(N)]
-            while sum(lens) > 48:
+            while sum(lens) > 56:
                 lens[rng.randrange(N)] = 0
         else:
             lens = [rng.choice([0, rng.randint(1, 20), rng.randint(20, 140)]) for _ in range(N)]
-            if sum(lens) <= 48:
-                lens[0] += 49
+            if sum(lens) <= 56:
+                lens[0] += 57
         H = rng.choice([1, 2, 4, 8])
         cases.append(dict(i=i, lens=lens, H=H, HV=H * rng.choice([1, 2, 4]),
                           l2=rng.random() < 0.4, with_state=rng.random() < 0.8,

@@ -64,7 +64,7 @@ def test_workspace_size_formula():
         assert lib.gdn_prefill_workspace_bytes(L, N, H, HV) == want, (L, N, H, HV)
         offsets = 0 if N == 1 or (N <= 64 and chunks * HV <= 2048) else 1
         assert lib.gdn_prefill_dispatches(L, N, HV) == (
-            0 if N == 0 else 1 if L <= 48 and N <= 65535 else
+            0 if N == 0 else 1 if L <= 56 and N <= 65535 else
             offsets + (4 if seg else 2)), (L, N, HV)
     assert lib.gdn_prefill_workspace_bytes(-1, 1, 4, 8) == 0
     assert lib.gdn_prefill_workspace_bytes(1, 1, 4, 0) == 0
