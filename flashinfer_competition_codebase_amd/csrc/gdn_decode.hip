@@ -614,6 +614,11 @@ int gdn_decode_graph_create(const gdn_decode_plan* const* plans, int n,
     }
   }
   const hipError_t d = hipStreamDestroy(s);
+  if (e == hipSuccess && d != hipSuccess) {
+    // a nonzero return never leaves a handle behind: the caller stores none
+    gdn_decode_graph_destroy(*graph);
+    *graph = nullptr;
+  }
   return e != hipSuccess ? e : d;
 }
 

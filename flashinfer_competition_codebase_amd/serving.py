@@ -116,8 +116,16 @@ class DecodeLayers:
     def __len__(self) -> int:
         return len(self.plans)
 
+    def _check_open(self) -> None:
+        # the native calls take the plans' raw pointers: never pass freed ones
+        if self._handles is None:
+            raise RuntimeError("the layers were closed")
+        if any(p._handle is None for p in self.plans):
+            raise RuntimeError("a layer's plan was closed")
+
     def run(self) -> None:
         """Every layer's step, in order, from one native call (no graph)."""
+        self._check_open()
         with _on_device(self.device):
             code = self._lib.gdn_decode_plan_run(self._handles, len(self.plans),
                                                  _lib.current_stream(self.device))
@@ -127,6 +135,7 @@ class DecodeLayers:
     def capture(self) -> None:
         """Record every layer's step, in order, in one HIP graph (replaces a
         previous one)."""
+        self._check_open()
         self.release_graph()
         graph = ctypes.c_void_p()
         with _on_device(self.device):
@@ -137,6 +146,7 @@ class DecodeLayers:
 
     def replay(self) -> None:
         """All layers' steps as one graph submission on torch's current stream."""
+        self._check_open()
         if self._graph is None:
             raise RuntimeError("capture() the graph before replaying it")
         with _on_device(self.device):
@@ -154,6 +164,7 @@ class DecodeLayers:
         self.release_graph()
         for p in self.plans:
             p.close()
+        self._handles = None
 
     def __del__(self):
         try:

@@ -202,3 +202,54 @@ def torch_empty_out(t):
 
     B, T, HV = t["v"].shape[0], t["v"].shape[1], t["v"].shape[2]
     return torch.empty(B, T, HV, 128, dtype=torch.bfloat16)
+
+
+def test_decode_layers_refuse_to_run_after_close():
+    """DecodeLayers passes its plans' raw pointers to the native calls: once
+    it or one of its plans is closed, run/capture/replay raise instead (no
+    freed plan pointer reaches the library).  Host logic only: a stub stands
+    in for the library and the plans."""
+    import ctypes as ct
+
+    from flashinfer_competition_codebase_amd.serving import DecodeLayers
+
+    calls = []
+
+    class StubLib:
+        def gdn_decode_plan_run(self, *a):
+            calls.append("run")
+            return 0
+
+        def gdn_decode_plan_destroy(self, h):
+            calls.append("destroy")
+
+        def gdn_decode_graph_destroy(self, g):
+            calls.append("graph_destroy")
+
+    class StubPlan:
+        def __init__(self, lib):
+            self._lib, self._handle = lib, ct.c_void_p(0x1000)
+
+        def close(self):
+            if self._handle is not None:
+                self._lib.gdn_decode_plan_destroy(self._handle)
+                self._handle = None
+
+    lib = StubLib()
+    layers = DecodeLayers.__new__(DecodeLayers)
+    layers.plans = [StubPlan(lib), StubPlan(lib)]
+    layers.device = -1
+    layers._handles = (ct.c_void_p * 2)(*[p._handle for p in layers.plans])
+    layers._lib = lib
+    layers._graph = None
+
+    layers.plans[1].close()                      # one plan closed on its own
+    for fn in (layers.run, layers.capture, layers.replay):
+        with pytest.raises(RuntimeError, match="plan was closed"):
+            fn()
+    layers.close()
+    for fn in (layers.run, layers.capture, layers.replay):
+        with pytest.raises(RuntimeError, match="layers were closed"):
+            fn()
+    assert "run" not in calls and calls.count("destroy") == 2
+    layers.close()                               # idempotent
