@@ -58,11 +58,16 @@
 // A[i][k] from lane i + 16 g, B[k][j] from lane j + 16 g (k = g for fp32;
 // for bf16 the lane's 8 items cover the 32-long k block), D[i][j] in lane
 // j + 16 (i / 4), register i % 4.  A bf16 product sums over its k block in
-// any order both operands share; here item e of lane group g stands for
+// any order both operands share.  Where the contracted index is a token,
+// item e of lane group g stands for
 //   k = 16 (e / 4) + 4 g + e % 4,
 // so a lane's 8 items are the 4-element runs at k = 4 g and 16 + 4 g, the
 // runs a 16 x 16 MFMA result holds per lane -- results become operands
-// without exchanging data between lanes.
+// without exchanging data between lanes.  Where it is a key (K and Q rows
+// read from LDS against the state), item e of lane group g is key 8 g + e of
+// the 32-key block: one 16-byte read per operand, and the 8 lanes that the
+// LDS serves together read 8 rows whose 272-byte stride puts them on
+// disjoint banks.  The state's registers hold its keys in that order.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -143,8 +148,17 @@ constexpr int kSlotFloats = kSlotRk + 3 * kChunk;     // padded to whole 1 KiB D
 static_assert(kSlotFloats % 256 == 0, "slots stay 1 KiB aligned");
 static_assert(tri_blk(3, 1) == kTriBlocks - 1, "six lower blocks");
 
-// k (0..31) of item e of lane group g inside a 32-long block.
+// Token (0..31) of item e of lane group g inside a 32-long block of a
+// token-contracted operand.
 __host__ __device__ constexpr int k_of(int g, int e) { return 16 * (e >> 2) + 4 * g + (e & 3); }
+
+// First of the 4 keys that register t of a state column holds in lane group
+// g (items e = 0..3 are that key + e): st[2 kb] and st[2 kb + 1] together
+// are keys 32 kb + 8 g .. + 7, the key order of frag().  A 16-row key tile
+// t of the state update is thus keys state_key(t, i / 4) + i % 4.
+__host__ __device__ constexpr int state_key(int t, int g) {
+  return 32 * (t >> 1) + 8 * g + 4 * (t & 1);
+}
 
 // LDS row strides (elements) chosen so MFMA operand reads spread over banks.
 constexpr int kBfStride = kDim + 8;       // bf16 rows of 128
@@ -206,10 +220,10 @@ __device__ __forceinline__ s16x8 cat(s16x4 a, s16x4 b) {
   return s16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
-// Operand items of lane group g for k block kb of a bf16 row (k contiguous).
+// Operand items of lane group g for key block kb of a bf16 row of 128 keys
+// in LDS: keys 32 kb + 8 g .. + 7, one 16-byte read (rows 16-byte aligned).
 __device__ __forceinline__ s16x8 frag(const uint16_t* row, int kb, int g) {
-  return cat(*reinterpret_cast<const s16x4*>(row + 32 * kb + 4 * g),
-             *reinterpret_cast<const s16x4*>(row + 32 * kb + 16 + 4 * g));
+  return *reinterpret_cast<const s16x8*>(row + 32 * kb + 8 * g);
 }
 
 struct Params {
@@ -1110,8 +1124,10 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
 // bf16, hi then lo (block ((t * 4 + kb) * 2 + hl) * 512).  Wave w holds
 // columns 16 w .. 16 w + 15, half w % 2 of block kb = w / 2: the selector
 // products of its state read as an operand with the columns as rows give
-// lane (col, g) the columns 16 w + 4 g + e of row 16 t + col, items
-// 4 (w % 2) .. + 3 of the block's lane.
+// lane (col, g) the columns 16 w + 4 g + e of row state_key(t, col / 4) +
+// col % 4, items 4 (w % 2) .. + 3 of the block's lane; those columns
+// started from start keys 32 kb + 8 g + item, the key order of the
+// combine's S operand.
 __device__ __forceinline__ void store_end(float* st_out, bool transition, const f32x4 (&st)[8],
                                           const s16x8 (&sels)[2]) {
   const int lane = threadIdx.x & 63;
@@ -1121,8 +1137,8 @@ __device__ __forceinline__ void store_end(float* st_out, bool transition, const 
   if (!transition) {
 #pragma unroll
     for (int t = 0; t < 8; ++t)
-      *reinterpret_cast<f32x4*>(st_out + static_cast<size_t>(wave * 16 + col) * kDim + t * 16 +
-                                g4 * 4) = st[t];
+      *reinterpret_cast<f32x4*>(st_out + static_cast<size_t>(wave * 16 + col) * kDim +
+                                state_key(t, g4)) = st[t];
     return;
   }
   uint16_t* ma = reinterpret_cast<uint16_t*>(st_out);
@@ -1255,18 +1271,23 @@ void scan_kernel(Params p) {
     seq_slots(s, slot0, nchunks);
   }
 
-  // state registers; k-last storage: 4 consecutive keys are one 16-byte vector
+  // state registers (keys in the order of state_key); k-last storage: 4
+  // consecutive keys are one 16-byte vector.  The identity start of a
+  // transition gives column 16 w + m the unit vector of the key in register
+  // position (w, m): key state_key(w, m / 4) + m % 4, so that its end column
+  // is that start key's column of M, in the key order of the combine's
+  // operand.
   f32x4 st[8];
   const int c = wave * 16 + col;
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
-    const int kr = t * 16 + g4 * 4;
     st[t] = st_in != nullptr && (end > start || pass_through)
-                ? *reinterpret_cast<const f32x4*>(st_in + static_cast<size_t>(c) * kDim + kr)
+                ? *reinterpret_cast<const f32x4*>(st_in + static_cast<size_t>(c) * kDim +
+                                                  state_key(t, g4))
                 : f32x4{0, 0, 0, 0};
     if (identity) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) st[t][e] = kr + e == c ? 1.0f : 0.0f;
+      for (int e = 0; e < 4; ++e) st[t][e] = t == wave && 4 * g4 + e == col ? 1.0f : 0.0f;
     }
   }
   // selector operands: Sel_h[k][j] = (k == 16 h + j) over a 32-long k block
@@ -1330,9 +1351,9 @@ void scan_kernel(Params p) {
 // hi/lo) and zero-start end B_j.  Combine: S_{j+1} = M_j S_j + B_j for j = 1
 // .. nseg-2, segment after segment, as bf16 MFMA with S_j split into hi + lo.
 // One workgroup per (sequence, v-head, 16 state columns); wave w computes row
-// tile w (rows 16 w .. 16 w + 15) and hands its rows of S_j to the other
-// waves as half of the B operand's k block w / 2 through LDS (two buffers:
-// one barrier a step).  A step is short (12 MFMAs a wave), so each wave's M
+// tile w (in the scan's key order: rows state_key(w, i / 4) + i % 4, the rows
+// of M's tile w) and hands its rows of S_j to the other waves as half of the
+// B operand's k block w / 2 through LDS (two buffers: one barrier a step).  A step is short (12 MFMAs a wave), so each wave's M
 // blocks and B tile are loaded three steps ahead, into three register sets
 // used in turn.  Every workgroup reads all of M_j: the eight of a (sequence,
 // v-head) are numbered hv + 8k within the sequence's (HV rounded up to 8
@@ -1369,7 +1390,7 @@ __global__ __launch_bounds__(64 * kCombWaves) void seg_combine_kernel(Params p) 
   }
   if (nseg < 3 || g0 + nseg > p.nseg) return; // nothing to chain; past the workspace's
   const int last = nseg - 2;                  // steps j = 1 .. last
-  const size_t tile = static_cast<size_t>(c0 + col) * kDim + wave * 16 + g4 * 4;
+  const size_t tile = static_cast<size_t>(c0 + col) * kDim + state_key(wave, g4);
   auto seg_blk = [&](const float* base, int j) {
     return base + (static_cast<size_t>(g0 + j) * p.HV + hv) * blk;
   };
