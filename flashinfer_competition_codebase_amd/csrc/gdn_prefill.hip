@@ -786,13 +786,14 @@ constexpr int kKtElems = 8 * 2 * 64 * 8;
 // P' operand blocks (the six lower (row block, token block) ones), hi then lo
 constexpr int kPElems = 2 * kTriBlocks * kBlk;
 
+// 16-byte aligned: the scan reads its row scales as 16-byte vectors.
 template <bool OUT> struct ScanBuf;
-template <> struct ScanBuf<true> {
+template <> struct __attribute__((aligned(16))) ScanBuf<true> {
   uint16_t Kr[kChunk * kRowStride];
   uint16_t Qr[kChunk * kRowStride];
   float slot[kSlotFloats];
 };
-template <> struct ScanBuf<false> {       // without outputs a chunk needs no Q
+template <> struct __attribute__((aligned(16))) ScanBuf<false> {  // without outputs: no Q
   uint16_t Kr[kChunk * kRowStride];
   float slot[kSlotFloats];
 };
@@ -903,9 +904,14 @@ __device__ __forceinline__ void scan_issue(ScanBuf<OUT>* buf, const ScanCtx& cx,
 // P' tiles (row tile r, token tile jt) of a chunk, 10 nonzero and the two
 // zero ones inside the stored blocks (0, 1) and (2, 3); wave w makes tiles w
 // and w + 8.
-__device__ constexpr int kPTiles = 12;
-__device__ constexpr int8_t kPTileR[kPTiles] = {0, 1, 1, 2, 2, 2, 3, 3, 3, 3, 0, 2};
-__device__ constexpr int8_t kPTileJ[kPTiles] = {0, 0, 1, 0, 1, 2, 0, 1, 2, 3, 1, 3};
+// Tile idx is (r, jt) = ((kPTileR >> 2 idx) & 3, (kPTileJ >> 2 idx) & 3):
+//   r  = 0, 1, 1, 2, 2, 2, 3, 3, 3, 3, 0, 2
+//   jt = 0, 0, 1, 0, 1, 2, 0, 1, 2, 3, 1, 3
+// (packed in immediates: a table in memory costs a global load and its wait
+// at the start of every chunk step).
+constexpr int kPTiles = 12;
+constexpr unsigned kPTileR = 0x8ffa94u;
+constexpr unsigned kPTileJ = 0xde4910u;
 
 // Chunk ci from buffer B, with the next chunk's DMA into Bn; Kt: the K^T
 // operand blocks; Pb: the P' operand blocks (OUT); Qn: the Q row scales
@@ -936,21 +942,18 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
   const int t0 = cx.start + ci * kChunk;
   const int n = min(kChunk, cx.end - t0);
   const u32x2 vf[4] = {vnext[0], vnext[1], vnext[2], vnext[3]};
-  // the chunk's row scales, and key tile `wave` of K^T (the selector
-  // products of the K row blocks (r, wave / 2) give lane (col, g) tokens
-  // 16 r + 4 g + e of key 16 wave + col), read before the DMA below is issued
-  f32x4 xg[4], ks[4];
-  float qs[4];
+  // key tile `wave` of K^T (the selector products of the K row blocks
+  // (r, wave / 2) give lane (col, g) tokens 16 r + 4 g + e of key
+  // state_key(wave, col / 4) + col % 4).  The chunk's row scales are read
+  // where they are used, so that they hold no registers across the products:
+  // B is restrict and 16-byte aligned, so each read is one ds_read_b128 that
+  // the compiler knows the DMA in flight into Bn does not write (reads it
+  // splits into pairs of 4-byte reads lose that, and wait for the DMA).
   s16x4 kt[4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    xg[r] = *reinterpret_cast<const f32x4*>(&B->slot[kSlotXg + r * 16 + g4 * 4]);
-    ks[r] = *reinterpret_cast<const f32x4*>(&B->slot[kSlotKs + r * 16 + g4 * 4]);
-    qs[r] = OUT ? cx.scale * B->slot[kSlotEg + r * 16 + col] : 0.0f;
+  for (int r = 0; r < 4; ++r)
     kt[r] = to_bf16x4(mfma_bf16(frag(&B->Kr[(r * 16 + col) * kRowStride], wave >> 1, g4), sel,
                                 f32x4{0, 0, 0, 0}));
-  }
-  const float gl = B->slot[kSlotGl];
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
     *reinterpret_cast<s16x8*>(Kt + ((wave * 2 + kb) * 64 + lane) * 8) =
@@ -962,7 +965,7 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
     for (int rep = 0; rep < 2; ++rep) {
       const int idx = wave + kScanWaves * rep;
       if (idx >= kPTiles) break;                       // uniform per wave
-      const int r = kPTileR[idx], jt = kPTileJ[idx];
+      const int r = (kPTileR >> (2 * idx)) & 3, jt = (kPTileJ >> (2 * idx)) & 3;
       f32x4 pv = {0, 0, 0, 0};
       if (jt <= r) {                                   // uniform per wave
         f32x4 acc = {0, 0, 0, 0};
@@ -1041,10 +1044,11 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
   // wave's 16 columns sit in the half `wave % 2` of a 32-column block)
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
+    const f32x4 xg = *reinterpret_cast<const f32x4*>(&B->slot[kSlotXg + r * 16 + g4 * 4]);
     const u32x2 vv = cx.values ? vf[r] : u32x2{0u, 0u};
     const u32x4 w4 = (wave & 1) ? u32x4{0u, 0u, vv.x, vv.y} : u32x4{vv.x, vv.y, 0u, 0u};
     const f32x4 v = mfma_bf16(__builtin_bit_cast(s16x8, w4), sel, f32x4{0, 0, 0, 0});
-    x[r] = v - xg[r] * x[r];
+    x[r] = v - xg * x[r];
   }
 
   // Delta = T diag(beta) X (T lower triangular: token blocks kb <= r / 2)
@@ -1068,6 +1072,10 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
 
   // Delta as operand: A of Delta^T P^T and, scaled by ks, B of the update
   s16x8 dh[2], dl[2], eh[2], el[2];
+  f32x4 ks[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    ks[r] = *reinterpret_cast<const f32x4*>(&B->slot[kSlotKs + r * 16 + g4 * 4]);
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
     if constexpr (OUT) dh[kb] = split_hi_lo(d[2 * kb], d[2 * kb + 1], dl[kb]);
@@ -1082,7 +1090,7 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
   if constexpr (OUT) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      o[r] = o[r] * qs[r];
+      o[r] = o[r] * (cx.scale * B->slot[kSlotEg + r * 16 + col]);
 #pragma unroll
       for (int kb = 0; kb <= (r >> 1); ++kb) {
         const int bo = tri_blk(r, kb) * kBlk + lane * 8;
@@ -1102,6 +1110,7 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
   }
 
   // S <- e^gamma_C S + K^T (ks (.) Delta), key tile t
+  const float gl = B->slot[kSlotGl];
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
     f32x4 acc = st[t] * gl;
