@@ -901,6 +901,53 @@ __device__ __forceinline__ void scan_issue(ScanBuf<OUT>* buf, const ScanCtx& cx,
          lane & 15, lane >> 4);
 }
 
+// Where chunk c's inputs come from (rows >= n repeat row n - 1).
+struct ChunkSrc {
+  const uint16_t* kbase;
+  const uint16_t* qbase;
+  const uint16_t* vbase;
+  const float* slot;
+  int n;
+};
+
+__device__ __forceinline__ ChunkSrc chunk_src(const ScanCtx& cx, int c) {
+  const int tc = cx.start + c * kChunk;
+  ChunkSrc s;
+  s.kbase = cx.k + (static_cast<size_t>(tc) * cx.H + cx.h) * kDim;
+  s.qbase = cx.q + (static_cast<size_t>(tc) * cx.H + cx.h) * kDim;
+  s.vbase = cx.v + (static_cast<size_t>(tc) * cx.HV + cx.hv) * kDim;
+  s.slot = cx.slot_base + c * cx.slot_step;
+  s.n = min(kChunk, cx.end - tc);
+  return s;
+}
+
+// Part `part` (0..3) of a chunk's DMA and V loads, so that a chunk step
+// spreads them over its products (issued at once, the eight waves' DMA
+// instructions queue behind each other and hold each wave at the issue for
+// 1-2.5 k cycles): parts 0..2 the K / Q row instructions w + 8 part, part 2
+// also slot instruction w, part 3 slot instruction w + 8 and the V loads.
+template <bool OUT>
+__device__ __forceinline__ void issue_part(ScanBuf<OUT>* __restrict__ Bn, const ScanCtx& cx,
+                                           const ChunkSrc& s, int part, u32x2 (&vf)[4]) {
+  const int wave = wave_index(), lane = threadIdx.x & 63;
+  if (part < 3) {
+    const int i = wave + kScanWaves * part;
+    if (i < kRowDma) {                                      // uniform per wave
+      const int pc = i * 64 + lane;
+      const int r = pc / kRowPieces, c = pc % kRowPieces;
+      const unsigned off =
+          static_cast<unsigned>(r < s.n ? r : s.n - 1) * cx.kstep + (c < 16 ? c : 15) * 8;
+      dma16(s.kbase + off, &Bn->Kr[i * 512]);
+      if constexpr (OUT) dma16(s.qbase + off, &Bn->Qr[i * 512]);
+    }
+  }
+  if (part >= 2) {
+    const int i = wave + kScanWaves * (part - 2);
+    if (i < kSlotDma) dma16(s.slot + (i * 64 + lane) * 4, &Bn->slot[i * 256]);
+  }
+  if (part == 3) load_v(vf, s.vbase, cx.vstep, s.n, wave, lane & 15, lane >> 4);
+}
+
 // P' tiles (row tile r, token tile jt) of a chunk, 10 nonzero and the two
 // zero ones inside the stored blocks (0, 1) and (2, 3); wave w makes tiles w
 // and w + 8.
@@ -912,6 +959,15 @@ __device__ __forceinline__ void scan_issue(ScanBuf<OUT>* buf, const ScanCtx& cx,
 constexpr int kPTiles = 12;
 constexpr unsigned kPTileR = 0x8ffa94u;
 constexpr unsigned kPTileJ = 0xde4910u;
+
+// Key block kb's product of P' tile IDX, (K Q^T)_(jt, r) over the block,
+// from the K and Q operands of the block's row tiles (in registers).
+template <int IDX>
+__device__ __forceinline__ void p_tile_mma(const s16x8 (&ak)[4], const s16x8 (&bq)[4],
+                                           f32x4& acc) {
+  constexpr int r = (kPTileR >> (2 * IDX)) & 3, jt = (kPTileJ >> (2 * IDX)) & 3;
+  if constexpr (jt <= r) acc = mfma_bf16(ak[jt], bq[r], acc);
+}
 
 // Chunk ci from buffer B, with the next chunk's DMA into Bn; Kt: the K^T
 // operand blocks; Pb: the P' operand blocks (OUT); Qn: the Q row scales
@@ -942,57 +998,14 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
   const int t0 = cx.start + ci * kChunk;
   const int n = min(kChunk, cx.end - t0);
   const u32x2 vf[4] = {vnext[0], vnext[1], vnext[2], vnext[3]};
-  // key tile `wave` of K^T (the selector products of the K row blocks
-  // (r, wave / 2) give lane (col, g) tokens 16 r + 4 g + e of key
-  // state_key(wave, col / 4) + col % 4).  The chunk's row scales are read
-  // where they are used, so that they hold no registers across the products:
-  // B is restrict and 16-byte aligned, so each read is one ds_read_b128 that
-  // the compiler knows the DMA in flight into Bn does not write (reads it
-  // splits into pairs of 4-byte reads lose that, and wait for the DMA).
-  s16x4 kt[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r)
-    kt[r] = to_bf16x4(mfma_bf16(frag(&B->Kr[(r * 16 + col) * kRowStride], wave >> 1, g4), sel,
-                                f32x4{0, 0, 0, 0}));
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
-    *reinterpret_cast<s16x8*>(Kt + ((wave * 2 + kb) * 64 + lane) * 8) =
-        cat(kt[2 * kb], kt[2 * kb + 1]);
-  if constexpr (OUT) {
-    // P' tiles (r, jt): lane (col, g) holds row i = 16 r + col, tokens
-    // j = 16 jt + 4 g + e; items 4 (jt % 2) .. + 3 of block (r, jt / 2)
-#pragma unroll
-    for (int rep = 0; rep < 2; ++rep) {
-      const int idx = wave + kScanWaves * rep;
-      if (idx >= kPTiles) break;                       // uniform per wave
-      const int r = (kPTileR >> (2 * idx)) & 3, jt = (kPTileJ >> (2 * idx)) & 3;
-      f32x4 pv = {0, 0, 0, 0};
-      if (jt <= r) {                                   // uniform per wave
-        f32x4 acc = {0, 0, 0, 0};
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-          acc = mfma_bf16(frag(&B->Kr[(jt * 16 + col) * kRowStride], kb, g4),
-                          frag(&B->Qr[(r * 16 + col) * kRowStride], kb, g4), acc);
-        const int i = r * 16 + col, j0 = jt * 16 + g4 * 4;
-        const float gi = B->slot[kSlotGa + i];
-        const f32x4 gj = *reinterpret_cast<const f32x4*>(&B->slot[kSlotGa + j0]);
-        const f32x4 rkj = *reinterpret_cast<const f32x4*>(&B->slot[kSlotRk + j0]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float x = cx.scale * rkj[e] * __expf(fminf(gi - gj[e], 0.0f)) * acc[e];
-          pv[e] = j0 + e <= i ? x : 0.0f;
-        }
-      }
-      s16x4 hi, lo;
-      split4(pv, hi, lo);
-      const int at = tri_blk(r, jt >> 1) * kBlk + lane * 8 + (jt & 1) * 4;
-      *reinterpret_cast<s16x4*>(Pb + at) = hi;
-      *reinterpret_cast<s16x4*>(Pb + kTriBlocks * kBlk + at) = lo;
-    }
-  }
-  // the next chunk's inputs into the other buffer (after the last chunk:
-  // this one's again, unused), in flight while this chunk computes
-  scan_issue(Bn, cx, ci + 1 < cx.nchunks ? ci + 1 : ci, vnext);
+  // The next chunk's inputs go into the other buffer (after the last chunk:
+  // this one's again, unused) in four parts spread over the K S products.
+  const ChunkSrc nsrc = chunk_src(cx, ci + 1 < cx.nchunks ? ci + 1 : ci);
+  // The chunk's row scales are read where they are used, so that they hold
+  // no registers across the products: B is restrict and 16-byte aligned, so
+  // each read is one ds_read_b128 that the compiler knows the DMA in flight
+  // into Bn does not write (reads it splits into pairs of 4-byte reads lose
+  // that, and wait for the DMA).
 
   // L2-norm: 1 / |q_i| of Q rows 8 wave .. 8 wave + 7 into Qn (lane: row
   // 8 wave + lane / 8, items 16 (lane % 8) .. + 15); read after the barrier
@@ -1018,25 +1031,102 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
   }
 
   // K S (token rows) and S^T Q^T (the output's first term, transposed),
-  // one 32-key block of the state at a time
-  f32x4 x[4], o[4];
+  // one 32-key block of the state at a time.  The K and Q operands of key
+  // block kb + 1 are read into the other of two register sets while block
+  // kb's products run, so the LDS latency is paid once, not per product.
+  // The same operands make this wave's key tile of K^T (key block wave / 2:
+  // the selector products of the K row tiles give lane (col, g) tokens
+  // 16 r + 4 g + e of key state_key(wave, col / 4) + col % 4) and its P'
+  // tiles' (K Q^T) products, shared with the other waves through LDS.
+  f32x4 x[4], o[4], pacc[2];
 #pragma unroll
   for (int r = 0; r < 4; ++r) x[r] = o[r] = f32x4{0, 0, 0, 0};
+  pacc[0] = pacc[1] = f32x4{0, 0, 0, 0};
+  s16x4 kt[4];
+  s16x8 ak[2][4], bq[2][4];
+  auto read_ops = [&](int kb, int set) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      ak[set][r] = frag(&B->Kr[(r * 16 + col) * kRowStride], kb, g4);
+      if constexpr (OUT) bq[set][r] = frag(&B->Qr[(r * 16 + col) * kRowStride], kb, g4);
+    }
+  };
+  read_ops(0, 0);
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
+    const int set = kb & 1;
+    if (kb < 3) read_ops(kb + 1, set ^ 1);
+    issue_part(Bn, cx, nsrc, kb, vnext);
+    if (kb == (wave >> 1)) {                                // uniform per wave
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        kt[r] = to_bf16x4(mfma_bf16(ak[set][r], sel, f32x4{0, 0, 0, 0}));
+    }
+    if constexpr (OUT) {
+      switch (wave) {                                       // uniform per wave
+        case 0: p_tile_mma<0>(ak[set], bq[set], pacc[0]); p_tile_mma<8>(ak[set], bq[set], pacc[1]); break;
+        case 1: p_tile_mma<1>(ak[set], bq[set], pacc[0]); p_tile_mma<9>(ak[set], bq[set], pacc[1]); break;
+        case 2: p_tile_mma<2>(ak[set], bq[set], pacc[0]); break;
+        case 3: p_tile_mma<3>(ak[set], bq[set], pacc[0]); break;
+        case 4: p_tile_mma<4>(ak[set], bq[set], pacc[0]); break;
+        case 5: p_tile_mma<5>(ak[set], bq[set], pacc[0]); break;
+        case 6: p_tile_mma<6>(ak[set], bq[set], pacc[0]); break;
+        default: p_tile_mma<7>(ak[set], bq[set], pacc[0]); break;
+      }
+    }
     s16x8 sl;
     const s16x8 sh = split_hi_lo(st[2 * kb], st[2 * kb + 1], sl);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const s16x8 ak = frag(&B->Kr[(r * 16 + col) * kRowStride], kb, g4);
-      x[r] = mfma_bf16(ak, sh, x[r]);
-      x[r] = mfma_bf16(ak, sl, x[r]);
-      if constexpr (OUT) {
-        const s16x8 bq = frag(&B->Qr[(r * 16 + col) * kRowStride], kb, g4);
-        o[r] = mfma_bf16(sh, bq, o[r]);
-        o[r] = mfma_bf16(sl, bq, o[r]);
-      }
+      x[r] = mfma_bf16(ak[set][r], sh, x[r]);
+      if constexpr (OUT) o[r] = mfma_bf16(sh, bq[set][r], o[r]);
     }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      x[r] = mfma_bf16(ak[set][r], sl, x[r]);
+      if constexpr (OUT) o[r] = mfma_bf16(sl, bq[set][r], o[r]);
+    }
+  }
+
+  // this wave's K^T tile and P' tiles into LDS (read after the barrier below)
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+    *reinterpret_cast<s16x8*>(Kt + ((wave * 2 + kb) * 64 + lane) * 8) =
+        cat(kt[2 * kb], kt[2 * kb + 1]);
+  if constexpr (OUT) {
+    // P' tile (r, jt): lane (col, g) holds row i = 16 r + col, tokens
+    // j = 16 jt + 4 g + e; items 4 (jt % 2) .. + 3 of block (r, jt / 2)
+#pragma unroll
+    for (int rep = 0; rep < 2; ++rep) {
+      const int idx = wave + kScanWaves * rep;
+      if (idx >= kPTiles) break;                       // uniform per wave
+      const int r = (kPTileR >> (2 * idx)) & 3, jt = (kPTileJ >> (2 * idx)) & 3;
+      f32x4 pv = {0, 0, 0, 0};
+      if (jt <= r) {                                   // uniform per wave
+        const int i = r * 16 + col, j0 = jt * 16 + g4 * 4;
+        const float gi = B->slot[kSlotGa + i];
+        const f32x4 gj = *reinterpret_cast<const f32x4*>(&B->slot[kSlotGa + j0]);
+        const f32x4 rkj = *reinterpret_cast<const f32x4*>(&B->slot[kSlotRk + j0]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x = cx.scale * rkj[e] * __expf(fminf(gi - gj[e], 0.0f)) * pacc[rep][e];
+          pv[e] = j0 + e <= i ? x : 0.0f;
+        }
+      }
+      s16x4 hi, lo;
+      split4(pv, hi, lo);
+      const int at = tri_blk(r, jt >> 1) * kBlk + lane * 8 + (jt & 1) * 4;
+      *reinterpret_cast<s16x4*>(Pb + at) = hi;
+      *reinterpret_cast<s16x4*>(Pb + kTriBlocks * kBlk + at) = lo;
+    }
+  }
+
+  // T diag(beta)'s six lower operand blocks (hi, lo), read while X is formed
+  s16x8 th[kTriBlocks], tl[kTriBlocks];
+#pragma unroll
+  for (int b = 0; b < kTriBlocks; ++b) {
+    th[b] = ld_op(&B->slot[kSlotTh + b * kBlkF + lane * 4]);
+    tl[b] = ld_op(&B->slot[kSlotTl + b * kBlkF + lane * 4]);
   }
 
   // X = V - diag(rk e^gamma) K S: lane (col, g) holds tokens 16 r + 4 g + e
@@ -1061,12 +1151,10 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
     d[r] = f32x4{0, 0, 0, 0};
 #pragma unroll
     for (int kb = 0; kb <= (r >> 1); ++kb) {
-      const int bo = tri_blk(r, kb) * kBlkF + lane * 4;
-      const s16x8 th = ld_op(&B->slot[kSlotTh + bo]);
-      const s16x8 tl = ld_op(&B->slot[kSlotTl + bo]);
-      d[r] = mfma_bf16(th, xh[kb], d[r]);
-      d[r] = mfma_bf16(th, xl[kb], d[r]);
-      d[r] = mfma_bf16(tl, xh[kb], d[r]);
+      const int b = tri_blk(r, kb);
+      d[r] = mfma_bf16(th[b], xh[kb], d[r]);
+      d[r] = mfma_bf16(th[b], xl[kb], d[r]);
+      d[r] = mfma_bf16(tl[b], xh[kb], d[r]);
     }
   }
 
@@ -1085,20 +1173,43 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
   // every wave's K^T tile and P' tiles are in LDS past this barrier
   barrier_lds_no_dma();
 
+  // The operands of the output products two row tiles ahead of their use,
+  // and those of the state update in two halves, the first read with the
+  // output's, the second while the first half's products run.
+  s16x8 ph[kTriBlocks], pl[kTriBlocks], kt_op[8][2];
+  auto read_p = [&](int r) {
+#pragma unroll
+    for (int kb = 0; kb <= (r >> 1); ++kb) {
+      const int b = tri_blk(r, kb);
+      ph[b] = ld_op(Pb + b * kBlk + lane * 8);
+      pl[b] = ld_op(Pb + (kTriBlocks + b) * kBlk + lane * 8);
+    }
+  };
+  if constexpr (OUT) {
+    read_p(0);
+    read_p(1);
+  }
+  auto read_kt = [&](int t0k) {
+#pragma unroll
+    for (int t = t0k; t < t0k + 4; ++t)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) kt_op[t][kb] = ld_op(Kt + ((t * 2 + kb) * 64 + lane) * 8);
+  };
+  read_kt(0);
+
   // O^T = rq (.) (qs (.) S^T Q^T + Delta^T P'^T); lane (col, g) ends with
   // columns 16 wave + 4 g + e of token 16 r + col, one 8-byte store
   if constexpr (OUT) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
+      if (r < 2) read_p(r + 2);
       o[r] = o[r] * (cx.scale * B->slot[kSlotEg + r * 16 + col]);
 #pragma unroll
       for (int kb = 0; kb <= (r >> 1); ++kb) {
-        const int bo = tri_blk(r, kb) * kBlk + lane * 8;
-        const s16x8 ph = ld_op(Pb + bo);
-        const s16x8 pl = ld_op(Pb + kTriBlocks * kBlk + bo);
-        o[r] = mfma_bf16(dh[kb], ph, o[r]);
-        o[r] = mfma_bf16(dh[kb], pl, o[r]);
-        o[r] = mfma_bf16(dl[kb], ph, o[r]);
+        const int b = tri_blk(r, kb);
+        o[r] = mfma_bf16(dh[kb], ph[b], o[r]);
+        o[r] = mfma_bf16(dh[kb], pl[b], o[r]);
+        o[r] = mfma_bf16(dl[kb], ph[b], o[r]);
       }
       if constexpr (L2) o[r] = o[r] * Qn[r * 16 + col];
       const int tok = r * 16 + col;
@@ -1113,12 +1224,12 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
   const float gl = B->slot[kSlotGl];
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
+    if (t == 1) read_kt(4);
     f32x4 acc = st[t] * gl;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      const s16x8 ak = ld_op(Kt + ((t * 2 + kb) * 64 + lane) * 8);
-      acc = mfma_bf16(ak, eh[kb], acc);
-      acc = mfma_bf16(ak, el[kb], acc);
+      acc = mfma_bf16(kt_op[t][kb], eh[kb], acc);
+      acc = mfma_bf16(kt_op[t][kb], el[kb], acc);
     }
     st[t] = acc;
   }
