@@ -81,6 +81,9 @@ sys.path.insert(0, str(ROOT))
 
 import flashinfer_competition_codebase_amd as gdn  # noqa: E402
 from flashinfer_competition_codebase_amd import _lib  # noqa: E402
+from flashinfer_competition_codebase_amd.build import (  # noqa: E402
+    DECODE_SOURCES, PREFILL_SOURCES)
+from flashinfer_competition_codebase_amd.build import sources_sha as _sources_sha  # noqa: E402
 
 METRIC = ("GDN decode µs/step at B=1; achieved HBM GB/s (% of peak) at B=256")
 PEAK_HBM_GBS = 8000.0
@@ -454,25 +457,11 @@ def decode_kernel_name(ns: int, waves: int, l2: bool, policy: int, bf16: bool = 
             f"false>")
 
 
-DECODE_SOURCES = ("flashinfer_competition_codebase_amd/csrc/gdn_decode_kernel.h",
-                  "flashinfer_competition_codebase_amd/csrc/gdn_decode_block.h",
-                  "flashinfer_competition_codebase_amd/csrc/gdn_decode.hip",
-                  "flashinfer_competition_codebase_amd/build.py")
-PREFILL_SOURCES = ("flashinfer_competition_codebase_amd/csrc/gdn_prefill.hip",
-                   "flashinfer_competition_codebase_amd/csrc/gdn_decode_kernel.h",
-                   "flashinfer_competition_codebase_amd/build.py")
 
 
 def sources_sha(paths) -> str:
-    """SHA-256 (16 hex digits) over the given source files, in order: the
-    code a counter summary was measured on."""
-    import hashlib
-
-    h = hashlib.sha256()
-    for rel in paths:
-        h.update(rel.encode())
-        h.update((ROOT / rel).read_bytes())
-    return h.hexdigest()[:16]
+    """Hash of the given sources under this checkout (``ROOT``)."""
+    return _sources_sha(paths, ROOT)
 
 
 def _traffic(kernel: str) -> tuple[int | None, str]:
@@ -819,18 +808,33 @@ def _prefill_traffic() -> dict | None:
 
 
 def prefill_roofline(prefill: dict) -> dict:
-    """Roofline of the largest prefill workload: its algorithmic FLOP rate
-    over the whole prefill (kernel time) against the bf16 dense MFMA peak;
-    the preparation kernel's HBM bytes (inputs read + workspace written) per
-    its time against the HBM peak; ``traffic``: measured HBM bytes of prep +
-    scan per prefill and the HBM rate they make over the kernels' times."""
+    """Roofline of the largest prefill workload against the roof that binds
+    it: its algorithmic bytes (q, k, v, a, b, output, states in and out) and
+    FLOP give a floor time on each roof (HBM at 8 TB/s, bf16 dense MFMA), and
+    the larger floor names ``bound``; ``achieved`` / ``frac`` are on that
+    roof over the whole prefill's kernel time, and ``mfma`` / ``hbm`` carry
+    both roofs' fractions.  ``prep``: the preparation kernel's HBM bytes
+    (inputs read + workspace written) per its time; ``traffic``: measured
+    HBM bytes of prep + scan per prefill and the HBM rate they make over the
+    kernels' times."""
     r = prefill[PREFILL_ROOFLINE_WORKLOAD]
     lens_h = PREFILL_CONFIGS[PREFILL_ROOFLINE_WORKLOAD]
     lens, H, HV = lens_h
     chunks = sum((n + 63) // 64 for n in lens)
     flop = chunks * HV * PREFILL_FLOP_PER_CHUNK_HEAD
+    alg_bytes = prefill_bytes(lens, H, HV)
     ku = r["kernel_us"]
     achieved = flop / (ku["kernels"] * 1e-6) / 1e12
+    hbm_gbs = alg_bytes / (ku["kernels"] * 1e-6) / 1e9
+    floor_hbm_us = alg_bytes / (PEAK_HBM_GBS * 1e3)
+    floor_mfma_us = flop / (PEAK_BF16_TFLOPS * 1e6)
+    mfma = {"achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "floor_us": round(floor_mfma_us, 1),
+            "flop": flop}
+    hbm = {"achieved": round(hbm_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+           "frac": round(hbm_gbs / PEAK_HBM_GBS, 4), "floor_us": round(floor_hbm_us, 1),
+           "algorithmic_bytes": alg_bytes}
+    binding = hbm if floor_hbm_us >= floor_mfma_us else mfma
     L = sum(lens)
     prep_in = L * (H * 128 * 2 + 2 * HV * 2)              # k, a, b
     prep_bytes = prep_in + r["prep_workspace_bytes"]
@@ -843,9 +847,10 @@ def prefill_roofline(prefill: dict) -> dict:
         traffic = {"bytes": total, "prep_bytes": tr["prep"], "scan_bytes": tr["scan"],
                    "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
                    "source": str(PREFILL_TRAFFIC_SUMMARY.relative_to(ROOT))}
-    return {"workload": PREFILL_ROOFLINE_WORKLOAD, "bound": "mfma",
-            "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+    return {"workload": PREFILL_ROOFLINE_WORKLOAD,
+            "bound": "hbm" if binding is hbm else "mfma",
+            "achieved": binding["achieved"], "peak": binding["peak"], "unit": binding["unit"],
+            "frac": binding["frac"], "hbm": hbm, "mfma": mfma, "traffic": traffic,
             "kernel_us": ku,
             "prep": {"hbm_bytes": prep_bytes, "gbs": round(prep_gbs, 1),
                      "frac_of_hbm_peak": round(prep_gbs / PEAK_HBM_GBS, 4)}}

@@ -41,6 +41,27 @@ OFFLOAD_ARCH = "gfx950"
 EXTRA_FLAGS = {PREFILL_PATH: ["-mllvm", "-amdgpu-mfma-vgpr-form"],
                LIB_PATH: ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 KERNARG_PRELOAD_ARGS = int(os.environ.get("GDN_KERNARG_PRELOAD_ARGS", "8"))
+# The files each library's kernels are built from (paths from the repository
+# root), in the order sources_sha hashes them.
+DECODE_SOURCES = ("flashinfer_competition_codebase_amd/csrc/gdn_decode_kernel.h",
+                  "flashinfer_competition_codebase_amd/csrc/gdn_decode_block.h",
+                  "flashinfer_competition_codebase_amd/csrc/gdn_decode.hip",
+                  "flashinfer_competition_codebase_amd/build.py")
+PREFILL_SOURCES = ("flashinfer_competition_codebase_amd/csrc/gdn_prefill.hip",
+                   "flashinfer_competition_codebase_amd/csrc/gdn_decode_kernel.h",
+                   "flashinfer_competition_codebase_amd/build.py")
+
+
+def sources_sha(paths, root: Path = REPO_ROOT) -> str:
+    """SHA-256 (16 hex digits) over the given source files (paths from
+    ``root``), in order: the code a measurement was made on."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for rel in paths:
+        h.update(rel.encode())
+        h.update((Path(root) / rel).read_bytes())
+    return h.hexdigest()[:16]
 
 
 def hipcc_path() -> str:

@@ -544,6 +544,7 @@ int gdn_decode_step_stamped(const void* q, const void* k, const void* v, const f
 
 struct gdn_decode_plan {
   gdn::StepArgs args;
+  int device;          // the device current at creation (the buffers' device)
 };
 
 struct gdn_decode_graph {
@@ -562,7 +563,9 @@ int gdn_decode_plan_create(const void* q, const void* k, const void* v, const vo
   choose_args_shape(s);
   const hipError_t e = validate(s);
   if (e != hipSuccess) return e;
-  gdn_decode_plan* p = new (std::nothrow) gdn_decode_plan{s};
+  int device = -1;                 // -1: no device (then runs switch none)
+  if (hipGetDevice(&device) != hipSuccess) device = -1;
+  gdn_decode_plan* p = new (std::nothrow) gdn_decode_plan{s, device};
   if (p == nullptr) return hipErrorOutOfMemory;
   *plan = p;
   return hipSuccess;
@@ -572,12 +575,28 @@ int gdn_decode_plan_run(const gdn_decode_plan* const* plans, int n, void* hip_st
   if (n < 0 || (n > 0 && plans == nullptr)) return hipErrorInvalidValue;
   for (int i = 0; i < n; ++i)
     if (plans[i] == nullptr) return hipErrorInvalidValue;
+  if (n == 0) return hipSuccess;
+  // each launch goes to its plan's device, made current for it (and the
+  // caller's current device restored after)
+  int caller = -1;
+  if (hipGetDevice(&caller) != hipSuccess) caller = -1;
   const hipStream_t stream = static_cast<hipStream_t>(hip_stream);
-  for (int i = 0; i < n; ++i) {
-    const hipError_t e = launch(plans[i]->args, stream, nullptr, nullptr);
-    if (e != hipSuccess) return e;
+  int cur = caller;
+  hipError_t e = hipSuccess;
+  for (int i = 0; i < n && e == hipSuccess; ++i) {
+    const int dev = plans[i]->device;
+    if (dev >= 0 && dev != cur) {
+      e = hipSetDevice(dev);
+      if (e != hipSuccess) break;
+      cur = dev;
+    }
+    e = launch(plans[i]->args, stream, nullptr, nullptr);
   }
-  return hipSuccess;
+  if (cur != caller && caller >= 0) {
+    const hipError_t r = hipSetDevice(caller);
+    if (e == hipSuccess) e = r;
+  }
+  return e;
 }
 
 void gdn_decode_plan_destroy(gdn_decode_plan* plan) { delete plan; }

@@ -288,7 +288,15 @@ class Manifest:
         self.calls.append([uuid, phase, dispatches])
 
     def write(self, path) -> None:
-        Path(path).write_text(json.dumps({"calls": self.calls}))
+        Path(path).write_text(json.dumps({"calls": self.calls, "sources_sha": run_sources_sha()}))
+
+
+def run_sources_sha() -> dict:
+    """Hash of the kernel sources of each library (build.sources_sha): what a
+    run measured, recorded in its manifest and printed with its results."""
+    from .build import DECODE_SOURCES, PREFILL_SOURCES, sources_sha
+
+    return {"decode": sources_sha(DECODE_SOURCES), "prefill": sources_sha(PREFILL_SOURCES)}
 
 
 def baseline_us(w, baseline: Optional[str]) -> Optional[float]:
@@ -558,9 +566,11 @@ def main(argv=None) -> int:
     args = _parser().parse_args(argv)
     prefill = args.definition == PREFILL_DEFINITION
     if args.cmd == "attribute":
-        calls = json.loads(args.manifest.read_text())["calls"]
+        doc = json.loads(args.manifest.read_text())
+        calls = doc["calls"]
         results = attribute_trace(args.trace, calls, baseline=args.baseline,
                                   kernel_substring=TRACE_KERNELS[args.definition])
+        print(f"Sources of the traced run (sources_sha): {doc.get('sources_sha', 'not recorded')}")
         print_results(results, definition=args.definition, baseline=args.baseline)
         if prefill:
             print(f"  per-workload median kernel time (µs): {per_workload_summary(results)}")
@@ -568,7 +578,8 @@ def main(argv=None) -> int:
             print(f"  per-batch median kernel time (µs): {per_batch_summary(results)}")
         if args.json:
             _dump(results, args.json, {"tier": "trace", "baseline": args.baseline,
-                                       "definition": args.definition})
+                                       "definition": args.definition,
+                                       "sources_sha": doc.get("sources_sha")})
         return 0
 
     from . import ENTRY_POINTS, NO_DPS
@@ -582,8 +593,8 @@ def main(argv=None) -> int:
     manifest = Manifest() if args.manifest else None
     print(f"Algorithm: {args.algo} ({'value-returning' if args.algo in NO_DPS else 'DPS'}), "
           f"{len(workloads)} workloads, tier {args.tier}, flush {args.flush}, "
-          f"{'one set of arguments' if args.no_clone else 'arguments cloned per call'}",
-          flush=True)
+          f"{'one set of arguments' if args.no_clone else 'arguments cloned per call'}; "
+          f"sources_sha {run_sources_sha()}", flush=True)
     results = evaluate(ENTRY_POINTS[args.algo], workloads, dps=args.algo not in NO_DPS,
                        warmup=args.warmup, iterations=args.iterations,
                        num_trials=args.num_trials, tier=args.tier, flush=args.flush,
@@ -600,7 +611,8 @@ def main(argv=None) -> int:
     if args.json:
         _dump(results, args.json, {"tier": args.tier, "baseline": args.baseline,
                                    "algo": args.algo, "flush": args.flush,
-                                   "clone": not args.no_clone, "definition": args.definition})
+                                   "clone": not args.no_clone, "definition": args.definition,
+                                   "sources_sha": run_sources_sha()})
     return 0
 
 

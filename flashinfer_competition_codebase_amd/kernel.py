@@ -37,7 +37,9 @@ launched.
 
 from __future__ import annotations
 
+import ctypes
 import math
+import weakref
 
 import torch
 
@@ -205,6 +207,72 @@ def _launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
             _lib.check(code, "gdn_decode_steps")
 
 
+class _Validated:
+    """A decode call that passed every check, bound once in a native plan
+    (``gdn_decode_plan_create``: the same checks on the C side, the launch
+    shape resolved).  It is recognised by the identities of its tensor
+    objects -- while they live: a weak reference to each evicts the entry
+    when that tensor is freed, so an id is never reused under a live entry
+    -- and by their data pointers, compared on every call (a tensor whose
+    storage was swapped in place is validated afresh)."""
+
+    __slots__ = ("key", "ptrs", "device", "handle", "arr", "refs", "__weakref__")
+
+    def __init__(self, key, tensors, device, handle):
+        self.key = key
+        self.ptrs = _data_ptrs(*tensors)
+        self.device = device
+        self.handle = handle
+        self.arr = (ctypes.c_void_p * 1)(handle)
+        self.refs = []
+
+    def destroy(self) -> None:
+        if self.handle is not None:
+            handle, self.handle = self.handle, None
+            try:
+                _lib.get_lib().gdn_decode_plan_destroy(handle)
+            except Exception:          # interpreter shutdown: the library may be gone
+                pass
+
+
+# Validated calls by the ids of their tensors, scale and flag (insertion order:
+# the oldest is evicted first).  A serving loop that calls the step with a
+# fixed set of buffers per layer runs every call after the first through here.
+_VALIDATED: dict = {}
+_VALIDATED_MAX = 256
+
+
+def _data_ptrs(q, k, v, state, A_log, a, dt_bias, b, output, new_state) -> tuple:
+    return (q.data_ptr(), k.data_ptr(), v.data_ptr(),
+            None if state is None else state.data_ptr(), A_log.data_ptr(), a.data_ptr(),
+            dt_bias.data_ptr(), b.data_ptr(), output.data_ptr(), new_state.data_ptr())
+
+
+def _evict(key) -> None:
+    entry = _VALIDATED.pop(key, None)
+    if entry is not None:
+        entry.destroy()
+
+
+def _bind(key, tensors, scale: float, B, T, H, HV, use_qk_l2norm) -> _Validated:
+    q, k, v, state, A_log, a, dt_bias, b, output, new_state = tensors
+    lib = _lib.get_lib()
+    handle = ctypes.c_void_p()
+    code = lib.gdn_decode_plan_create(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), None if state is None else state.data_ptr(),
+        A_log.data_ptr(), a.data_ptr(), dt_bias.data_ptr(), b.data_ptr(), scale,
+        output.data_ptr(), new_state.data_ptr(), B, T, H, HV, K_DIM, V_DIM,
+        int(new_state.dtype == torch.bfloat16), int(bool(use_qk_l2norm)), ctypes.byref(handle))
+    _lib.check(code, "gdn_decode_plan_create")
+    entry = _Validated(key, tensors, q.get_device(), handle)
+    if len(_VALIDATED) >= _VALIDATED_MAX:
+        _evict(next(iter(_VALIDATED)))
+    _VALIDATED[key] = entry
+    evict = lambda _ref, key=key: _evict(key)   # noqa: E731
+    entry.refs = [weakref.ref(t, evict) for t in tensors if t is not None]
+    return entry
+
+
 def kernel_hip(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
                *, use_qk_l2norm: bool = False):
     """Destination-passing decode step (reference DPS form,
@@ -213,15 +281,45 @@ def kernel_hip(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
     Writes ``output`` [B, T, HV, 128] bf16 and ``new_state``
     [B, HV, 128, 128] (the state's dtype).  ``new_state is state`` updates in
     place; ``state=None`` starts from zeros (solution/triton/kernel.py:83-86).
+
+    A call with the same tensor objects (unchanged data pointers), a float or
+    None scale and the same flag as an earlier validated call -- a decode
+    loop's steady state -- skips the checks and launches the native plan
+    bound then: one three-argument native call.
     """
+    tp = type(scale)
+    if scale is None or tp is float or tp is int:
+        key = (id(q), id(k), id(v), id(state), id(A_log), id(a), id(dt_bias), id(b),
+               id(output), id(new_state), scale, bool(use_qk_l2norm))
+        entry = _VALIDATED.get(key)
+        if entry is not None and entry.ptrs == _data_ptrs(q, k, v, state, A_log, a, dt_bias,
+                                                          b, output, new_state):
+            # the plan makes its own device current for the launch
+            code = _lib.get_lib().gdn_decode_plan_run(entry.arr, 1,
+                                                      _lib.current_stream(entry.device))
+            if code:
+                _lib.check(code, "gdn_decode_plan_run")
+            return None
+    else:
+        key = None
     if output is None or new_state is None:
         raise ValueError("kernel_hip needs preallocated output and new_state")
     B, T, H, HV = check_inputs(q, k, v, state, A_log, a, dt_bias, b, output, new_state)
-    scale = resolve_scale(scale, q.shape[-1])
+    scale_f = resolve_scale(scale, q.shape[-1])
     if B == 0:
         return None
+    if key is not None:
+        _evict(key)                    # the same objects with new storage
+        with _on_device(q.get_device()):      # the plan records the current device
+            entry = _bind(key, (q, k, v, state, A_log, a, dt_bias, b, output, new_state),
+                          scale_f, B, T, H, HV, use_qk_l2norm)
+        code = _lib.get_lib().gdn_decode_plan_run(entry.arr, 1,
+                                                  _lib.current_stream(entry.device))
+        if code:
+            _lib.check(code, "gdn_decode_plan_run")
+        return None
     # state=None: the kernel starts from zeros and only writes new_state
-    _launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
+    _launch(q, k, v, state, A_log, a, dt_bias, b, scale_f, output, new_state,
             B, T, H, HV, use_qk_l2norm)
     return None
 
@@ -259,8 +357,10 @@ def run(q, k, v, state, A_log, a, dt_bias, b, scale, *, use_qk_l2norm: bool = Fa
     sdtype = torch.float32 if state is None else state.dtype
     output = torch.empty((B, T, HV, V_DIM), dtype=torch.bfloat16, device=q.device)
     new_state = torch.empty((B, HV, V_DIM, K_DIM), dtype=sdtype, device=q.device)
-    kernel_hip(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
-               use_qk_l2norm=use_qk_l2norm)
+    if B > 0:
+        # fresh outputs every call: launched directly, not bound for reuse
+        _launch(q, k, v, state, A_log, a, dt_bias, b, resolve_scale(scale, q.shape[-1]),
+                output, new_state, B, T, H, HV, use_qk_l2norm)
     return output, new_state
 
 

@@ -52,12 +52,14 @@ class DecodePlan:
         scale = resolve_scale(scale, q.shape[-1])
         self._lib = _lib.get_lib()
         handle = ctypes.c_void_p()
-        code = self._lib.gdn_decode_plan_create(
-            q.data_ptr(), k.data_ptr(), v.data_ptr(),
-            None if state is None else state.data_ptr(), A_log.data_ptr(), a.data_ptr(),
-            dt_bias.data_ptr(), b.data_ptr(), scale, output.data_ptr(), new_state.data_ptr(),
-            B, T, H, HV, q.shape[-1], v.shape[-1], int(new_state.dtype == torch.bfloat16),
-            int(bool(use_qk_l2norm)), ctypes.byref(handle))
+        with _on_device(self.device):          # the plan records the current device
+            code = self._lib.gdn_decode_plan_create(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                None if state is None else state.data_ptr(), A_log.data_ptr(), a.data_ptr(),
+                dt_bias.data_ptr(), b.data_ptr(), scale, output.data_ptr(),
+                new_state.data_ptr(), B, T, H, HV, q.shape[-1], v.shape[-1],
+                int(new_state.dtype == torch.bfloat16), int(bool(use_qk_l2norm)),
+                ctypes.byref(handle))
         _lib.check(code, "gdn_decode_plan_create")
         self._handle = handle
         self._one = (ctypes.c_void_p * 1)(handle)
@@ -74,8 +76,8 @@ class DecodePlan:
     def run(self) -> None:
         """One decode step on torch's current stream of the plan's device."""
         self.handle                                # raises once closed
-        with _on_device(self.device):
-            code = self._lib.gdn_decode_plan_run(self._one, 1, _lib.current_stream(self.device))
+        # the plan makes its own device current for the launch
+        code = self._lib.gdn_decode_plan_run(self._one, 1, _lib.current_stream(self.device))
         if code:
             _lib.check(code, "gdn_decode_plan_run")
 
@@ -126,9 +128,8 @@ class DecodeLayers:
     def run(self) -> None:
         """Every layer's step, in order, from one native call (no graph)."""
         self._check_open()
-        with _on_device(self.device):
-            code = self._lib.gdn_decode_plan_run(self._handles, len(self.plans),
-                                                 _lib.current_stream(self.device))
+        code = self._lib.gdn_decode_plan_run(self._handles, len(self.plans),
+                                             _lib.current_stream(self.device))
         if code:
             _lib.check(code, "gdn_decode_plan_run")
 

@@ -159,8 +159,11 @@ int gdn_decode_launch_shape(int B, int T, int HV, int state_bf16,
  * per-call checks.  The pointed-to buffers must stay allocated while the
  * plan (or a graph built from it) is used; their contents may change
  * between runs (the caller writes the next token's q, k, v, a and b into
- * them).  gdn_decode_plan_run launches plans[0 .. n-1] in order on
- * hip_stream.  gdn_decode_plan_create returns the codes gdn_decode_steps
+ * them).  A plan records the device current at its creation (the
+ * buffers' device); gdn_decode_plan_run launches plans[0 .. n-1] in order on
+ * hip_stream (a stream of their device), each with its plan's device made
+ * current for the launch and the caller's restored after.
+ * gdn_decode_plan_create returns the codes gdn_decode_steps
  * returns for the same arguments (hipErrorOutOfMemory if the host
  * allocation fails) and sets *plan to NULL on error.
  *

@@ -154,9 +154,10 @@ def test_validation_rejects_misaligned_and_overlapping_state():
 
 
 def test_plans_validate_once_and_run_without_checks():
-    """gdn_decode_plan_create applies gdn_decode_steps' validation (no HIP
-    call); an empty batch makes a plan whose runs launch nothing; plan_run
-    and graph_create reject null or empty plan lists before any HIP call."""
+    """gdn_decode_plan_create applies gdn_decode_steps' validation (nothing
+    is launched; without a device the plan records none); an empty batch
+    makes a plan whose runs launch nothing; plan_run and graph_create reject
+    null or empty plan lists before any HIP call."""
     lib = _lib.get_lib()
     nulls = [None] * 8
     f = ctypes.c_float(0.1)

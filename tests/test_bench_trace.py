@@ -197,3 +197,24 @@ def test_trace_groups_splits_after_read(tmp_path):
     assert g[2]["grid"] == "256x16x2 / 256" and g[2]["median_us_after_read"] is None
     assert "| `gdn::gdn_decode_block<4, 2, true, true>` | 128x16x1 / 128 | 1 |" in \
         rocprof.groups_table(g)
+
+
+def test_prefill_roofline_reports_the_binding_roof(monkeypatch):
+    """The prefill line names the roof whose floor time is larger (the 64 x
+    512 qk16_v32 workload: 175 FLOP/B, under the bf16 ridge of 312 FLOP/B,
+    so HBM) and carries both roofs' fractions, each computed from the
+    workload's algorithmic bytes / FLOP over the kernel time."""
+    monkeypatch.setattr(bench, "_prefill_traffic", lambda: None)
+    lens, H, HV = bench.PREFILL_CONFIGS[bench.PREFILL_ROOFLINE_WORKLOAD]
+    ku = {"offsets": 6.0, "prep": 110.0, "scan": 400.0, "kernels": 516.0}
+    res = bench.prefill_roofline({bench.PREFILL_ROOFLINE_WORKLOAD: {
+        "kernel_us": ku, "prep_workspace_bytes": 0}})
+    alg = bench.prefill_bytes(lens, H, HV)
+    flop = sum((n + 63) // 64 for n in lens) * HV * bench.PREFILL_FLOP_PER_CHUNK_HEAD
+    assert flop / alg < bench.PEAK_BF16_TFLOPS * 1e12 / (bench.PEAK_HBM_GBS * 1e9)
+    assert res["bound"] == "hbm" and res["unit"] == "GB/s"
+    hbm_frac = alg / 516e-6 / 1e9 / bench.PEAK_HBM_GBS
+    assert res["frac"] == pytest.approx(hbm_frac, abs=1e-4) == res["hbm"]["frac"]
+    assert res["mfma"]["frac"] == pytest.approx(
+        flop / 516e-6 / 1e12 / bench.PEAK_BF16_TFLOPS, abs=1e-4)
+    assert res["hbm"]["floor_us"] > res["mfma"]["floor_us"]

@@ -155,3 +155,52 @@ def test_graph_of_mixed_shapes_and_the_bf16_state(hip_device):
         layers.close()
     for (o_e, s_e), (o_g, s_g) in zip(*runs):
         assert torch.equal(o_e, o_g) and torch.equal(s_e, s_g)
+
+
+def test_repeat_calls_reuse_the_validated_launch(hip_device):
+    """kernel_hip binds a validated call once and reruns its native plan for
+    the same tensor objects: new inputs written into them between calls are
+    used (each step against the oracle from the previous step's state), a
+    tensor whose storage was replaced is validated and bound afresh, a
+    tensor scale always takes the checked path, and freeing a bound tensor
+    evicts its entry."""
+    import gc
+
+    import flashinfer_competition_codebase_amd as gdn
+    from flashinfer_competition_codebase_amd import kernel as kmod
+
+    _announce("kernel_hip repeat calls through the validated path")
+    B, H, HV = 2, 4, 8
+    t = make_inputs(B, H, HV, seed=5300)
+    d = {n: (x.to(hip_device) if isinstance(x, torch.Tensor) else x) for n, x in t.items()}
+    d["output"] = torch.empty(B, 1, HV, 128, dtype=torch.bfloat16, device=hip_device)
+    d["new_state"] = d["state"]
+    ref = t["state"].clone()
+    sizes = []
+    for step in range(4):
+        fresh = make_inputs(B, H, HV, seed=5310 + step)
+        for n in INPUTS:
+            d[n].copy_(fresh[n].to(hip_device))
+            t[n] = fresh[n]
+        if step == 2:                            # same object, new storage
+            d["state"].data = d["state"].clone()
+            d["new_state"] = d["state"]
+        gdn.kernel_hip(**d, use_qk_l2norm=True)
+        torch.cuda.synchronize()
+        ref = _check_step(f"repeat step {step}", t, d, ref, True)
+        sizes.append(len(kmod._VALIDATED))
+    assert sizes[1] == sizes[0] and sizes[3] == sizes[2], sizes   # hits add no entry
+    key_count = sizes[-1]
+    # a 0-d tensor scale is re-read every call: no entry for it
+    gdn.kernel_hip(**{**d, "scale": torch.tensor(t["scale"])}, use_qk_l2norm=True)
+    torch.cuda.synchronize()
+    ref = _check_step("tensor scale", t, d, ref, True)
+    assert len(kmod._VALIDATED) == key_count
+    # freeing a bound tensor evicts the entry (no tensor is kept alive)
+    out = d.pop("output")
+    gdn.kernel_hip(**d, output=out, use_qk_l2norm=True)
+    torch.cuda.synchronize()
+    before = len(kmod._VALIDATED)
+    del out
+    gc.collect()
+    assert len(kmod._VALIDATED) == before - 1
