@@ -122,6 +122,9 @@ bool few_seqs(long long L, long long N, long long HV) {
 // known on the host.
 constexpr int kSmallTokens = 56;
 constexpr float kL2Eps = 1e-6f;
+// v-heads of a GVA group whose gate inputs the preparation kernel loads with
+// the chunk's K rows (the others' when it reaches them).
+constexpr int kPrepGateHeads = 2;
 constexpr float kSoftplusThreshold = 20.0f;
 constexpr float kLn2 = 0.693147180559945309f;
 
@@ -433,13 +436,39 @@ __global__ __launch_bounds__(kThreads) void chunk_offsets_kernel(Params p, int32
 
 // Gates of token t, v-head hv: log-space decay and beta
 // (g = exp(-exp(A_log) softplus(a + dt_bias)), beta = sigmoid(b)).
+__device__ __forceinline__ void gates_of(uint16_t a_raw, uint16_t b_raw, float dt_bias,
+                                         float A_log, float& logg, float& beta) {
+  const float x = bf16_to_f32(a_raw) + dt_bias;
+  const float sp = x > kSoftplusThreshold ? x : __builtin_amdgcn_logf(1.0f + __expf(x)) * kLn2;
+  logg = -__expf(A_log) * sp;
+  beta = __builtin_amdgcn_rcpf(1.0f + __expf(-bf16_to_f32(b_raw)));
+}
+
 __device__ __forceinline__ void token_gates(const Params& p, int t, int hv, float& logg,
                                             float& beta) {
-  const float x = bf16_to_f32(p.a[static_cast<size_t>(t) * p.HV + hv]) + p.dt_bias[hv];
-  const float sp = x > kSoftplusThreshold ? x : __builtin_amdgcn_logf(1.0f + __expf(x)) * kLn2;
-  logg = -__expf(p.A_log[hv]) * sp;
-  const float bb = bf16_to_f32(p.b[static_cast<size_t>(t) * p.HV + hv]);
-  beta = __builtin_amdgcn_rcpf(1.0f + __expf(-bb));
+  gates_of(p.a[static_cast<size_t>(t) * p.HV + hv], p.b[static_cast<size_t>(t) * p.HV + hv],
+           p.dt_bias[hv], p.A_log[hv], logg, beta);
+}
+
+// One DPP step of a wave scan: x from the lane CTRL names (0 where it names
+// none, or in rows ROW_MASK leaves out).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add_src(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),
+                                                               CTRL, ROW_MASK, 0xf, false));
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave: shifts by 1, 2, 4 and 8
+// within each row of 16 lanes (row_shr), then lane 15's total added to rows
+// 1 and 3 and lane 31's to rows 2 and 3 (row_bcast:15, row_bcast:31).
+__device__ __forceinline__ float wave_prefix_sum(float x) {
+  x += dpp_add_src<0x111, 0xf>(x);
+  x += dpp_add_src<0x112, 0xf>(x);
+  x += dpp_add_src<0x114, 0xf>(x);
+  x += dpp_add_src<0x118, 0xf>(x);
+  x += dpp_add_src<0x142, 0xa>(x);
+  x += dpp_add_src<0x143, 0xc>(x);
+  return x;
 }
 
 // Rows [0, 64) of a [*, stride, 128] bf16 tensor (row r at base + r * step
@@ -480,7 +509,7 @@ __device__ __forceinline__ void store_rows_bf16(uint16_t* dst, const u32x4 (&val
 // barrier between its last K read and the first write of A).  The 32 x 32
 // scratch of the block recursion is T's upper-right quarter, which T never
 // uses (rows 0..31, columns 32..63).
-struct PrepLds {
+struct __attribute__((aligned(16))) PrepLds {
   union {
     uint16_t K[kChunk * kBfStride];   // the chunk's K rows, until K K^T
     float A[kChunk * kF64Stride];     // then: strict lower part of (I + A) minus I
@@ -551,6 +580,21 @@ void prep_kernel(Params p) {
   u32x4 kreg[4];
   load_rows_bf16(kreg, p.k + (static_cast<size_t>(t0) * p.H + h) * kDim,
                  static_cast<size_t>(p.H) * kDim, n);
+  // wave 0's gate inputs (a, b of token t0 + lane) of the group's first
+  // kPrepGateHeads v-heads, in flight with the K rows
+  uint16_t a_raw[kPrepGateHeads], b_raw[kPrepGateHeads];
+  float dtb[kPrepGateHeads], alog[kPrepGateHeads];
+  if (wave == 0) {
+    const size_t tk = static_cast<size_t>(t0 + (lane < n ? lane : n - 1)) * p.HV + h * p.ratio;
+#pragma unroll
+    for (int j = 0; j < kPrepGateHeads; ++j) {
+      const int jj = j < p.ratio ? j : 0;
+      a_raw[j] = p.a[tk + jj];
+      b_raw[j] = p.b[tk + jj];
+      dtb[j] = p.dt_bias[h * p.ratio + jj];
+      alog[j] = p.A_log[h * p.ratio + jj];
+    }
+  }
 
   store_rows_bf16(lds.K, kreg, n);
   // T's upper blocks that the block recursion multiplies, T_01 and T_23, are
@@ -612,15 +656,18 @@ void prep_kernel(Params p) {
     // inclusive scan of the log-decay over the chunk
     if (wave == 0) {
       float logg, beta;
-      token_gates(p, t0 + (lane < n ? lane : n - 1), hv, logg, beta);
-      if (lane >= n) logg = beta = 0.0f;
-      float g = logg;
+      if (j < kPrepGateHeads) {
+        uint16_t ar = a_raw[0], br = b_raw[0];
+        float dt = dtb[0], al = alog[0];
 #pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const float y = __shfl_up(g, d, 64);
-        if (lane >= d) g += y;
+        for (int jj = 1; jj < kPrepGateHeads; ++jj)
+          if (j == jj) { ar = a_raw[jj]; br = b_raw[jj]; dt = dtb[jj]; al = alog[jj]; }
+        gates_of(ar, br, dt, al, logg, beta);
+      } else {
+        token_gates(p, t0 + (lane < n ? lane : n - 1), hv, logg, beta);
       }
-      lds.gamma[lane] = g;
+      if (lane >= n) logg = beta = 0.0f;
+      lds.gamma[lane] = wave_prefix_sum(logg);
       lds.beta[lane] = beta;
     }
     block_sync_lds();
@@ -653,15 +700,27 @@ void prep_kernel(Params p) {
     // triangular, so T is unit lower triangular; the upper blocks stay zero):
     // 1. each wave inverts one diagonal block by forward substitution (one
     //    column per lane, two partial sums per dot product);
+    //    Row r's entries of A are read as 16-byte vectors a row ahead of
+    //    their use (read when used, their LDS latency was most of the
+    //    substitution's).
     if (lane < 16) {
       const int b0 = wave * 16;
+      const float* arow = &lds.A[b0 * kF64Stride + b0];
       float t[16];
+      f32x4 ar[16][4];
+      auto read_row = [&](int r) {
+#pragma unroll
+        for (int q = 0; q < (r + 3) / 4; ++q)
+          ar[r][q] = *reinterpret_cast<const f32x4*>(&arow[r * kF64Stride + 4 * q]);
+      };
+      read_row(1);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
+        if (r + 1 < 16) read_row(r + 1);
         float s0 = (r == lane) ? 1.0f : 0.0f, s1 = 0.0f;
 #pragma unroll
         for (int j = 0; j < r; ++j) {
-          const float aij = lds.A[(b0 + r) * kF64Stride + b0 + j];
+          const float aij = ar[r][j >> 2][j & 3];
           if (j & 1) s1 = fmaf(-aij, t[j], s1); else s0 = fmaf(-aij, t[j], s0);
         }
         t[r] = s0 + s1;
