@@ -93,11 +93,11 @@ hipError_t launch_one(bool l2, const Params& p, unsigned nb, const Launch& l) {
   if (l.start || l.stop) {
     hipExtLaunchKernelGGL(kern, grid, block, 0, l.stream, l.start, l.stop, 0, p.state, p.q,
                           p.k, p.v, p.a, p.b, h_ratio, p.T, p.A_log, p.dt_bias, p.out,
-                          p.new_state, p.scale, no_seqlens, 0);
+                          p.new_state, p.scale, no_seqlens, 0, 0);
   } else {
     hipLaunchKernelGGL(kern, grid, block, 0, l.stream, p.state, p.q, p.k, p.v, p.a, p.b,
                        h_ratio, p.T, p.A_log, p.dt_bias, p.out, p.new_state, p.scale,
-                       no_seqlens, 0);
+                       no_seqlens, 0, 0);
   }
   return hipGetLastError();
 }

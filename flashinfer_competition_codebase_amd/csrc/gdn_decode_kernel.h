@@ -500,8 +500,10 @@ __device__ __forceinline__ void token_rows_lazy(float (&s)[NS][8], const TokenHe
 // (b, hv) head per workgroup.  VARLEN (multi-token only): sequence b is the
 // token rows [cu_seqlens[b], cu_seqlens[b + 1]) of packed [L, H|HV, ...]
 // inputs (the prefill layout), clamped to [0, L]; a sequence with no tokens
-// gets a zero state.  MULTI: a null state starts from zeros (the state
-// stream is then only written).
+// gets a zero state; with short_limit > 0 (at most 64 sequences) the
+// workgroups run only if every sequence has at most short_limit tokens.
+// MULTI: a null state starts from zeros (the state stream is then only
+// written).
 //
 // The arguments are scalars rather than one struct so that the first 14
 // dwords -- every pointer and size the first loads need: six pointers, H and
@@ -554,7 +556,7 @@ __device__ __forceinline__ void decode_body(
     const void* state, const uint16_t* q, const uint16_t* k, const uint16_t* v,
     const uint16_t* a, const uint16_t* b, unsigned h_ratio, int T_arg, const float* A_log_p,
     const float* dt_bias_p, uint16_t* out, void* new_state, float scale,
-    const int32_t* cu_seqlens, int total_tokens, unsigned long long* stamps) {
+    const int32_t* cu_seqlens, int total_tokens, int short_limit, unsigned long long* stamps) {
   static_assert(MULTI || !VARLEN, "variable-length sequences run the multi-token loop");
   static_assert(!STAMP || (!MULTI && !BF16), "phase stamps: the fp32 single-token kernel");
   unsigned long long st[kStampsPerWave] = {};
@@ -607,6 +609,20 @@ __device__ __forceinline__ void decode_body(
     s1 = s1 < s0 ? s0 : (s1 > total_tokens ? total_tokens : s1);
     tok0 = static_cast<size_t>(s0);
     T = s1 - s0;
+    if (short_limit > 0) {
+      // Only if every sequence of the batch (gridDim.z <= 64 of them) has at
+      // most short_limit tokens; else the chunkwise kernels launched after
+      // this one run the whole batch.  One read per lane, the same clamping.
+      int len = 0;
+      if (lane < static_cast<int>(gridDim.z)) {
+        int c0 = cu_seqlens[lane];
+        int c1 = cu_seqlens[lane + 1];
+        c0 = c0 < 0 ? 0 : (c0 > total_tokens ? total_tokens : c0);
+        c1 = c1 < c0 ? c0 : (c1 > total_tokens ? total_tokens : c1);
+        len = c1 - c0;
+      }
+      if (__ballot(len > short_limit) != 0) return;      // uniform per block
+    }
     if (T == 0) {                      // no tokens: a zero state (uniform per block)
       const float zero[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -803,10 +819,10 @@ __attribute__((amdgpu_waves_per_eu(1, (MULTI && !BF16 && NS == 2) ? 6 : 8))) voi
     const void* state, const uint16_t* q, const uint16_t* k, const uint16_t* v,
     const uint16_t* a, const uint16_t* b, unsigned h_ratio, int T_arg, const float* A_log_p,
     const float* dt_bias_p, uint16_t* out, void* new_state, float scale,
-    const int32_t* cu_seqlens, int total_tokens) {
+    const int32_t* cu_seqlens, int total_tokens, int short_limit) {
   decode_body<NS, WAVES, L2NORM, POLICY, BF16, MULTI, VARLEN, false>(
       state, q, k, v, a, b, h_ratio, T_arg, A_log_p, dt_bias_p, out, new_state, scale,
-      cu_seqlens, total_tokens, nullptr);
+      cu_seqlens, total_tokens, short_limit, nullptr);
 }
 
 // The fp32 single-token kernel with phase stamps (kStampsPerWave per wave,
@@ -821,7 +837,7 @@ void gdn_decode_k128_stamped(
     const int32_t* cu_seqlens, int total_tokens, unsigned long long* stamps) {
   decode_body<NS, WAVES, L2NORM, kPolicyNtBoth, false, false, false, true>(
       state, q, k, v, a, b, h_ratio, T_arg, A_log_p, dt_bias_p, out, new_state, scale,
-      cu_seqlens, total_tokens, stamps);
+      cu_seqlens, total_tokens, 0, stamps);
 }
 
 }  // namespace gdn

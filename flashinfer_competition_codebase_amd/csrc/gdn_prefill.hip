@@ -118,9 +118,19 @@ bool few_seqs(long long L, long long N, long long HV) {
 // the last event of the timed entry): the token path is 1-3.5 us faster up to
 // 56 tokens at qk4_v8 and qk16_v32, the chunkwise kernels faster from 64.
 // Several short sequences favour the token path far more (4 x 20 tokens: 21.2
-// against 33.5 us at qk4_v8), but past the switch the longest sequence is not
-// known on the host.
+// against 33.5 us at qk4_v8); past the switch the longest sequence is known
+// only on the device (maybe_all_short below).
 constexpr int kSmallTokens = 56;
+
+// Batches of 2..kFewSeqs sequences with at most kSmallTokens tokens a
+// sequence on average may have no longer sequence, which only cu_seqlens on
+// the device tells: they launch the token-by-token kernel first (it runs
+// only if every sequence is that short) and then the chunkwise kernels
+// (which return at once in that case).  4 sequences of 20 tokens at qk4_v8
+// then take the token kernel's time instead of the chunkwise kernels'.
+bool maybe_all_short(long long L, long long N) {
+  return L > kSmallTokens && N >= 2 && N <= kFewSeqs && L <= N * kSmallTokens;
+}
 constexpr float kL2Eps = 1e-6f;
 // v-heads of a GVA group whose gate inputs the preparation kernel loads with
 // the chunk's K rows (the others' when it reaches them).
@@ -265,6 +275,10 @@ struct Params {
   float* seg_S;              // [nseg, HV] state at each segment's start (1 .. nseg-1)
   float* seg_B;              // [nseg, HV] state at its end from a zero start
   float* seg_M;              // [nseg, HV] its transition: end = M start + B (M[k][k'])
+  // > 0: the token-by-token kernel was launched first with this limit (at
+  // most kFewSeqs sequences); if every sequence has at most this many tokens
+  // it ran the whole prefill and these kernels return at once.
+  int short_limit;
 };
 
 // Token range [start, end) of sequence s, clamped to [0, L] so that no
@@ -276,6 +290,19 @@ __device__ __forceinline__ void seq_range(const Params& p, int s, int& start, in
   s1 = s1 < s0 ? s0 : (s1 > p.L ? p.L : s1);
   start = s0;
   end = s1;
+}
+
+// Whether every sequence of a batch of at most 64 has at most `limit`
+// tokens (one read per lane, the clamping of seq_range; uniform).
+__device__ __forceinline__ bool all_within(const Params& p, int limit) {
+  const int lane = threadIdx.x & 63;
+  int len = 0;
+  if (lane < p.N) {
+    int s0, s1;
+    seq_range(p, lane, s0, s1);
+    len = s1 - s0;
+  }
+  return __ballot(len > limit) == 0;
 }
 
 // Chunk slots of a batch of at most 64 sequences, from cu_seqlens in one
@@ -384,6 +411,7 @@ __global__ __launch_bounds__(kThreads) void chunk_offsets_kernel(Params p, int32
   __shared__ int32_t grp_end[kThreads];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  if (p.short_limit > 0 && all_within(p, p.short_limit)) return;    // uniform
   long long carry = 0;
   if (threadIdx.x == 0) offs[0] = 0;
   for (int base = 0; base < p.N; base += kThreads) {
@@ -547,6 +575,7 @@ void prep_kernel(Params p) {
   __shared__ PrepLds lds;
   const int c = blockIdx.x;
   const int h = blockIdx.y;
+  if (p.short_limit > 0 && all_within(p, p.short_limit)) return;    // uniform
   int t0, n;                                       // n: 1..64, 0 past the last slot
   if (p.single) {
     int start, end;
@@ -1369,6 +1398,7 @@ void scan_kernel(Params p) {
   const long long units = SEG ? (OUT ? p.nseg : seg_units1(p.nseg, p.N))
                               : static_cast<long long>(p.N);
   if (pair >= units * p.H) return;                              // uniform per workgroup
+  if (p.short_limit > 0 && all_within(p, p.short_limit)) return;  // uniform
   const int unit = static_cast<int>(pair / p.H);
   const int h = static_cast<int>(pair % p.H);
   const int hv = h * ratio + jr;
@@ -1725,7 +1755,7 @@ static hipError_t small_prefill(const void* q, const void* k, const void* v, con
                                 const float* A_log, const void* a, const float* dt_bias,
                                 const void* b, const int32_t* cu_seqlens, float scale,
                                 void* output, float* new_state, int L, int N, int H, int HV,
-                                bool l2, hipStream_t stream) {
+                                bool l2, int short_limit, hipStream_t stream) {
   constexpr int kNs = 1;
   constexpr int kPolicy = gdn::kPolicyDefault;   // the next decode step re-reads the state
   const unsigned ratio = static_cast<unsigned>(HV / H);
@@ -1742,14 +1772,16 @@ static hipError_t small_prefill(const void* q, const void* k, const void* v, con
     auto* kern = l2 ? gdn::gdn_decode_k128<kNs, kW, true, kPolicy, false, true, true>
                     : gdn::gdn_decode_k128<kNs, kW, false, kPolicy, false, true, true>;
     hipLaunchKernelGGL(kern, grid, dim3(64 * kW), 0, stream, state, q16, k16, v16, a16, b16,
-                       h_ratio, 0, A_log, dt_bias, out16, new_state, scale, cu_seqlens, L);
+                       h_ratio, 0, A_log, dt_bias, out16, new_state, scale, cu_seqlens, L,
+                       short_limit);
   } else {
     constexpr int kW = 4;
     const dim3 grid(ratio * (kDim / (gdn::kLaneGroups * kNs * kW)), H, N);
     auto* kern = l2 ? gdn::gdn_decode_k128<kNs, kW, true, kPolicy, false, true, true>
                     : gdn::gdn_decode_k128<kNs, kW, false, kPolicy, false, true, true>;
     hipLaunchKernelGGL(kern, grid, dim3(64 * kW), 0, stream, state, q16, k16, v16, a16, b16,
-                       h_ratio, 0, A_log, dt_bias, out16, new_state, scale, cu_seqlens, L);
+                       h_ratio, 0, A_log, dt_bias, out16, new_state, scale, cu_seqlens, L,
+                       short_limit);
   }
   return hipGetLastError();
 }
@@ -1879,6 +1911,7 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
   p.single = num_seqs == 1;
   p.few = few_seqs(total_seq_len, num_seqs, HV);
   p.max_slots = slots;
+  p.short_limit = maybe_all_short(total_seq_len, num_seqs) ? kSmallTokens : 0;
 
   hipStream_t stream = static_cast<hipStream_t>(hip_stream);
   // events[i] (optional) is recorded before launch i and events[3] after the last
@@ -1893,12 +1926,22 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
     if (e == hipSuccess) e = mark(2);
     if (e != hipSuccess) return e;
     e = small_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output,
-                      new_state, total_seq_len, num_seqs, H, HV, use_qk_l2norm != 0, stream);
+                      new_state, total_seq_len, num_seqs, H, HV, use_qk_l2norm != 0, 0, stream);
     if (e == hipSuccess) e = mark(3);
     return e;
   }
   hipError_t e = mark(0);
   if (e != hipSuccess) return e;
+  if (p.short_limit > 0) {
+    // A batch whose sequences may all be short: the token-by-token kernel
+    // first, running only if every sequence has at most kSmallTokens tokens
+    // (decided on the device from cu_seqlens); the chunkwise kernels after it
+    // return at once in that case and run the whole batch otherwise.
+    e = small_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output,
+                      new_state, total_seq_len, num_seqs, H, HV, use_qk_l2norm != 0,
+                      p.short_limit, stream);
+    if (e != hipSuccess) return e;
+  }
   if (!p.single && !p.few)
     hipLaunchKernelGGL(chunk_offsets_kernel, dim3(1), dim3(kThreads), 0, stream, p, offs,
                        slot_info);
@@ -1999,8 +2042,9 @@ int gdn_prefill_dispatches(int total_seq_len, int num_seqs, int HV) {
   if (num_seqs <= 0 || total_seq_len < 0 || HV <= 0) return 0;
   if (total_seq_len <= kSmallTokens && num_seqs <= 65535) return 1;
   const int offsets = num_seqs == 1 || few_seqs(total_seq_len, num_seqs, HV) ? 0 : 1;
-  if (use_segments(total_seq_len, num_seqs, HV)) return offsets + 4;
-  return offsets + 2;
+  const int token = maybe_all_short(total_seq_len, num_seqs) ? 1 : 0;
+  if (use_segments(total_seq_len, num_seqs, HV)) return token + offsets + 4;
+  return token + offsets + 2;
 }
 
 int gdn_prefill_abi_version(void) { return 6; }

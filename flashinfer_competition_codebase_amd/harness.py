@@ -158,9 +158,10 @@ class PrefillWorkload:
 
 
 def prefill_workloads() -> list:
-    """A seeded mix of 20 qk4_v8 prefill workloads: the reference's workload 0
+    """A seeded mix of 21 qk4_v8 prefill workloads: the reference's workload 0
     (one 6-token sequence), single sequences across the chunk boundaries and
-    up to 16384 tokens, uniform and ragged batches, and empty sequences."""
+    up to 16384 tokens, uniform and ragged batches, empty sequences, and a
+    batch of short sequences past the total-token switch (4 x 20)."""
     g = torch.Generator().manual_seed(4242)
 
     def ragged(n, hi):
@@ -170,6 +171,7 @@ def prefill_workloads() -> list:
         (6,), (1,), (64,), (65,), (127,), (512,), (1000,), (2048,), (4096,), (8192,),
         (16384,), (100, 200, 300, 400), (128,) * 8, (256,) * 16, (1024,) * 16,
         (512,) * 32, (64,) * 64, ragged(24, 2048), ragged(8, 8192), (0, 17, 0, 300),
+        (20,) * 4,
     ]
     return [PrefillWorkload(uuid=f"prefill-w{i:02d}", lens=lens, seed=20_000 + i)
             for i, lens in enumerate(mixes)]

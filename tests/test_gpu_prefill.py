@@ -565,3 +565,66 @@ def test_small_prefill_in_place_and_timed(hip_device):
     finally:
         for e in evs:
             hip.hipEventDestroy(e)
+
+
+@pytest.mark.parametrize("seqlens,H,HV,l2", [
+    ([20] * 4, 4, 8, False),          # 80 tokens: all short, the token kernel runs
+    ([5] * 64, 4, 8, False),          # 64 sequences, all short
+    ([56, 56], 16, 32, True),         # exactly at the limit: token kernel
+    ([57, 50], 4, 8, False),          # one sequence past the limit: the chunkwise kernels
+    ([150] + [3] * 10, 2, 6, False),  # one long among short ones: chunkwise
+    ([0, 30, 0, 40], 4, 8, True),     # empty sequences among short ones
+])
+def test_batches_that_may_all_be_short(seqlens, H, HV, l2, hip_device):
+    """Batches of 2..64 sequences of at most 56 tokens on average: the token
+    kernel is launched first and runs only if every sequence has at most 56
+    tokens (read from cu_seqlens on the device), the chunkwise kernels after
+    it return at once then and run the whole batch otherwise; either way
+    every output row and state matches the oracle."""
+    L, N = sum(seqlens), len(seqlens)
+    assert L > gdn.prefill.token_path_max_tokens()
+    assert gdn.prefill.prefill_dispatches(L, N, HV) >= 3
+    _announce(f"may-all-be-short batch seqlens={seqlens[:6]}.. N={N} H={H} HV={HV} l2={l2}")
+    t = make_prefill_inputs(seqlens, H, HV, seed=600 + L + N)
+    out = torch.full((L, HV, 128), float("nan"), dtype=torch.bfloat16, device=hip_device)
+    st = torch.full((N, HV, 128, 128), float("nan"), device=hip_device)
+    gdn.kernel_prefill_hip(**_dev(t, hip_device), output=out, new_state=st, use_qk_l2norm=l2)
+    torch.cuda.synchronize()
+    _check(t, out, st, l2=l2)
+
+
+@pytest.mark.parametrize("cu,n0", [
+    ([0, 30, 10, 50, 45, 90], 30),    # clamped lengths 30, 0, 40, 0, 45: the token kernel
+    ([0, 60, 10, 70, 65, 90], 60),    # the first is 60 tokens: the chunkwise kernels
+])
+def test_malformed_cu_seqlens_when_all_may_be_short(cu, n0, hip_device):
+    """Decreasing cu_seqlens in a batch that may be all short (every path
+    clamps the ranges alike, so exactly one of them writes each result): the
+    call completes with finite results, twice the same states (the output
+    rows of overlapping ranges are written by several sequences, in no fixed
+    order), and the first, well-formed sequence gets the state it gets alone
+    (alone it takes the same path: the token kernel at 30 tokens, the
+    chunkwise ones at 60)."""
+    L = 90
+    N = len(cu) - 1
+    assert gdn.prefill.prefill_dispatches(L, N, 8) >= 3
+    _announce(f"malformed cu_seqlens, may-all-be-short batch N={N} L={L}")
+    t = make_prefill_inputs([L] + [0] * (N - 1), 4, 8, seed=93)
+    t["cu_seqlens"] = torch.tensor(cu, dtype=torch.int32)
+    d = _dev(t, hip_device)
+    runs = []
+    for _ in range(2):
+        out = torch.zeros(L, 8, 128, dtype=torch.bfloat16, device=hip_device)
+        st = torch.full((N, 8, 128, 128), float("nan"), device=hip_device)
+        gdn.kernel_prefill_hip(**d, output=out, new_state=st)
+        torch.cuda.synchronize()
+        runs.append((out, st))
+    out, st = runs[0]
+    assert bool(torch.isfinite(out.float()).all()) and bool(torch.isfinite(st).all())
+    assert bool(torch.isfinite(runs[1][0].float()).all()) and torch.equal(runs[1][1], st)
+    alone = {**t, "q": t["q"][:n0], "k": t["k"][:n0], "v": t["v"][:n0], "a": t["a"][:n0],
+             "b": t["b"][:n0], "state": t["state"][:1],
+             "cu_seqlens": torch.tensor([0, n0], dtype=torch.int32)}
+    _, st1 = gdn.prefill_run(**_dev(alone, hip_device))
+    torch.cuda.synchronize()
+    assert torch.equal(st[:1], st1)

@@ -153,8 +153,9 @@ def test_evaluate_rejects_unknown_tier_and_flush():
 
 def test_prefill_mix():
     ws = harness.prefill_workloads()
-    assert len(ws) == 20
-    assert len({w.uuid for w in ws}) == 20 and len({w.seed for w in ws}) == 20
+    assert len(ws) == 21
+    assert len({w.uuid for w in ws}) == 21 and len({w.seed for w in ws}) == 21
+    assert ws[20].lens == (20,) * 4                  # short sequences past the total switch
     assert ws[0].lens == (6,)                        # the reference's workload 0
     assert all((w.H, w.HV, w.use_qk_l2norm) == (4, 8, False) for w in ws)
     assert any(0 in w.lens for w in ws)              # empty sequences
@@ -168,9 +169,10 @@ def test_prefill_mix():
         if w.L <= small:
             return 1                                  # the token path
         offsets = 0 if w.N == 1 or (w.N <= 64 and slots * w.HV <= 2048) else 1
+        token = 1 if 2 <= w.N <= 64 and w.L <= w.N * small else 0   # token kernel first
         if prefill_segment_plan(w.L, w.N, w.HV)[0]:
-            return offsets + 4                        # segments
-        return offsets + 2
+            return token + offsets + 4                # segments
+        return token + offsets + 2
 
     assert all(w.dispatches == expected(w) for w in ws)
     assert harness.prefill_workloads() == ws         # seeded: the same mix every time
@@ -281,9 +283,15 @@ def test_prefill_dispatch_count_follows_the_token_path_threshold():
     m = token_path_max_tokens()
     assert m == 56
     assert prefill_dispatches(m, 1, 8) == 1 and prefill_dispatches(0, 5, 8) == 1
-    assert prefill_dispatches(m + 1, 1, 8) == 2 and prefill_dispatches(m + 1, 2, 8) == 2
-    assert prefill_dispatches(m + 1, 64, 8) == 2          # slots found in the kernels
+    assert prefill_dispatches(m + 1, 1, 8) == 2           # one longer sequence
+    # 2..64 sequences of at most m tokens on average: the token kernel first
+    # (it runs if every sequence is that short), then prep and scan
+    assert prefill_dispatches(m + 1, 2, 8) == 3
+    assert prefill_dispatches(2 * m, 2, 8) == 3 and prefill_dispatches(2 * m + 1, 2, 8) == 2
+    assert prefill_dispatches(80, 4, 8) == 3              # 4 x 20 tokens
+    assert prefill_dispatches(m + 1, 64, 8) == 3          # slots found in the kernels
     assert prefill_dispatches(m + 1, 65, 8) == 3          # the chunk-offsets scan first
+    assert prefill_dispatches(65 * m + 1, 65, 8) == 3
     assert prefill_dispatches(640, 8, 8) == 2             # 10 chunks + 8: slots in the kernels
     assert prefill_dispatches(8192, 8, 8) == 4            # 8 x 16 chunks at 8 v-heads: segments
     assert prefill_dispatches(8192, 16, 32) == 3          # (128 + 16) x 32 = 4608, 512 heads

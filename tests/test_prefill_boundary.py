@@ -63,9 +63,11 @@ def test_workspace_size_formula():
             want += 3 * a256(nseg * HV * 128 * 128 * 4)
         assert lib.gdn_prefill_workspace_bytes(L, N, H, HV) == want, (L, N, H, HV)
         offsets = 0 if N == 1 or (N <= 64 and chunks * HV <= 2048) else 1
+        # 2..64 sequences of at most 56 tokens on average: the token kernel first
+        token = 1 if 2 <= N <= 64 and 56 < L <= 56 * N else 0
         assert lib.gdn_prefill_dispatches(L, N, HV) == (
             0 if N == 0 else 1 if L <= 56 and N <= 65535 else
-            offsets + (4 if seg else 2)), (L, N, HV)
+            token + offsets + (4 if seg else 2)), (L, N, HV)
     assert lib.gdn_prefill_workspace_bytes(-1, 1, 4, 8) == 0
     assert lib.gdn_prefill_workspace_bytes(1, 1, 4, 0) == 0
     assert lib.gdn_prefill_workspace_bytes(1, 1, 3, 8) == 0              # HV % H != 0
