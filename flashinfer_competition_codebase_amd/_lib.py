@@ -137,16 +137,21 @@ def get_prefill_lib() -> ctypes.CDLL:
 _raw_stream = None
 
 
-def current_stream(device_index: int) -> int:
-    """Raw ``hipStream_t`` of torch's current stream on ``device_index``
-    (torch's raw accessor where it has one: the public ``current_stream``
-    builds a Stream object per call)."""
+def raw_stream_accessor():
+    """The function ``device_index -> raw hipStream_t`` of torch's current
+    stream on that device (torch's raw accessor where it has one: the public
+    ``current_stream`` builds a Stream object per call)."""
     global _raw_stream
     if _raw_stream is None:
         import torch
         _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None) or (
             lambda i: torch.cuda.current_stream(i).cuda_stream)
-    return _raw_stream(device_index)
+    return _raw_stream
+
+
+def current_stream(device_index: int) -> int:
+    """Raw ``hipStream_t`` of torch's current stream on ``device_index``."""
+    return (_raw_stream or raw_stream_accessor())(device_index)
 
 
 def error_string(code: int) -> str:

@@ -897,6 +897,20 @@ __device__ __forceinline__ void dma16(const void* src_l, void* dst) {
   __builtin_amdgcn_global_load_lds((global_void*)src_l, (lds_void*)dst, 16, 0, 0);
 }
 
+// The same from a workgroup-uniform base and a 32-bit byte offset per lane:
+// the address form of the instruction with the base in scalar registers, so
+// no lane forms a 64-bit address.
+__device__ __forceinline__ void dma16_at(const void* base, unsigned byte_off, void* dst) {
+  dma16(static_cast<const char*>(base) + byte_off, dst);
+}
+
+// Byte offset of element `item` of token row `row` (< 64) of a bf16 matrix
+// whose rows are `step` (< 2^24) elements apart: a 24-bit product, one
+// full-rate instruction where a 32-bit one takes four.
+__device__ __forceinline__ unsigned row_bytes(int row, unsigned step, unsigned item) {
+  return 2u * (__umul24(static_cast<unsigned>(row), step) + item);
+}
+
 // Wait for this wave's outstanding vector memory operations (its DMA among
 // them): s_waitcnt vmcnt(0), the other counters left alone.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
@@ -922,12 +936,12 @@ __device__ __forceinline__ void scan_dma(ScanBuf<OUT>& B, const uint16_t* kbase,
   for (int i = wave; i < kRowDma; i += kScanWaves) {        // uniform per wave
     const int pc = i * 64 + lane;
     const int r = pc / kRowPieces, c = pc % kRowPieces;
-    const unsigned off = static_cast<unsigned>(r < n ? r : n - 1) * step + (c < 16 ? c : 15) * 8;
-    dma16(kbase + off, &B.Kr[i * 512]);
-    if constexpr (OUT) dma16(qbase + off, &B.Qr[i * 512]);
+    const unsigned off = row_bytes(r < n ? r : n - 1, step, (c < 16 ? c : 15) * 8);
+    dma16_at(kbase, off, &B.Kr[i * 512]);
+    if constexpr (OUT) dma16_at(qbase, off, &B.Qr[i * 512]);
   }
   for (int i = wave; i < kSlotDma; i += kScanWaves)
-    dma16(slot + (i * 64 + lane) * 4, &B.slot[i * 256]);
+    dma16_at(slot, static_cast<unsigned>(i * 64 + lane) * 16u, &B.slot[i * 256]);
 }
 
 // This wave's 16 columns of V for token tile r (lane (col, g): token
@@ -937,8 +951,9 @@ __device__ __forceinline__ void load_v(u32x2 (&f)[4], const uint16_t* vbase, uns
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int row = r * 16 + col;
-    f[r] = *reinterpret_cast<const u32x2*>(vbase + static_cast<unsigned>(row < n ? row : n - 1) *
-                                                       step + wave * 16 + g4 * 4);
+    f[r] = *reinterpret_cast<const u32x2*>(
+        reinterpret_cast<const char*>(vbase) + row_bytes(row < n ? row : n - 1, step,
+                                                         wave * 16 + g4 * 4));
   }
 }
 
@@ -1023,15 +1038,15 @@ __device__ __forceinline__ void issue_part(ScanBuf<OUT>* __restrict__ Bn, const 
     if (i < kRowDma) {                                      // uniform per wave
       const int pc = i * 64 + lane;
       const int r = pc / kRowPieces, c = pc % kRowPieces;
-      const unsigned off =
-          static_cast<unsigned>(r < s.n ? r : s.n - 1) * cx.kstep + (c < 16 ? c : 15) * 8;
-      dma16(s.kbase + off, &Bn->Kr[i * 512]);
-      if constexpr (OUT) dma16(s.qbase + off, &Bn->Qr[i * 512]);
+      const unsigned off = row_bytes(r < s.n ? r : s.n - 1, cx.kstep, (c < 16 ? c : 15) * 8);
+      dma16_at(s.kbase, off, &Bn->Kr[i * 512]);
+      if constexpr (OUT) dma16_at(s.qbase, off, &Bn->Qr[i * 512]);
     }
   }
   if (part >= 2) {
     const int i = wave + kScanWaves * (part - 2);
-    if (i < kSlotDma) dma16(s.slot + (i * 64 + lane) * 4, &Bn->slot[i * 256]);
+    if (i < kSlotDma)
+      dma16_at(s.slot, static_cast<unsigned>(i * 64 + lane) * 16u, &Bn->slot[i * 256]);
   }
   if (part == 3) load_v(vf, s.vbase, cx.vstep, s.n, wave, lane & 15, lane >> 4);
 }
@@ -1288,6 +1303,7 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
   // O^T = rq (.) (qs (.) S^T Q^T + Delta^T P'^T); lane (col, g) ends with
   // columns 16 wave + 4 g + e of token 16 r + col, one 8-byte store
   if constexpr (OUT) {
+    uint16_t* const obase = cx.out + (static_cast<size_t>(t0) * cx.HV + cx.hv) * kDim;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       if (r < 2) read_p(r + 2);
@@ -1303,8 +1319,8 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
       const int tok = r * 16 + col;
       const u32x2 ob = {pack_bf16x2(o[r][0], o[r][1]), pack_bf16x2(o[r][2], o[r][3])};
       if (tok < n)
-        *reinterpret_cast<u32x2*>(cx.out + ((static_cast<size_t>(t0) + tok) * cx.HV + cx.hv) *
-                                               kDim + wave * 16 + g4 * 4) = ob;
+        *reinterpret_cast<u32x2*>(reinterpret_cast<char*>(obase) +
+                                  row_bytes(tok, cx.vstep, wave * 16 + g4 * 4)) = ob;
     }
   }
 

@@ -38,6 +38,7 @@ launched.
 from __future__ import annotations
 
 import ctypes
+import functools
 import math
 import weakref
 
@@ -214,9 +215,10 @@ class _Validated:
     objects -- while they live: a weak reference to each evicts the entry
     when that tensor is freed, so an id is never reused under a live entry
     -- and by their data pointers, compared on every call (a tensor whose
-    storage was swapped in place is validated afresh)."""
+    storage was swapped in place is validated afresh).  ``run(stream)`` is
+    the bound native call ``gdn_decode_plan_run(plan, 1, stream)``."""
 
-    __slots__ = ("key", "ptrs", "device", "handle", "arr", "refs", "__weakref__")
+    __slots__ = ("key", "ptrs", "device", "handle", "arr", "refs", "run", "__weakref__")
 
     def __init__(self, key, tensors, device, handle):
         self.key = key
@@ -225,6 +227,7 @@ class _Validated:
         self.handle = handle
         self.arr = (ctypes.c_void_p * 1)(handle)
         self.refs = []
+        self.run = functools.partial(_lib.get_lib().gdn_decode_plan_run, self.arr, 1)
 
     def destroy(self) -> None:
         if self.handle is not None:
@@ -240,18 +243,26 @@ class _Validated:
 # fixed set of buffers per layer runs every call after the first through here.
 _VALIDATED: dict = {}
 _VALIDATED_MAX = 256
+_dp = torch.Tensor.data_ptr
+_stream_of = _lib.raw_stream_accessor()
 
 
 def _data_ptrs(q, k, v, state, A_log, a, dt_bias, b, output, new_state) -> tuple:
-    return (q.data_ptr(), k.data_ptr(), v.data_ptr(),
-            None if state is None else state.data_ptr(), A_log.data_ptr(), a.data_ptr(),
-            dt_bias.data_ptr(), b.data_ptr(), output.data_ptr(), new_state.data_ptr())
+    return (_dp(q), _dp(k), _dp(v), None if state is None else _dp(state), _dp(A_log),
+            _dp(a), _dp(dt_bias), _dp(b), _dp(output), _dp(new_state))
 
 
-def _evict(key) -> None:
-    entry = _VALIDATED.pop(key, None)
+def _evict(key, _table=_VALIDATED) -> None:
+    entry = _table.pop(key, None)
     if entry is not None:
         entry.destroy()
+
+
+def _on_free(key):
+    """Weak-reference callback that evicts ``key``; bound to its own
+    references so it still works while the interpreter tears the module's
+    globals down."""
+    return lambda _ref, key=key, evict=_evict: evict(key)
 
 
 def _bind(key, tensors, scale: float, B, T, H, HV, use_qk_l2norm) -> _Validated:
@@ -268,7 +279,7 @@ def _bind(key, tensors, scale: float, B, T, H, HV, use_qk_l2norm) -> _Validated:
     if len(_VALIDATED) >= _VALIDATED_MAX:
         _evict(next(iter(_VALIDATED)))
     _VALIDATED[key] = entry
-    evict = lambda _ref, key=key: _evict(key)   # noqa: E731
+    evict = _on_free(key)
     entry.refs = [weakref.ref(t, evict) for t in tensors if t is not None]
     return entry
 
@@ -292,11 +303,11 @@ def kernel_hip(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
         key = (id(q), id(k), id(v), id(state), id(A_log), id(a), id(dt_bias), id(b),
                id(output), id(new_state), scale, bool(use_qk_l2norm))
         entry = _VALIDATED.get(key)
-        if entry is not None and entry.ptrs == _data_ptrs(q, k, v, state, A_log, a, dt_bias,
-                                                          b, output, new_state):
+        if entry is not None and entry.ptrs == (
+                _dp(q), _dp(k), _dp(v), None if state is None else _dp(state), _dp(A_log),
+                _dp(a), _dp(dt_bias), _dp(b), _dp(output), _dp(new_state)):
             # the plan makes its own device current for the launch
-            code = _lib.get_lib().gdn_decode_plan_run(entry.arr, 1,
-                                                      _lib.current_stream(entry.device))
+            code = entry.run(_stream_of(entry.device))
             if code:
                 _lib.check(code, "gdn_decode_plan_run")
             return None
@@ -313,8 +324,7 @@ def kernel_hip(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
         with _on_device(q.get_device()):      # the plan records the current device
             entry = _bind(key, (q, k, v, state, A_log, a, dt_bias, b, output, new_state),
                           scale_f, B, T, H, HV, use_qk_l2norm)
-        code = _lib.get_lib().gdn_decode_plan_run(entry.arr, 1,
-                                                  _lib.current_stream(entry.device))
+        code = entry.run(_lib.current_stream(entry.device))
         if code:
             _lib.check(code, "gdn_decode_plan_run")
         return None
