@@ -135,6 +135,15 @@ constexpr float kL2Eps = 1e-6f;
 // v-heads of a GVA group whose gate inputs the preparation kernel loads with
 // the chunk's K rows (the others' when it reaches them).
 constexpr int kPrepGateHeads = 2;
+// A preparation workgroup takes a whole GVA group of v-heads (K K^T made
+// once for all of them, the v-heads one after another) unless one workgroup
+// per (slot, v-head) all fit on the GPU at once (4 a CU, 256 CUs): then each
+// takes one v-head, and the chain of one workgroup -- the preparation's time
+// on a grid that small -- is one v-head's (15k against 25k cycles at ratio 2).
+constexpr long long kPrepSplitMaxWorkgroups = 1024;
+inline bool prep_split(long long slots, int HV) {
+  return slots * HV <= kPrepSplitMaxWorkgroups;
+}
 constexpr float kSoftplusThreshold = 20.0f;
 constexpr float kLn2 = 0.693147180559945309f;
 
@@ -279,6 +288,7 @@ struct Params {
   // most kFewSeqs sequences); if every sequence has at most this many tokens
   // it ran the whole prefill and these kernels return at once.
   int short_limit;
+  int prep_heads;            // v-heads per preparation workgroup: ratio, or 1
 };
 
 // Token range [start, end) of sequence s, clamped to [0, L] so that no
@@ -574,7 +584,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4)))
 void prep_kernel(Params p) {
   __shared__ PrepLds lds;
   const int c = blockIdx.x;
-  const int h = blockIdx.y;
+  // v-heads hv0 .. hv0 + prep_heads - 1, all of q/k head h
+  const int hv0 = static_cast<int>(blockIdx.y) * p.prep_heads;
+  const int h = hv0 / p.ratio;
   if (p.short_limit > 0 && all_within(p, p.short_limit)) return;    // uniform
   int t0, n;                                       // n: 1..64, 0 past the last slot
   if (p.single) {
@@ -614,14 +626,14 @@ void prep_kernel(Params p) {
   uint16_t a_raw[kPrepGateHeads], b_raw[kPrepGateHeads];
   float dtb[kPrepGateHeads], alog[kPrepGateHeads];
   if (wave == 0) {
-    const size_t tk = static_cast<size_t>(t0 + (lane < n ? lane : n - 1)) * p.HV + h * p.ratio;
+    const size_t tk = static_cast<size_t>(t0 + (lane < n ? lane : n - 1)) * p.HV + hv0;
 #pragma unroll
     for (int j = 0; j < kPrepGateHeads; ++j) {
-      const int jj = j < p.ratio ? j : 0;
+      const int jj = j < p.prep_heads ? j : 0;
       a_raw[j] = p.a[tk + jj];
       b_raw[j] = p.b[tk + jj];
-      dtb[j] = p.dt_bias[h * p.ratio + jj];
-      alog[j] = p.A_log[h * p.ratio + jj];
+      dtb[j] = p.dt_bias[hv0 + jj];
+      alog[j] = p.A_log[hv0 + jj];
     }
   }
 
@@ -677,8 +689,8 @@ void prep_kernel(Params p) {
   // Each v-head of the group: its gates, A from the shared product, T, and
   // its slot.  The LDS the previous v-head used (gamma, beta, A, T)
   // is rewritten only after the barrier that ends its use.
-  for (int j = 0; j < p.ratio; ++j) {
-    const int hv = h * p.ratio + j;
+  for (int j = 0; j < p.prep_heads; ++j) {
+    const int hv = hv0 + j;
     float* slot = p.slots + (static_cast<size_t>(c) * p.HV + hv) * kSlotFloats;
     uint16_t* slot16 = reinterpret_cast<uint16_t*>(slot);
     // gates of token t0 + lane (padded rows: no decay, no update), and the
@@ -1928,6 +1940,7 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
   p.few = few_seqs(total_seq_len, num_seqs, HV);
   p.max_slots = slots;
   p.short_limit = maybe_all_short(total_seq_len, num_seqs) ? kSmallTokens : 0;
+  p.prep_heads = prep_split(slots, HV) ? 1 : p.ratio;
 
   hipStream_t stream = static_cast<hipStream_t>(hip_stream);
   // events[i] (optional) is recorded before launch i and events[3] after the last
@@ -1966,8 +1979,8 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
   if (e != hipSuccess) return e;
   if (slots > 0) {
     auto* prep = p.few ? prep_kernel<true> : prep_kernel<false>;
-    hipLaunchKernelGGL(prep, dim3(static_cast<unsigned>(slots), H), dim3(kThreads), 0,
-                       stream, p);
+    hipLaunchKernelGGL(prep, dim3(static_cast<unsigned>(slots), HV / p.prep_heads),
+                       dim3(kThreads), 0, stream, p);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
