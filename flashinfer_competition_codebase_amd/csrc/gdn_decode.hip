@@ -88,8 +88,10 @@ hipError_t launch_one(bool l2, const Params& p, unsigned nb, const Launch& l) {
   auto* kern = l2 ? gdn_decode_k128<NS, W, true, POL, BF16, MULTI, false>
                   : gdn_decode_k128<NS, W, false, POL, BF16, MULTI, false>;
   const int32_t* no_seqlens = nullptr;
-  // H and HV/H are each below 2^16 (checked by the caller).
-  const unsigned h_ratio = static_cast<unsigned>(p.H) | (static_cast<unsigned>(p.ratio) << 16);
+  // H below 2^15 and HV/H below 2^16 (checked by the caller); the grouping
+  // flag for launches of many sequences
+  const unsigned h_ratio = static_cast<unsigned>(p.H) | (static_cast<unsigned>(p.ratio) << 16) |
+                           (nb >= kGroupMinSeqs ? kGroupFlag : 0u);
   if (l.start || l.stop) {
     hipExtLaunchKernelGGL(kern, grid, block, 0, l.stream, l.start, l.stop, 0, p.state, p.q,
                           p.k, p.v, p.a, p.b, h_ratio, p.T, p.A_log, p.dt_bias, p.out,
@@ -150,7 +152,8 @@ hipError_t launch_block(bool l2, const Params& p, unsigned nb, const Launch& l) 
   const dim3 grid(static_cast<unsigned>(p.ratio) * kT, static_cast<unsigned>(p.H), nb);
   const dim3 block(64 * W);
   auto* kern = l2 ? gdn_decode_block<R, W, true, BF16> : gdn_decode_block<R, W, false, BF16>;
-  const unsigned h_ratio = static_cast<unsigned>(p.H) | (static_cast<unsigned>(p.ratio) << 16);
+  const unsigned h_ratio = static_cast<unsigned>(p.H) | (static_cast<unsigned>(p.ratio) << 16) |
+                           (nb >= kGroupMinSeqs ? kGroupFlag : 0u);
   if (l.start || l.stop) {
     hipExtLaunchKernelGGL(kern, grid, block, 0, l.stream, l.start, l.stop, 0, p.state, p.q,
                           p.k, p.v, p.a, p.b, h_ratio, p.T, p.A_log, p.dt_bias, p.out,
@@ -339,7 +342,7 @@ Variant variant_of(const StepArgs& s) {
 // and misaligned pointers, partial overlap of state and new_state.
 hipError_t validate(const StepArgs& s) {
   if (s.B < 0 || s.T < 1 || s.H <= 0 || s.HV <= 0 || s.HV % s.H != 0) return hipErrorInvalidValue;
-  if (s.H > 65535) return hipErrorInvalidValue;  // grid y
+  if (s.H > 32767) return hipErrorInvalidValue;  // packed in 15 bits (and grid y)
   if (s.HV / s.H > 65535) return hipErrorInvalidValue;  // packed with H into 32 bits
   if (s.K != kDim || s.V != kDim) return hipErrorInvalidValue;
   if (s.state_bf16 != 0 && s.state_bf16 != 1) return hipErrorInvalidValue;

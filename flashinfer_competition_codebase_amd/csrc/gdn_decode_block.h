@@ -132,7 +132,7 @@ void gdn_decode_block(
   static_assert(kDim % kRowsPerBlock == 0, "rows per block must divide 128");
   static_assert((kTiles & (kTiles - 1)) == 0, "tiles per head is a power of two");
 
-  const int H = static_cast<int>(h_ratio & 0xffffu);
+  const int H = packed_heads(h_ratio);
   const int ratio = static_cast<int>(h_ratio >> 16);
   const int HV = H * ratio;
   const int lane = threadIdx.x & 63;
@@ -140,10 +140,11 @@ void gdn_decode_block(
   const int n = lane & 15;
   const int g = lane >> 4;
 
-  const int tile = static_cast<int>(blockIdx.x) & (kTiles - 1);
-  const int hq = static_cast<int>(blockIdx.y);
-  const int bi = static_cast<int>(blockIdx.z);
-  const int hv = hq * ratio + static_cast<int>(blockIdx.x) / kTiles;
+  const GridPos pos = decode_grid_pos<!BF16>(h_ratio);
+  const int tile = pos.x & (kTiles - 1);
+  const int hq = pos.y;
+  const int bi = pos.z;
+  const int hv = hq * ratio + pos.x / kTiles;
   const int head = bi * HV + hv;
   const int row0 = tile * kRowsPerBlock + wave * kRowsPerWave;
   const size_t tok0 = static_cast<size_t>(bi) * T;

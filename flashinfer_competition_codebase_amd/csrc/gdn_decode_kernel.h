@@ -550,6 +550,69 @@ __device__ __forceinline__ float scalar_read(const float* ptr) {
   return *(ConstantFloat*)ptr;  // generic -> constant address space: a C-style cast
 }
 
+// This workgroup's place (x, y, z) in a decode grid (row tiles and v-heads
+// of a GVA group, q/k head, sequence).  The gridDim.x workgroups of one
+// (y, z) all read that sequence's q and k rows of that head, and its gate
+// inputs.  Workgroups go to the eight XCDs round-robin in dispatch order (x
+// fastest), so in plain order those gridDim.x workgroups land on as many
+// XCDs, each fetching the rows from HBM into its own L2 (B=256 qk16_v32
+// T=1: 1.016x the algorithmic bytes).  With GROUP (an fp32 state) and the
+// host's flag (kGroupFlag in the packed head counts: at least 128 sequences
+// in the launch) the workgroups are renumbered: in each
+// run of 8 (y, z) groups, dispatch slot L (in the run) runs member L / 8 of
+// group L % 8, so a group's workgroups share an XCD (1.0002x; kernel-stamped
+// A/B, bitwise identical results: B=128 81.5 -> 80.7 us, B=256 164.1 ->
+// 160.3 us, B=512 332.1 -> 321.2 us, T=4 B=256 178.6 -> 177.0 us); a last
+// run of fewer than 8 groups keeps the plain order.  Smaller launches and a
+// bf16 state keep the plain order: there the renumbering measured no faster
+// or slower (B=32: +1%; qk4_v8 B=32 and B=48: +5% and +19%; the fp32 block
+// kernel at B=32 and 64: +2%; bf16 state at B=256: even).  The flag rides in
+// a preloaded argument: deciding on gridDim, which a workgroup loads from
+// the dispatch packet, delayed every small launch's first loads (qk4_v8
+// B=48: +6%).
+// Power-of-two grid sizes (the usual head counts) take shifts only.
+struct GridPos {
+  int x, y, z;
+};
+// Packed head counts of a decode launch: H in bits 0-14, the grouping flag
+// in bit 15, the GVA ratio HV / H in bits 16-31.
+constexpr unsigned kGroupFlag = 0x8000u;
+constexpr long long kGroupMinSeqs = 128;
+__host__ __device__ inline int packed_heads(unsigned h_ratio) {
+  return static_cast<int>(h_ratio & 0x7fffu);
+}
+template <bool GROUP>
+__device__ __forceinline__ GridPos decode_grid_pos(unsigned h_ratio) {
+  if (!GROUP || (h_ratio & kGroupFlag) == 0) {
+    return GridPos{static_cast<int>(blockIdx.x), static_cast<int>(blockIdx.y),
+                   static_cast<int>(blockIdx.z)};
+  }
+  const unsigned X = gridDim.x, Y = gridDim.y, Z = gridDim.z;
+  const unsigned L = blockIdx.x + X * (blockIdx.y + Y * blockIdx.z);   // < 2^31
+  unsigned g, m;
+  if (((X & (X - 1)) | (Y & (Y - 1))) == 0) {
+    const unsigned lx = __builtin_ctz(X), ly = __builtin_ctz(Y);
+    const unsigned run = L >> (lx + 3);
+    if (((run + 1) << 3) <= (Z << ly)) {
+      g = (run << 3) + (L & 7u);
+      m = (L >> 3) & (X - 1);
+    } else {
+      g = L >> lx;
+      m = L & (X - 1);
+    }
+    return GridPos{static_cast<int>(m), static_cast<int>(g & (Y - 1)), static_cast<int>(g >> ly)};
+  }
+  const unsigned run = L / (8u * X);
+  if (run * 8u + 8u <= Y * Z) {
+    g = run * 8u + (L & 7u);
+    m = (L >> 3) - run * X;
+  } else {
+    g = blockIdx.y + Y * blockIdx.z;
+    m = blockIdx.x;
+  }
+  return GridPos{static_cast<int>(m), static_cast<int>(g % Y), static_cast<int>(g / Y)};
+}
+
 template <int NS, int WAVES, bool L2NORM, int POLICY, bool BF16, bool MULTI, bool VARLEN,
           bool STAMP>
 __device__ __forceinline__ void decode_body(
@@ -577,7 +640,7 @@ __device__ __forceinline__ void decode_body(
   p.new_state = new_state;
   p.scale = scale;
   p.T = MULTI ? T_arg : 1;
-  p.H = static_cast<int>(h_ratio & 0xffffu);
+  p.H = packed_heads(h_ratio);
   p.ratio = static_cast<int>(h_ratio >> 16);
   p.HV = p.H * p.ratio;
   constexpr int kRowsPerWave = kLaneGroups * NS;
@@ -591,10 +654,11 @@ __device__ __forceinline__ void decode_body(
   const int grp = lane >> 4;
   const int j = lane & 15;
 
-  const int tile = static_cast<int>(blockIdx.x) & (kTiles - 1);
-  const int hq = static_cast<int>(blockIdx.y);          // q/k head
-  const int bi = static_cast<int>(blockIdx.z);
-  const int hv = hq * p.ratio + static_cast<int>(blockIdx.x) / kTiles;
+  const GridPos pos = decode_grid_pos<!BF16>(h_ratio);
+  const int tile = pos.x & (kTiles - 1);
+  const int hq = pos.y;                                  // q/k head
+  const int bi = pos.z;
+  const int hv = hq * p.ratio + pos.x / kTiles;
   const int head = bi * p.HV + hv;
   const int row0 = tile * kRowsPerBlock + wave * kRowsPerWave + grp * NS;
   const size_t row_base = static_cast<size_t>(head) * kDim + row0;  // state row index

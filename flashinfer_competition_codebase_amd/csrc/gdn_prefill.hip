@@ -1863,6 +1863,7 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
     return hipErrorInvalidValue;
   if (K != kDim || V != kDim) return hipErrorInvalidValue;
   if (HV > 65535) return hipErrorInvalidValue;      // grid y
+  if (H > 32767) return hipErrorInvalidValue;       // packed in 15 bits for the token kernel
   if (num_seqs == 0) return hipSuccess;
   if (!cu_seqlens || !A_log || !dt_bias || !new_state || (!workspace && !fixed_scratch))
     return hipErrorInvalidValue;

@@ -5,7 +5,7 @@
  * the reference's tensor layouts (T = 1 token per sequence for the
  * reference's decode; T > 1 for multi-token decode):
  *
- *   q, k       [B, T, H,  K]   bf16   (K = 128)
+ *   q, k       [B, T, H,  K]   bf16   (K = 128, H <= 32767)
  *   v          [B, T, HV, V]   bf16   (V = 128, HV % H == 0, GVA ratio HV/H)
  *   state      [B, HV, V, K]   fp32   "k-last": element (k, v) at v*K + k
  *                                     (bf16 with gdn_decode_steps' state_bf16);

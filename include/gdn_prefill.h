@@ -4,7 +4,7 @@
  * Variable-length prefill over N sequences packed along the token axis, in
  * the reference's tensor layouts (solution/triton/prefill_kernel.py:96-114):
  *
- *   q, k        [L, H,  K]        bf16   (K = 128; L = total tokens)
+ *   q, k        [L, H,  K]        bf16   (K = 128, H <= 32767; L = total tokens)
  *   v           [L, HV, V]        bf16   (V = 128, HV % H == 0)
  *   state       [N, HV, V, K]     fp32   k-last; NULL means zeros
  *   A_log       [HV]              fp32
