@@ -150,6 +150,8 @@ def test_validation_rejects_misaligned_and_overlapping_state():
         pytest.skip("made-up pointers are only passed where no device exists")
     lib = _lib.get_lib()
     assert _step(lib, ptr=0x100002) == 1                       # 2-byte aligned
+    # H is packed in 15 bits of a kernel argument (bit 15 carries a launch flag)
+    assert _step(lib, H=32768, HV=32768, ptr=0x100000) == 1
     assert _step(lib, ptr=0x100000, new_state=0x100010) == 1   # partial overlap
 
 

@@ -105,6 +105,9 @@ def test_c_side_validation_rejects_before_launching():
         assert lib.gdn_prefill_workspace_bytes(big, 1, 16, 32) > (128 << 20)
         assert lib.gdn_prefill_noalloc(*fake, 0x90000, f, 0xa0000, 0xb0000, big, 1, 16, 32, 128,
                                        128, 0, None) == 2
+        # H above 32767 (the token kernel packs it in 15 bits) is refused
+        assert lib.gdn_prefill(*fake, 0x90000, f, 0xa0000, 0xb0000, 6, 1, 32768, 32768, 128, 128,
+                               0, 0xc0000, 1 << 30, None) == 1
 
 
 def _cpu_inputs():
