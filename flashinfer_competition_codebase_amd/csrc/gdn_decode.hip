@@ -221,19 +221,23 @@ bool aligned(const void* p, uintptr_t a) {
 // wave per block: 6-14% faster there than 2 rows x 4 waves); large batches
 // stream at ~6.5 TB/s with 2 rows x 4 waves at T = 1, while at T = 4 the
 // per-token arithmetic is large enough that 4 rows per lane group (per-head
-// work shared by more rows) wins.
+// work shared by more rows) wins.  Past 4096 heads (the launches whose
+// workgroups are grouped by XCD) fewer waves a block measured faster
+// (kernel-stamped sweep of every shape, qk16_v32: B=256 T=1 2 x 2 159.2 us
+// against 2 x 4 160.6, B=512 317.3 against 323.1; B=256 T=4 4 x 1 171.0
+// against 4 x 2 173.4; B=128 within 0.2%).
 struct ShapeRow {
   long long max_heads;
   int ns;
   int waves;
 };
 constexpr ShapeRow kShapeFp32[] = {
-    {16, 1, 1}, {64, 2, 2}, {256, 4, 1}, {384, 8, 1}, {-1, 2, 4}};
+    {16, 1, 1}, {64, 2, 2}, {256, 4, 1}, {384, 8, 1}, {4096, 2, 4}, {-1, 2, 2}};
 constexpr ShapeRow kShapeT2[] = {
     {16, 1, 1}, {32, 1, 4}, {64, 2, 1}, {128, 2, 4}, {256, 4, 1}, {768, 8, 1}, {-1, 2, 4}};
 constexpr ShapeRow kShapeT3Plus[] = {
     {16, 1, 1}, {32, 1, 4}, {64, 2, 1}, {256, 2, 2}, {384, 4, 1}, {768, 4, 2},
-    {1536, 8, 1}, {-1, 4, 2}};
+    {1536, 8, 1}, {4096, 4, 2}, {-1, 4, 1}};
 constexpr ShapeRow kShapeBf16[] = {
     {16, 1, 2}, {32, 1, 4}, {64, 2, 4}, {128, 2, 2}, {256, 2, 1}, {384, 2, 4},
     {768, 4, 4}, {2048, 2, 4}, {-1, 4, 4}};
