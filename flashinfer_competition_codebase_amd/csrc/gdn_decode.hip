@@ -225,7 +225,8 @@ bool aligned(const void* p, uintptr_t a) {
 // workgroups are grouped by XCD) fewer waves a block measured faster
 // (kernel-stamped sweep of every shape, qk16_v32: B=256 T=1 2 x 2 159.2 us
 // against 2 x 4 160.6, B=512 317.3 against 323.1; B=256 T=4 4 x 1 171.0
-// against 4 x 2 173.4; B=128 within 0.2%).
+// against 4 x 2 173.4; T=2 2 x 8 165.9 against 2 x 4 171.0; B=128 within
+// 0.2%).
 struct ShapeRow {
   long long max_heads;
   int ns;
@@ -234,7 +235,8 @@ struct ShapeRow {
 constexpr ShapeRow kShapeFp32[] = {
     {16, 1, 1}, {64, 2, 2}, {256, 4, 1}, {384, 8, 1}, {4096, 2, 4}, {-1, 2, 2}};
 constexpr ShapeRow kShapeT2[] = {
-    {16, 1, 1}, {32, 1, 4}, {64, 2, 1}, {128, 2, 4}, {256, 4, 1}, {768, 8, 1}, {-1, 2, 4}};
+    {16, 1, 1}, {32, 1, 4}, {64, 2, 1}, {128, 2, 4}, {256, 4, 1}, {768, 8, 1}, {4096, 2, 4},
+    {-1, 2, 8}};
 constexpr ShapeRow kShapeT3Plus[] = {
     {16, 1, 1}, {32, 1, 4}, {64, 2, 1}, {256, 2, 2}, {384, 4, 1}, {768, 4, 2},
     {1536, 8, 1}, {4096, 4, 2}, {-1, 4, 1}};
