@@ -757,7 +757,7 @@ PREFILL_ROOFLINE_WORKLOAD = "prefill_qk16_v32_64x512"
 
 
 PREFILL_PREP_KERNEL = "gdn_pf::prep_kernel<false>"
-PREFILL_SCAN_KERNEL = "gdn_pf::scan_kernel<false, false, true, false>"
+PREFILL_SCAN_KERNEL = "gdn_pf::scan_kernel<false, false, true, false, 8>"
 PMC_PREFILL_COMMANDS = [
     "cd /tmp && export TMPDIR=/tmp && timeout -s KILL 90 rocprofv3 --pmc FETCH_SIZE "
     "--output-format csv -d $REPO/gpurun_out/pmcp1 -o p -- python3 $REPO/bench.py --pmc-prefill",

@@ -876,6 +876,13 @@ void prep_kernel(Params p) {
 // the state update).
 constexpr int kScanWaves = 8;
 constexpr int kScanThreads = 64 * kScanWaves;
+// A scan workgroup of W waves holds 16 W state columns: W = 8, the whole
+// state, or W = 4, half of it (columns 64 half .. + 63), two workgroups per
+// (sequence, v-head).  A workgroup holds a CU alone (its LDS), so with W = 4
+// each SIMD runs one wave instead of two: a chunk step costs about half
+// (its instruction issue, which the two waves of a SIMD share, sets it), for
+// twice the workgroups -- the form for batches whose whole-state workgroups
+// would fill at most half the CUs.
 constexpr int kRowPieces = kDim / 8 + 1;          // 16-byte pieces per K / Q row, one of padding
 constexpr int kRowStride = kRowPieces * 8;        // bf16 (68 dwords)
 constexpr int kRowDma = kChunk * kRowPieces / 64; // DMA instructions per K / Q chunk (17)
@@ -940,32 +947,33 @@ __device__ __forceinline__ void barrier_lds_no_dma() {
 
 // DMA of a chunk's K rows, Q rows (OUT; rows >= n repeat row n - 1; each
 // row's padding piece repeats its last piece) and slot into one LDS buffer;
-// wave w issues instructions w, w + 8, ....
-template <bool OUT>
+// wave w of W issues instructions w, w + W, ....
+template <bool OUT, int W>
 __device__ __forceinline__ void scan_dma(ScanBuf<OUT>& B, const uint16_t* kbase,
                                          const uint16_t* qbase, unsigned step, int n,
                                          const float* slot, int wave, int lane) {
-  for (int i = wave; i < kRowDma; i += kScanWaves) {        // uniform per wave
+  for (int i = wave; i < kRowDma; i += W) {                 // uniform per wave
     const int pc = i * 64 + lane;
     const int r = pc / kRowPieces, c = pc % kRowPieces;
     const unsigned off = row_bytes(r < n ? r : n - 1, step, (c < 16 ? c : 15) * 8);
     dma16_at(kbase, off, &B.Kr[i * 512]);
     if constexpr (OUT) dma16_at(qbase, off, &B.Qr[i * 512]);
   }
-  for (int i = wave; i < kSlotDma; i += kScanWaves)
+  for (int i = wave; i < kSlotDma; i += W)
     dma16_at(slot, static_cast<unsigned>(i * 64 + lane) * 16u, &B.slot[i * 256]);
 }
 
 // This wave's 16 columns of V for token tile r (lane (col, g): token
-// 16 r + col, columns 16 w + 4 g .. + 3; rows >= n repeat row n - 1).
+// 16 r + col, columns 16 cw + 4 g .. + 3, cw the wave's column wave; rows
+// >= n repeat row n - 1).
 __device__ __forceinline__ void load_v(u32x2 (&f)[4], const uint16_t* vbase, unsigned step, int n,
-                                       int wave, int col, int g4) {
+                                       int cw, int col, int g4) {
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int row = r * 16 + col;
     f[r] = *reinterpret_cast<const u32x2*>(
         reinterpret_cast<const char*>(vbase) + row_bytes(row < n ? row : n - 1, step,
-                                                         wave * 16 + g4 * 4));
+                                                         cw * 16 + g4 * 4));
   }
 }
 
@@ -1000,20 +1008,28 @@ struct ScanCtx {
   int H, HV, h, hv;
   float scale;
   bool values;
+  int cw0;                     // the first wave's column wave: 0, or 4 for the second half
 };
 
+// Column wave of wave `wave` (columns 16 cw .. 16 cw + 15): with W = 8 the
+// wave itself (cw0 is 0; known here at compile time).
+template <int W>
+__device__ __forceinline__ int column_wave(const ScanCtx& cx, int wave) {
+  return W == kScanWaves ? wave : cx.cw0 + wave;
+}
+
 // Chunk c's DMA into buf and its V into registers.
-template <bool OUT>
+template <bool OUT, int W>
 __device__ __forceinline__ void scan_issue(ScanBuf<OUT>* buf, const ScanCtx& cx, int c,
                                            u32x2 (&vf)[4]) {
   const int wave = wave_index(), lane = threadIdx.x & 63;
   const int tc = cx.start + c * kChunk;
   const int nc = min(kChunk, cx.end - tc);
-  scan_dma(*buf, cx.k + (static_cast<size_t>(tc) * cx.H + cx.h) * kDim,
-           cx.q + (static_cast<size_t>(tc) * cx.H + cx.h) * kDim, cx.kstep, nc,
-           cx.slot_base + c * cx.slot_step, wave, lane);
-  load_v(vf, cx.v + (static_cast<size_t>(tc) * cx.HV + cx.hv) * kDim, cx.vstep, nc, wave,
-         lane & 15, lane >> 4);
+  scan_dma<OUT, W>(*buf, cx.k + (static_cast<size_t>(tc) * cx.H + cx.h) * kDim,
+                   cx.q + (static_cast<size_t>(tc) * cx.H + cx.h) * kDim, cx.kstep, nc,
+                   cx.slot_base + c * cx.slot_step, wave, lane);
+  load_v(vf, cx.v + (static_cast<size_t>(tc) * cx.HV + cx.hv) * kDim, cx.vstep, nc,
+         column_wave<W>(cx, wave), lane & 15, lane >> 4);
 }
 
 // Where chunk c's inputs come from (rows >= n repeat row n - 1).
@@ -1039,28 +1055,39 @@ __device__ __forceinline__ ChunkSrc chunk_src(const ScanCtx& cx, int c) {
 // Part `part` (0..3) of a chunk's DMA and V loads, so that a chunk step
 // spreads them over its products (issued at once, the eight waves' DMA
 // instructions queue behind each other and hold each wave at the issue for
-// 1-2.5 k cycles): parts 0..2 the K / Q row instructions w + 8 part, part 2
-// also slot instruction w, part 3 slot instruction w + 8 and the V loads.
-template <bool OUT>
+// 1-2.5 k cycles): with W = 8, parts 0..2 the K / Q row instructions w + 8
+// part, part 2 also slot instruction w, part 3 slot instruction w + 8 and the
+// V loads; with W = 4 each part issues twice as many, instructions w + 4 j
+// for j = 2 part, 2 part + 1 (rows) and j = 2 (part - 2), 2 (part - 2) + 1
+// (slot).
+template <bool OUT, int W>
 __device__ __forceinline__ void issue_part(ScanBuf<OUT>* __restrict__ Bn, const ScanCtx& cx,
                                            const ChunkSrc& s, int part, u32x2 (&vf)[4]) {
+  constexpr int kPer = kScanWaves / W;                      // instructions a wave a part
   const int wave = wave_index(), lane = threadIdx.x & 63;
   if (part < 3) {
-    const int i = wave + kScanWaves * part;
-    if (i < kRowDma) {                                      // uniform per wave
-      const int pc = i * 64 + lane;
-      const int r = pc / kRowPieces, c = pc % kRowPieces;
-      const unsigned off = row_bytes(r < s.n ? r : s.n - 1, cx.kstep, (c < 16 ? c : 15) * 8);
-      dma16_at(s.kbase, off, &Bn->Kr[i * 512]);
-      if constexpr (OUT) dma16_at(s.qbase, off, &Bn->Qr[i * 512]);
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = wave + W * (kPer * part + j);
+      if (i < kRowDma) {                                    // uniform per wave
+        const int pc = i * 64 + lane;
+        const int r = pc / kRowPieces, c = pc % kRowPieces;
+        const unsigned off = row_bytes(r < s.n ? r : s.n - 1, cx.kstep, (c < 16 ? c : 15) * 8);
+        dma16_at(s.kbase, off, &Bn->Kr[i * 512]);
+        if constexpr (OUT) dma16_at(s.qbase, off, &Bn->Qr[i * 512]);
+      }
     }
   }
   if (part >= 2) {
-    const int i = wave + kScanWaves * (part - 2);
-    if (i < kSlotDma)
-      dma16_at(s.slot, static_cast<unsigned>(i * 64 + lane) * 16u, &Bn->slot[i * 256]);
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = wave + W * (kPer * (part - 2) + j);
+      if (i < kSlotDma)
+        dma16_at(s.slot, static_cast<unsigned>(i * 64 + lane) * 16u, &Bn->slot[i * 256]);
+    }
   }
-  if (part == 3) load_v(vf, s.vbase, cx.vstep, s.n, wave, lane & 15, lane >> 4);
+  if (part == 3)
+    load_v(vf, s.vbase, cx.vstep, s.n, column_wave<W>(cx, wave), lane & 15, lane >> 4);
 }
 
 // P' tiles (row tile r, token tile jt) of a chunk, 10 nonzero and the two
@@ -1099,7 +1126,7 @@ __device__ __forceinline__ void p_tile_mma(const s16x8 (&ak)[4], const s16x8 (&b
 // operand of Delta^T P'^T.  The Q row scales rq = 1 / |q_i| (L2-norm; each
 // wave computes eight rows' from the Q rows in LDS and shares them through
 // Qn) scale the output row: O = diag(rq) (diag(scale e^gamma) Q S + P' Delta).
-template <bool OUT, bool L2>
+template <bool OUT, bool L2, int W>
 __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
                                            ScanBuf<OUT>* __restrict__ Bn,
                                            uint16_t* __restrict__ Kt, uint16_t* __restrict__ Pb,
@@ -1112,6 +1139,7 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
   const int g4 = lane >> 4;
   const int t0 = cx.start + ci * kChunk;
   const int n = min(kChunk, cx.end - t0);
+  const int cw = column_wave<W>(cx, wave);   // columns 16 cw .. 16 cw + 15
   const u32x2 vf[4] = {vnext[0], vnext[1], vnext[2], vnext[3]};
   // The next chunk's inputs go into the other buffer (after the last chunk:
   // this one's again, unused) in four parts spread over the K S products.
@@ -1122,42 +1150,50 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
   // into Bn does not write (reads it splits into pairs of 4-byte reads lose
   // that, and wait for the DMA).
 
-  // L2-norm: 1 / |q_i| of Q rows 8 wave .. 8 wave + 7 into Qn (lane: row
-  // 8 wave + lane / 8, items 16 (lane % 8) .. + 15); read after the barrier
-  // below.  (The previous chunk's reads of Qn ended before its last barrier.)
+  // L2-norm: 1 / |q_i| of Q rows 8 v .. 8 v + 7 into Qn, v = wave + W rep
+  // (lane: row 8 v + lane / 8, items 16 (lane % 8) .. + 15); read after the
+  // barrier below.  (The previous chunk's reads of Qn ended before its last
+  // barrier.)
   if constexpr (L2) {
-    const int row = 8 * wave + (lane >> 3);
-    const uint16_t* qr = &B->Qr[row * kRowStride + (lane & 7) * 16];
-    const u32x4 w[2] = {*reinterpret_cast<const u32x4*>(qr),
-                        *reinterpret_cast<const u32x4*>(qr + 8)};
-    float q2 = 0.0f;
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int rep = 0; rep < kScanWaves / W; ++rep) {
+      const int row = 8 * (wave + W * rep) + (lane >> 3);
+      const uint16_t* qr = &B->Qr[row * kRowStride + (lane & 7) * 16];
+      const u32x4 w[2] = {*reinterpret_cast<const u32x4*>(qr),
+                          *reinterpret_cast<const u32x4*>(qr + 8)};
+      float q2 = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float lo = __uint_as_float(w[h][i] << 16);
-        const float hi = __uint_as_float(w[h][i] & 0xffff0000u);
-        q2 = fmaf(hi, hi, fmaf(lo, lo, q2));
-      }
-    q2 += __shfl_xor(q2, 1, 64);
-    q2 += __shfl_xor(q2, 2, 64);
-    q2 += __shfl_xor(q2, 4, 64);
-    if ((lane & 7) == 0) Qn[row] = __builtin_amdgcn_rsqf(q2 + kL2Eps);
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float lo = __uint_as_float(w[h][i] << 16);
+          const float hi = __uint_as_float(w[h][i] & 0xffff0000u);
+          q2 = fmaf(hi, hi, fmaf(lo, lo, q2));
+        }
+      q2 += __shfl_xor(q2, 1, 64);
+      q2 += __shfl_xor(q2, 2, 64);
+      q2 += __shfl_xor(q2, 4, 64);
+      if ((lane & 7) == 0) Qn[row] = __builtin_amdgcn_rsqf(q2 + kL2Eps);
+    }
   }
 
   // K S (token rows) and S^T Q^T (the output's first term, transposed),
   // one 32-key block of the state at a time.  The K and Q operands of key
   // block kb + 1 are read into the other of two register sets while block
   // kb's products run, so the LDS latency is paid once, not per product.
-  // The same operands make this wave's key tile of K^T (key block wave / 2:
-  // the selector products of the K row tiles give lane (col, g) tokens
-  // 16 r + 4 g + e of key state_key(wave, col / 4) + col % 4) and its P'
-  // tiles' (K Q^T) products, shared with the other waves through LDS.
-  f32x4 x[4], o[4], pacc[2];
+  // The same operands make this wave's key tiles of K^T (tiles t = wave +
+  // W m, key block t / 2: the selector products of the K row tiles give lane
+  // (col, g) tokens 16 r + 4 g + e of key state_key(t, col / 4) + col % 4)
+  // and its P' tiles' (K Q^T) products, shared with the other waves through
+  // LDS.
+  constexpr int kKtTiles = kScanWaves / W;                  // K^T tiles a wave makes
+  constexpr int kPReps = (kPTiles + W - 1) / W;             // P' tiles a wave makes, at most
+  f32x4 x[4], o[4], pacc[kPReps];
 #pragma unroll
   for (int r = 0; r < 4; ++r) x[r] = o[r] = f32x4{0, 0, 0, 0};
-  pacc[0] = pacc[1] = f32x4{0, 0, 0, 0};
-  s16x4 kt[4];
+#pragma unroll
+  for (int i = 0; i < kPReps; ++i) pacc[i] = f32x4{0, 0, 0, 0};
+  s16x4 kt[kKtTiles][4];
   s16x8 ak[2][4], bq[2][4];
   auto read_ops = [&](int kb, int set) {
 #pragma unroll
@@ -1171,13 +1207,16 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
   for (int kb = 0; kb < 4; ++kb) {
     const int set = kb & 1;
     if (kb < 3) read_ops(kb + 1, set ^ 1);
-    issue_part(Bn, cx, nsrc, kb, vnext);
-    if (kb == (wave >> 1)) {                                // uniform per wave
+    issue_part<OUT, W>(Bn, cx, nsrc, kb, vnext);
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        kt[r] = to_bf16x4(mfma_bf16(ak[set][r], sel, f32x4{0, 0, 0, 0}));
+    for (int m = 0; m < kKtTiles; ++m) {
+      if (kb == ((wave + W * m) >> 1)) {                    // uniform per wave
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          kt[m][r] = to_bf16x4(mfma_bf16(ak[set][r], sel, f32x4{0, 0, 0, 0}));
+      }
     }
-    if constexpr (OUT) {
+    if constexpr (OUT && W == 8) {
       switch (wave) {                                       // uniform per wave
         case 0: p_tile_mma<0>(ak[set], bq[set], pacc[0]); p_tile_mma<8>(ak[set], bq[set], pacc[1]); break;
         case 1: p_tile_mma<1>(ak[set], bq[set], pacc[0]); p_tile_mma<9>(ak[set], bq[set], pacc[1]); break;
@@ -1187,6 +1226,17 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
         case 5: p_tile_mma<5>(ak[set], bq[set], pacc[0]); break;
         case 6: p_tile_mma<6>(ak[set], bq[set], pacc[0]); break;
         default: p_tile_mma<7>(ak[set], bq[set], pacc[0]); break;
+      }
+    } else if constexpr (OUT) {                             // W = 4: tiles w, w + 4, w + 8
+      switch (wave) {                                       // uniform per wave
+        case 0: p_tile_mma<0>(ak[set], bq[set], pacc[0]); p_tile_mma<4>(ak[set], bq[set], pacc[1]);
+                p_tile_mma<8>(ak[set], bq[set], pacc[2]); break;
+        case 1: p_tile_mma<1>(ak[set], bq[set], pacc[0]); p_tile_mma<5>(ak[set], bq[set], pacc[1]);
+                p_tile_mma<9>(ak[set], bq[set], pacc[2]); break;
+        case 2: p_tile_mma<2>(ak[set], bq[set], pacc[0]); p_tile_mma<6>(ak[set], bq[set], pacc[1]);
+                p_tile_mma<10>(ak[set], bq[set], pacc[2]); break;
+        default: p_tile_mma<3>(ak[set], bq[set], pacc[0]); p_tile_mma<7>(ak[set], bq[set], pacc[1]);
+                 p_tile_mma<11>(ak[set], bq[set], pacc[2]); break;
       }
     }
     s16x8 sl;
@@ -1203,17 +1253,19 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
     }
   }
 
-  // this wave's K^T tile and P' tiles into LDS (read after the barrier below)
+  // this wave's K^T tiles and P' tiles into LDS (read after the barrier below)
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
-    *reinterpret_cast<s16x8*>(Kt + ((wave * 2 + kb) * 64 + lane) * 8) =
-        cat(kt[2 * kb], kt[2 * kb + 1]);
+  for (int m = 0; m < kKtTiles; ++m)
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+      *reinterpret_cast<s16x8*>(Kt + (((wave + W * m) * 2 + kb) * 64 + lane) * 8) =
+          cat(kt[m][2 * kb], kt[m][2 * kb + 1]);
   if constexpr (OUT) {
     // P' tile (r, jt): lane (col, g) holds row i = 16 r + col, tokens
     // j = 16 jt + 4 g + e; items 4 (jt % 2) .. + 3 of block (r, jt / 2)
 #pragma unroll
-    for (int rep = 0; rep < 2; ++rep) {
-      const int idx = wave + kScanWaves * rep;
+    for (int rep = 0; rep < kPReps; ++rep) {
+      const int idx = wave + W * rep;
       if (idx >= kPTiles) break;                       // uniform per wave
       const int r = (kPTileR >> (2 * idx)) & 3, jt = (kPTileJ >> (2 * idx)) & 3;
       f32x4 pv = {0, 0, 0, 0};
@@ -1245,8 +1297,9 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
   }
 
   // X = V - diag(rk e^gamma) K S: lane (col, g) holds tokens 16 r + 4 g + e
-  // of column 16 wave + col; V^T tiles from the selector products (the
-  // wave's 16 columns sit in the half `wave % 2` of a 32-column block)
+  // of column 16 cw + col; V^T tiles from the selector products (the
+  // wave's 16 columns sit in the half `cw % 2` = `wave % 2` of a 32-column
+  // block)
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const f32x4 xg = *reinterpret_cast<const f32x4*>(&B->slot[kSlotXg + r * 16 + g4 * 4]);
@@ -1313,7 +1366,7 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
   read_kt(0);
 
   // O^T = rq (.) (qs (.) S^T Q^T + Delta^T P'^T); lane (col, g) ends with
-  // columns 16 wave + 4 g + e of token 16 r + col, one 8-byte store
+  // columns 16 cw + 4 g + e of token 16 r + col, one 8-byte store
   if constexpr (OUT) {
     uint16_t* const obase = cx.out + (static_cast<size_t>(t0) * cx.HV + cx.hv) * kDim;
 #pragma unroll
@@ -1332,7 +1385,7 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
       const u32x2 ob = {pack_bf16x2(o[r][0], o[r][1]), pack_bf16x2(o[r][2], o[r][3])};
       if (tok < n)
         *reinterpret_cast<u32x2*>(reinterpret_cast<char*>(obase) +
-                                  row_bytes(tok, cx.vstep, wave * 16 + g4 * 4)) = ob;
+                                  row_bytes(tok, cx.vstep, cw * 16 + g4 * 4)) = ob;
     }
   }
 
@@ -1357,17 +1410,17 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
 // The end state of a scan: k-last fp32 (element (k, c) at c * 128 + k), or,
 // for a transition M (identity start), as the A operand blocks of the
 // combine's product M S: for row tile t and column block kb, 64 lanes x 8
-// bf16, hi then lo (block ((t * 4 + kb) * 2 + hl) * 512).  Wave w holds
-// columns 16 w .. 16 w + 15, half w % 2 of block kb = w / 2: the selector
-// products of its state read as an operand with the columns as rows give
-// lane (col, g) the columns 16 w + 4 g + e of row state_key(t, col / 4) +
-// col % 4, items 4 (w % 2) .. + 3 of the block's lane; those columns
-// started from start keys 32 kb + 8 g + item, the key order of the
+// bf16, hi then lo (block ((t * 4 + kb) * 2 + hl) * 512).  Column wave w
+// (cw: the wave's columns 16 w .. 16 w + 15) is half w % 2 of block kb = w /
+// 2: the selector products of its state read as an operand with the columns
+// as rows give lane (col, g) the columns 16 w + 4 g + e of row state_key(t,
+// col / 4) + col % 4, items 4 (w % 2) .. + 3 of the block's lane; those
+// columns started from start keys 32 kb + 8 g + item, the key order of the
 // combine's S operand.
 __device__ __forceinline__ void store_end(float* st_out, bool transition, const f32x4 (&st)[8],
-                                          const s16x8 (&sels)[2]) {
+                                          const s16x8 (&sels)[2], int cw) {
   const int lane = threadIdx.x & 63;
-  const int wave = wave_index();
+  const int wave = cw;
   const int col = lane & 15;
   const int g4 = lane >> 4;
   if (!transition) {
@@ -1395,22 +1448,27 @@ __device__ __forceinline__ void store_end(float* st_out, bool transition, const 
   }
 }
 
-// Grid: (unit, q/k head) pairs in groups of 8 times the GVA ratio.
-// Workgroup b serves pair 8 (b / (8 ratio)) + b % 8 and its v-head
-// (b / 8) % ratio: the v-heads that read the same K and Q are dispatched 8
-// apart, all to XCD b % 8 (workgroups go to the XCDs round-robin), and share
-// its L2 copy.  A unit is a sequence, or with SEG a role of one segment of
+// Grid: (unit, q/k head) pairs in groups of 8 times the GVA ratio times the
+// column halves (W = 4: 2, W = 8: 1).  Workgroup b serves pair 8 (b / (8
+// ratio halves)) + b % 8 and, with m = (b / 8) % (ratio halves), its v-head
+// m % ratio and half m / ratio: the workgroups that read the same K and Q
+// are dispatched 8 apart, all to XCD b % 8 (workgroups go to the XCDs
+// round-robin), and share its L2 copy.  A unit is a sequence, or with SEG a role of one segment of
 // sequence 0.  The first segment launch (OUT false, no outputs) runs
 // segment 0 from the sequence's state (end: seg_S[1]) and segments
 // 1 .. nseg-2 from a zero start (end: seg_B) and from the identity without
 // values (end: seg_M, as the combine's operand); the second (OUT) runs every
 // segment from its start (segment 0: the sequence's state, then seg_S) with
 // the outputs, the last one's end being the new state.
-template <bool FEW, bool SEG, bool OUT, bool L2>
-__global__ __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template <bool FEW, bool SEG, bool OUT, bool L2, int W>
+__global__ __launch_bounds__(64 * W)
+__attribute__((amdgpu_waves_per_eu(W == kScanWaves ? 2 : 1, W == kScanWaves ? 2 : 1)))
 void scan_kernel(Params p) {
   static_assert(OUT || SEG, "only segments run without outputs");
   static_assert(OUT || !L2, "the L2-norm scales outputs only");
+  static_assert(W == kScanWaves || (W == kScanWaves / 2 && !SEG),
+                "half-state workgroups run plain scans only");
+  constexpr int kHalves = kScanWaves / W;
   // separate LDS objects, so that the compiler sees that the DMA into one
   // buffer never writes what the chunk reads from the other
   __shared__ ScanBuf<OUT> L0, L1;
@@ -1419,8 +1477,10 @@ void scan_kernel(Params p) {
   __shared__ float Qn[L2 ? kChunk : 1];    // 1 / |q_i| of the chunk's Q rows (L2-norm)
   const long long b = blockIdx.x;
   const int ratio = p.ratio;
-  const long long pair = (b / (8LL * ratio)) * 8 + (b & 7);
-  const int jr = static_cast<int>((b >> 3) % ratio);
+  const long long pair = (b / (8LL * ratio * kHalves)) * 8 + (b & 7);
+  const int member = static_cast<int>((b >> 3) % (ratio * kHalves));
+  const int jr = member % ratio;
+  const int cw0 = W == kScanWaves ? 0 : (member / ratio) * W;   // the first wave's column wave
   // units the grid covers: with SEG the launch's bound, each workgroup
   // finding its sequence's segment below (those past the batch's exit)
   const long long units = SEG ? (OUT ? p.nseg : seg_units1(p.nseg, p.N))
@@ -1513,9 +1573,10 @@ void scan_kernel(Params p) {
   // transition gives column 16 w + m the unit vector of the key in register
   // position (w, m): key state_key(w, m / 4) + m % 4, so that its end column
   // is that start key's column of M, in the key order of the combine's
-  // operand.
+  // operand.  (w: the column wave, cw0 + wave.)
   f32x4 st[8];
-  const int c = wave * 16 + col;
+  const int cw = cw0 + wave;
+  const int c = cw * 16 + col;
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
     st[t] = st_in != nullptr && (end > start || pass_through)
@@ -1524,7 +1585,7 @@ void scan_kernel(Params p) {
                 : f32x4{0, 0, 0, 0};
     if (identity) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) st[t][e] = t == wave && 4 * g4 + e == col ? 1.0f : 0.0f;
+      for (int e = 0; e < 4; ++e) st[t][e] = t == cw && 4 * g4 + e == col ? 1.0f : 0.0f;
     }
   }
   // selector operands: Sel_h[k][j] = (k == 16 h + j) over a 32-long k block
@@ -1545,7 +1606,7 @@ void scan_kernel(Params p) {
 #pragma unroll
         for (int t = 0; t < 8; ++t) st[t] = f32x4{0, 0, 0, 0};
       }
-      store_end(st_out, identity, st, sels);
+      store_end(st_out, identity, st, sels, cw);
     }
     return;
   }
@@ -1567,17 +1628,19 @@ void scan_kernel(Params p) {
   cx.hv = hv;
   cx.values = values;
   cx.scale = p.scale;
+  cx.cw0 = cw0;
 
   const s16x8 sel = sels[wave & 1];       // this wave's half of a 32-key / 32-column block
   u32x2 vnext[4];
-  scan_issue<OUT>(&L0, cx, 0, vnext);
+  scan_issue<OUT, W>(&L0, cx, 0, vnext);
   wait_vmem();
   block_sync_lds();
   for (int ci = 0; ci < nchunks; ci += 2) {
-    scan_chunk<OUT, L2>(&L0, &L1, Kt, Pb, Qn, cx, st, vnext, sel, ci);
-    if (ci + 1 < nchunks) scan_chunk<OUT, L2>(&L1, &L0, Kt, Pb, Qn, cx, st, vnext, sel, ci + 1);  // uniform
+    scan_chunk<OUT, L2, W>(&L0, &L1, Kt, Pb, Qn, cx, st, vnext, sel, ci);
+    if (ci + 1 < nchunks)                                                      // uniform
+      scan_chunk<OUT, L2, W>(&L1, &L0, Kt, Pb, Qn, cx, st, vnext, sel, ci + 1);
   }
-  if (st_out != nullptr) store_end(st_out, identity, st, sels);
+  if (st_out != nullptr) store_end(st_out, identity, st, sels, cw);
 }
 
 // ---------------------------------------------------------------------------
@@ -1738,6 +1801,11 @@ SegPlan seg_plan(long long L, long long N, long long HV) {
   }
   return best;
 }
+
+// A plain scan whose whole-state workgroups (N HV) would fill at most half
+// the CUs runs as half-state workgroups of 4 waves (two per (sequence,
+// v-head), one wave a SIMD): chunk steps at about half the cost.
+bool half_state_scan(long long N, long long HV) { return N >= 1 && 2 * N * HV <= kCUs; }
 
 bool use_segments(long long L, long long N, long long HV) {
   if (N < 1 || N > kFewSeqs || N * HV > kSegMaxHeads) return false;
@@ -1987,18 +2055,18 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
   }
   e = mark(2);
   if (e != hipSuccess) return e;
-  // One workgroup per (sequence or segment role, v-head), in groups of 8
-  // (unit, q/k head) pairs times the GVA ratio.
-  auto scan_grid = [&](long long units) {
-    return dim3(static_cast<unsigned>((units * H + 7) / 8 * 8 * p.ratio));
+  // One workgroup per (sequence or segment role, v-head, column half), in
+  // groups of 8 (unit, q/k head) pairs times the GVA ratio times the halves.
+  auto scan_grid = [&](long long units, int halves) {
+    return dim3(static_cast<unsigned>((units * H + 7) / 8 * 8 * p.ratio * halves));
   };
   if (p.seg_chunks > 0) {
     // segments: transitions and zero-start ends, the starts, then every
     // segment with its outputs (grids: the workspace's segments bound the
     // batch's units; workgroups past them exit)
-    auto* scan1 = p.few ? scan_kernel<true, true, false, false>
-                        : scan_kernel<false, true, false, false>;
-    hipLaunchKernelGGL(scan1, scan_grid(seg_units1(p.nseg, num_seqs)), dim3(kScanThreads), 0,
+    auto* scan1 = p.few ? scan_kernel<true, true, false, false, kScanWaves>
+                        : scan_kernel<false, true, false, false, kScanWaves>;
+    hipLaunchKernelGGL(scan1, scan_grid(seg_units1(p.nseg, num_seqs), 1), dim3(kScanThreads), 0,
                        stream, p);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -2007,17 +2075,24 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
                        dim3(64 * kCombWaves), 0, stream, p);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    auto* scan = p.few ? (p.l2norm ? scan_kernel<true, true, true, true>
-                                   : scan_kernel<true, true, true, false>)
-                       : (p.l2norm ? scan_kernel<false, true, true, true>
-                                   : scan_kernel<false, true, true, false>);
-    hipLaunchKernelGGL(scan, scan_grid(p.nseg), dim3(kScanThreads), 0, stream, p);
+    auto* scan = p.few ? (p.l2norm ? scan_kernel<true, true, true, true, kScanWaves>
+                                   : scan_kernel<true, true, true, false, kScanWaves>)
+                       : (p.l2norm ? scan_kernel<false, true, true, true, kScanWaves>
+                                   : scan_kernel<false, true, true, false, kScanWaves>);
+    hipLaunchKernelGGL(scan, scan_grid(p.nseg, 1), dim3(kScanThreads), 0, stream, p);
+  } else if (half_state_scan(num_seqs, HV)) {
+    constexpr int kHalfW = kScanWaves / 2;
+    auto* scan = p.few ? (p.l2norm ? scan_kernel<true, false, true, true, kHalfW>
+                                   : scan_kernel<true, false, true, false, kHalfW>)
+                       : (p.l2norm ? scan_kernel<false, false, true, true, kHalfW>
+                                   : scan_kernel<false, false, true, false, kHalfW>);
+    hipLaunchKernelGGL(scan, scan_grid(num_seqs, 2), dim3(64 * kHalfW), 0, stream, p);
   } else {
-    auto* scan = p.few ? (p.l2norm ? scan_kernel<true, false, true, true>
-                                   : scan_kernel<true, false, true, false>)
-                       : (p.l2norm ? scan_kernel<false, false, true, true>
-                                   : scan_kernel<false, false, true, false>);
-    hipLaunchKernelGGL(scan, scan_grid(num_seqs), dim3(kScanThreads), 0, stream, p);
+    auto* scan = p.few ? (p.l2norm ? scan_kernel<true, false, true, true, kScanWaves>
+                                   : scan_kernel<true, false, true, false, kScanWaves>)
+                       : (p.l2norm ? scan_kernel<false, false, true, true, kScanWaves>
+                                   : scan_kernel<false, false, true, false, kScanWaves>);
+    hipLaunchKernelGGL(scan, scan_grid(num_seqs, 1), dim3(kScanThreads), 0, stream, p);
   }
   e = hipGetLastError();
   if (e == hipSuccess) e = mark(3);

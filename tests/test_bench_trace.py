@@ -145,7 +145,7 @@ def test_prefill_counter_summary_and_its_sources_check(tmp_path, monkeypatch):
 
     copy = "__amd_rocclr_copyBuffer"
     prep = "void gdn_pf::prep_kernel<false>(gdn_pf::Params)"
-    scan = "void gdn_pf::scan_kernel<false, false, true, false>(gdn_pf::Params)"
+    scan = "void gdn_pf::scan_kernel<false, false, true, false, 8>(gdn_pf::Params)"
     off = "gdn_pf::chunk_offsets_kernel(gdn_pf::Params, int*, int __vector(4)*)"
     mib = 1024 * 1024
     calls = [(off, 1.0), (prep, 5.0), (scan, 7.0)] + [(off, 1.0), (prep, 100.0), (scan, 300.0)] * 2
