@@ -195,3 +195,34 @@ def test_multi_token_full_size(hip_device):
     ref_o, ref_s = oracle_tokens(oracle_vec, **t, use_qk_l2norm=True)
     assert_output_close(out.cpu(), ref_o)
     assert_state_close(new_state.cpu(), ref_s)
+
+
+@pytest.mark.parametrize("B,H,HV,T", [
+    (129, 4, 8, 1),     # power-of-two grid sizes, a last run of 4 groups (shift path)
+    (130, 3, 9, 1),     # GVA ratio 3 (division path), a last run of 6 groups
+    (128, 5, 15, 2),    # multi-token loop, division path, whole runs
+    (200, 3, 6, 4),     # T = 4 on the block kernel (1200 heads), division path
+])
+def test_xcd_grouped_launches(B, H, HV, T, hip_device):
+    """Launches of 128 or more sequences with an fp32 state renumber their
+    workgroups so that one sequence's share an XCD.  Against the oracle, and
+    bitwise against the same batch as two launches of fewer than 128
+    sequences (plain order: the per-head arithmetic does not depend on the
+    mapping)."""
+    _announce(f"xcd-grouped B={B} H={H} HV={HV} T={T}")
+    t = make_inputs(B, H, HV, seed=5700 + B + T, T=T)
+    td = _dev(t, hip_device)
+    out, new_state = gdn.run(**td, use_qk_l2norm=True)
+    torch.cuda.synchronize()
+    ref_o, ref_s, o64, s64 = _oracle(t, True, torch.float32)
+    assert_output_close(out.cpu(), ref_o, tight_ref64=o64, what="output")
+    assert_state_close(new_state.cpu(), ref_s)
+    half = B // 2
+    parts = []
+    for lo, hi in ((0, half), (half, B)):
+        sl = {n: (x[lo:hi] if isinstance(x, torch.Tensor) and n not in ("A_log", "dt_bias")
+                  else x) for n, x in td.items()}
+        parts.append(gdn.run(**sl, use_qk_l2norm=True))
+    torch.cuda.synchronize()
+    assert torch.equal(out, torch.cat([p[0] for p in parts]))
+    assert torch.equal(new_state, torch.cat([p[1] for p in parts]))
