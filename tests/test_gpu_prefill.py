@@ -59,6 +59,7 @@ def _check(t, out, st, l2=False, loop=True):
 @pytest.mark.parametrize("seqlens,H,HV", [
     ([70] + [1] * 63, 4, 8),          # 64 sequences: chunk slots found in the kernels
     ([70] + [1] * 64, 4, 8),          # 65: the chunk-offsets scan
+    ([70] + [1] * 99, 1, 1),          # 100: the offsets scan, then half-state scan workgroups
     ([0, 130, 0, 0, 64, 1, 0], 2, 4), # empty sequences among few
     ([6], 4, 8),                      # the size of the reference's prefill workload 0
     ([1], 4, 8),
