@@ -24,7 +24,10 @@
 // variable-length mode (gdn_decode_kernel.h) applies the recurrence token by
 // token with the state in registers, one workgroup per (sequence, v-head,
 // row tile), reading each sequence's token range from cu_seqlens on the
-// device.  Larger prefills run the chunkwise kernels.
+// device.  Larger prefills run the chunkwise kernels -- after that launch,
+// for 2..64 sequences that may all be that short (the host knows only the
+// total): it runs only if every sequence is, and the chunkwise kernels then
+// return at once.
 //
 // Kernels (one stream, in order):
 //   1. chunk_offsets: one workgroup turns cu_seqlens into the first chunk
@@ -32,18 +35,22 @@
 //      and writes each slot's sequence, first token and token count.  With
 //      one sequence, or a few (their slots found in the kernels), it is not
 //      launched.
-//   2. prep, grid (chunk slots, H), four workgroups per CU: what does not
-//      depend on the state, for all chunks at once -- K K^T (bf16 MFMA: the
-//      inputs are bf16, once per q/k head), then per v-head the gates and
+//   2. prep, grid (chunk slots, H) -- or (chunk slots, HV), one v-head a
+//      workgroup, when all of those fit on the GPU at once -- four
+//      workgroups per CU: what does not depend on the state, for all chunks
+//      at once -- K K^T (bf16 MFMA: the inputs are bf16, once per q/k head
+//      and workgroup), then per v-head the gates and
 //      gamma and T by block recursion (fp32 MFMA) -- into a 14 KiB workspace
 //      slot per (chunk, v-head): the lower blocks of T diag(beta), split
 //      into bf16 hi + lo in the order the scan's MFMAs read them, and the
 //      row scales.
 //   3. scan, one workgroup per (sequence, v-head), XCD-aware order: the
 //      sequential part chunk after chunk with the whole 128 x 128 state in
-//      the registers of four wavefronts (32 columns each); the chunk's K,
-//      Q rows and slot reach LDS by DMA a chunk ahead, into the other of two
-//      buffers.  Products with fp32 operands run as bf16 MFMA on hi/lo
+//      the registers of eight wavefronts (16 columns each) -- or, for a batch
+//      that would fill at most half the CUs, two workgroups of four
+//      wavefronts per (sequence, v-head), half the state each; the chunk's
+//      K, Q rows and slot reach LDS by DMA a chunk ahead, into the other of
+//      two buffers.  Products with fp32 operands run as bf16 MFMA on hi/lo
 //      splits.  Each workgroup reads its chunks' inputs once, so the
 //      workspace is the only HBM traffic beyond the algorithmic bytes.
 //   One long sequence at few v-heads is cut into segments, since its scan
@@ -848,14 +855,17 @@ void prep_kernel(Params p) {
 }
 
 // ---------------------------------------------------------------------------
-// 3. the scan: one workgroup per (sequence, v-head), the whole state
+// 3. the scan: one workgroup per (sequence, v-head) and the whole state, or
+//    two per (sequence, v-head) and half the state each
 // ---------------------------------------------------------------------------
-// Eight waves, two per SIMD: wave w keeps state columns 16 w .. 16 w + 15 of
-// all 128 keys in registers, in the MFMA result layout: st[t] holds keys
-// 16 t + 4 g + e of column 16 w + col.  Read as runs of the k order, the
-// same registers are the state's operand of a product over keys in either
-// role (B of K S, A of S^T Q^T), and every per-chunk result is the next
-// product's operand in place.  Per chunk, with S its start state:
+// W waves (8, two per SIMD; or 4, one per SIMD): the wave of column wave w
+// keeps state columns 16 w .. 16 w + 15 of all 128 keys in registers, st[t]
+// holding keys state_key(t, g) + e of column 16 w + col (lane (col, g)).
+// Read as pairs (st[2 kb], st[2 kb + 1]: keys 32 kb + 8 g .. + 7), the same
+// registers are the state's operand of a product over keys in either role
+// (B of K S, A of S^T Q^T), in the key order of the K and Q operands read
+// from LDS, and every per-chunk result is the next product's operand in
+// place.  Per chunk, with S its start state:
 //   X      = V - diag(rk e^gamma) K S
 //   Delta  = T diag(beta) X
 //   O^T    = S^T Q^T diag(scale rq e^gamma) + Delta^T P^T
@@ -871,9 +881,9 @@ void prep_kernel(Params p) {
 // contracted index come from products with a selector (a 32 x 16 block of
 // the identity), which moves a 16 x 32 row block's columns into the result
 // layout exactly: V^T tiles (each wave's own 16 columns of V, loaded into
-// registers a chunk ahead) and K^T tiles (wave w makes key tile w from the K
-// rows in LDS and shares it through LDS: a second barrier per chunk, before
-// the state update).
+// registers a chunk ahead) and K^T tiles (wave w makes key tiles w, w + W,
+// ... from the K rows in LDS and shares them through LDS: a second barrier
+// per chunk, before the state update).
 constexpr int kScanWaves = 8;
 constexpr int kScanThreads = 64 * kScanWaves;
 // A scan workgroup of W waves holds 16 W state columns: W = 8, the whole
@@ -1091,8 +1101,8 @@ __device__ __forceinline__ void issue_part(ScanBuf<OUT>* __restrict__ Bn, const 
 }
 
 // P' tiles (row tile r, token tile jt) of a chunk, 10 nonzero and the two
-// zero ones inside the stored blocks (0, 1) and (2, 3); wave w makes tiles w
-// and w + 8.
+// zero ones inside the stored blocks (0, 1) and (2, 3); wave w of W makes
+// tiles w, w + W, ....
 // Tile idx is (r, jt) = ((kPTileR >> 2 idx) & 3, (kPTileJ >> 2 idx) & 3):
 //   r  = 0, 1, 1, 2, 2, 2, 3, 3, 3, 3, 0, 2
 //   jt = 0, 0, 1, 0, 1, 2, 0, 1, 2, 3, 1, 3
