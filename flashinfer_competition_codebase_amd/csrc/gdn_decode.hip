@@ -29,7 +29,10 @@
 //   * grid (ratio*R, H, B) with ratio = HV/H: x = (v-head within its GVA
 //     group, row tile), y = q/k head, z = batch.  Every index is a shift or
 //     a multiply-add (no integer division before the first load), and the
-//     x-fastest dispatch order walks the state in memory order;
+//     x-fastest dispatch order walks the state in memory order -- except in
+//     launches of 128 or more sequences with an fp32 state, whose workgroups
+//     are renumbered so that those of one (sequence, q/k head) share an XCD
+//     (decode_grid_pos; shifts for power-of-two grid sizes);
 //   * dot products over K reduce inside the 16-lane row with four DPP adds
 //     (quad_perm xor1, quad_perm xor2, row_half_mirror, row_mirror), so no
 //     LDS or cross-row traffic is needed.
