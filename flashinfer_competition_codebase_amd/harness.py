@@ -49,10 +49,11 @@ Command line (arguments as scripts/shared.py:93-142):
     python -m flashinfer_competition_codebase_amd.harness attribute \\
         --trace out/run_kernel_trace.csv --manifest calls.json [--definition ...]
 
-In the trace tier a prefill call is its chunk-offsets (several sequences),
-preparation and scan dispatches -- or its one dispatch of the token-by-token
-kernel for a prefill of at most 56 tokens -- timed from the first one's
-start to the last one's end.
+In the trace tier a prefill call is its dispatches (``prefill_dispatches``:
+the chunk-offsets scan for several sequences, preparation and scan, two more
+with segments, the token-by-token kernel first for a batch that may be all
+short sequences -- or that kernel alone for a prefill of at most 56 tokens),
+timed from the first one's start to the last one's end.
 """
 
 from __future__ import annotations

@@ -62,10 +62,12 @@ def token_path_max_tokens() -> int:
 
 def prefill_dispatches(total_seq_len: int, num_seqs: int, HV: int) -> int:
     """Kernel dispatches of one prefill call over HV v-heads, as the library
-    makes them: 1 on the token-by-token path, else 2 (preparation, scan) for
-    one sequence or a few small ones (at most 64, at most 2048 preparation
-    workgroups) and 3 (the chunk-offsets scan first) otherwise; 0 for no
-    sequences."""
+    makes them (``gdn_prefill_dispatches``): 0 for no sequences, 1 on the
+    token-by-token path; else 2 (preparation, scan) or, for a batch scanned
+    in segments, 4 (preparation, two segment scans and their combine), plus
+    the chunk-offsets scan first unless there is one sequence or at most 64
+    with at most 2048 (slot, v-head) pairs, plus the token-by-token kernel
+    first for 2..64 sequences of at most 56 tokens on average."""
     return int(_lib.get_prefill_lib().gdn_prefill_dispatches(int(total_seq_len), int(num_seqs),
                                                             int(HV)))
 

@@ -74,10 +74,15 @@ size_t gdn_prefill_workspace_bytes(int total_seq_len, int num_seqs, int H, int H
  * q, k, v, output, state and new_state must be 16-byte aligned.
  * Launches one kernel when total_seq_len <= gdn_prefill_token_path_max_tokens()
  * (and num_seqs <= 65535), else the chunkwise kernels: the chunk-offsets
- * scan (only when gdn_prefill_dispatches returns 3 or 5), preparation, scan
- * (for a few sequences whose scans would leave most CUs idle: their
- * segments scanned at once in two launches with the combination of their
- * starts between them, see gdn_prefill_dispatches).
+ * scan (not for one sequence, nor for at most 64 whose slots the kernels
+ * find themselves), preparation, scan (for a few sequences whose scans would
+ * leave most CUs idle: their segments scanned at once in two launches with
+ * the combination of their starts between them).  For 2..64 sequences of at
+ * most gdn_prefill_token_path_max_tokens() tokens on average, the
+ * token-by-token kernel is launched first: it runs only if every sequence
+ * is that short (read from cu_seqlens on the device), and the chunkwise
+ * kernels after it then return at once; otherwise they run the whole batch.
+ * gdn_prefill_dispatches gives the launch count.
  */
 int gdn_prefill(const void* q, const void* k, const void* v, const float* state,
                 const float* A_log, const void* a, const float* dt_bias, const void* b,
@@ -140,14 +145,15 @@ int gdn_prefill_token_path_max_tokens(void);
 
 /*
  * Kernel launches gdn_prefill makes for these sizes: 0 for no sequences, 1
- * on the token-by-token path, 4 (preparation, first segment scan, combine,
- * second segment scan) for a batch scanned in segments (5 with the
- * chunk-offsets scan first, as below), 2
- * (preparation, scan) for another single sequence or for
- * at most 64 with at most 2048 preparation workgroups (min(ceil(L / 64) + N,
- * L) x HV; the kernels then find the chunk slots from cu_seqlens
- * themselves), 3 (the chunk-offsets scan first) otherwise.  No counterpart in the
- * reference; for callers that attribute kernel traces to calls.
+ * on the token-by-token path; else the chunkwise kernels -- 2 (preparation,
+ * scan), or 4 for a batch scanned in segments (preparation, first segment
+ * scan, combine, second segment scan) -- plus 1 for the chunk-offsets scan
+ * first, except for a single sequence and for at most 64 with at most 2048
+ * (slot, v-head) pairs (min(ceil(L / 64) + N, L) x HV; the kernels then find
+ * the chunk slots from cu_seqlens themselves), plus 1 for the token-by-token
+ * kernel launched before them for 2..64 sequences of at most
+ * gdn_prefill_token_path_max_tokens() tokens on average.  No counterpart in
+ * the reference; for callers that attribute kernel traces to calls.
  */
 int gdn_prefill_dispatches(int total_seq_len, int num_seqs, int HV);
 
