@@ -15,6 +15,18 @@ exceeds 1 (raw N(0,1) keys, |k|^2 ~ 128, multiply a state's k-component by
 ~|1 - 128 beta| per token, so after a few tokens entries of 1e3-1e4 make
 one fp32 rounding ~1e-3 and an entry that cancels to near zero cannot meet
 a fixed 1e-5), and within 1e-3 in relative Frobenius norm.
+
+Two more sweeps reach the sizes the first two keep clear of: decode batches
+up to 256 (the launch-shape table's larger rows, the XCD-grouped launches,
+the block kernel) at up to 8 tokens, and prefills of up to 100 sequences
+(the chunk-offsets scan) and up to 1500 tokens a sequence (segments), at up
+to 32 v-heads.  Their decode keys are raw N(0, 1) rows only for single
+tokens: over several tokens without the L2-norm they are scaled to unit norm
+first (the normalisation the model applies before this step; raw keys grow
+the state to 400-1400 within 2 to 4 tokens, where the fp32 oracle itself
+misses a 1e-4 absolute bar against the float64 result), and their fp32
+states meet both the oracle's bar (1e-3 relative + 1e-5) and 1e-4 absolute
+against float64.
 """
 
 from __future__ import annotations
@@ -31,7 +43,7 @@ import flashinfer_competition_codebase_amd as gdn
 from flashinfer_competition_codebase_amd import _lib
 from oracle.gdn_decode_oracle import make_inputs, oracle_loop, oracle_tokens, oracle_vec
 from oracle.gdn_prefill_oracle import make_prefill_inputs, prefill_chunked_fp64, prefill_loop
-from tests.gdn_cases import assert_output_close
+from tests.gdn_cases import assert_output_close, assert_state_close
 
 pytestmark = pytest.mark.gpu
 
@@ -194,3 +206,99 @@ def test_prefill_sweep(c, hip_device):
     for s, n in enumerate(lens):                      # empty sequences: zero state
         if n == 0:
             assert torch.count_nonzero(st[s]) == 0
+
+
+# (q/k heads, v-heads) of the larger sweeps
+_HEADS = [(1, 1), (1, 4), (2, 4), (3, 12), (4, 8), (5, 15), (8, 32), (16, 32), (2, 16), (4, 4)]
+
+
+def _bf16_state_ok(st, ref_s, s64):
+    sc = st.cpu().double()
+    d_ref = (sc - ref_s.double()).abs()
+    assert bool((d_ref <= 2.0 ** -7 * ref_s.double().abs() + 1e-6).all()), "beyond one bf16 ulp"
+    assert (d_ref > 0).double().mean().item() <= 1e-3, "too many elements off the oracle's"
+    assert bool(((sc - s64).abs() <= 2.0 ** -8 * s64.abs() + 1e-6).all()), "not the RNE"
+
+
+def _large_decode_case(i):
+    r = random.Random(9100 + i)
+    H, HV = r.choice(_HEADS)
+    l2 = r.random() < 0.6
+    T = r.choice([1, 1, 1, 2, 3, 4, 5, 8])
+    bf16 = r.random() < 0.3
+    B = r.choice([1, 2, 3, 5, 8, 17, 33, 64, 100, 128, 129, 200, 256])
+    while B * HV > 4096:
+        B //= 2
+    return B, H, HV, T, l2, bf16, r.random() < 0.5
+
+
+@pytest.mark.parametrize("i", range(24))
+def test_decode_sweep_large_batches(i, hip_device):
+    B, H, HV, T, l2, bf16, in_place = _large_decode_case(i)
+    _announce(f"decode sweep, large batches {i}: B={B} H={H} HV={HV} T={T} l2={l2} "
+              f"bf16={bf16} in_place={in_place}")
+    t = make_inputs(B, H, HV, seed=9200 + i, T=T)
+    if T > 1 and not l2:
+        for n in ("q", "k"):
+            x = t[n].float()
+            t[n] = (x / x.norm(dim=-1, keepdim=True).clamp_min(1e-6)).to(torch.bfloat16)
+    sd = torch.bfloat16 if bf16 else torch.float32
+    t["state"] = t["state"].to(sd)
+    td = _dev(t, hip_device)
+    if in_place:
+        out = torch.empty(B, T, HV, 128, dtype=torch.bfloat16, device=hip_device)
+        st = td["state"].clone()
+        gdn.kernel_hip(**{**td, "state": st}, output=out, new_state=st, use_qk_l2norm=l2)
+    else:
+        out, st = gdn.run(**td, use_qk_l2norm=l2)
+    torch.cuda.synchronize()
+    step = oracle_loop if B * HV <= 256 else oracle_vec
+    ref_o, ref_s = oracle_tokens(step, **t, use_qk_l2norm=l2, state_dtype=sd)
+
+    def vec64(*args, **kw):
+        return oracle_vec(*args, **kw, output_fp32=True, dtype=torch.float64)
+
+    o64, s64 = oracle_tokens(vec64, **t, use_qk_l2norm=l2, state_dtype=None)
+    assert_output_close(out.cpu(), ref_o, tight_ref64=o64, what="output")
+    if bf16:
+        _bf16_state_ok(st, ref_s, s64)
+    else:
+        assert_state_close(st.cpu(), ref_s)
+        assert (st.cpu().double() - s64).abs().max().item() < 1e-4
+
+
+def _long_prefill_case(i):
+    r = random.Random(9300 + i)
+    H, HV = r.choice(_HEADS[:7] + [(2, 16)])
+    N = r.choice([1, 1, 2, 3, 5, 8, 16, 40, 64, 65, 100])
+    longest = r.choice([8, 56, 64, 130, 300, 1500])
+    lens = [r.choice([0, 1, r.randint(1, longest)]) if r.random() < 0.2 else r.randint(1, longest)
+            for _ in range(N)]
+    while sum(lens) * HV > 24000:
+        lens = [x // 2 for x in lens]
+    return lens, H, HV, r.random() < 0.5, r.random() < 0.8
+
+
+@pytest.mark.parametrize("i", range(24))
+def test_prefill_sweep_many_and_long_sequences(i, hip_device):
+    lens, H, HV, l2, with_state = _long_prefill_case(i)
+    _announce(f"prefill sweep, many and long sequences {i}: N={len(lens)} L={sum(lens)} "
+              f"longest={max(lens)} H={H} HV={HV} l2={l2} state={with_state}")
+    t = make_prefill_inputs(lens, H, HV, seed=9400 + i, with_state=with_state)
+    out, st = gdn.prefill_run(**_dev(t, hip_device), use_qk_l2norm=l2)
+    torch.cuda.synchronize()
+    out, st = out.cpu(), st.cpu()
+    o64, s64 = prefill_chunked_fp64(**t, use_qk_l2norm=l2)
+    of = out.double().numpy()
+    assert np.all(np.isfinite(of))
+    d64 = np.abs(of - o64)
+    assert np.all(d64 <= 2.0 ** -7 * np.abs(o64) + 1e-5), f"output vs fp64: max {d64.max():.3e}"
+    if sum(lens) * HV <= 2400:
+        ref_o, _ = prefill_loop(**t, use_qk_l2norm=l2)
+        dl = (out.float() - ref_o.float()).abs()
+        assert bool((dl <= 1e-2 + 1e-2 * ref_o.float().abs()).all()), f"output vs loop {dl.max()}"
+    sd = st.double().numpy()
+    ds = np.abs(sd - s64)
+    assert np.all(ds <= 1e-3 * np.abs(s64) + 1e-5), f"state vs fp64: max {ds.max():.3e}"
+    rel = np.linalg.norm(sd - s64) / max(np.linalg.norm(s64), 1e-30)
+    assert rel <= 1e-4, rel
