@@ -302,3 +302,25 @@ def test_prefill_sweep_many_and_long_sequences(i, hip_device):
     assert np.all(ds <= 1e-3 * np.abs(s64) + 1e-5), f"state vs fp64: max {ds.max():.3e}"
     rel = np.linalg.norm(sd - s64) / max(np.linalg.norm(s64), 1e-30)
     assert rel <= 1e-4, rel
+
+
+@pytest.mark.parametrize("N,longest,H,HV,seed", [(1000, 20, 3, 6, 56004), (2000, 8, 4, 8, 56008)])
+def test_prefill_thousands_of_sequences(N, longest, H, HV, seed, hip_device):
+    """Thousands of short sequences (a tenth of them empty): the chunk-offsets
+    scan over all of them and thousands of scan workgroups."""
+    _announce(f"prefill of {N} sequences of at most {longest} tokens, H={H} HV={HV}")
+    r = random.Random(seed)
+    lens = [0 if r.random() < 0.1 else r.randint(1, longest) for _ in range(N)]
+    t = make_prefill_inputs(lens, H, HV, seed=seed)
+    out, st = gdn.prefill_run(**_dev(t, hip_device))
+    torch.cuda.synchronize()
+    o64, s64 = prefill_chunked_fp64(**t)
+    of = out.cpu().double().numpy()
+    d64 = np.abs(of - o64)
+    assert np.all(d64 <= 2.0 ** -7 * np.abs(o64) + 1e-5), f"output vs fp64: max {d64.max():.3e}"
+    sd = st.cpu().double().numpy()
+    ds = np.abs(sd - s64)
+    assert np.all(ds <= 1e-3 * np.abs(s64) + 1e-5), f"state vs fp64: max {ds.max():.3e}"
+    for s, n in enumerate(lens):
+        if n == 0:
+            assert not np.any(sd[s])
