@@ -296,7 +296,10 @@ def kernel_hip(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
     A call with the same tensor objects (unchanged data pointers), a float or
     None scale and the same flag as an earlier validated call -- a decode
     loop's steady state -- skips the checks and launches the native plan
-    bound then: one three-argument native call.
+    bound then: one three-argument native call.  Shapes are not compared on
+    that path: a tensor reshaped in place with its data pointer unchanged
+    (``resize_`` within its storage, ``as_strided_``) is used with the sizes
+    it was validated with; pass a new tensor object (a view) instead.
     """
     tp = type(scale)
     if scale is None or tp is float or tp is int:
