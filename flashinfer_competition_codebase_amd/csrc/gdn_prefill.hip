@@ -24,8 +24,13 @@
 // variable-length mode (gdn_decode_kernel.h) applies the recurrence token by
 // token with the state in registers, one workgroup per (sequence, v-head,
 // row tile), reading each sequence's token range from cu_seqlens on the
-// device.  Larger prefills run the chunkwise kernels -- after that launch,
-// for 2..64 sequences that may all be that short (the host knows only the
+// device.  Prefills of 57 to 64 tokens in all (every sequence one chunk)
+// whose (sequence, v-head) pairs fill at most half the CUs run one launch of
+// the one-chunk kernel: each half-state scan workgroup prepares its
+// sequence's chunk in its own LDS (kernel 2's code) and scans it (kernel
+// 3's), so the slot never goes through the workspace.  Larger prefills run
+// the chunkwise kernels -- after the token kernel's launch, for 2..64
+// sequences that may all be at most 56 tokens long (the host knows only the
 // total): it runs only if every sequence is, and the chunkwise kernels then
 // return at once.
 //
@@ -583,42 +588,13 @@ __device__ __forceinline__ void store16(float* D, int ldd, const f32x4& v, float
   for (int e = 0; e < 4; ++e) D[(4 * g4 + e) * ldd + col] = sign * v[e];
 }
 
-// FEW: the batch's chunk slots come from cu_seqlens in the kernel (few
-// sequences, no offsets kernel); a template flag, so that the kernels of the
-// other modes are compiled without that code.
-template <bool FEW>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4)))
-void prep_kernel(Params p) {
-  __shared__ PrepLds lds;
-  const int c = blockIdx.x;
-  // v-heads hv0 .. hv0 + prep_heads - 1, all of q/k head h
-  const int hv0 = static_cast<int>(blockIdx.y) * p.prep_heads;
-  const int h = hv0 / p.ratio;
-  if (p.short_limit > 0 && all_within(p, p.short_limit)) return;    // uniform
-  int t0, n;                                       // n: 1..64, 0 past the last slot
-  if (p.single) {
-    int start, end;
-    seq_range(p, 0, start, end);
-    t0 = start + c * kChunk;
-    n = min(kChunk, end - t0);
-  } else if (FEW) {
-    // slot c belongs to the sequence whose slots [excl, incl) hold it
-    const FewSlots f = few_slots(p);
-    const unsigned long long own = __ballot(f.excl <= c && c < f.incl);
-    t0 = 0;
-    n = 0;
-    if (own != 0) {
-      const int s = __builtin_ctzll(own);
-      const long long first = __shfl(f.excl, s, 64);
-      t0 = __shfl(f.start, s, 64) + static_cast<int>(c - first) * kChunk;
-      n = min(kChunk, __shfl(f.end, s, 64) - t0);
-    }
-  } else {
-    const i32x4 info = p.slot_info[c];
-    t0 = info.y;
-    n = info.z;
-  }
-  if (n <= 0) return;                              // uniform per workgroup
+// One chunk's preparation, tokens t0 .. t0 + n - 1 (n: 1..64) of q/k head h,
+// for v-heads hv0 .. hv0 + prep_heads - 1, by the 256 threads of the calling
+// workgroup: the slots go to the workspace (slot c), or with LDS_SLOT (one
+// v-head) to lds_slot in the calling workgroup's LDS.
+template <bool LDS_SLOT>
+__device__ __forceinline__ void prep_chunk(Params p, int c, int t0, int n, int hv0, int h,
+                                           int prep_heads, PrepLds& lds, float* lds_slot) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int col = lane & 15;
@@ -636,7 +612,7 @@ void prep_kernel(Params p) {
     const size_t tk = static_cast<size_t>(t0 + (lane < n ? lane : n - 1)) * p.HV + hv0;
 #pragma unroll
     for (int j = 0; j < kPrepGateHeads; ++j) {
-      const int jj = j < p.prep_heads ? j : 0;
+      const int jj = j < prep_heads ? j : 0;
       a_raw[j] = p.a[tk + jj];
       b_raw[j] = p.b[tk + jj];
       dtb[j] = p.dt_bias[hv0 + jj];
@@ -696,9 +672,10 @@ void prep_kernel(Params p) {
   // Each v-head of the group: its gates, A from the shared product, T, and
   // its slot.  The LDS the previous v-head used (gamma, beta, A, T)
   // is rewritten only after the barrier that ends its use.
-  for (int j = 0; j < p.prep_heads; ++j) {
+  for (int j = 0; j < prep_heads; ++j) {
     const int hv = hv0 + j;
-    float* slot = p.slots + (static_cast<size_t>(c) * p.HV + hv) * kSlotFloats;
+    float* slot = LDS_SLOT ? lds_slot
+                           : p.slots + (static_cast<size_t>(c) * p.HV + hv) * kSlotFloats;
     uint16_t* slot16 = reinterpret_cast<uint16_t*>(slot);
     // gates of token t0 + lane (padded rows: no decay, no update), and the
     // inclusive scan of the log-decay over the chunk
@@ -854,6 +831,45 @@ void prep_kernel(Params p) {
   }
 }
 
+// FEW: the batch's chunk slots come from cu_seqlens in the kernel (few
+// sequences, no offsets kernel); a template flag, so that the kernels of the
+// other modes are compiled without that code.
+template <bool FEW>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4)))
+void prep_kernel(Params p) {
+  __shared__ PrepLds lds;
+  const int c = blockIdx.x;
+  // v-heads hv0 .. hv0 + prep_heads - 1, all of q/k head h
+  const int hv0 = static_cast<int>(blockIdx.y) * p.prep_heads;
+  const int h = hv0 / p.ratio;
+  if (p.short_limit > 0 && all_within(p, p.short_limit)) return;    // uniform
+  int t0, n;                                       // n: 1..64, 0 past the last slot
+  if (p.single) {
+    int start, end;
+    seq_range(p, 0, start, end);
+    t0 = start + c * kChunk;
+    n = min(kChunk, end - t0);
+  } else if (FEW) {
+    // slot c belongs to the sequence whose slots [excl, incl) hold it
+    const FewSlots f = few_slots(p);
+    const unsigned long long own = __ballot(f.excl <= c && c < f.incl);
+    t0 = 0;
+    n = 0;
+    if (own != 0) {
+      const int s = __builtin_ctzll(own);
+      const long long first = __shfl(f.excl, s, 64);
+      t0 = __shfl(f.start, s, 64) + static_cast<int>(c - first) * kChunk;
+      n = min(kChunk, __shfl(f.end, s, 64) - t0);
+    }
+  } else {
+    const i32x4 info = p.slot_info[c];
+    t0 = info.y;
+    n = info.z;
+  }
+  if (n <= 0) return;                              // uniform per workgroup
+  prep_chunk<false>(p, c, t0, n, hv0, h, p.prep_heads, lds, nullptr);
+}
+
 // ---------------------------------------------------------------------------
 // 3. the scan: one workgroup per (sequence, v-head) and the whole state, or
 //    two per (sequence, v-head) and half the state each
@@ -956,9 +972,9 @@ __device__ __forceinline__ void barrier_lds_no_dma() {
 }
 
 // DMA of a chunk's K rows, Q rows (OUT; rows >= n repeat row n - 1; each
-// row's padding piece repeats its last piece) and slot into one LDS buffer;
-// wave w of W issues instructions w, w + W, ....
-template <bool OUT, int W>
+// row's padding piece repeats its last piece) and slot (SLOT) into one LDS
+// buffer; wave w of W issues instructions w, w + W, ....
+template <bool OUT, int W, bool SLOT = true>
 __device__ __forceinline__ void scan_dma(ScanBuf<OUT>& B, const uint16_t* kbase,
                                          const uint16_t* qbase, unsigned step, int n,
                                          const float* slot, int wave, int lane) {
@@ -969,8 +985,10 @@ __device__ __forceinline__ void scan_dma(ScanBuf<OUT>& B, const uint16_t* kbase,
     dma16_at(kbase, off, &B.Kr[i * 512]);
     if constexpr (OUT) dma16_at(qbase, off, &B.Qr[i * 512]);
   }
-  for (int i = wave; i < kSlotDma; i += W)
-    dma16_at(slot, static_cast<unsigned>(i * 64 + lane) * 16u, &B.slot[i * 256]);
+  if constexpr (SLOT) {
+    for (int i = wave; i < kSlotDma; i += W)
+      dma16_at(slot, static_cast<unsigned>(i * 64 + lane) * 16u, &B.slot[i * 256]);
+  }
 }
 
 // This wave's 16 columns of V for token tile r (lane (col, g): token
@@ -1028,14 +1046,14 @@ __device__ __forceinline__ int column_wave(const ScanCtx& cx, int wave) {
   return W == kScanWaves ? wave : cx.cw0 + wave;
 }
 
-// Chunk c's DMA into buf and its V into registers.
-template <bool OUT, int W>
+// Chunk c's DMA into buf (its slot with SLOT) and its V into registers.
+template <bool OUT, int W, bool SLOT = true>
 __device__ __forceinline__ void scan_issue(ScanBuf<OUT>* buf, const ScanCtx& cx, int c,
                                            u32x2 (&vf)[4]) {
   const int wave = wave_index(), lane = threadIdx.x & 63;
   const int tc = cx.start + c * kChunk;
   const int nc = min(kChunk, cx.end - tc);
-  scan_dma<OUT, W>(*buf, cx.k + (static_cast<size_t>(tc) * cx.H + cx.h) * kDim,
+  scan_dma<OUT, W, SLOT>(*buf, cx.k + (static_cast<size_t>(tc) * cx.H + cx.h) * kDim,
                    cx.q + (static_cast<size_t>(tc) * cx.H + cx.h) * kDim, cx.kstep, nc,
                    cx.slot_base + c * cx.slot_step, wave, lane);
   load_v(vf, cx.v + (static_cast<size_t>(tc) * cx.HV + cx.hv) * kDim, cx.vstep, nc,
@@ -1136,7 +1154,7 @@ __device__ __forceinline__ void p_tile_mma(const s16x8 (&ak)[4], const s16x8 (&b
 // operand of Delta^T P'^T.  The Q row scales rq = 1 / |q_i| (L2-norm; each
 // wave computes eight rows' from the Q rows in LDS and shares them through
 // Qn) scale the output row: O = diag(rq) (diag(scale e^gamma) Q S + P' Delta).
-template <bool OUT, bool L2, int W>
+template <bool OUT, bool L2, int W, bool FUSE = false>
 __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
                                            ScanBuf<OUT>* __restrict__ Bn,
                                            uint16_t* __restrict__ Kt, uint16_t* __restrict__ Pb,
@@ -1217,7 +1235,7 @@ __device__ __forceinline__ void scan_chunk(const ScanBuf<OUT>* __restrict__ B,
   for (int kb = 0; kb < 4; ++kb) {
     const int set = kb & 1;
     if (kb < 3) read_ops(kb + 1, set ^ 1);
-    issue_part<OUT, W>(Bn, cx, nsrc, kb, vnext);
+    if constexpr (!FUSE) issue_part<OUT, W>(Bn, cx, nsrc, kb, vnext);   // FUSE: one chunk
 #pragma unroll
     for (int m = 0; m < kKtTiles; ++m) {
       if (kb == ((wave + W * m) >> 1)) {                    // uniform per wave
@@ -1470,11 +1488,11 @@ __device__ __forceinline__ void store_end(float* st_out, bool transition, const 
 // values (end: seg_M, as the combine's operand); the second (OUT) runs every
 // segment from its start (segment 0: the sequence's state, then seg_S) with
 // the outputs, the last one's end being the new state.
-template <bool FEW, bool SEG, bool OUT, bool L2, int W>
-__global__ __launch_bounds__(64 * W)
-__attribute__((amdgpu_waves_per_eu(W == kScanWaves ? 2 : 1, W == kScanWaves ? 2 : 1)))
-void scan_kernel(Params p) {
+template <bool FEW, bool SEG, bool OUT, bool L2, int W, bool FUSE>
+__device__ __forceinline__ void scan_body(Params p) {
   static_assert(OUT || SEG, "only segments run without outputs");
+  static_assert(!FUSE || (!FEW && !SEG && OUT && W == kThreads / 64),
+                "the one-chunk kernel: half-state workgroups of the preparation's width");
   static_assert(OUT || !L2, "the L2-norm scales outputs only");
   static_assert(W == kScanWaves || (W == kScanWaves / 2 && !SEG),
                 "half-state workgroups run plain scans only");
@@ -1575,7 +1593,10 @@ void scan_kernel(Params p) {
     seq_range(p, s, start, end);
     st_in = p.state ? p.state + (static_cast<size_t>(s) * p.HV + hv) * blk : nullptr;
     st_out = p.new_state + (static_cast<size_t>(s) * p.HV + hv) * blk;
-    seq_slots(s, slot0, nchunks);
+    if constexpr (FUSE)
+      nchunks = end > start ? 1 : 0;    // every sequence is one chunk (at most 64 tokens in all)
+    else
+      seq_slots(s, slot0, nchunks);
   }
 
   // state registers (keys in the order of state_key); k-last storage: 4
@@ -1642,6 +1663,20 @@ void scan_kernel(Params p) {
 
   const s16x8 sel = sels[wave & 1];       // this wave's half of a 32-key / 32-column block
   u32x2 vnext[4];
+  if constexpr (FUSE) {
+    // The chunk's K and Q rows by DMA and its V while this workgroup prepares
+    // its slot in LDS (the preparation's LDS in the second buffer, which one
+    // chunk never uses), then its one chunk step.
+    static_assert(sizeof(PrepLds) <= sizeof(ScanBuf<OUT>), "the preparation fits a buffer");
+    scan_issue<OUT, W, false>(&L0, cx, 0, vnext);
+    prep_chunk<true>(p, 0, start, end - start, hv, h, 1, *reinterpret_cast<PrepLds*>(&L1),
+                     L0.slot);
+    wait_vmem();
+    block_sync_lds();
+    scan_chunk<OUT, L2, W, true>(&L0, &L1, Kt, Pb, Qn, cx, st, vnext, sel, 0);
+    if (st_out != nullptr) store_end(st_out, identity, st, sels, cw);
+    return;
+  }
   scan_issue<OUT, W>(&L0, cx, 0, vnext);
   wait_vmem();
   block_sync_lds();
@@ -1651,6 +1686,21 @@ void scan_kernel(Params p) {
       scan_chunk<OUT, L2, W>(&L1, &L0, Kt, Pb, Qn, cx, st, vnext, sel, ci + 1);
   }
   if (st_out != nullptr) store_end(st_out, identity, st, sels, cw);
+}
+
+template <bool FEW, bool SEG, bool OUT, bool L2, int W>
+__global__ __launch_bounds__(64 * W)
+__attribute__((amdgpu_waves_per_eu(W == kScanWaves ? 2 : 1, W == kScanWaves ? 2 : 1)))
+void scan_kernel(Params p) {
+  scan_body<FEW, SEG, OUT, L2, W, false>(p);
+}
+
+// Prefills whose tokens all fit one chunk: each (sequence, v-head, half)
+// workgroup prepares its sequence's chunk in LDS and scans it, in one launch.
+template <bool L2>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void one_chunk_kernel(Params p) {
+  scan_body<false, false, true, L2, kThreads / 64, true>(p);
 }
 
 // ---------------------------------------------------------------------------
@@ -1816,6 +1866,15 @@ SegPlan seg_plan(long long L, long long N, long long HV) {
 // the CUs runs as half-state workgroups of 4 waves (two per (sequence,
 // v-head), one wave a SIMD): chunk steps at about half the cost.
 bool half_state_scan(long long N, long long HV) { return N >= 1 && 2 * N * HV <= kCUs; }
+
+// Prefills past the token path whose tokens all fit one chunk (so every
+// sequence is one chunk), with half-state workgroups that fit the GPU at
+// once: one launch in which each (sequence, v-head, half) workgroup prepares
+// its chunk in LDS and scans it -- no workspace round trip and one launch
+// instead of the preparation's and the scan's.
+bool fused_prefill(long long L, long long N, long long HV) {
+  return L > kSmallTokens && L <= kChunk && half_state_scan(N, HV);
+}
 
 bool use_segments(long long L, long long N, long long HV) {
   if (N < 1 || N > kFewSeqs || N * HV > kSegMaxHeads) return false;
@@ -2038,6 +2097,26 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
     if (e == hipSuccess) e = mark(3);
     return e;
   }
+  // One workgroup per (sequence or segment role, v-head, column half), in
+  // groups of 8 (unit, q/k head) pairs times the GVA ratio times the halves.
+  auto scan_grid = [&](long long units, int halves) {
+    return dim3(static_cast<unsigned>((units * H + 7) / 8 * 8 * p.ratio * halves));
+  };
+  if (fused_prefill(total_seq_len, num_seqs, HV)) {
+    // one launch (the timed form's intervals as on the token path)
+    hipError_t e = mark(0);
+    if (e == hipSuccess) e = mark(1);
+    if (e == hipSuccess) e = mark(2);
+    if (e != hipSuccess) return e;
+    p.short_limit = 0;
+    constexpr int kHalfW = kScanWaves / 2;
+    static_assert(kHalfW == kThreads / 64, "the one-chunk kernel's workgroups are half-state");
+    auto* fused = p.l2norm ? one_chunk_kernel<true> : one_chunk_kernel<false>;
+    hipLaunchKernelGGL(fused, scan_grid(num_seqs, 2), dim3(kThreads), 0, stream, p);
+    e = hipGetLastError();
+    if (e == hipSuccess) e = mark(3);
+    return e;
+  }
   hipError_t e = mark(0);
   if (e != hipSuccess) return e;
   if (p.short_limit > 0) {
@@ -2065,11 +2144,6 @@ static int prefill_impl(const void* q, const void* k, const void* v, const float
   }
   e = mark(2);
   if (e != hipSuccess) return e;
-  // One workgroup per (sequence or segment role, v-head, column half), in
-  // groups of 8 (unit, q/k head) pairs times the GVA ratio times the halves.
-  auto scan_grid = [&](long long units, int halves) {
-    return dim3(static_cast<unsigned>((units * H + 7) / 8 * 8 * p.ratio * halves));
-  };
   if (p.seg_chunks > 0) {
     // segments: transitions and zero-start ends, the starts, then every
     // segment with its outputs (grids: the workspace's segments bound the
@@ -2156,6 +2230,7 @@ int gdn_prefill_token_path_max_tokens(void) { return kSmallTokens; }
 int gdn_prefill_dispatches(int total_seq_len, int num_seqs, int HV) {
   if (num_seqs <= 0 || total_seq_len < 0 || HV <= 0) return 0;
   if (total_seq_len <= kSmallTokens && num_seqs <= 65535) return 1;
+  if (fused_prefill(total_seq_len, num_seqs, HV)) return 1;
   const int offsets = num_seqs == 1 || few_seqs(total_seq_len, num_seqs, HV) ? 0 : 1;
   const int token = maybe_all_short(total_seq_len, num_seqs) ? 1 : 0;
   if (use_segments(total_seq_len, num_seqs, HV)) return token + offsets + 4;

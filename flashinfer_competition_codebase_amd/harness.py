@@ -52,8 +52,9 @@ Command line (arguments as scripts/shared.py:93-142):
 In the trace tier a prefill call is its dispatches (``prefill_dispatches``:
 the chunk-offsets scan for several sequences, preparation and scan, two more
 with segments, the token-by-token kernel first for a batch that may be all
-short sequences -- or that kernel alone for a prefill of at most 56 tokens),
-timed from the first one's start to the last one's end.
+short sequences -- or that kernel alone for a prefill of at most 56 tokens,
+or the one-chunk kernel alone for 57 to 64), timed from the first one's
+start to the last one's end.
 """
 
 from __future__ import annotations

@@ -62,8 +62,9 @@ def token_path_max_tokens() -> int:
 
 def prefill_dispatches(total_seq_len: int, num_seqs: int, HV: int) -> int:
     """Kernel dispatches of one prefill call over HV v-heads, as the library
-    makes them (``gdn_prefill_dispatches``): 0 for no sequences, 1 on the
-    token-by-token path; else 2 (preparation, scan) or, for a batch scanned
+    makes them (``gdn_prefill_dispatches``): 0 for no sequences, 1 for the
+    token-by-token kernel or the one-chunk kernel (57..64 tokens in all, at
+    most 128 (sequence, v-head) pairs); else 2 (preparation, scan) or, for a batch scanned
     in segments, 4 (preparation, two segment scans and their combine), plus
     the chunk-offsets scan first unless there is one sequence or at most 64
     with at most 2048 (slot, v-head) pairs, plus the token-by-token kernel

@@ -73,7 +73,11 @@ size_t gdn_prefill_workspace_bytes(int total_seq_len, int num_seqs, int H, int H
  * Python caller), and bad arguments return an error instead of launching.
  * q, k, v, output, state and new_state must be 16-byte aligned.
  * Launches one kernel when total_seq_len <= gdn_prefill_token_path_max_tokens()
- * (and num_seqs <= 65535), else the chunkwise kernels: the chunk-offsets
+ * (and num_seqs <= 65535): the token-by-token kernel; one kernel when
+ * total_seq_len is past that but at most 64 (every sequence one chunk) and
+ * num_seqs x HV <= 128: the one-chunk kernel, each workgroup of which
+ * prepares its sequence's chunk in LDS and scans it; else the chunkwise
+ * kernels: the chunk-offsets
  * scan (not for one sequence, nor for at most 64 whose slots the kernels
  * find themselves), preparation, scan (for a few sequences whose scans would
  * leave most CUs idle: their segments scanned at once in two launches with
@@ -98,9 +102,9 @@ int gdn_prefill(const void* q, const void* k, const void* v, const float* state,
  * hipEventElapsedTime gives each kernel's time (the segmented scan's two or
  * three launches lie between events 2 and 3).  Without an offsets launch
  * (one sequence, or few: see gdn_prefill_dispatches) events 0 and 1 are
- * recorded back to back; on the
- * token-by-token path events 0..2 are, and its one launch lies between
- * events 2 and 3.  Nothing is recorded when num_seqs is 0.
+ * recorded back to back; with one kernel (the token-by-token kernel or the
+ * one-chunk kernel) events 0..2 are, and its launch lies between events 2
+ * and 3.  Nothing is recorded when num_seqs is 0.
  */
 int gdn_prefill_timed(const void* q, const void* k, const void* v, const float* state,
                       const float* A_log, const void* a, const float* dt_bias, const void* b,
@@ -145,7 +149,8 @@ int gdn_prefill_token_path_max_tokens(void);
 
 /*
  * Kernel launches gdn_prefill makes for these sizes: 0 for no sequences, 1
- * on the token-by-token path; else the chunkwise kernels -- 2 (preparation,
+ * for the token-by-token kernel or the one-chunk kernel; else the chunkwise
+ * kernels -- 2 (preparation,
  * scan), or 4 for a batch scanned in segments (preparation, first segment
  * scan, combine, second segment scan) -- plus 1 for the chunk-offsets scan
  * first, except for a single sequence and for at most 64 with at most 2048

@@ -604,8 +604,9 @@ def test_malformed_cu_seqlens_when_all_may_be_short(cu, n0, hip_device):
     call completes with finite results, twice the same states (the output
     rows of overlapping ranges are written by several sequences, in no fixed
     order), and the first, well-formed sequence gets the state it gets alone
-    (alone it takes the same path: the token kernel at 30 tokens, the
-    chunkwise ones at 60)."""
+    (alone: the token kernel at 30 tokens, as in the batch; the one-chunk
+    kernel at 60, which runs the chunkwise kernels' arithmetic, bit for
+    bit)."""
     L = 90
     N = len(cu) - 1
     assert gdn.prefill.prefill_dispatches(L, N, 8) >= 3
@@ -629,3 +630,74 @@ def test_malformed_cu_seqlens_when_all_may_be_short(cu, n0, hip_device):
     _, st1 = gdn.prefill_run(**_dev(alone, hip_device))
     torch.cuda.synchronize()
     assert torch.equal(st[:1], st1)
+
+
+@pytest.mark.parametrize("seqlens,H,HV,l2,with_state", [
+    ([64], 4, 8, False, True),            # one full chunk
+    ([57], 16, 32, True, True),           # just past the token path, qk16_v32, L2-norm
+    ([60], 1, 1, False, False),           # one head, no initial state
+    ([30, 30], 4, 8, False, True),
+    ([0, 64, 0], 2, 4, True, True),       # empty sequences around a full chunk
+    ([16] * 4, 16, 32, False, True),      # 4 x 32 = 128 (sequence, v-head) pairs: the most
+    ([8] * 8, 4, 8, True, False),
+    ([1, 63], 3, 12, False, True),        # GVA ratio 4, a one-token sequence
+])
+def test_one_chunk_kernel(seqlens, H, HV, l2, with_state, hip_device):
+    """Prefills of 57..64 tokens in all (so every sequence is one chunk) with
+    at most 128 (sequence, v-head) pairs: one launch of the one-chunk kernel,
+    in which each workgroup prepares its chunk in LDS and scans it.  Against
+    the oracle; in place equal to out of place bitwise; the timed entry's
+    third interval is the launch."""
+    import ctypes
+    L, N = sum(seqlens), len(seqlens)
+    assert L > gdn.prefill.token_path_max_tokens()
+    assert gdn.prefill.prefill_dispatches(L, N, HV) == 1
+    _announce(f"one-chunk kernel seqlens={seqlens} H={H} HV={HV} l2={l2} state={with_state}")
+    t = make_prefill_inputs(seqlens, H, HV, seed=700 + L + N + H, with_state=with_state)
+    td = _dev(t, hip_device)
+    out, st = gdn.prefill_run(**td, use_qk_l2norm=l2)
+    torch.cuda.synchronize()
+    _check(t, out, st, l2=l2)
+    if with_state:
+        state = td["state"].clone()
+        out2 = torch.empty_like(out)
+        gdn.kernel_prefill_hip(**{**td, "state": state}, output=out2, new_state=state,
+                               use_qk_l2norm=l2)
+        torch.cuda.synchronize()
+        assert torch.equal(out2, out) and torch.equal(state, st)
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    evs = []
+    for _ in range(4):
+        e = ctypes.c_void_p()
+        assert hip.hipEventCreate(ctypes.byref(e)) == 0
+        evs.append(e)
+    try:
+        out3, st3 = torch.empty_like(out), torch.empty_like(st)
+        gdn.kernel_prefill_hip_timed(**td, output=out3, new_state=st3, events=evs,
+                                     use_qk_l2norm=l2)
+        torch.cuda.synchronize()
+        assert torch.equal(out3, out) and torch.equal(st3, st)
+        x = ctypes.c_float()
+        assert hip.hipEventElapsedTime(ctypes.byref(x), evs[2], evs[3]) == 0 and x.value > 0.0
+    finally:
+        for e in evs:
+            hip.hipEventDestroy(e)
+
+
+@pytest.mark.parametrize("l2", [False, True])
+def test_one_chunk_kernel_matches_the_chunkwise_kernels_bitwise(l2, hip_device):
+    """A 64-token sequence alone (the one-chunk kernel) and first in a batch
+    of 64 + 65 tokens (the preparation kernel, one v-head a workgroup, and
+    the half-state scan): the same bits, since the one-chunk kernel runs
+    those kernels' arithmetic with the slot kept in LDS."""
+    _announce(f"one-chunk kernel vs chunkwise kernels, bitwise, l2={l2}")
+    t = make_prefill_inputs([64, 65], 4, 8, seed=71)
+    assert gdn.prefill.prefill_dispatches(129, 2, 8) == 2
+    assert gdn.prefill.prefill_dispatches(64, 1, 8) == 1
+    out_c, st_c = gdn.prefill_run(**_dev(t, hip_device), use_qk_l2norm=l2)
+    alone = {**t, "q": t["q"][:64], "k": t["k"][:64], "v": t["v"][:64], "a": t["a"][:64],
+             "b": t["b"][:64], "state": t["state"][:1],
+             "cu_seqlens": torch.tensor([0, 64], dtype=torch.int32)}
+    out_1, st_1 = gdn.prefill_run(**_dev(alone, hip_device), use_qk_l2norm=l2)
+    torch.cuda.synchronize()
+    assert torch.equal(out_1, out_c[:64]) and torch.equal(st_1, st_c[:1])

@@ -160,7 +160,8 @@ def test_prefill_mix():
     assert all((w.H, w.HV, w.use_qk_l2norm) == (4, 8, False) for w in ws)
     assert any(0 in w.lens for w in ws)              # empty sequences
     assert max(max(w.lens) for w in ws) == 16384   # longest single sequence
-    assert [w.dispatches for w in ws[:3]] == [1, 1, 2]   # 6 and 1 tokens: the token path
+    # 6 and 1 tokens: the token path; 64 tokens: the one-chunk kernel; 65: prep and scan
+    assert [w.dispatches for w in ws[:4]] == [1, 1, 1, 2]
     from flashinfer_competition_codebase_amd.prefill import token_path_max_tokens
     from tests.gdn_cases import prefill_segment_plan
     small = token_path_max_tokens()
@@ -168,6 +169,8 @@ def test_prefill_mix():
         slots = min((w.L + 63) // 64 + w.N, w.L)
         if w.L <= small:
             return 1                                  # the token path
+        if w.L <= 64 and 2 * w.N * w.HV <= 256:
+            return 1                                  # the one-chunk kernel
         offsets = 0 if w.N == 1 or (w.N <= 64 and slots * w.HV <= 2048) else 1
         token = 1 if 2 <= w.N <= 64 and w.L <= w.N * small else 0   # token kernel first
         if prefill_segment_plan(w.L, w.N, w.HV)[0]:
@@ -233,7 +236,7 @@ def _prefill_trace_csv(tmp_path, calls):
 
 def test_prefill_trace_attribution_spans_the_calls_dispatches(tmp_path):
     ws = harness.prefill_workloads()
-    w0, w2 = ws[0], ws[2]                            # 1 and 2 dispatches per call
+    w0, w2 = ws[0], ws[3]                            # 1 and 2 dispatches per call
     w11 = harness.PrefillWorkload(uuid="prefill-70x1", lens=(1,) * 70, seed=1)   # 3
     assert (w0.dispatches, w2.dispatches, w11.dispatches) == (1, 2, 3)
     m = harness.Manifest()
@@ -283,10 +286,15 @@ def test_prefill_dispatch_count_follows_the_token_path_threshold():
     m = token_path_max_tokens()
     assert m == 56
     assert prefill_dispatches(m, 1, 8) == 1 and prefill_dispatches(0, 5, 8) == 1
-    assert prefill_dispatches(m + 1, 1, 8) == 2           # one longer sequence
+    # past it, at most one chunk (64 tokens) in all and at most 128 (sequence,
+    # v-head) pairs: the one-chunk kernel alone
+    assert prefill_dispatches(m + 1, 1, 8) == 1 and prefill_dispatches(64, 1, 8) == 1
+    assert prefill_dispatches(64, 16, 8) == 1 and prefill_dispatches(64, 4, 32) == 1
+    assert prefill_dispatches(65, 1, 8) == 2              # two chunks: prep and scan
     # 2..64 sequences of at most m tokens on average: the token kernel first
     # (it runs if every sequence is that short), then prep and scan
-    assert prefill_dispatches(m + 1, 2, 8) == 3
+    assert prefill_dispatches(64, 17, 8) == 3             # 136 pairs: no one-chunk kernel
+    assert prefill_dispatches(65, 2, 8) == 3
     assert prefill_dispatches(2 * m, 2, 8) == 3 and prefill_dispatches(2 * m + 1, 2, 8) == 2
     assert prefill_dispatches(80, 4, 8) == 3              # 4 x 20 tokens
     assert prefill_dispatches(m + 1, 64, 8) == 3          # slots found in the kernels

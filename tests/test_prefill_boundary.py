@@ -51,7 +51,8 @@ def test_workspace_size_formula():
                         (8192, 1, 16, 64), (2048, 1, 4, 8), (384, 1, 4, 8), (320, 1, 4, 8),
                         (1024, 1, 16, 32), (4096, 1, 16, 32), (700, 1, 2, 2),
                         (39503, 8, 4, 8), (3600, 3, 4, 8), (5000, 2, 16, 32), (8192, 8, 16, 32),
-                        (20000, 64, 1, 2), (3000, 65, 1, 1)):
+                        (20000, 64, 1, 2), (3000, 65, 1, 1), (64, 1, 4, 8), (57, 2, 16, 32),
+                        (64, 4, 16, 32), (60, 5, 16, 32), (64, 16, 4, 8), (64, 17, 4, 8)):
         chunks = min((L + 63) // 64 + N, L)          # the most a well-formed batch has
         offs = a256((N + 1) * 4)
         table = a256(chunks * 16)                                        # per-chunk slot table
@@ -65,8 +66,11 @@ def test_workspace_size_formula():
         offsets = 0 if N == 1 or (N <= 64 and chunks * HV <= 2048) else 1
         # 2..64 sequences of at most 56 tokens on average: the token kernel first
         token = 1 if 2 <= N <= 64 and 56 < L <= 56 * N else 0
+        # at most one chunk in all, half-state workgroups on at most all CUs:
+        # the one-chunk kernel alone
+        one_chunk = 56 < L <= 64 and 2 * N * HV <= 256
         assert lib.gdn_prefill_dispatches(L, N, HV) == (
-            0 if N == 0 else 1 if L <= 56 and N <= 65535 else
+            0 if N == 0 else 1 if (L <= 56 and N <= 65535) or one_chunk else
             token + offsets + (4 if seg else 2)), (L, N, HV)
     assert lib.gdn_prefill_workspace_bytes(-1, 1, 4, 8) == 0
     assert lib.gdn_prefill_workspace_bytes(1, 1, 4, 0) == 0
