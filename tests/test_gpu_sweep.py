@@ -20,7 +20,9 @@ Two more sweeps reach the sizes the first two keep clear of: decode batches
 up to 256 (the launch-shape table's larger rows, the XCD-grouped launches,
 the block kernel) at up to 8 tokens, and prefills of up to 100 sequences
 (the chunk-offsets scan) and up to 1500 tokens a sequence (segments), at up
-to 32 v-heads.  Their decode keys are raw N(0, 1) rows only for single
+to 32 v-heads, and ragged batches of 57 to 64 tokens in all through the
+one-chunk kernel, bit for bit against the chunkwise kernels.  The larger
+decode sweep's keys are raw N(0, 1) rows only for single
 tokens: over several tokens without the L2-norm they are scaled to unit norm
 first (the normalisation the model applies before this step; raw keys grow
 the state to 400-1400 within 2 to 4 tokens, where the fp32 oracle itself
@@ -324,3 +326,40 @@ def test_prefill_thousands_of_sequences(N, longest, H, HV, seed, hip_device):
     for s, n in enumerate(lens):
         if n == 0:
             assert not np.any(sd[s])
+
+
+def _one_chunk_case(i):
+    r = random.Random(88000 + i)
+    H, HV = r.choice([(1, 1), (1, 4), (2, 4), (4, 8), (3, 12), (2, 16), (8, 32), (16, 32), (1, 8)])
+    while True:
+        N = r.randint(1, 16)
+        if 2 * N * HV <= 256:
+            break
+    L = r.randint(57, 64)
+    cuts = sorted(r.randint(0, L) for _ in range(N - 1))
+    return [b - a for a, b in zip([0] + cuts, cuts + [L])], H, HV, r.random() < 0.5, r.random() < 0.8
+
+
+@pytest.mark.parametrize("i", range(24))
+def test_one_chunk_sweep(i, hip_device):
+    """Ragged batches of 57..64 tokens in all (empty sequences among them):
+    the one-chunk kernel against the float64 oracle, and bit for bit against
+    the chunkwise kernels, which run the same batch with a 65-token sequence
+    appended."""
+    lens, H, HV, l2, with_state = _one_chunk_case(i)
+    L, N = sum(lens), len(lens)
+    _announce(f"one-chunk sweep {i}: lens={lens} H={H} HV={HV} l2={l2} state={with_state}")
+    assert gdn.prefill.prefill_dispatches(L, N, HV) == 1
+    t = make_prefill_inputs(lens + [65], H, HV, seed=89000 + i, with_state=with_state)
+    tb = {**t, "q": t["q"][:L], "k": t["k"][:L], "v": t["v"][:L], "a": t["a"][:L],
+          "b": t["b"][:L], "state": None if t["state"] is None else t["state"][:N],
+          "cu_seqlens": t["cu_seqlens"][:N + 1]}
+    out1, st1 = gdn.prefill_run(**_dev(tb, hip_device), use_qk_l2norm=l2)
+    out_c, st_c = gdn.prefill_run(**_dev(t, hip_device), use_qk_l2norm=l2)
+    torch.cuda.synchronize()
+    o64, s64 = prefill_chunked_fp64(**tb, use_qk_l2norm=l2)
+    d64 = np.abs(out1.cpu().double().numpy() - o64)
+    assert np.all(d64 <= 2.0 ** -7 * np.abs(o64) + 1e-5), f"output vs fp64: max {d64.max():.3e}"
+    ds = np.abs(st1.cpu().double().numpy() - s64)
+    assert np.all(ds <= 1e-3 * np.abs(s64) + 1e-5), f"state vs fp64: max {ds.max():.3e}"
+    assert torch.equal(out1, out_c[:L]) and torch.equal(st1, st_c[:N])
