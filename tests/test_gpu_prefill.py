@@ -339,8 +339,8 @@ def test_many_empty_sequences_past_the_token_paths_grid(hip_device):
 
 @pytest.mark.parametrize("cu,L", [
     ([0, 30, 5, 40, 100], 40),         # decreasing and past L; 40 tokens: the token path
-    ([0, 58, 10, 60, 200, 30], 60),    # the same at 60 tokens: chunkwise, slots in the kernels
-    ([0, 58] + [10, 60, 200, 30] * 20, 60),   # 81 sequences: the chunk-offsets scan
+    ([0, 58, 10, 60, 200, 30], 60),    # the same at 60 tokens: the one-chunk kernel
+    ([0, 58] + [10, 60, 200, 30] * 20, 60),   # 81 sequences: chunkwise, the chunk-offsets scan
 ])
 def test_malformed_cu_seqlens_stay_in_bounds(cu, L, hip_device):
     """cu_seqlens that decrease or pass L: every kernel clamps each range to
@@ -348,7 +348,8 @@ def test_malformed_cu_seqlens_stay_in_bounds(cu, L, hip_device):
     the first sequence, a well-formed range, gets the state that a call with
     it alone gives (bitwise: the same arithmetic on every path; past 40 tokens
     the first sequence is longer than the token-path switch, so that alone it
-    runs chunkwise too)."""
+    runs the one-chunk kernel, the chunkwise kernels' arithmetic in one
+    launch)."""
     N = len(cu) - 1
     _announce(f"malformed cu_seqlens N={N} L={L}")
     t = make_prefill_inputs([L] + [0] * (N - 1), 4, 8, seed=91)
